@@ -1,0 +1,251 @@
+"""Benchmark of the GPT-OSS-120B MoE decode hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B] [--packed] [--skip-cpu]
+
+Workload (configuration 1 of the benchmark plan): all 36 layers x 128 experts resident in one HBM pool (60.9 GB raw
+MXFP4 slots: uniform E2M1 codes, E8M0 exponents uniform in [119, 125]); B decode tokens; per token and layer, top-4
+of 128 experts from random router logits, softmax weights.  One STEP = the expert body of all 36 layers in sequence
+(per layer: gate_up GEMV + bias + clamped SwiGLU, down GEMV + bias + routing weight, top-k combine), captured as
+one hipGraph per routing set; 16 routing sets are cycled so the 256 MB Infinity Cache never serves a repeated
+expert.  value = decode tokens per second of that step (B tokens per step), whole job.
+
+Also printed on the same JSON line:
+  roofline      the dominant kernel (gate_up): algorithmic bytes per launch (distinct experts x 8,812,800 B of codes +
+                E8M0 scales) / its average launch duration, measured with events timestamped by the dispatches
+                themselves (hipExtLaunchKernel) on the launch stream, over an eager pass of the same steps; peak = 8 TB/s.
+  cpu_baseline  the reference's own C expert kernel (kernels/gptoss_cpu_multi.c, AVX-512, or gptoss_cpu_portable.c,
+                built from source into oracle/_ref/) on this host's cores over a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode tok/s GPT-OSS-120B shape; MXFP4 expert GEMV HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+GATE_UP_BYTES = 5760 * 1440 + 5760 * 90          # codes + E8M0 scales of one expert's gate_up rows
+DOWN_BYTES = 2880 * 1440 + 2880 * 90
+SLOT_ALGO_BYTES = GATE_UP_BYTES + DOWN_BYTES      # 13,219,200
+N_LAYERS, N_EXPERTS, TOPK, H = 36, 128, 4, 2880
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def routing_sets(rng, n_sets, B):
+    """[n_sets, 36, B, 4] int64 ids and bf16-valued fp32 weights from random router logits (top-4, softmax)."""
+    logits = rng.standard_normal((n_sets, N_LAYERS, B, N_EXPERTS)).astype(np.float32)
+    ids = np.argsort(-logits, axis=-1, kind="stable")[..., :TOPK]
+    top = np.take_along_axis(logits, ids, axis=-1)
+    e = np.exp(top - top[..., :1])
+    w = (e / e.sum(-1, keepdims=True)).astype(np.float32)
+    return ids.astype(np.int64), w
+
+
+def cpu_baseline(pool_dev, ids, B, seconds=12.0):
+    """The reference C kernel on host cores: gptoss_experts(4, ...) per token per layer (the reference has no batched
+    CPU decode), over a 32-expert host copy of the pool rotated per call so the L3 stays cold."""
+    import torch
+
+    from oracle.refkernels import RefExperts, cpu_has
+
+    name = "multi" if cpu_has("avx512f") else "portable"
+    ref = RefExperts(name)
+    threads = min(16, os.cpu_count() or 1)
+    uniq = []
+    for e in ids.reshape(-1).tolist():
+        if e not in uniq:
+            uniq.append(e)
+        if len(uniq) == 32:
+            break
+    host = [pool_dev[e].cpu().numpy() for e in uniq]          # slots of layer 0
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(H).astype(np.float32)
+    bgu = [np.zeros(5760, np.float32)] * 4
+    bdn = [np.zeros(2880, np.float32)] * 4
+    w = np.full(4, 0.25, np.float32)
+    scratch = np.zeros(4 * (5760 + 3 * H) + H + 64, np.float32)
+    ref.experts(host[:4], x, bgu, bdn, w, threads=threads, scratch=scratch)      # warm-up (thread pool start)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        sel = [host[(4 * n + j) % len(host)] for j in range(4)]
+        ref.experts(sel, x, bgu, bdn, w, threads=threads, scratch=scratch)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= N_LAYERS:
+            break
+    t_call = el / n
+    tok_s = 1.0 / (N_LAYERS * t_call)
+    return {"value": round(tok_s, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "sample": f"{n} calls of gptoss_experts(E=4) (libgptoss_{name}.so, {threads} OpenMP threads) over a "
+                      f"{len(host)}-expert host copy rotated per call; one call = one layer of one token; "
+                      f"{t_call * 1e3:.3f} ms/call -> {4 * SLOT_ALGO_BYTES / t_call / 1e9:.1f} GB/s; "
+                      f"tok/s = 1 / (36 x ms/call)",
+            "gbps": round(4 * SLOT_ALGO_BYTES / t_call / 1e9, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--packed", action="store_true", help="PS4 scale layout instead of raw")
+    ap.add_argument("--sets", type=int, default=16, help="routing sets (graphs) cycled over the steps")
+    ap.add_argument("--roofline-steps", type=int, default=20)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--gu-pairs", type=int, default=16)
+    ap.add_argument("--dn-pairs", type=int, default=8)
+    A = ap.parse_args()
+    if A.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {A.gpus} is not supported (the design note on "
+              f"sharding across GPUs is in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if not 1 <= A.batch <= 8:
+        sys.exit("--batch must be in [1, 8]")
+
+    import torch
+
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4
+    from neural_amd import synth
+
+    dev = torch.device("cuda", 0)
+    L = GPTOSS_LAYOUT_PS4 if A.packed else GPTOSS_LAYOUT
+    n_slots = N_LAYERS * N_EXPERTS
+    log(f"allocating pool {n_slots} x {L.slot_bytes} B = {n_slots * L.slot_bytes / 1e9:.1f} GB ({L.weight_repr})")
+    pool = torch.empty((n_slots, L.slot_bytes), dtype=torch.uint8, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    cb = L.gate_pack_bytes + L.down_pack_bytes
+    pool[:, :cb].random_(0, 256, generator=g)
+    if A.packed:
+        # PS4 rows: base in [119, 125 - 15]... keep exponents in [119, 125]: base 119, deltas 0..6 per nibble
+        sc = pool[:, cb:].view(n_slots, -1, 46)
+        sc[:, :, 0].fill_(119)
+        lo = torch.randint(0, 7, sc[:, :, 1:].shape, dtype=torch.uint8, device=dev, generator=g)
+        hi = torch.randint(0, 7, sc[:, :, 1:].shape, dtype=torch.uint8, device=dev, generator=g)
+        sc[:, :, 1:] = lo | (hi << 4)
+        del lo, hi
+    else:
+        pool[:, cb:].random_(synth.SCALE_LO, synth.SCALE_HI + 1, generator=g)
+    torch.cuda.synchronize()
+    log("pool filled")
+    bias_gu = torch.zeros(n_slots, L.gate_up_n, dtype=torch.bfloat16, device=dev)
+    bias_dn = torch.zeros(n_slots, L.down_n, dtype=torch.bfloat16, device=dev)
+    rx = ResidentExperts(pool, L, bias_gu, bias_dn, gu_pairs_per_wg=A.gu_pairs, dn_pairs_per_wg=A.dn_pairs)
+
+    B = A.batch
+    rng = np.random.default_rng(2026)
+    ids_np, w_np = routing_sets(rng, A.sets, B)
+    distinct = np.array([[len(set(ids_np[s, l].reshape(-1).tolist())) for l in range(N_LAYERS)]
+                         for s in range(A.sets)])
+    ids = torch.from_numpy(ids_np).to(dev)
+    wts = torch.from_numpy(w_np).to(torch.bfloat16).to(dev)
+    x = synth.bf16_normal(rng, (N_LAYERS, B, H)).to(dev)
+    out = torch.empty(N_LAYERS, B, H, dtype=torch.bfloat16, device=dev)
+
+    def step(s, events=None):
+        for l in range(N_LAYERS):
+            rx.forward_decode(l, x[l], ids[s, l], wts[s, l], out=out[l],
+                              events=None if events is None else events[l])
+
+    # eager warm-up, then one graph per routing set
+    step(0)
+    torch.cuda.synchronize()
+    graphs = []
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        step(0)
+    torch.cuda.current_stream().wait_stream(cs)
+    for s in range(A.sets):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            step(s)
+        graphs.append(gr)
+    torch.cuda.synchronize()
+    log(f"captured {len(graphs)} graphs of {3 * N_LAYERS} kernels; warm-up {A.warmup} steps")
+    for i in range(A.warmup):
+        graphs[i % A.sets].replay()
+    torch.cuda.synchronize()
+
+    # ------------------------------------------------------------------ timed region
+    t0 = time.perf_counter()
+    for i in range(A.steps):
+        graphs[i % A.sets].replay()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    ms_step = el / A.steps * 1e3
+    tok_s = B * A.steps / el
+    step_bytes = np.mean([distinct[i % A.sets].sum() for i in range(A.steps)]) * SLOT_ALGO_BYTES
+    log(f"timed {A.steps} steps: {ms_step:.3f} ms/step, {tok_s:.1f} tok/s, "
+        f"{step_bytes / (ms_step * 1e-3) / 1e9:.0f} GB/s whole-step")
+
+    # ------------------------------------------------------------------ roofline pass (per-kernel events)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(N_LAYERS)]
+    for row in ev:
+        for e in row:
+            e.record()
+    torch.cuda.synchronize()
+    tot = {"gate_up": [0.0, 0.0, 0], "down": [0.0, 0.0, 0], "combine": [0.0, 0.0, 0]}
+    for r in range(A.roofline_steps):
+        s = r % A.sets
+        step(s, events=ev)
+        torch.cuda.synchronize()
+        for l in range(N_LAYERS):
+            d = int(distinct[s, l])
+            for k, (nm, per) in enumerate((("gate_up", GATE_UP_BYTES), ("down", DOWN_BYTES), ("combine", 0))):
+                ms = ev[l][2 * k].elapsed_time(ev[l][2 * k + 1])
+                tot[nm][0] += ms
+                tot[nm][1] += d * per
+                tot[nm][2] += 1
+    kern = {nm: {"avg_us": v[0] / v[2] * 1e3, "gbps": (v[1] / (v[0] * 1e-3) / 1e9) if v[0] else 0.0}
+            for nm, v in tot.items()}
+    for nm, v in kern.items():
+        log(f"kernel {nm}: avg {v['avg_us']:.2f} us/launch, {v['gbps']:.0f} GB/s algorithmic")
+    gu = kern["gate_up"]
+    per_launch = tot["gate_up"][1] / tot["gate_up"][2]
+    roofline = {"bound": "hbm", "achieved": round(gu["gbps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gu["gbps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "k_moe_gate_up", "avg_launch_us": round(gu["avg_us"], 3),
+                "algorithmic_bytes_per_launch": int(per_launch),
+                "down_kernel_gbps": round(kern["down"]["gbps"], 1), "down_avg_launch_us": round(kern["down"]["avg_us"], 3),
+                "combine_avg_launch_us": round(kern["combine"]["avg_us"], 3)}
+
+    cpu = None
+    if not A.skip_cpu:
+        try:
+            log("cpu baseline (reference C kernel) ...")
+            cpu = cpu_baseline(pool, ids_np[0, 0], B, A.cpu_seconds)
+            log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads ({cpu['gbps']} GB/s)")
+        except Exception as e:      # the baseline is reported, not required
+            log(f"cpu baseline unavailable: {e!r}")
+            cpu = {"value": None, "unit": "tok/s", "cores": 0, "kind": "reference", "sample": f"unavailable: {e}"}
+
+    res = {"metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": A.steps,
+           "warmup": A.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+           "config": {"workload": f"config1: decode expert body (gate_up+SwiGLU-clamp+down+combine), 36 layers x "
+                                  f"128 experts resident ({L.weight_repr}), batch {B}, random top-4 routing",
+                      "batch": B, "layers": N_LAYERS, "experts_resident": n_slots,
+                      "pool_gb": round(n_slots * L.slot_bytes / 1e9, 2),
+                      "distinct_experts_per_layer": round(float(distinct.mean()), 3),
+                      "step_algorithmic_gb": round(step_bytes / 1e9, 4),
+                      "step_hbm_gbps": round(step_bytes / (ms_step * 1e-3) / 1e9, 1)},
+           "roofline": roofline, "cpu_baseline": cpu}
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,75 @@
+/* neural_amd: C ABI of the MI355X (gfx950) GPT-OSS-120B MoE hot path.
+ *
+ * Every entry point takes raw device pointers, plain sizes and the hipStream_t to launch on; it allocates nothing,
+ * never synchronises and never reads device data on the host, so it can be recorded into a hipGraph.  Return value:
+ * 0 = launched, -1 = invalid arguments (nothing launched), -2 = launch error (hipGetLastError), -3 = a size beyond
+ * the kernel's fixed limits (nothing launched).
+ *
+ * Data conventions: bf16 tensors are arrays of uint16 bit patterns; expert slots follow the store layout of the
+ * reference (neural/moe/layout.py:143-186): gate_codes [5760][90][16] | down_codes [2880][90][16] | scales, with raw
+ * (one E8M0 byte per group, 13,219,200 B) or PS4 (46-byte rows: base + 4-bit deltas, 12,839,040 B) scale rows.
+ *
+ * Each declaration names the reference interface it replaces (file:line under the reference repository).
+ */
+#ifndef NEURAL_AMD_H
+#define NEURAL_AMD_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library ABI version (1). */
+int na_version(void);
+
+/* Device self-check of the E2M1 -> bf16 conversion the kernels use: out = 768 uint16 (see csrc/abi.hip). */
+int na_selftest_fp4(void* out, hipStream_t stream);
+
+/* Decode GEMV over expert slots.  Replaces neural/q80/mxfp4_kernels.py:474-489 (mxfp4_gemv) and, with `active`,
+ * :542-569 (mxfp4_gemv_masked).
+ *   x        bf16 [1, K] (per_expert_x = 0) or [E, K] (per_expert_x = 1), K = 2880
+ *   blocks   u8 view [cap, N, 90, 16] with slot stride sb_slot bytes (rows contiguous)
+ *   scales   u8 view [cap, N, 90] (packed = 0) or [cap, N, 46] (packed = 1), slot stride ss_slot bytes
+ *   slots    int64 [E] physical slot of each output row block
+ *   active   optional per-slot weight (active_dtype 1 = bf16, 2 = fp32, 0 = none): a zero writes +0 rows and reads
+ *            no weights; NaN or nonzero computes
+ *   out      bf16 [E, N], N even
+ *   pairs_per_wg  row pairs streamed by one workgroup (<= 0: default 16) */
+int na_mxfp4_gemv(const void* x, int per_expert_x, const void* blocks, long long sb_slot, const void* scales,
+                  long long ss_slot, int packed, const int64_t* slots, int E, const void* active, int active_dtype,
+                  void* out, int N, int K, int pairs_per_wg, hipStream_t stream);
+
+/* Fused decode expert body for B <= 8 tokens.  Replaces the reference's b_body (server.py:508-518: gate_up GEMV ->
+ * + bias -> clamped SwiGLU (neural/q80/expert_runtime.py:63-72) -> down GEMV -> + bias -> routing-weighted sum)
+ * and its graph twin _ExpertGraphV4._compute (neural/q80/expert_runtime.py:1361-1427), for an all-resident pool.
+ *   x          bf16 [B, 2880] (post-attention RMSNorm output)
+ *   topk_ids   int64 [B, 4] expert ids within the layer; topk_w bf16 [B, 4] routing weights
+ *   pool       u8 [n_slots, slot_bytes]; slot of expert id e = slot_tab ? slot_tab[expert_base + e] : expert_base + e
+ *   bias_gu    bf16 [*, 5760] / bias_dn bf16 [*, 2880] rows indexed by expert_base + e (NULL = no bias)
+ *   h_scratch  bf16 [4B, 2880], yw_scratch bf16 [4B, 2880]: caller-owned intermediates
+ *   out        bf16 [B, 2880]
+ *   alpha, limit  activation constants (1.702, 7.0)
+ *   gu_pairs_per_wg / dn_pairs_per_wg  row pairs per workgroup of the two products (<= 0: defaults 16 / 8)
+ *   events     NULL, or 6 hipEvent_t: start/stop of the gate_up, down and combine kernels, timestamped by the
+ *              dispatches themselves (hipExtLaunchKernel); for measurement only, not for graph capture
+ * Each distinct expert's weights are read once per call for all tokens routed to it. */
+int na_moe_decode(const void* x, const int64_t* topk_ids, const void* topk_w, int B, const void* pool,
+                  long long slot_bytes, int packed, const int64_t* slot_tab, long long expert_base,
+                  const void* bias_gu, const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha,
+                  float limit, int gu_pairs_per_wg, int dn_pairs_per_wg, void* const* events, hipStream_t stream);
+
+/* Router GEMV + top-4 + softmax.  Replaces fused_core.py:417-441 (k_router, logits part) and :460-486 (k_topk,
+ * selection and weights; the slot-table and host-pack bookkeeping of the offload design are not part of it).
+ *   xn bf16 [B, 2880], w_router bf16 [n_exp, 2880], b_router bf16 [n_exp] or NULL, n_exp <= 128
+ *   logits fp32 [B, n_exp] scratch; counter: one uint32 that must be 0 before the first call (left at 0)
+ *   ids_out int64 [B, 4], w_out bf16 [B, 4] */
+int na_router_topk(const void* xn, int B, const void* w_router, const void* b_router, int n_exp, float* logits,
+                   unsigned int* counter, int64_t* ids_out, void* w_out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NEURAL_AMD_H */

@@ -1,0 +1,76 @@
+"""ctypes binding of the C-ABI library neural_amd/_lib/libneural_amd.so (declared in include/neural_amd.h).
+
+torch is imported first on purpose: its wheel carries its own libamdhip64.so.7, and loading our library afterwards
+makes the dynamic linker resolve our DT_NEEDED libamdhip64.so.7 to that same runtime, so the hipStream_t values
+torch hands out (torch.cuda.current_stream().cuda_stream) are valid streams for our launches.
+
+There is no fallback: a missing library raises NativeLibraryMissing on first use.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede the CDLL load, see above)
+
+from .build import LIB_PATH
+
+VP, I32, I64, F32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_float
+
+# name -> argtypes (every entry point returns int: 0 = launched, < 0 = error code)
+SIGNATURES = {
+    "na_version": [],
+    "na_selftest_fp4": [VP, VP],
+    "na_mxfp4_gemv": [VP, I32, VP, I64, VP, I64, I32, VP, I32, VP, I32, VP, I32, I32, I32, VP],
+    "na_moe_decode": [VP, VP, VP, I32, VP, I64, I32, VP, I64, VP, VP, VP, VP, VP, F32, F32, I32, I32, VP, VP],
+    "na_router_topk": [VP, I32, VP, VP, I32, VP, VP, VP, VP, VP],
+}
+
+ERRORS = {-1: "invalid arguments", -2: "kernel launch failed", -3: "size beyond the kernel's limits"}
+
+
+class NativeLibraryMissing(RuntimeError):
+    pass
+
+
+_LIB = None
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise NativeLibraryMissing(f"{LIB_PATH} is missing: build it with `python -m neural_amd.build` "
+                                       "(there is no CPU fallback)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = I32
+        _LIB = handle
+    return _LIB
+
+
+def call(name: str, *args) -> None:
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        raise RuntimeError(f"{name}: {ERRORS.get(rc, 'error')} (status {rc})")
+
+
+def stream(device=None) -> int:
+    """Raw hipStream_t of torch's current stream on ``device``."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def events_array(events):
+    """ctypes array of raw hipEvent_t handles of recorded torch.cuda.Event objects (None -> NULL)."""
+    if events is None:
+        return None
+    handles = [e.cuda_event for e in events]
+    if not all(handles):
+        raise ValueError("timing events must have been recorded once (torch creates them lazily)")
+    return (VP * len(handles))(*handles)

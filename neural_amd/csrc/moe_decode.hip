@@ -1,0 +1,475 @@
+// Decode-time MXFP4 expert products for GPT-OSS-120B on gfx950 (MI355X): bandwidth kernels.
+//
+// What the reference does (Triton): neural/q80/mxfp4_kernels.py:430-569 (_mxfp4_gemv / _mxfp4_gemv_masked) and the
+// decode expert body server.py:508-518 (gate_up GEMV -> +bias -> clamped SwiGLU -> down GEMV -> +bias -> weighted sum).
+//
+// How this file does it:
+//   * A wavefront streams one ROW PAIR at a time: 2 x 1440 code bytes = 180 16-byte chunks (one chunk = one group of
+//     32 E2M1 codes).  Lane l loads chunks c = 64k + l (k = 0..2, c < 180) with 128-bit global loads: every load
+//     instruction is a contiguous run of 16-byte chunks of one row (or of the two rows when they are adjacent).
+//   * The lane -> (row of the pair, group) map is the same for every row pair, so a lane touches only 3 of the 90
+//     groups of x; x sits in LDS (padded to dodge bank conflicts) or, for <= 2 tokens, in registers.
+//   * Dequantisation is in registers: v_cvt_scalef32_pk_bf16_fp4 (exact) + v_dot2_f32_bf16 per code byte, then the
+//     group partial is scaled by 2^(s-127) with v_ldexp_f32 (exact) and accumulated in fp32.
+//   * Each row-pair's two sums are reduced across the wavefront; bf16 rounding points of the epilogues follow the
+//     reference's torch op sequence (common.h).
+//   * Decode routing is read on the device (top-k expert ids), so a step never syncs with the host and is
+//     hipGraph-capturable: work item w of a launch is the w-th DISTINCT expert of the batch (first-appearance order);
+//     it reads that expert's weights once for every token routed to it.
+#include "common.h"
+#include <hip/hip_ext.h>
+
+namespace na {
+
+constexpr int kWave = 64;
+constexpr int kWaves = 4;                 // waves per workgroup
+constexpr int kThreads = kWave * kWaves;
+constexpr int kXG = 20;                   // LDS dwords per x group (16 used, padded: 80 B stride, conflict-free b128)
+constexpr int kXTok = kGK * kXG;          // LDS dwords per staged token
+constexpr int kMaxTok = 8;                // tokens per expert per launch (decode batch <= 8)
+constexpr int kExpertsPerLayer = 128;
+
+// ----------------------------------------------------------------------------------------------- scales
+template <int PS4>
+NA_DEVICE int load_scale(const uint8_t* srow, int g) {
+  if (PS4) {
+    const int base = srow[0];
+    const int b = srow[1 + (g >> 1)];
+    return base + ((g & 1) ? (b >> 4) : (b & 15));
+  }
+  return srow[g];
+}
+
+// Lane -> chunk map of a row pair (GK = 90: 180 chunks over 3 wave-wide loads).
+struct LaneMap {
+  int g[3];
+  bool isB[3];
+  bool valid[3];
+};
+
+NA_DEVICE LaneMap lane_map(int lane) {
+  LaneMap m;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int c = 64 * k + lane;
+    m.valid[k] = c < 2 * kGK;
+    m.isB[k] = c >= kGK;
+    m.g[k] = m.isB[k] ? c - kGK : c;
+    if (!m.valid[k]) m.g[k] = 0;
+  }
+  return m;
+}
+
+// Stage token vectors [nt][2880] bf16 into LDS groups of kXG dwords.
+NA_DEVICE void stage_x(uint32_t* xs, const uint16_t* const* xsrc, int nt) {
+  for (int t = 0; t < nt; ++t) {
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(xsrc[t]);
+    for (int i = threadIdx.x; i < kGK * 4; i += kThreads) {      // 16-byte pieces: 4 per group
+      const int g = i >> 2, q = i & 3;
+      const uint4 v = *reinterpret_cast<const uint4*>(src + g * 16 + q * 4);
+      *reinterpret_cast<uint4*>(xs + t * kXTok + g * kXG + q * 4) = v;
+    }
+  }
+}
+
+// One row pair: A and B are two code rows (1440 B each) with their scale rows.
+// Accumulates acc[t][0] (row A) and acc[t][1] (row B) for t < nt, lane-partial (not yet reduced).
+template <int NT, int PS4, bool XREG>
+NA_DEVICE void rowpair_accumulate(const LaneMap& m, const uint8_t* cA, const uint8_t* cB, const uint8_t* sA,
+                                  const uint8_t* sB, const uint32_t* xs, const uint32_t (*xr)[3][16], int nt,
+                                  float (*acc)[2]) {
+  uint4 c[3];
+  int s[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    if (m.valid[k]) {
+      const uint8_t* row = m.isB[k] ? cB : cA;
+      c[k] = load16(row + 16 * m.g[k]);
+      s[k] = load_scale<PS4>(m.isB[k] ? sB : sA, m.g[k]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    if (m.valid[k]) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        if (t < nt) {
+          const uint32_t* xv;
+          if constexpr (XREG) xv = xr[t][k];
+          else xv = xs + t * kXTok + m.g[k] * kXG;
+          const float p = e8m0_scale(group_dot(c[k], xv), s[k]);
+          acc[t][m.isB[k] ? 1 : 0] += p;
+        }
+      }
+    }
+  }
+}
+
+template <int NT>
+NA_DEVICE void load_xreg(const LaneMap& m, const uint32_t* xs, int nt, uint32_t (*xr)[3][16]) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xr[t][k][i] = (t < nt) ? xs[t * kXTok + m.g[k] * kXG + i] : 0u;
+}
+
+// ----------------------------------------------------------------------------- routing of a decode batch
+// Pairs are (token b, rank k) flattened as p = 4b + k.  Returns false when this work item has no expert.
+struct Route {
+  int64_t expert;        // expert id within the layer
+  int nt;                // tokens routed to it
+  int pair[kMaxTok];     // their pair indices, ascending
+};
+
+NA_DEVICE bool route_item(const int64_t* ids, int npairs, int item, Route& r) {
+  const int lane = threadIdx.x & 63;
+  const long long my = lane < npairs ? ids[lane] : -1;
+  bool dup = false;
+  for (int j = 0; j < 32; ++j) {
+    const long long o = __shfl(my, j, 64);
+    dup |= (j < lane) && (o == my);
+  }
+  const bool first = lane < npairs && !dup;
+  uint64_t fm = __ballot(first);
+  if (item >= __popcll(fm)) return false;
+  for (int i = 0; i < item; ++i) fm &= fm - 1;         // drop the lowest `item` set bits
+  const int leader = __ffsll((long long)fm) - 1;
+  r.expert = __shfl(my, leader, 64);
+  if (r.expert < 0 || r.expert >= kExpertsPerLayer) return false;   // invalid id: no weights are touched
+  uint64_t users = __ballot(lane < npairs && my == r.expert);
+  r.nt = 0;
+  for (int t = 0; t < kMaxTok; ++t) {
+    r.pair[t] = 0;
+    if (users) {
+      r.pair[t] = __ffsll((long long)users) - 1;
+      users &= users - 1;
+      r.nt = t + 1;
+    }
+  }
+  return true;
+}
+
+// ======================================================================= generic GEMV (reference API mirror)
+// out[e, n] = bf16(sum_k x_e[k] w_e[n, k]),  rows processed as adjacent pairs (2i, 2i+1).
+// active (optional): a zero weight writes +0 and reads no weights (reference mxfp4_kernels.py:492-539).
+template <int PS4>
+__global__ __launch_bounds__(kThreads) void k_mxfp4_gemv(
+    const uint16_t* __restrict__ x, long long x_estride, const uint8_t* __restrict__ blocks, long long sb_slot,
+    const uint8_t* __restrict__ scales, long long ss_slot, const int64_t* __restrict__ slots,
+    const void* __restrict__ active, int active_dtype, uint16_t* __restrict__ out, int N, int pairs_per_wg) {
+  __shared__ uint32_t xs[kXTok];
+  const int e = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int p0 = blockIdx.y * pairs_per_wg;
+  const int npairs = N / 2;
+  const int p1 = min(p0 + pairs_per_wg, npairs);
+  bool on = true;
+  if (active_dtype == 1) on = (reinterpret_cast<const uint16_t*>(active)[e] & 0x7fff) != 0;
+  if (active_dtype == 2) on = reinterpret_cast<const float*>(active)[e] != 0.0f;
+  if (!on) {
+    for (int n = 2 * p0 + threadIdx.x; n < 2 * p1; n += kThreads) out[(long long)e * N + n] = 0;
+    return;
+  }
+  const uint16_t* xe = x + (long long)e * x_estride;
+  stage_x(xs, &xe, 1);
+  __syncthreads();
+  const LaneMap m = lane_map(lane);
+  uint32_t xr[1][3][16];
+  load_xreg<1>(m, xs, 1, xr);
+  const long long slot = slots[e];
+  const uint8_t* cb = blocks + slot * sb_slot;
+  const int srow = PS4 ? kPs4Row : kGK;
+  const uint8_t* sb = scales + slot * ss_slot;
+  for (int p = p0 + wave; p < p1; p += kWaves) {
+    float acc[1][2] = {{0.f, 0.f}};
+    const int ra = 2 * p, rbw = 2 * p + 1;
+    rowpair_accumulate<1, PS4, true>(m, cb + (long long)ra * kRowBytes, cb + (long long)rbw * kRowBytes,
+                                     sb + (long long)ra * srow, sb + (long long)rbw * srow, xs, xr, 1, acc);
+    const float a = wave_sum(acc[0][0]);
+    const float b = wave_sum(acc[0][1]);
+    if (lane == 0) {
+      const uint32_t packed = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+      *reinterpret_cast<uint32_t*>(out + (long long)e * N + ra) = packed;
+    }
+  }
+}
+
+// ================================================================ fused decode expert body (server.py:508-518)
+// Kernel 1: gate_up GEMV for row pair (gate j, up 2880 + j) of the distinct expert of this work item, for every
+// token routed to it, then + bias (bf16), clamped SwiGLU (bf16 op by op) -> h[pair, j].
+template <int NT, int PS4>
+__global__ __launch_bounds__(kThreads) void k_moe_gate_up(
+    const uint16_t* __restrict__ x, const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool,
+    long long slot_bytes, const int64_t* __restrict__ slot_tab, long long expert_base,
+    const uint16_t* __restrict__ bias_gu, uint16_t* __restrict__ h, float alpha, float limit, int pairs_per_wg) {
+  __shared__ uint32_t xs[NT * kXTok];
+  Route r;
+  if (!route_item(ids, 4 * B, blockIdx.x, r)) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint16_t* xsrc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) xsrc[t] = x + (long long)(r.pair[t] >> 2) * kH;
+  const int nt = min(r.nt, NT);
+  stage_x(xs, xsrc, nt);
+  __syncthreads();
+  const LaneMap m = lane_map(lane);
+  constexpr bool XREG = NT <= 2;
+  uint32_t xr[XREG ? NT : 1][3][16];
+  if constexpr (XREG) load_xreg<NT>(m, xs, nt, xr);
+  const long long gid = expert_base + r.expert;
+  const long long slot = slot_tab ? slot_tab[gid] : gid;
+  const uint8_t* base = pool + slot * slot_bytes;
+  const uint8_t* sb = base + kOffGateScales;
+  const int srow = PS4 ? kPs4Row : kGK;
+  const uint16_t* bg = bias_gu ? bias_gu + gid * kGU : nullptr;
+  const int j0 = blockIdx.y * pairs_per_wg;
+  const int j1 = min(j0 + pairs_per_wg, kI);
+  for (int j = j0 + wave; j < j1; j += kWaves) {
+    float acc[NT][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = 0.f;
+    rowpair_accumulate<NT, PS4, XREG>(m, base + (long long)j * kRowBytes, base + (long long)(kI + j) * kRowBytes,
+                                      sb + (long long)j * srow, sb + (long long)(kI + j) * srow, xs, xr, nt, acc);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const float g = wave_sum(acc[t][0]);
+      const float u = wave_sum(acc[t][1]);
+      if (lane == t && t < nt) {
+        float gb = rb(g), ub = rb(u);
+        if (bg) {
+          gb = rb(gb + bf16_to_f32(bg[j]));
+          ub = rb(ub + bf16_to_f32(bg[kI + j]));
+        }
+        h[(long long)r.pair[t] * kI + j] = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
+      }
+    }
+  }
+}
+
+// Kernel 2: down GEMV for row pair (2i, 2i+1) from each routed token's own h, + bias, x routing weight (bf16
+// product, server.py:518) -> yw[pair, n].
+template <int NT, int PS4>
+__global__ __launch_bounds__(kThreads) void k_moe_down(
+    const uint16_t* __restrict__ h, const int64_t* __restrict__ ids, const uint16_t* __restrict__ wts, int B,
+    const uint8_t* __restrict__ pool, long long slot_bytes, const int64_t* __restrict__ slot_tab,
+    long long expert_base, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw, int pairs_per_wg) {
+  __shared__ uint32_t xs[NT * kXTok];
+  Route r;
+  if (!route_item(ids, 4 * B, blockIdx.x, r)) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint16_t* xsrc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) xsrc[t] = h + (long long)r.pair[t] * kI;
+  const int nt = min(r.nt, NT);
+  stage_x(xs, xsrc, nt);
+  __syncthreads();
+  const LaneMap m = lane_map(lane);
+  constexpr bool XREG = NT <= 2;
+  uint32_t xr[XREG ? NT : 1][3][16];
+  if constexpr (XREG) load_xreg<NT>(m, xs, nt, xr);
+  const long long gid = expert_base + r.expert;
+  const long long slot = slot_tab ? slot_tab[gid] : gid;
+  const uint8_t* base = pool + slot * slot_bytes;
+  const int srow = PS4 ? kPs4Row : kGK;
+  const uint8_t* cd = base + kOffDownCodes;
+  const uint8_t* sd = base + kOffGateScales + (long long)kGU * srow;
+  const uint16_t* bd = bias_dn ? bias_dn + gid * kH : nullptr;
+  float wt[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) wt[t] = bf16_to_f32(wts[r.pair[t]]);
+  const int p0 = blockIdx.y * pairs_per_wg;
+  const int p1 = min(p0 + pairs_per_wg, kH / 2);
+  for (int p = p0 + wave; p < p1; p += kWaves) {
+    const int na = 2 * p;
+    float acc[NT][2];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = 0.f;
+    rowpair_accumulate<NT, PS4, XREG>(m, cd + (long long)na * kRowBytes, cd + (long long)(na + 1) * kRowBytes,
+                                      sd + (long long)na * srow, sd + (long long)(na + 1) * srow, xs, xr, nt, acc);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const float a = wave_sum(acc[t][0]);
+      const float b = wave_sum(acc[t][1]);
+      if (lane == t && t < nt) {
+        float ya = rb(a), yb = rb(b);
+        if (bd) {
+          ya = rb(ya + bf16_to_f32(bd[na]));
+          yb = rb(yb + bf16_to_f32(bd[na + 1]));
+        }
+        const uint32_t packed =
+            (uint32_t)f32_to_bf16(ya * wt[t]) | ((uint32_t)f32_to_bf16(yb * wt[t]) << 16);
+        *reinterpret_cast<uint32_t*>(yw + (long long)r.pair[t] * kH + na) = packed;
+      }
+    }
+  }
+}
+
+// Kernel 3: out[b, n] = bf16(sum_k fp32(yw[4b + k, n])) in top-k order (server.py:518; prefill twin :2340-2341).
+__global__ __launch_bounds__(256) void k_moe_combine(const uint16_t* __restrict__ yw, int B, int topk,
+                                                     uint16_t* __restrict__ out) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= B * kH) return;
+  const int b = i / kH, n = i - b * kH;
+  float a = 0.f;
+  for (int k = 0; k < topk; ++k) a += bf16_to_f32(yw[(long long)(b * topk + k) * kH + n]);
+  out[i] = f32_to_bf16(a);
+}
+
+// ===================================================================================== router + top-k
+// logits[b, e] = bf16(xn_b . Wr[e] + br[e]) (fused_core.py:431-441); the LAST workgroup to finish (atomic counter,
+// no spinning) selects top-4 per token by repeated argmax (lowest index on ties) and writes softmax weights
+// bf16(exp(v_i - v_0) / sum) (fused_core.py:460-486) and int64 ids.  The counter is reset by that workgroup, so the
+// launch can be replayed in a graph.
+constexpr int kRouterRowsPerWg = 8;   // 2 rows per wave
+
+__global__ __launch_bounds__(kThreads) void k_router(const uint16_t* __restrict__ xn, int B,
+                                                     const uint16_t* __restrict__ wr, const uint16_t* __restrict__ br,
+                                                     int n_exp, float* __restrict__ logits,
+                                                     unsigned int* __restrict__ counter, int64_t* __restrict__ ids_out,
+                                                     uint16_t* __restrict__ w_out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int rr = 0; rr < kRouterRowsPerWg / kWaves; ++rr) {
+    const int e = blockIdx.x * kRouterRowsPerWg + wave * (kRouterRowsPerWg / kWaves) + rr;
+    if (e >= n_exp) break;
+    const uint4* wrow = reinterpret_cast<const uint4*>(wr + (long long)e * kH);   // 360 x 16 B
+    for (int b = 0; b < B; ++b) {
+      const uint4* xrow = reinterpret_cast<const uint4*>(xn + (long long)b * kH);
+      float a = 0.f;
+      for (int i = lane; i < kH / 8; i += 64) {
+        const uint4 w4 = wrow[i], x4 = xrow[i];
+        a = dot2_bf16(w4.x, x4.x, a);
+        a = dot2_bf16(w4.y, x4.y, a);
+        a = dot2_bf16(w4.z, x4.z, a);
+        a = dot2_bf16(w4.w, x4.w, a);
+      }
+      a = wave_sum(a);
+      if (lane == 0) logits[b * n_exp + e] = rb(a + (br ? bf16_to_f32(br[e]) : 0.f));
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  __shared__ unsigned int last;
+  if (threadIdx.x == 0) last = (atomicAdd(counter, 1u) == gridDim.x - 1);
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  if (threadIdx.x == 0) *counter = 0u;
+  if (wave != 0) return;
+  for (int b = 0; b < B; ++b) {
+    // each lane holds experts lane and lane + 64 (n_exp <= 128)
+    const volatile float* lg = logits + b * n_exp;
+    float v0 = lane < n_exp ? lg[lane] : -__builtin_inff();
+    float v1 = lane + 64 < n_exp ? lg[lane + 64] : -__builtin_inff();
+    float top_v[4];
+    int top_i[4];
+    for (int k = 0; k < 4; ++k) {
+      // (value, -index) max over the wave: larger value wins, then smaller index
+      float bv = v0;
+      int bi = lane;
+      if (v1 > bv) { bv = v1; bi = lane + 64; }
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+      }
+      top_v[k] = bv;
+      top_i[k] = bi;
+      if (bi == lane) v0 = -__builtin_inff();
+      if (bi == lane + 64) v1 = -__builtin_inff();
+    }
+    if (lane == 0) {
+      float ex[4], s = 0.f;
+      for (int k = 0; k < 4; ++k) { ex[k] = expf(top_v[k] - top_v[0]); s += ex[k]; }
+      for (int k = 0; k < 4; ++k) {
+        ids_out[b * 4 + k] = top_i[k];
+        w_out[b * 4 + k] = f32_to_bf16(ex[k] / s);
+      }
+    }
+  }
+}
+
+// ======================================================================================= host launchers
+static int pick_nt(int B) { return B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8; }
+
+// Launch on `stream`; with a start/stop event pair the dispatch itself timestamps the kernel (hipExtLaunchKernel),
+// so the measured interval is the kernel's execution whatever the host does between launches.
+template <typename... KArgs, typename... Args>
+static void launch(void (*kern)(KArgs...), dim3 grid, dim3 block, hipStream_t stream, hipEvent_t e0, hipEvent_t e1,
+                   Args... args) {
+  if (e0 || e1)
+    hipExtLaunchKernelGGL(kern, grid, block, 0, stream, e0, e1, 0, static_cast<KArgs>(args)...);
+  else
+    hipLaunchKernelGGL(kern, grid, block, 0, stream, static_cast<KArgs>(args)...);
+}
+
+template <int PS4>
+static auto gate_up_kernel(int nt) {
+  return nt == 1 ? k_moe_gate_up<1, PS4> : nt == 2 ? k_moe_gate_up<2, PS4> : nt == 4 ? k_moe_gate_up<4, PS4>
+                                                                                    : k_moe_gate_up<8, PS4>;
+}
+template <int PS4>
+static auto down_kernel(int nt) {
+  return nt == 1 ? k_moe_down<1, PS4> : nt == 2 ? k_moe_down<2, PS4> : nt == 4 ? k_moe_down<4, PS4>
+                                                                              : k_moe_down<8, PS4>;
+}
+
+}  // namespace na
+
+using namespace na;
+
+extern "C" {
+
+int na_mxfp4_gemv(const void* x, int per_expert_x, const void* blocks, long long sb_slot, const void* scales,
+                  long long ss_slot, int packed, const int64_t* slots, int E, const void* active, int active_dtype,
+                  void* out, int N, int K, int pairs_per_wg, hipStream_t stream) {
+  if (!x || !blocks || !scales || !slots || !out || E <= 0 || N <= 0 || (N & 1) || K != kH) return kErrArgs;
+  if (active_dtype < 0 || active_dtype > 2 || (active_dtype && !active)) return kErrArgs;
+  if (pairs_per_wg <= 0) pairs_per_wg = 16;
+  dim3 grid(E, (N / 2 + pairs_per_wg - 1) / pairs_per_wg);
+  const long long xs = per_expert_x ? K : 0;
+  auto kern = packed ? k_mxfp4_gemv<1> : k_mxfp4_gemv<0>;
+  launch(kern, grid, dim3(kThreads), stream, nullptr, nullptr, (const uint16_t*)x, xs, (const uint8_t*)blocks,
+         sb_slot, (const uint8_t*)scales, ss_slot, slots, active, active_dtype, (uint16_t*)out, N, pairs_per_wg);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int na_moe_decode(const void* x, const int64_t* topk_ids, const void* topk_w, int B, const void* pool,
+                  long long slot_bytes, int packed, const int64_t* slot_tab, long long expert_base,
+                  const void* bias_gu, const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha,
+                  float limit, int gu_pairs_per_wg, int dn_pairs_per_wg, void* const* events, hipStream_t stream) {
+  if (!x || !topk_ids || !topk_w || !pool || !h_scratch || !yw_scratch || !out || B <= 0) return kErrArgs;
+  if (B > kMaxTok) return kErrTooLarge;
+  if (slot_bytes < (packed ? kSlotPs4 : kSlotRaw)) return kErrArgs;
+  if (gu_pairs_per_wg <= 0) gu_pairs_per_wg = 16;
+  if (dn_pairs_per_wg <= 0) dn_pairs_per_wg = 8;
+  hipEvent_t ev[6] = {};
+  if (events)
+    for (int i = 0; i < 6; ++i) ev[i] = (hipEvent_t)events[i];
+  const int nt = pick_nt(B);
+  const int items = 4 * B;
+  dim3 g1(items, (kI + gu_pairs_per_wg - 1) / gu_pairs_per_wg);
+  launch(packed ? gate_up_kernel<1>(nt) : gate_up_kernel<0>(nt), g1, dim3(kThreads), stream, ev[0], ev[1],
+         (const uint16_t*)x, topk_ids, B, (const uint8_t*)pool, slot_bytes, slot_tab, expert_base,
+         (const uint16_t*)bias_gu, (uint16_t*)h_scratch, alpha, limit, gu_pairs_per_wg);
+  dim3 g2(items, (kH / 2 + dn_pairs_per_wg - 1) / dn_pairs_per_wg);
+  launch(packed ? down_kernel<1>(nt) : down_kernel<0>(nt), g2, dim3(kThreads), stream, ev[2], ev[3],
+         (const uint16_t*)h_scratch, topk_ids, (const uint16_t*)topk_w, B, (const uint8_t*)pool, slot_bytes,
+         slot_tab, expert_base, (const uint16_t*)bias_dn, (uint16_t*)yw_scratch, dn_pairs_per_wg);
+  launch(k_moe_combine, dim3((B * kH + 255) / 256), dim3(256), stream, ev[4], ev[5], (const uint16_t*)yw_scratch, B,
+         4, (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int na_router_topk(const void* xn, int B, const void* w_router, const void* b_router, int n_exp, float* logits,
+                   unsigned int* counter, int64_t* ids_out, void* w_out, hipStream_t stream) {
+  if (!xn || !w_router || !logits || !counter || !ids_out || !w_out || B <= 0 || n_exp <= 4 || n_exp > 128)
+    return kErrArgs;
+  dim3 grid((n_exp + kRouterRowsPerWg - 1) / kRouterRowsPerWg);
+  launch(k_router, grid, dim3(kThreads), stream, nullptr, nullptr, (const uint16_t*)xn, B, (const uint16_t*)w_router,
+         (const uint16_t*)b_router, n_exp, logits, counter, ids_out, (uint16_t*)w_out);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // extern "C"

@@ -1,0 +1,108 @@
+"""All-resident GPT-OSS-120B experts on one MI355X: the ``experts.forward(hidden_states, router_indices,
+routing_weights)`` seam the reference installs per layer (reference neural/moe/gptoss_adapter.py:267-284), backed by
+one HBM slot pool [n_layers * n_experts, slot_bytes] that holds every expert (60.9 GB raw; nothing is offloaded).
+
+Decode (T <= 8 tokens) runs the fused expert body of the reference's b_body (server.py:508-518) as three HIP launches
+(gate_up + bias + clamped SwiGLU, down + bias + routing weight, top-k combine); routing is read on the device, so
+``forward_decode`` never synchronises and can be captured in a hipGraph.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _native as N
+from .layout import GPTOSS_LAYOUT, ExpertLayout
+
+MAX_DECODE_TOKENS = 8
+
+
+class ResidentExperts:
+    def __init__(self, pool: torch.Tensor, layout: ExpertLayout = GPTOSS_LAYOUT, bias_gu: torch.Tensor | None = None,
+                 bias_dn: torch.Tensor | None = None, slot_tab: torch.Tensor | None = None,
+                 max_batch: int = MAX_DECODE_TOKENS, gu_pairs_per_wg: int = 16, dn_pairs_per_wg: int = 8):
+        if layout.weight_repr not in ("mxfp4_g32", "mxfp4_g32_ps4"):
+            raise ValueError(f"ResidentExperts serves the raw and PS4 slot layouts, not {layout.weight_repr}")
+        if pool.dtype is not torch.uint8 or pool.ndim != 2 or pool.shape[1] != layout.slot_bytes:
+            raise ValueError(f"pool must be uint8 [n, {layout.slot_bytes}]")
+        if not pool.is_contiguous() or pool.device.type != "cuda":
+            raise ValueError("pool must be a contiguous CUDA tensor")
+        n = layout.n_layers * layout.n_experts
+        if slot_tab is None and pool.shape[0] < n:
+            raise ValueError(f"pool holds {pool.shape[0]} slots; without a slot table it must hold all {n}")
+        for b, w, nm in ((bias_gu, layout.gate_up_n, "bias_gu"), (bias_dn, layout.down_n, "bias_dn")):
+            if b is not None and (b.dtype is not torch.bfloat16 or tuple(b.shape) != (n, w) or not b.is_contiguous()
+                                  or b.device != pool.device):
+                raise ValueError(f"{nm} must be contiguous bf16 [{n}, {w}] on the pool's device")
+        if slot_tab is not None and (slot_tab.dtype is not torch.int64 or slot_tab.numel() != n
+                                     or slot_tab.device != pool.device):
+            raise ValueError(f"slot_tab must be int64 [{n}] on the pool's device")
+        if not 1 <= max_batch <= MAX_DECODE_TOKENS:
+            raise ValueError(f"max_batch must be in [1, {MAX_DECODE_TOKENS}]")
+        self.pool, self.layout = pool, layout
+        self.bias_gu, self.bias_dn, self.slot_tab = bias_gu, bias_dn, slot_tab
+        self.max_batch = max_batch
+        self.gu_pairs, self.dn_pairs = int(gu_pairs_per_wg), int(dn_pairs_per_wg)
+        dev = pool.device
+        self.h = torch.empty(max_batch * layout.top_k, layout.down_k, dtype=torch.bfloat16, device=dev)
+        self.yw = torch.empty(max_batch * layout.top_k, layout.down_n, dtype=torch.bfloat16, device=dev)
+
+    def forward_decode(self, layer: int, hidden: torch.Tensor, router_indices: torch.Tensor,
+                       routing_weights: torch.Tensor, out: torch.Tensor | None = None, events=None) -> torch.Tensor:
+        """hidden [B, 2880] bf16, router_indices [B, 4] int64 (expert ids within the layer), routing_weights [B, 4]
+        bf16 -> [B, 2880] bf16 = bf16(sum_k bf16(bf16(expert_k(h) + b_dn) * w_k)) in top-k order.
+        events: None, or six recorded timing torch.cuda.Event objects (start/stop of the gate_up, down and combine
+        kernels), timestamped by the dispatches themselves (measurement only; not for graph capture)."""
+        L = self.layout
+        B = hidden.shape[0]
+        if hidden.dtype is not torch.bfloat16 or hidden.ndim != 2 or hidden.shape[1] != L.hidden \
+                or not hidden.is_contiguous():
+            raise ValueError("hidden must be contiguous bf16 [B, hidden]")
+        if not 1 <= B <= self.max_batch:
+            raise ValueError(f"decode batch {B} outside [1, {self.max_batch}]")
+        if router_indices.dtype is not torch.int64 or tuple(router_indices.shape) != (B, L.top_k) \
+                or not router_indices.is_contiguous():
+            raise ValueError("router_indices must be contiguous int64 [B, top_k]")
+        if routing_weights.dtype is not torch.bfloat16 or tuple(routing_weights.shape) != (B, L.top_k) \
+                or not routing_weights.is_contiguous():
+            raise ValueError("routing_weights must be contiguous bf16 [B, top_k]")
+        if not 0 <= layer < L.n_layers:
+            raise ValueError(f"layer {layer} outside [0, {L.n_layers})")
+        if out is None:
+            out = torch.empty(B, L.hidden, dtype=torch.bfloat16, device=hidden.device)
+        elif out.dtype is not torch.bfloat16 or tuple(out.shape) != (B, L.hidden) or not out.is_contiguous():
+            raise ValueError("out must be contiguous bf16 [B, hidden]")
+        N.call("na_moe_decode", hidden.data_ptr(), router_indices.data_ptr(), routing_weights.data_ptr(), B,
+               self.pool.data_ptr(), L.slot_bytes, L.scale_layout_mode, N.ptr(self.slot_tab), layer * L.n_experts,
+               N.ptr(self.bias_gu), N.ptr(self.bias_dn), self.h.data_ptr(), self.yw.data_ptr(), out.data_ptr(),
+               float(L.act_alpha), float(L.act_limit), self.gu_pairs, self.dn_pairs, N.events_array(events),
+               N.stream(hidden.device))
+        return out
+
+
+class Router:
+    """Router GEMV + top-4 + softmax of one layer (reference fused_core.py:417-502 k_router / k_topk, without the
+    offload bookkeeping): logits = bf16(xn . Wr^T + br); ids int64 [B, 4]; weights bf16 [B, 4]."""
+
+    def __init__(self, device, max_batch: int = MAX_DECODE_TOKENS, n_experts: int = 128):
+        self.n_experts = n_experts
+        self.logits = torch.zeros(max_batch, n_experts, dtype=torch.float32, device=device)
+        self.counter = torch.zeros(1, dtype=torch.int32, device=device)
+        self.max_batch = max_batch
+
+    def __call__(self, xn: torch.Tensor, w_router: torch.Tensor, b_router: torch.Tensor | None,
+                 ids_out: torch.Tensor, w_out: torch.Tensor) -> None:
+        B = xn.shape[0]
+        if not 1 <= B <= self.max_batch or xn.dtype is not torch.bfloat16 or not xn.is_contiguous() \
+                or xn.shape[1] != 2880:
+            raise ValueError("xn must be contiguous bf16 [B <= max_batch, 2880]")
+        if w_router.dtype is not torch.bfloat16 or tuple(w_router.shape) != (self.n_experts, 2880) \
+                or not w_router.is_contiguous():
+            raise ValueError("w_router must be contiguous bf16 [n_experts, 2880]")
+        if b_router is not None and (b_router.dtype is not torch.bfloat16 or b_router.numel() != self.n_experts):
+            raise ValueError("b_router must be bf16 [n_experts]")
+        if ids_out.dtype is not torch.int64 or ids_out.numel() != 4 * B or w_out.dtype is not torch.bfloat16 \
+                or w_out.numel() != 4 * B:
+            raise ValueError("ids_out int64 [B, 4] and w_out bf16 [B, 4] required")
+        N.call("na_router_topk", xn.data_ptr(), B, w_router.data_ptr(), N.ptr(b_router), self.n_experts,
+               self.logits.data_ptr(), self.counter.data_ptr(), ids_out.data_ptr(), w_out.data_ptr(),
+               N.stream(xn.device))

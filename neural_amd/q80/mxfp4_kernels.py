@@ -1,0 +1,200 @@
+"""MXFP4 expert products on MI355X: the Python call surface of the reference's ``neural/q80/mxfp4_kernels.py``,
+dispatching to hand-written gfx950 HIP kernels (neural_amd/csrc) through the C-ABI library.
+
+Kept from the reference (same names, argument meaning and error behaviour):
+  * ``mxfp4_gemv`` / ``mxfp4_gemv_masked`` (reference :474-489, :542-569): decode GEMV over slots, out [E, N] bf16;
+  * ``mxfp4_gemm`` / ``mxfp4_gemm_into`` (:202-231), ``GroupedGemmPlan`` (:318-382), ``mxfp4_gemm_grouped_into``
+    (:385-419), ``_grouped_tile_rows`` (:298-315): prefill products;
+  * ``_scale_layout`` (:72-84): the raw / PS4 scale layout is read off the scales view, an explicit ``packed=`` is
+    checked against it and never trusted over it;
+  * the module switches FAST_LAUNCH, PREFILL_BLOCK_M, PREFILL_GROUP, PREFILL_GROUPED_GEMM, PREFILL_GROUP_ROWS,
+    PREFILL_GROUP_EXPERTS (:35-59), read from the same environment variables.
+Triton tiling knobs (block_n, block_g, num_warps) are accepted; block_n maps to the rows a workgroup streams, the
+others have no meaning for these kernels and are ignored.
+
+Arithmetic: exact E2M1 x 2^(s-127) dequant in registers, fp32 accumulation, one bf16 rounding of each output
+(the reference's contract, :1-7).  Deterministic: fixed grid, fixed reduction order, no atomics in the products;
+every launch goes on torch's current stream and allocates nothing beyond the returned tensor, so calls are
+hipGraph-capturable.
+"""
+from __future__ import annotations
+
+import operator
+import os
+
+import torch
+
+from .. import _native as N
+
+FAST_LAUNCH = os.environ.get("NEURAL_FAST_LAUNCH", "1") != "0"
+PREFILL_BLOCK_M = int(os.environ.get("NEURAL_PREFILL_BM", "64"))
+if PREFILL_BLOCK_M < 16 or PREFILL_BLOCK_M & (PREFILL_BLOCK_M - 1):
+    raise ValueError(f"NEURAL_PREFILL_BM={PREFILL_BLOCK_M}: BLOCK_M must be a power of two >= 16")
+PREFILL_GROUP = os.environ.get("NEURAL_PREFILL_GROUP", "0") != "0"
+PREFILL_GROUPED_GEMM = os.environ.get("NEURAL_PREFILL_GROUPED_GEMM", "0") != "0"
+PREFILL_GROUP_ROWS = int(os.environ.get("NEURAL_PREFILL_GROUP_ROWS", "16384"))
+PREFILL_GROUP_EXPERTS = int(os.environ.get("NEURAL_PREFILL_GROUP_EXPERTS", "0"))
+if PREFILL_GROUP_ROWS < 1 or PREFILL_GROUP_EXPERTS < 0:
+    raise ValueError(f"NEURAL_PREFILL_GROUP_ROWS={PREFILL_GROUP_ROWS} (>= 1), NEURAL_PREFILL_GROUP_EXPERTS="
+                     f"{PREFILL_GROUP_EXPERTS} (>= 0)")
+
+GK_SUPPORTED = 90          # K = 2880: the GPT-OSS-120B geometry these kernels are built for
+
+
+def _scale_layout(scales: torch.Tensor, GK: int, packed) -> bool:
+    """True when ``scales`` (..., N, w) holds PS4 rows (w == GK//2 + 1), False for raw rows (w == GK); ``packed``
+    (None = infer) is checked against the view (reference mxfp4_kernels.py:72-84)."""
+    w = scales.shape[-1]
+    inferred = (w == GK // 2 + 1)
+    if not (inferred or w == GK):
+        raise ValueError(f"scales view has row width {w}: want {GK} (raw E8M0) or {GK // 2 + 1} (packed 4-bit)")
+    if packed is not None and bool(packed) != inferred:
+        raise ValueError(f"packed={packed} but the scales view row width {w} says "
+                         f"{'packed' if inferred else 'raw'} (GK={GK})")
+    if scales.stride(-1) != 1 or scales.stride(-2) != w:
+        raise ValueError(f"scales rows must be contiguous (strides {tuple(scales.stride())}, row width {w})")
+    return inferred
+
+
+def _check_pool_views(blocks: torch.Tensor, scales: torch.Tensor, x: torch.Tensor, slots: torch.Tensor):
+    if blocks.ndim != 4 or blocks.shape[-1] != 16 or blocks.dtype is not torch.uint8:
+        raise ValueError("blocks must be a uint8 [cap, N, GK, 16] view")
+    cap, n, gk, _ = blocks.shape
+    if tuple(blocks.stride()[1:]) != (gk * 16, 16, 1):
+        raise ValueError("blocks rows must be contiguous")
+    if scales.dtype is not torch.uint8 or scales.ndim != 3 or tuple(scales.shape[:2]) != (cap, n):
+        raise ValueError("scales must be a uint8 [cap, N, w] view matching blocks")
+    if gk != GK_SUPPORTED:
+        raise ValueError(f"GK={gk}: these kernels are built for K = {GK_SUPPORTED * 32} (GPT-OSS-120B)")
+    if n % 2:
+        raise ValueError(f"N={n}: rows are streamed in pairs, N must be even")
+    for t, nm in ((blocks, "blocks"), (scales, "scales"), (slots, "slots")):
+        if t.device != x.device or t.device.type != "cuda":
+            raise ValueError(f"{nm} must be on the input's CUDA device")
+    if slots.dtype is not torch.int64 or not slots.is_contiguous():
+        raise ValueError("slots must be a contiguous int64 tensor")
+    return cap, n, gk
+
+
+def _gemv(x, blocks, scales, slots, active, per_expert_x, block_n, packed):
+    E = slots.numel()
+    cap, n, gk = _check_pool_views(blocks, scales, x, slots)
+    pk = _scale_layout(scales, gk, packed)
+    if (x.dtype is not torch.bfloat16 or not x.is_contiguous() or x.ndim != 2
+            or tuple(x.shape) != ((E if per_expert_x else 1), gk * 32)):
+        raise ValueError("GEMV requires contiguous bf16 x[1,K] or per-expert x[E,K]")
+    out = torch.empty(E, n, dtype=torch.bfloat16, device=x.device)
+    if E == 0:
+        return out
+    adt = 0
+    if active is not None:
+        adt = 1 if active.dtype is torch.bfloat16 else 2
+    pairs = max(1, int(block_n) // 4)     # block_n rows of the Triton kernel ~ block_n/2 row pairs; keep WGs small
+    N.call("na_mxfp4_gemv", x.data_ptr(), int(per_expert_x), blocks.data_ptr(), blocks.stride(0),
+           scales.data_ptr(), scales.stride(0), int(pk), slots.data_ptr(), E, N.ptr(active), adt, out.data_ptr(),
+           n, gk * 32, pairs, N.stream(x.device))
+    return out
+
+
+def mxfp4_gemv(x: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor, slots: torch.Tensor, *,
+               per_expert_x: bool = False, block_n: int = 64, block_g: int = 4, num_warps: int = 4,
+               packed: bool | None = None) -> torch.Tensor:
+    """Decode GEMV: x [1, K] shared, or [E, K] with per_expert_x=True.  Returns [E, N] bf16 with
+    out[e, n] = bf16(sum_k x[k] * w_slot[e][n, k]) (reference mxfp4_kernels.py:474-489)."""
+    return _gemv(x, blocks, scales, slots, None, per_expert_x, block_n, packed)
+
+
+def mxfp4_gemv_masked(x: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor, slots: torch.Tensor,
+                      active_weights: torch.Tensor, *, per_expert_x=False, block_n=64, block_g=4, num_warps=4,
+                      packed=None):
+    """GEMV with zero-weight experts skipped: a slot whose active weight is +-0 writes +0 rows and reads none of its
+    weights; NaN and nonzero weights take the stock arithmetic (reference mxfp4_kernels.py:492-569)."""
+    E = slots.numel()
+    if (active_weights.ndim != 1 or active_weights.numel() != E or not active_weights.is_contiguous()
+            or active_weights.device != x.device or active_weights.dtype not in (torch.bfloat16, torch.float32)):
+        raise ValueError("active_weights needs one contiguous bf16/fp32 scalar per slot on the input device")
+    if (x.dtype is not torch.bfloat16 or not x.is_contiguous() or x.ndim != 2
+            or x.shape[1] != blocks.shape[2] * 32 or x.shape[0] != (E if per_expert_x else 1)):
+        raise ValueError("masked GEMV requires contiguous bf16 x[1,K] or per-expert x[E,K]")
+    if slots.device != x.device or blocks.device != x.device or scales.device != x.device:
+        raise ValueError("masked GEMV tensors must share a device")
+    return _gemv(x, blocks, scales, slots, active_weights, per_expert_x, block_n, packed)
+
+
+# ------------------------------------------------------------------------------------------ prefill planning
+def _grouped_tile_rows(pair_descriptors, block_m):
+    """Host plan builder (reference mxfp4_kernels.py:298-315): (x address, y address, slot, M) per pair ->
+    pair-local tiles (x, y, slot, M, pm) for pm in range(ceil(M / block_m)); empty pairs give no tile."""
+    block_m = operator.index(block_m)
+    if block_m < 16 or block_m & (block_m - 1):
+        raise ValueError("block_m must be a power of two >= 16")
+    rows = []
+    for desc in pair_descriptors:
+        if len(desc) != 4:
+            raise ValueError("pair descriptor must have four integers")
+        xptr, yptr, slot, m = (operator.index(v) for v in desc)
+        if xptr < 0 or yptr < 0 or slot < 0 or not 0 <= m <= 2 ** 31 - 1:
+            raise ValueError("invalid pointer, slot or pair row count")
+        rows.extend((xptr, yptr, slot, m, pm) for pm in range(-(-m // block_m)))
+    return rows
+
+
+class GroupedGemmPlan:
+    """Owned metadata of one ragged grouped GEMM launch (reference mxfp4_kernels.py:318-382).
+
+    ``pairs``: iterable of (contiguous bf16 x[M, K], physical slot, contiguous bf16 out[M, N]).  Inputs may repeat;
+    outputs must be disjoint and may not overlap any input.  The tile table [ntiles, 5] int64 (x address, out
+    address, slot, M, pm) is uploaded once from pinned memory; the plan keeps the upload source and every pair tensor
+    alive.  A CPU plan can be built for validation; launching needs a GPU."""
+    __slots__ = ("pairs", "metadata_host", "metadata", "block_m", "K", "N",
+                 "device", "slots", "ntiles", "aligned")
+
+    def __init__(self, pairs, *, block_m=64):
+        self.pairs = tuple(pairs)
+        self.block_m = operator.index(block_m)
+        _grouped_tile_rows((), self.block_m)
+        self.K = self.N = None
+        self.device = None
+        self.aligned = True
+        descs, reads, writes, slots = [], [], [], []
+        for x, slot, out in self.pairs:
+            slot = operator.index(slot)
+            if x.ndim != 2 or out.ndim != 2 or x.shape[0] != out.shape[0]:
+                raise ValueError("each grouped pair needs x[M,K] and out[M,N]")
+            if x.dtype is not torch.bfloat16 or out.dtype is not torch.bfloat16:
+                raise ValueError("grouped GEMM inputs and outputs must be bf16")
+            if not x.is_contiguous() or not out.is_contiguous():
+                raise ValueError("grouped GEMM pair matrices must be contiguous")
+            if x.device != out.device:
+                raise ValueError("a grouped pair's input/output must share a device")
+            if self.device is None:
+                self.device, self.K, self.N = x.device, x.shape[1], out.shape[1]
+            if (x.device != self.device or x.shape[1] != self.K or out.shape[1] != self.N
+                    or self.K < 32 or self.K % 32 or self.N < 1):
+                raise ValueError("grouped pairs need one device, common K (multiple of 32), and common N")
+            m = x.shape[0]
+            descs.append((x.data_ptr(), out.data_ptr(), slot, m))
+            slots.append(slot)
+            if m:
+                self.aligned &= (x.data_ptr() % 16 == 0 and out.data_ptr() % 16 == 0
+                                 and x.shape[1] * x.element_size() % 16 == 0
+                                 and out.shape[1] * out.element_size() % 16 == 0)
+                reads.append((x.data_ptr(), x.data_ptr() + x.numel() * x.element_size()))
+                writes.append((out.data_ptr(), out.data_ptr() + out.numel() * out.element_size()))
+        ordered = sorted(writes)
+        if any(a[1] > b[0] for a, b in zip(ordered, ordered[1:])):
+            raise ValueError("grouped output slices overlap")
+        wi = 0
+        for lo, hi in sorted(reads):                 # sweep: no input may overlap any output
+            while wi < len(ordered) and ordered[wi][1] <= lo:
+                wi += 1
+            if wi < len(ordered) and ordered[wi][0] < hi:
+                raise ValueError("grouped outputs overlap an input slice")
+        tiles = _grouped_tile_rows(descs, self.block_m)
+        self.slots = tuple(slots)
+        self.ntiles = len(tiles)
+        on_gpu = self.device is not None and self.device.type == "cuda"
+        self.metadata_host = torch.empty((self.ntiles, 5), dtype=torch.int64, pin_memory=on_gpu)
+        if tiles:
+            self.metadata_host.copy_(torch.tensor(tiles, dtype=torch.int64))
+        self.metadata = (self.metadata_host.to(self.device, non_blocking=True) if on_gpu else self.metadata_host)
