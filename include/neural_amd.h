@@ -36,29 +36,33 @@ int na_selftest_fp4(void* out, hipStream_t stream);
  *   active   optional per-slot weight (active_dtype 1 = bf16, 2 = fp32, 0 = none): a zero writes +0 rows and reads
  *            no weights; NaN or nonzero computes
  *   out      bf16 [E, N], N even
- *   pairs_per_wg  row pairs streamed by one workgroup (<= 0: default 16) */
+ *   pairs_per_wave  row pairs streamed per wavefront: 1, 2 or 4 (<= 0: default 2) */
 int na_mxfp4_gemv(const void* x, int per_expert_x, const void* blocks, long long sb_slot, const void* scales,
                   long long ss_slot, int packed, const int64_t* slots, int E, const void* active, int active_dtype,
-                  void* out, int N, int K, int pairs_per_wg, hipStream_t stream);
+                  void* out, int N, int K, int pairs_per_wave, hipStream_t stream);
 
-/* Fused decode expert body for B <= 8 tokens.  Replaces the reference's b_body (server.py:508-518: gate_up GEMV ->
- * + bias -> clamped SwiGLU (neural/q80/expert_runtime.py:63-72) -> down GEMV -> + bias -> routing-weighted sum)
- * and its graph twin _ExpertGraphV4._compute (neural/q80/expert_runtime.py:1361-1427), for an all-resident pool.
+/* Fused decode expert body for B <= 8 tokens: gate_up GEMV (+ bias, clamped SwiGLU), down GEMV (+ bias, x routing
+ * weight) and, when `out` is not NULL, the top-k combine; three launches.  Replaces the reference's b_body
+ * (server.py:508-518: gate_up GEMV -> + bias -> clamped SwiGLU (neural/q80/expert_runtime.py:63-72) -> down GEMV ->
+ * + bias -> routing-weighted sum) and its graph twin _ExpertGraphV4._compute (neural/q80/expert_runtime.py:1361-1427),
+ * for an all-resident pool.
  *   x          bf16 [B, 2880] (post-attention RMSNorm output)
- *   topk_ids   int64 [B, 4] expert ids within the layer; topk_w bf16 [B, 4] routing weights
+ *   topk_ids   int64 [B, 4] expert ids within the layer; topk_w bf16 [B, 4] routing weights.  Ids outside [0, 128)
+ *              contribute +0 and read no weights.
  *   pool       u8 [n_slots, slot_bytes]; slot of expert id e = slot_tab ? slot_tab[expert_base + e] : expert_base + e
  *   bias_gu    bf16 [*, 5760] / bias_dn bf16 [*, 2880] rows indexed by expert_base + e (NULL = no bias)
- *   h_scratch  bf16 [4B, 2880], yw_scratch bf16 [4B, 2880]: caller-owned intermediates
- *   out        bf16 [B, 2880]
+ *   h_scratch  bf16 [4B, 2880]: activations; yw_scratch bf16 [4B, 2880]: weighted expert outputs, row 4b + k
+ *   out        bf16 [B, 2880] = bf16(sum_k fp32(yw[4b + k])) in top-k order, or NULL to leave the combine to the
+ *              consumer (yw_scratch then holds the result).  Calls that overlap on one device must not share scratch.
  *   alpha, limit  activation constants (1.702, 7.0)
- *   gu_pairs_per_wg / dn_pairs_per_wg  row pairs per workgroup of the two products (<= 0: defaults 16 / 8)
+ *   gu_pairs_per_wave / dn_pairs_per_wave  row pairs streamed per wavefront, 1, 2 or 4 (<= 0: defaults 4 / 2)
  *   events     NULL, or 6 hipEvent_t: start/stop of the gate_up, down and combine kernels, timestamped by the
  *              dispatches themselves (hipExtLaunchKernel); for measurement only, not for graph capture
  * Each distinct expert's weights are read once per call for all tokens routed to it. */
 int na_moe_decode(const void* x, const int64_t* topk_ids, const void* topk_w, int B, const void* pool,
                   long long slot_bytes, int packed, const int64_t* slot_tab, long long expert_base,
                   const void* bias_gu, const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha,
-                  float limit, int gu_pairs_per_wg, int dn_pairs_per_wg, void* const* events, hipStream_t stream);
+                  float limit, int gu_pairs_per_wave, int dn_pairs_per_wave, void* const* events, hipStream_t stream);
 
 /* Router GEMV + top-4 + softmax.  Replaces fused_core.py:417-441 (k_router, logits part) and :460-486 (k_topk,
  * selection and weights; the slot-table and host-pack bookkeeping of the offload design are not part of it).

@@ -98,6 +98,25 @@ NA_DEVICE float wave_sum(float v) {
   return v;
 }
 
+template <int CTRL>
+NA_DEVICE float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wavefront, returned (wave-uniform) to every lane.  Must run with all lanes active.
+// Fixed order: lane pairs, quads (DPP quad_perm), rows of 16 (DPP row_ror 4, 8), then the four row sums.
+NA_DEVICE float wave_total(float v) {
+  v += dpp<0xB1>(v);      // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);      // quad_perm [2,3,0,1]
+  v += dpp<0x124>(v);     // row_ror:4
+  v += dpp<0x128>(v);     // row_ror:8
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 // Clamped SwiGLU of one (gate, up) element pair with torch's bf16 op-by-op rounding
 // (reference neural/q80/expert_runtime.py:63-72, server.py:2014-2021): inputs are bf16 values.
 NA_DEVICE float swiglu_clamp_bf16(float g, float u, float alpha, float limit) {

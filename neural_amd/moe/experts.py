@@ -3,7 +3,7 @@ routing_weights)`` seam the reference installs per layer (reference neural/moe/g
 one HBM slot pool [n_layers * n_experts, slot_bytes] that holds every expert (60.9 GB raw; nothing is offloaded).
 
 Decode (T <= 8 tokens) runs the fused expert body of the reference's b_body (server.py:508-518) as three HIP launches
-(gate_up + bias + clamped SwiGLU, down + bias + routing weight, top-k combine); routing is read on the device, so
+(gate_up + bias + clamped SwiGLU; down + bias + routing weight; top-k combine); routing is read on the device, so
 ``forward_decode`` never synchronises and can be captured in a hipGraph.
 """
 from __future__ import annotations
@@ -19,7 +19,7 @@ MAX_DECODE_TOKENS = 8
 class ResidentExperts:
     def __init__(self, pool: torch.Tensor, layout: ExpertLayout = GPTOSS_LAYOUT, bias_gu: torch.Tensor | None = None,
                  bias_dn: torch.Tensor | None = None, slot_tab: torch.Tensor | None = None,
-                 max_batch: int = MAX_DECODE_TOKENS, gu_pairs_per_wg: int = 16, dn_pairs_per_wg: int = 8):
+                 max_batch: int = MAX_DECODE_TOKENS, gu_pairs_per_wave: int = 4, dn_pairs_per_wave: int = 2):
         if layout.weight_repr not in ("mxfp4_g32", "mxfp4_g32_ps4"):
             raise ValueError(f"ResidentExperts serves the raw and PS4 slot layouts, not {layout.weight_repr}")
         if pool.dtype is not torch.uint8 or pool.ndim != 2 or pool.shape[1] != layout.slot_bytes:
@@ -41,7 +41,9 @@ class ResidentExperts:
         self.pool, self.layout = pool, layout
         self.bias_gu, self.bias_dn, self.slot_tab = bias_gu, bias_dn, slot_tab
         self.max_batch = max_batch
-        self.gu_pairs, self.dn_pairs = int(gu_pairs_per_wg), int(dn_pairs_per_wg)
+        if gu_pairs_per_wave not in (1, 2, 4) or dn_pairs_per_wave not in (1, 2, 4):
+            raise ValueError("row pairs per wave must be 1, 2 or 4")
+        self.gu_pairs, self.dn_pairs = int(gu_pairs_per_wave), int(dn_pairs_per_wave)
         dev = pool.device
         self.h = torch.empty(max_batch * layout.top_k, layout.down_k, dtype=torch.bfloat16, device=dev)
         self.yw = torch.empty(max_batch * layout.top_k, layout.down_n, dtype=torch.bfloat16, device=dev)
@@ -51,7 +53,8 @@ class ResidentExperts:
         """hidden [B, 2880] bf16, router_indices [B, 4] int64 (expert ids within the layer), routing_weights [B, 4]
         bf16 -> [B, 2880] bf16 = bf16(sum_k bf16(bf16(expert_k(h) + b_dn) * w_k)) in top-k order.
         events: None, or six recorded timing torch.cuda.Event objects (start/stop of the gate_up, down and combine
-        kernels), timestamped by the dispatches themselves (measurement only; not for graph capture)."""
+        kernels), timestamped by the dispatches themselves (measurement only; not for graph capture).
+        Calls that overlap on one device must use different ResidentExperts objects (they share scratch)."""
         L = self.layout
         B = hidden.shape[0]
         if hidden.dtype is not torch.bfloat16 or hidden.ndim != 2 or hidden.shape[1] != L.hidden \
