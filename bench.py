@@ -75,6 +75,9 @@ def cpu_baseline(pool_dev, ids, B, seconds=12.0):
             uniq.append(g)
         g += 1
     host = [pool_dev[g].cpu().numpy() for g in uniq]
+    if host[0].size != SLOT_ALGO_BYTES:                    # t950 pool: the reference kernel reads the store layout
+        from neural_amd import tiles
+        host = [tiles.t950_to_slot(h) for h in host]
     rng = np.random.default_rng(5)
     x = rng.standard_normal(H).astype(np.float32)
     bgu = [np.zeros(5760, np.float32)] * 4
@@ -106,7 +109,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--batch", type=int, default=1)
-    ap.add_argument("--packed", action="store_true", help="PS4 scale layout instead of raw")
+    ap.add_argument("--layout", choices=("t950", "raw", "ps4"), default="t950",
+                    help="resident slot layout: gfx950 tiles (MFMA kernels) or the store layouts (VALU kernels)")
+    ap.add_argument("--k-split", type=int, default=4, help="t950: waves per workgroup splitting K (1, 2, 4)")
     ap.add_argument("--sets", type=int, default=16, help="routing sets (graphs) cycled over the steps")
     ap.add_argument("--roofline-steps", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
@@ -124,33 +129,46 @@ def main():
     import torch
 
     from neural_amd.moe.experts import ResidentExperts
-    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4
-    from neural_amd import synth
+    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4, GPTOSS_LAYOUT_T950
+    from neural_amd import synth, tiles
 
     dev = torch.device("cuda", 0)
-    L = GPTOSS_LAYOUT_PS4 if A.packed else GPTOSS_LAYOUT
+    L = {"t950": GPTOSS_LAYOUT_T950, "raw": GPTOSS_LAYOUT, "ps4": GPTOSS_LAYOUT_PS4}[A.layout]
     n_slots = N_LAYERS * N_EXPERTS
     log(f"allocating pool {n_slots} x {L.slot_bytes} B = {n_slots * L.slot_bytes / 1e9:.1f} GB ({L.weight_repr})")
     pool = torch.empty((n_slots, L.slot_bytes), dtype=torch.uint8, device=dev)
     g = torch.Generator(device=dev)
     g.manual_seed(1234)
-    cb = L.gate_pack_bytes + L.down_pack_bytes
-    pool[:, :cb].random_(0, 256, generator=g)
-    if A.packed:
-        # PS4 rows: base in [119, 125 - 15]... keep exponents in [119, 125]: base 119, deltas 0..6 per nibble
-        sc = pool[:, cb:].view(n_slots, -1, 46)
-        sc[:, :, 0].fill_(119)
-        lo = torch.randint(0, 7, sc[:, :, 1:].shape, dtype=torch.uint8, device=dev, generator=g)
-        hi = torch.randint(0, 7, sc[:, :, 1:].shape, dtype=torch.uint8, device=dev, generator=g)
-        sc[:, :, 1:] = lo | (hi << 4)
-        del lo, hi
+
+    def fill_store(dst, ps4):
+        """uniform code bytes; E8M0 exponents uniform in [119, 125] (PS4: base 119, deltas 0..6)"""
+        cb = GPTOSS_LAYOUT.gate_pack_bytes + GPTOSS_LAYOUT.down_pack_bytes
+        dst[:, :cb].random_(0, 256, generator=g)
+        if ps4:
+            sc = dst[:, cb:].view(dst.shape[0], -1, 46)
+            sc[:, :, 0].fill_(synth.SCALE_LO)
+            lo = torch.randint(0, 7, sc[:, :, 1:].shape, dtype=torch.uint8, device=dev, generator=g)
+            hi = torch.randint(0, 7, sc[:, :, 1:].shape, dtype=torch.uint8, device=dev, generator=g)
+            sc[:, :, 1:] = lo | (hi << 4)
+        else:
+            dst[:, cb:].random_(synth.SCALE_LO, synth.SCALE_HI + 1, generator=g)
+
+    if A.layout == "t950":
+        # the resident layout is produced the way a store is loaded: raw slots repacked on the device, 128 at a time
+        chunk = torch.empty((N_EXPERTS, GPTOSS_LAYOUT.slot_bytes), dtype=torch.uint8, device=dev)
+        for c0 in range(0, n_slots, N_EXPERTS):
+            fill_store(chunk, False)
+            tiles.repack_to_t950(chunk, pool[c0:c0 + N_EXPERTS])
+        torch.cuda.synchronize()
+        del chunk
     else:
-        pool[:, cb:].random_(synth.SCALE_LO, synth.SCALE_HI + 1, generator=g)
+        fill_store(pool, A.layout == "ps4")
     torch.cuda.synchronize()
     log("pool filled")
     bias_gu = torch.zeros(n_slots, L.gate_up_n, dtype=torch.bfloat16, device=dev)
     bias_dn = torch.zeros(n_slots, L.down_n, dtype=torch.bfloat16, device=dev)
-    rx = ResidentExperts(pool, L, bias_gu, bias_dn, gu_pairs_per_wave=A.gu_pairs, dn_pairs_per_wave=A.dn_pairs)
+    rx = ResidentExperts(pool, L, bias_gu, bias_dn, gu_pairs_per_wave=A.gu_pairs, dn_pairs_per_wave=A.dn_pairs,
+                         k_split=A.k_split)
 
     B = A.batch
     rng = np.random.default_rng(2026)
@@ -225,7 +243,8 @@ def main():
     per_launch = tot["gate_up"][1] / tot["gate_up"][2]
     roofline = {"bound": "hbm", "achieved": round(gu["gbps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gu["gbps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "k_moe_gate_up", "avg_launch_us": round(gu["avg_us"], 3),
+                "kernel": "k_moe_gate_up_t950" if A.layout == "t950" else "k_moe_gate_up",
+                "avg_launch_us": round(gu["avg_us"], 3),
                 "algorithmic_bytes_per_launch": int(per_launch),
                 "down_kernel_gbps": round(kern["down"]["gbps"], 1),
                 "down_avg_launch_us": round(kern["down"]["avg_us"], 3),

@@ -72,6 +72,34 @@ int na_moe_decode(const void* x, const int64_t* topk_ids, const void* topk_w, in
 int na_router_topk(const void* xn, int B, const void* w_router, const void* b_router, int n_exp, float* logits,
                    unsigned int* counter, int64_t* ids_out, void* w_out, hipStream_t stream);
 
+/* Device self-check of the MFMA operand layout the tile kernels use: d [16, 16] fp32 = a [16, 32] x b [32, 16] bf16. */
+int na_selftest_mfma(const void* a, const void* b, float* d, hipStream_t stream);
+
+/* ---- gfx950 tile layout ("t950", weight_repr "mxfp4_g32_t950").  No counterpart in the reference's store; it is
+ * this build's resident layout, a lossless permutation of the reference's slot (neural/moe/layout.py:143-186,
+ * tools/scale_pack.py:6-12): 540 blocks of 16 rows, each 22.5 KiB of codes in v_mfma_f32_16x16x32_bf16 B-operand
+ * order followed by 16 x 96-byte E8M0 scale rows.  13,271,040 bytes per slot. */
+long long na_t950_slot_bytes(void);
+
+/* Repack n_slots store slots (raw, or PS4 with src_ps4 = 1; row stride src_stride) into t950 (row stride dst_stride).
+ * Replaces the role of the reference's offline store converters tools/pack_store.py / tools/build_store.py for the
+ * GPU-resident layout: lossless, src and dst must not overlap. */
+int na_repack_to_t950(const void* src, long long src_stride, int src_ps4, void* dst, long long dst_stride,
+                      int n_slots, hipStream_t stream);
+
+/* Inverse of na_repack_to_t950: t950 -> raw (dst_ps4 = 0) or canonical PS4 (dst_ps4 = 1: base = row minimum, the
+ * encoding of tools/scale_pack.py:49-64). */
+int na_repack_from_t950(const void* src, long long src_stride, void* dst, long long dst_stride, int dst_ps4,
+                        int n_slots, hipStream_t stream);
+
+/* na_moe_decode over a t950 pool (slot_bytes >= 13,271,040, 16-byte aligned): the same contract and results as
+ * na_moe_decode (server.py:508-518), computed with v_mfma_f32_16x16x32_bf16 on in-register dequantised codes.
+ * k_split = waves per workgroup splitting K (1, 2 or 4; <= 0: 4). */
+int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_w, int B, const void* pool,
+                       long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
+                       const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha, float limit,
+                       int k_split, void* const* events, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

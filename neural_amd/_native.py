@@ -24,7 +24,13 @@ SIGNATURES = {
     "na_mxfp4_gemv": [VP, I32, VP, I64, VP, I64, I32, VP, I32, VP, I32, VP, I32, I32, I32, VP],
     "na_moe_decode": [VP, VP, VP, I32, VP, I64, I32, VP, I64, VP, VP, VP, VP, VP, F32, F32, I32, I32, VP, VP],
     "na_router_topk": [VP, I32, VP, VP, I32, VP, VP, VP, VP, VP],
+    "na_selftest_mfma": [VP, VP, VP, VP],
+    "na_t950_slot_bytes": [],
+    "na_repack_to_t950": [VP, I64, I32, VP, I64, I32, VP],
+    "na_repack_from_t950": [VP, I64, VP, I64, I32, I32, VP],
+    "na_moe_decode_t950": [VP, VP, VP, I32, VP, I64, VP, I64, VP, VP, VP, VP, VP, F32, F32, I32, VP, VP],
 }
+RESTYPES = {"na_t950_slot_bytes": I64}
 
 ERRORS = {-1: "invalid arguments", -2: "kernel launch failed", -3: "size beyond the kernel's limits"}
 
@@ -46,7 +52,7 @@ def lib() -> ctypes.CDLL:
         for name, args in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = args
-            fn.restype = I32
+            fn.restype = RESTYPES.get(name, I32)
         _LIB = handle
     return _LIB
 

@@ -15,6 +15,21 @@ __global__ void k_selftest_fp4(uint16_t* out) {
   out[512 + b] = same ? 1 : 0;
 }
 
+// One v_mfma_f32_16x16x32_bf16 with A[m][k] = a_in[m * 32 + k], B[k][n] = b_in[k * 16 + n] (bf16 bits) under the
+// operand layout the tile kernels assume: lane l holds A[l % 16][8 (l / 16) + 0..7], B[8 (l / 16) + 0..7][l % 16] and
+// receives D[4 (l / 16) + r][l % 16], r = 0..3.  d_out[m * 16 + n] = D[m][n].
+__global__ void k_selftest_mfma(const uint16_t* a_in, const uint16_t* b_in, float* d_out) {
+  const int l = threadIdx.x, m = l % 16, q = l / 16;
+  bf16x8_t a, b;
+  for (int i = 0; i < 8; ++i) {
+    a[i] = __builtin_bit_cast(__bf16, a_in[m * 32 + 8 * q + i]);
+    b[i] = __builtin_bit_cast(__bf16, b_in[(8 * q + i) * 16 + m]);
+  }
+  f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  for (int r = 0; r < 4; ++r) d_out[(4 * q + r) * 16 + m] = c[r];
+}
+
 }  // namespace na
 
 extern "C" {
@@ -26,6 +41,13 @@ int na_version(void) { return 1; }
 int na_selftest_fp4(void* out, hipStream_t stream) {
   if (!out) return na::kErrArgs;
   hipLaunchKernelGGL(na::k_selftest_fp4, dim3(1), dim3(256), 0, stream, (uint16_t*)out);
+  return hipGetLastError() == hipSuccess ? na::kOk : na::kErrLaunch;
+}
+
+// D = A x B for A [16, 32], B [32, 16] bf16 (row-major), D [16, 16] fp32, through the tile kernels' MFMA layout.
+int na_selftest_mfma(const void* a, const void* b, float* d, hipStream_t stream) {
+  if (!a || !b || !d) return na::kErrArgs;
+  hipLaunchKernelGGL(na::k_selftest_mfma, dim3(1), dim3(64), 0, stream, (const uint16_t*)a, (const uint16_t*)b, d);
   return hipGetLastError() == hipSuccess ? na::kOk : na::kErrLaunch;
 }
 

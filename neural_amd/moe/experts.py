@@ -11,7 +11,7 @@ from __future__ import annotations
 import torch
 
 from .. import _native as N
-from .layout import GPTOSS_LAYOUT, ExpertLayout
+from .layout import GPTOSS_LAYOUT, TILE_REPR, ExpertLayout
 
 MAX_DECODE_TOKENS = 8
 
@@ -19,9 +19,17 @@ MAX_DECODE_TOKENS = 8
 class ResidentExperts:
     def __init__(self, pool: torch.Tensor, layout: ExpertLayout = GPTOSS_LAYOUT, bias_gu: torch.Tensor | None = None,
                  bias_dn: torch.Tensor | None = None, slot_tab: torch.Tensor | None = None,
-                 max_batch: int = MAX_DECODE_TOKENS, gu_pairs_per_wave: int = 4, dn_pairs_per_wave: int = 2):
-        if layout.weight_repr not in ("mxfp4_g32", "mxfp4_g32_ps4"):
-            raise ValueError(f"ResidentExperts serves the raw and PS4 slot layouts, not {layout.weight_repr}")
+                 max_batch: int = MAX_DECODE_TOKENS, gu_pairs_per_wave: int = 4, dn_pairs_per_wave: int = 2,
+                 k_split: int = 4):
+        """pool: uint8 [n, layout.slot_bytes] in the raw, PS4 or t950 (gfx950 tile) layout.  The t950 layout runs the
+        MFMA decode kernels (k_split waves per workgroup split K); the store layouts run the VALU kernels
+        (gu/dn_pairs_per_wave row pairs per wavefront)."""
+        if layout.weight_repr not in ("mxfp4_g32", "mxfp4_g32_ps4", TILE_REPR):
+            raise ValueError(f"ResidentExperts serves the raw, PS4 and t950 slot layouts, not {layout.weight_repr}")
+        if k_split not in (1, 2, 4):
+            raise ValueError("k_split must be 1, 2 or 4")
+        self.k_split = int(k_split)
+        self.tiled = layout.weight_repr == TILE_REPR
         if pool.dtype is not torch.uint8 or pool.ndim != 2 or pool.shape[1] != layout.slot_bytes:
             raise ValueError(f"pool must be uint8 [n, {layout.slot_bytes}]")
         if not pool.is_contiguous() or pool.device.type != "cuda":
@@ -74,6 +82,13 @@ class ResidentExperts:
             out = torch.empty(B, L.hidden, dtype=torch.bfloat16, device=hidden.device)
         elif out.dtype is not torch.bfloat16 or tuple(out.shape) != (B, L.hidden) or not out.is_contiguous():
             raise ValueError("out must be contiguous bf16 [B, hidden]")
+        if self.tiled:
+            N.call("na_moe_decode_t950", hidden.data_ptr(), router_indices.data_ptr(), routing_weights.data_ptr(), B,
+                   self.pool.data_ptr(), L.slot_bytes, N.ptr(self.slot_tab), layer * L.n_experts,
+                   N.ptr(self.bias_gu), N.ptr(self.bias_dn), self.h.data_ptr(), self.yw.data_ptr(), out.data_ptr(),
+                   float(L.act_alpha), float(L.act_limit), self.k_split, N.events_array(events),
+                   N.stream(hidden.device))
+            return out
         N.call("na_moe_decode", hidden.data_ptr(), router_indices.data_ptr(), routing_weights.data_ptr(), B,
                self.pool.data_ptr(), L.slot_bytes, L.scale_layout_mode, N.ptr(self.slot_tab), layer * L.n_experts,
                N.ptr(self.bias_gu), N.ptr(self.bias_dn), self.h.data_ptr(), self.yw.data_ptr(), out.data_ptr(),

@@ -83,6 +83,9 @@ class ExpertLayout:
 
     @property
     def slot_bytes(self) -> int:
+        if self.weight_repr == TILE_REPR:
+            # 16-row blocks of 24,576 B: codes in MFMA-operand tiles, then 16 padded 96-byte E8M0 rows
+            return (self.gate_up_n + self.down_n) // 16 * (self.hidden // 2 * 16 + 16 * 96)
         return self.gate_pack_bytes + self.down_pack_bytes + self.gate_saz_bytes + self.down_saz_bytes
 
     @property
@@ -129,6 +132,8 @@ _GPTOSS = dict(n_layers=36, n_experts=128, top_k=4, hidden=2880, gate_up_n=5760,
 
 GPTOSS_LAYOUT = ExpertLayout("gpt-oss-120b", weight_repr="mxfp4_g32", **_GPTOSS)
 GPTOSS_LAYOUT_PS4 = ExpertLayout("gpt-oss-120b-ps4", weight_repr="mxfp4_g32_ps4", **_GPTOSS)
+GPTOSS_LAYOUT_T950 = ExpertLayout("gpt-oss-120b-t950", weight_repr=TILE_REPR, **_GPTOSS)
+assert GPTOSS_LAYOUT_T950.slot_bytes == 13_271_040
 # raw slot byte count: codes 8,294,400 + 4,147,200, scales 518,400 + 259,200 (reference layout.py:147,155)
 assert GPTOSS_LAYOUT.slot_bytes == 13_219_200
 assert GPTOSS_LAYOUT_PS4.slot_bytes == 12_839_040

@@ -170,7 +170,7 @@ def test_reject_bad_shapes_dtypes_and_strides():
 # -------------------------------------------------------------------------------------------------------- ABI
 def _declared_symbols():
     text = open(os.path.join(ROOT, "include", "neural_amd.h")).read()
-    return sorted(set(re.findall(r"\bint\s+(na_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(?:int|long long)\s+(na_\w+)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -183,6 +183,7 @@ def test_library_exports_every_declared_symbol():
         assert s in N.SIGNATURES, f"{s} has no ctypes signature"
     assert set(N.SIGNATURES) == set(syms)
     assert lib.na_version() == 1
+    assert lib.na_t950_slot_bytes() == 13_271_040
 
 
 def test_library_rejects_bad_arguments_without_launching():

@@ -1,0 +1,217 @@
+"""gfx950 tile layout (t950): the host codec against the independent byte-map restatement (oracle/tiles_oracle.py),
+exact round trips raw -> t950 -> raw and PS4 -> t950 -> PS4, the map is a bijection onto the non-padding bytes, and
+dequantising through the tile layout reproduces the store's dequantised weights (CPU).  On the GPU: the repack
+kernels equal the host codec bit for bit, and the MFMA decode over a t950 pool matches the oracle and the
+store-layout kernels."""
+import numpy as np
+import pytest
+
+from oracle import mxfp4_oracle as mo
+from oracle import tiles_oracle as to
+from neural_amd import scale_pack as sp
+from neural_amd import synth
+from neural_amd import tiles
+
+
+@pytest.fixture(scope="module")
+def slot():
+    return synth.slot_raw(np.random.default_rng(31))
+
+
+def test_codec_matches_byte_map(slot):
+    assert tiles.SLOT_T950 == to.SLOT_T950 == 13_271_040
+    assert np.array_equal(tiles.slot_to_t950(slot), to.to_t950(slot))
+
+
+def test_byte_map_is_a_bijection_onto_non_padding_bytes():
+    m = to.source_to_dest_map()
+    assert np.unique(m).size == m.size == sp.SLOT_RAW
+    pad = np.setdiff1d(np.arange(to.SLOT_T950), m)
+    assert pad.size == to.SLOT_T950 - sp.SLOT_RAW
+    off = pad % to.BLOCK
+    assert (off >= to.CODE).all() and ((off - to.CODE) % to.PITCH >= 90).all()     # only scale-row padding
+    # spot-check the closed form at the tile boundaries
+    assert to.code_dest(0, 0, 0, 0) == 0 and to.code_dest(0, 1, 0, 0) == 16
+    assert to.code_dest(0, 0, 0, 4) == 256 and to.code_dest(0, 0, 1, 0) == 4 and to.code_dest(0, 0, 4, 0) == 1024
+    assert to.code_dest(0, 0, 88, 0) == 22 * 1024 and to.code_dest(1, 0, 0, 0) == 360 * to.BLOCK
+
+
+def test_round_trips(slot):
+    t = tiles.slot_to_t950(slot)
+    assert np.array_equal(tiles.t950_to_slot(t), slot)
+    pk = sp.pack_slot(slot)
+    t2 = tiles.slot_to_t950(pk, packed=True)
+    assert np.array_equal(t2, t)
+    assert np.array_equal(tiles.t950_to_slot(t2, packed=True), pk)
+    # negative control: a changed byte must not survive the round trip unchanged
+    bad = t.copy()
+    bad[12345] ^= 0x10
+    assert not np.array_equal(tiles.t950_to_slot(bad), slot)
+
+
+def test_dequant_through_tiles_matches_store(slot):
+    """Decode lanes of one t950 block the way the MFMA kernels read them and compare with the store's dequant."""
+    t = tiles.slot_to_t950(slot).reshape(540, tiles.BLOCK_BYTES)
+    wg, _ = mo.expert_weights(slot)
+    for blk in (0, 7, 359):
+        b = t[blk]
+        sc = b[tiles.CODE_BYTES:].reshape(16, 96)
+        for tt in (0, 13, 22):
+            for lane in (0, 17, 63):
+                n, q = lane % 16, lane // 16
+                ng = 4 if tt < 22 else 2
+                piece = b[tt * 1024 + 16 * lane: tt * 1024 + 16 * lane + 16] if tt < 22 else \
+                    b[22 * 1024 + 8 * lane: 22 * 1024 + 8 * lane + 8]
+                for j in range(ng):
+                    g = 4 * tt + j
+                    word = piece[4 * j: 4 * j + 4]
+                    vals = np.empty(8, np.float32)
+                    vals[0::2] = mo.E2M1[word & 15]
+                    vals[1::2] = mo.E2M1[word >> 4]
+                    vals *= mo.e8m0_value(sc[n, g])
+                    row = 16 * blk + n
+                    assert np.array_equal(vals, wg[row, 32 * g + 8 * q: 32 * g + 8 * q + 8])
+
+
+# ================================================================================================ GPU
+def _dev():
+    import torch
+    from neural_amd import _native as N
+    N.lib()
+    return torch.device("cuda", 0)
+
+
+@pytest.mark.gpu
+def test_mfma_operand_layout():
+    import torch
+    from neural_amd import _native as N
+    dev = _dev()
+    rng = np.random.default_rng(4)
+    a = synth.bf16_normal(rng, (16, 32))
+    b = synth.bf16_normal(rng, (32, 16))
+    d = torch.zeros(16, 16, dtype=torch.float32, device=dev)
+    ad, bd = a.to(dev), b.to(dev)                 # keep the device copies alive across the launch
+    N.call("na_selftest_mfma", ad.data_ptr(), bd.data_ptr(), d.data_ptr(), N.stream(dev))
+    torch.cuda.synchronize()
+    want = a.double().numpy() @ b.double().numpy()
+    assert np.abs(d.cpu().numpy() - want).max() <= 1e-4 * np.abs(want).max()
+
+
+@pytest.mark.gpu
+def test_repack_kernels_equal_host_codec_and_round_trip():
+    import torch
+    dev = _dev()
+    rng = np.random.default_rng(8)
+    raws = [synth.slot_raw(rng) for _ in range(3)]
+    raws[1][sp.OFF_GS:] = synth.slot_raw(rng, 100, 115)[sp.OFF_GS:]      # other exponents, span 15
+    want = np.stack([tiles.slot_to_t950(r) for r in raws])
+    src = torch.from_numpy(np.stack(raws)).to(dev)
+    dst = torch.full((3, tiles.SLOT_T950), 0xAB, dtype=torch.uint8, device=dev)
+    print("case repack raw -> t950 (3 slots)", flush=True)
+    tiles.repack_to_t950(src, dst)
+    torch.cuda.synchronize()
+    assert np.array_equal(dst.cpu().numpy(), want)
+    pk = torch.from_numpy(np.stack([sp.pack_slot(r) for r in raws])).to(dev)
+    dst2 = torch.zeros_like(dst)
+    tiles.repack_to_t950(pk, dst2, packed=True)
+    back = torch.zeros_like(src)
+    tiles.repack_from_t950(dst, back)
+    back_pk = torch.zeros_like(pk)
+    tiles.repack_from_t950(dst, back_pk, packed=True)
+    torch.cuda.synchronize()
+    assert torch.equal(dst2, dst)
+    assert torch.equal(back, src)
+    assert torch.equal(back_pk, pk)
+
+
+def _t950_case(B, seed, bias, nslot=10):
+    rng = np.random.default_rng(seed)
+    slots = [synth.slot_raw(rng) for _ in range(nslot)]
+    x = synth.bf16_normal(rng, (B, 2880))
+    ids = np.stack([rng.choice(128, 4, replace=False) for _ in range(B)]).astype(np.int64)
+    if B >= 2:
+        ids[1, 1] = ids[0, 3]
+    if B >= 4:
+        ids[3, 0] = ids[0, 3]                                  # one expert shared by three tokens
+    w = mo.rb(np.full((B, 4), 0.25, np.float32) + rng.uniform(-0.1, 0.1, (B, 4)).astype(np.float32))
+    n = 36 * 128
+    tab = (np.arange(n) % nslot).astype(np.int64)
+    bgu = synth.bf16_normal(rng, (n, 5760), 0.02) if bias else None
+    bdn = synth.bf16_normal(rng, (n, 2880), 0.02) if bias else None
+    return slots, x, ids, w, tab, bgu, bdn
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B,k_split,bias", [(1, 4, False), (1, 1, True), (2, 2, True), (4, 4, True), (8, 4, False),
+                                            (8, 2, True)])
+def test_moe_decode_t950_matches_oracle_and_store_path(B, k_split, bias):
+    import torch
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_T950
+    dev = _dev()
+    slots, x, ids, w, tab, bgu, bdn = _t950_case(B, 500 + B + k_split, bias)
+    print(f"case moe_decode_t950 B={B} k_split={k_split} bias={bias}", flush=True)
+    raw = torch.from_numpy(np.stack(slots)).to(dev)
+    tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
+    tiles.repack_to_t950(raw, tp)
+    tabd = torch.from_numpy(tab).to(dev)
+    bg = None if bgu is None else bgu.to(dev)
+    bd = None if bdn is None else bdn.to(dev)
+    rt = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=k_split)
+    rr = ResidentExperts(raw, GPTOSS_LAYOUT, bg, bd, tabd)
+    xd, idd = x.to(dev), torch.from_numpy(ids).to(dev)
+    wd = torch.from_numpy(w).to(torch.bfloat16).to(dev)
+    layer = 7
+    got = rt.forward_decode(layer, xd, idd, wd).float().cpu().numpy()
+    ref_store = rr.forward_decode(layer, xd, idd, wd).float().cpu().numpy()
+    torch.cuda.synchronize()
+    cache = {}
+    for b in range(B):
+        ys = []
+        for k in range(4):
+            g = layer * 128 + int(ids[b, k])
+            s = int(tab[g])
+            if s not in cache:
+                cache[s] = mo.expert_weights(slots[s])
+            bgv = np.zeros(5760, np.float32) if bgu is None else bgu[g].float().numpy()
+            bdv = np.zeros(2880, np.float32) if bdn is None else bdn[g].float().numpy()
+            ys.append(mo.expert_forward_bf16(x[b:b + 1].float().numpy(), None, bgv, bdv, weights=cache[s])[0])
+        want = mo.combine_bf16(np.stack(ys), w[b])
+        scale = np.abs(want).max()
+        for name, arr in (("t950", got[b]), ("store", ref_store[b])):
+            d = np.abs(arr - want)
+            assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale, (name, b, d.max(), d.mean(), scale)
+
+
+@pytest.mark.gpu
+def test_moe_decode_t950_graph_replay():
+    import torch
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
+    dev = _dev()
+    B = 2
+    slots, x, ids, w, tab, bgu, bdn = _t950_case(B, 77, True, nslot=6)
+    raw = torch.from_numpy(np.stack(slots)).to(dev)
+    tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
+    tiles.repack_to_t950(raw, tp)
+    rt = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bgu.to(dev), bdn.to(dev), torch.from_numpy(tab).to(dev))
+    xd, idd = x.to(dev), torch.from_numpy(ids).to(dev)
+    wd = torch.from_numpy(w).to(torch.bfloat16).to(dev)
+    out = torch.empty(B, 2880, dtype=torch.bfloat16, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        rt.forward_decode(2, xd, idd, wd, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rt.forward_decode(2, xd, idd, wd, out=out)
+    rng = np.random.default_rng(3)
+    for rep in range(3):
+        xd.copy_(synth.bf16_normal(rng, (B, 2880)).to(dev))
+        idd.copy_(torch.from_numpy(np.stack([rng.choice(128, 4, replace=False) for _ in range(B)])).to(dev))
+        g.replay()
+        torch.cuda.synchronize()
+        eager = rt.forward_decode(2, xd, idd, wd)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), rep
