@@ -37,6 +37,37 @@ SLOT_ALGO_BYTES = GATE_UP_BYTES + DOWN_BYTES      # 13,219,200
 N_LAYERS, N_EXPERTS, TOPK, H = 36, 128, 4, 2880
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+KERNEL_SOURCES = ("neural_amd/csrc/common.h", "neural_amd/csrc/tiles.hip", "neural_amd/csrc/moe_decode.hip")
+
+
+def sources_sha256():
+    import hashlib
+    h = hashlib.sha256()
+    for f in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()
+
+
+def measured_traffic(kernel, layout, batch, k_split):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE per
+    dispatch, each scaled by the factor a 1 GiB copy kernel calibrates), or None when no entry was measured on the
+    current kernel sources for this workload."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            tab = json.load(fh)
+    except (OSError, ValueError):
+        return None, "no traffic table"
+    sha = sources_sha256()
+    for e in tab.get("entries", []):
+        if (e["kernel"], e["layout"], e["batch"], e["k_split"]) == (kernel, layout, batch, k_split):
+            if e["sources_sha256"] != sha:
+                return None, "traffic table measured on other kernel sources"
+            return int(e["hbm_bytes_per_launch"]), "ok"
+    return None, "workload not in traffic table"
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -118,6 +149,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--gu-pairs", type=int, default=4, help="gate_up row pairs per wavefront (1, 2, 4)")
     ap.add_argument("--dn-pairs", type=int, default=2, help="down row pairs per wavefront (1, 2, 4)")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="run one device-to-device copy of this many MB first (a known-size kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
     A = ap.parse_args()
     if A.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {A.gpus} is not supported (the design note on "
@@ -133,6 +167,14 @@ def main():
     from neural_amd import synth, tiles
 
     dev = torch.device("cuda", 0)
+    if A.calib_copy_mb:
+        src = torch.empty(A.calib_copy_mb << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     L = {"t950": GPTOSS_LAYOUT_T950, "raw": GPTOSS_LAYOUT, "ps4": GPTOSS_LAYOUT_PS4}[A.layout]
     n_slots = N_LAYERS * N_EXPERTS
     log(f"allocating pool {n_slots} x {L.slot_bytes} B = {n_slots * L.slot_bytes / 1e9:.1f} GB ({L.weight_repr})")
@@ -241,9 +283,12 @@ def main():
         log(f"kernel {nm}: avg {v['avg_us']:.2f} us/launch, {v['gbps']:.0f} GB/s algorithmic")
     gu = kern["gate_up"]
     per_launch = tot["gate_up"][1] / tot["gate_up"][2]
+    kname = "k_moe_gate_up_t950" if A.layout == "t950" else "k_moe_gate_up"
+    traffic, why = measured_traffic(kname, A.layout, B, A.k_split)
+    log(f"traffic: {traffic} ({why})")
     roofline = {"bound": "hbm", "achieved": round(gu["gbps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gu["gbps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "k_moe_gate_up_t950" if A.layout == "t950" else "k_moe_gate_up",
+                "frac": round(gu["gbps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": kname,
                 "avg_launch_us": round(gu["avg_us"], 3),
                 "algorithmic_bytes_per_launch": int(per_launch),
                 "down_kernel_gbps": round(kern["down"]["gbps"], 1),

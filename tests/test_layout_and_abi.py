@@ -193,3 +193,13 @@ def test_library_rejects_bad_arguments_without_launching():
     assert lib.na_mxfp4_gemv(None, 0, None, 0, None, 0, 0, None, 4, None, 0, None, 5760, 2880, 0, None) == -1
     assert lib.na_moe_decode(None, None, None, 1, None, 0, 0, None, 0, None, None, None, None, None,
                              ctypes.c_float(1.702), ctypes.c_float(7.0), 0, 0, None, None) == -1
+
+
+def test_product_code_never_touches_the_oracle():
+    """The oracle is the checker only: no module of the package imports, loads or runs anything under oracle/."""
+    pkg = os.path.join(ROOT, "neural_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert not re.search(r"\boracle\b", text), f"{f} mentions the oracle"
