@@ -7,12 +7,14 @@ MXFP4 slots: uniform E2M1 codes, E8M0 exponents uniform in [119, 125]); B decode
 of 128 experts from random router logits, softmax weights.  One STEP = the expert body of all 36 layers in sequence
 (per layer: gate_up GEMV + bias + clamped SwiGLU; down GEMV + bias + routing weight; top-k combine), captured as
 one hipGraph per routing set; 16 routing sets are cycled so the 256 MB Infinity Cache never serves a repeated
-expert.  value = decode tokens per second of that step (B tokens per step), whole job.
+expert.  With the t950 layout and B <= 2 the body of a layer is two launches (gate_up; down with the top-k combine),
+else three.  value = decode tokens per second of that step (B tokens per step), whole job.
 
 Also printed on the same JSON line:
-  roofline      the dominant kernel (gate_up): algorithmic bytes per launch (distinct experts x 8,812,800 B of codes +
-                E8M0 scales) / its average launch duration, measured with events timestamped by the dispatches
-                themselves (hipExtLaunchKernel) on the launch stream, over an eager pass of the same steps; peak = 8 TB/s.
+  roofline      the dominant kernel (gate_up): algorithmic bytes per launch (distinct experts x 8,812,800 B of E2M1
+                codes + E8M0 scales) / its average launch duration, measured with events timestamped by the
+                dispatches themselves (hipExtLaunchKernel) on the launch stream, over an eager pass of the same
+                steps; peak = 8 TB/s.
   cpu_baseline  the reference's own C expert kernel (kernels/gptoss_cpu_multi.c, AVX-512, or gptoss_cpu_portable.c,
                 built from source into oracle/_ref/) on this host's cores over a bounded sample of the same workload.
 """
@@ -143,6 +145,9 @@ def main():
     ap.add_argument("--layout", choices=("t950", "raw", "ps4"), default="t950",
                     help="resident slot layout: gfx950 tiles (MFMA kernels) or the store layouts (VALU kernels)")
     ap.add_argument("--k-split", type=int, default=4, help="t950: waves per workgroup splitting K (1, 2, 4)")
+    ap.add_argument("--down", choices=("combine", "expert"), default="combine",
+                    help="t950, batch <= 2: down kernel that also does the top-k combine (default), or expert-major "
+                         "down + combine kernel")
     ap.add_argument("--sets", type=int, default=16, help="routing sets (graphs) cycled over the steps")
     ap.add_argument("--roofline-steps", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
@@ -210,7 +215,9 @@ def main():
     bias_gu = torch.zeros(n_slots, L.gate_up_n, dtype=torch.bfloat16, device=dev)
     bias_dn = torch.zeros(n_slots, L.down_n, dtype=torch.bfloat16, device=dev)
     rx = ResidentExperts(pool, L, bias_gu, bias_dn, gu_pairs_per_wave=A.gu_pairs, dn_pairs_per_wave=A.dn_pairs,
-                         k_split=A.k_split)
+                         k_split=A.k_split, combine_in_down=A.down == "combine")
+    launches = rx.launches(A.batch)
+    per_layer = len(launches)
 
     B = A.batch
     rng = np.random.default_rng(2026)
@@ -242,7 +249,7 @@ def main():
             step(s)
         graphs.append(gr)
     torch.cuda.synchronize()
-    log(f"captured {len(graphs)} graphs of {3 * N_LAYERS} kernels; warm-up {A.warmup} steps")
+    log(f"captured {len(graphs)} graphs of {per_layer * N_LAYERS} kernels; warm-up {A.warmup} steps")
     for i in range(A.warmup):
         graphs[i % A.sets].replay()
     torch.cuda.synchronize()
@@ -260,19 +267,21 @@ def main():
         f"{step_bytes / (ms_step * 1e-3) / 1e9:.0f} GB/s whole-step")
 
     # ------------------------------------------------------------------ roofline pass (per-kernel events)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(N_LAYERS)]
+    per_kernel_bytes = {"gate_up": GATE_UP_BYTES, "down": DOWN_BYTES, "down_combine": DOWN_BYTES, "combine": 0}
+    kernels = tuple((nm, per_kernel_bytes[nm]) for nm in launches)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * len(kernels))] for _ in range(N_LAYERS)]
     for row in ev:
         for e in row:
             e.record()
     torch.cuda.synchronize()
-    tot = {"gate_up": [0.0, 0.0, 0], "down": [0.0, 0.0, 0], "combine": [0.0, 0.0, 0]}
+    tot = {nm: [0.0, 0.0, 0] for nm, _ in kernels}
     for r in range(A.roofline_steps):
         s = r % A.sets
         step(s, events=ev)
         torch.cuda.synchronize()
         for l in range(N_LAYERS):
             d = int(distinct[s, l])
-            for k, (nm, per) in enumerate((("gate_up", GATE_UP_BYTES), ("down", DOWN_BYTES), ("combine", 0))):
+            for k, (nm, per) in enumerate(kernels):
                 ms = ev[l][2 * k].elapsed_time(ev[l][2 * k + 1])
                 tot[nm][0] += ms
                 tot[nm][1] += d * per
@@ -281,19 +290,22 @@ def main():
             for nm, v in tot.items()}
     for nm, v in kern.items():
         log(f"kernel {nm}: avg {v['avg_us']:.2f} us/launch, {v['gbps']:.0f} GB/s algorithmic")
-    gu = kern["gate_up"]
-    per_launch = tot["gate_up"][1] / tot["gate_up"][2]
+    dom = kernels[0][0]
+    top = kern[dom]
+    per_launch = tot[dom][1] / tot[dom][2]
     kname = "k_moe_gate_up_t950" if A.layout == "t950" else "k_moe_gate_up"
     traffic, why = measured_traffic(kname, A.layout, B, A.k_split)
     log(f"traffic: {traffic} ({why})")
-    roofline = {"bound": "hbm", "achieved": round(gu["gbps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gu["gbps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+    roofline = {"bound": "hbm", "achieved": round(top["gbps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(top["gbps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "kernel": kname,
-                "avg_launch_us": round(gu["avg_us"], 3),
-                "algorithmic_bytes_per_launch": int(per_launch),
-                "down_kernel_gbps": round(kern["down"]["gbps"], 1),
-                "down_avg_launch_us": round(kern["down"]["avg_us"], 3),
-                "combine_avg_launch_us": round(kern["combine"]["avg_us"], 3)}
+                "avg_launch_us": round(top["avg_us"], 3),
+                "algorithmic_bytes_per_launch": int(per_launch)}
+    for nm, v in kern.items():
+        if nm != dom:
+            roofline[f"{nm}_avg_launch_us"] = round(v["avg_us"], 3)
+            if v["gbps"]:
+                roofline[f"{nm}_kernel_gbps"] = round(v["gbps"], 1)
 
     cpu = None
     if not A.skip_cpu:

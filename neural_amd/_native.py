@@ -28,7 +28,7 @@ SIGNATURES = {
     "na_t950_slot_bytes": [],
     "na_repack_to_t950": [VP, I64, I32, VP, I64, I32, VP],
     "na_repack_from_t950": [VP, I64, VP, I64, I32, I32, VP],
-    "na_moe_decode_t950": [VP, VP, VP, I32, VP, I64, VP, I64, VP, VP, VP, VP, VP, F32, F32, I32, VP, VP],
+    "na_moe_decode_t950": [VP, VP, VP, I32, VP, I64, VP, I64, VP, VP, VP, VP, VP, F32, F32, I32, I32, VP, VP],
 }
 RESTYPES = {"na_t950_slot_bytes": I64}
 

@@ -146,8 +146,14 @@ __global__ __launch_bounds__(256) void k_repack_from_t950(const uint8_t* __restr
 // B = codes dequantised in registers by v_cvt_scalef32_pk_bf16_fp4 with the group's E8M0 scale), and the partial D
 // tiles are summed in a fixed order through LDS.  No cross-lane reduction and no per-group scaling pass: the MFMA
 // accumulates over all of K.  Exact dequant: E2M1 x 2^(s-127) is a bf16 for the configured exponent range.
+// Code tiles are read with non-temporal 128-bit loads (each weight byte is used once per step); a row block's 1,536
+// scale bytes are read by the workgroup with coalesced 16-byte loads and staged in LDS, so that each wave reads its
+// scales from LDS instead of issuing one scattered 64-lane load per tile.
 constexpr int kMaxTokT = 16;                 // tokens per expert the MFMA M dimension holds
 constexpr int kXPitch = kH * 2 + 16;         // LDS bytes per staged token row (padded against bank conflicts)
+constexpr int kScPitch = 112;                // LDS bytes per staged scale row: 28 dwords, so 16 rows hit 16 banks
+constexpr int kScLds = kTRows * kScPitch;    // 1,792 LDS bytes per staged row block
+constexpr int kScPieces = kTRows * kTScalePitch / 16;   // 96 16-byte pieces of scales per row block
 
 NA_DEVICE float e8m0_f32(uint32_t s) { return __uint_as_float(s << 23); }
 
@@ -169,89 +175,127 @@ NA_DEVICE void ktile_range(int w, int& t0, int& t1) {
   t1 = (kTTiles * (w + 1)) / KS;
 }
 
-constexpr int kMaxTilesPerWave = 23;
-
-// Accumulate one row block over k-tiles [t0, t1) of this wave.  Code and scale loads of every tile are issued first.
-// Code and scale registers of one row block over this wave's k-tiles [t0, t1).
+// Code registers of one row block over this wave's k-tiles [t0, t1).
 template <int MT>
-struct BlockRegs {
+struct CodeRegs {
   uint4 c[MT];
-  uint32_t sc[MT];
 };
 
+// Branch-free: every wave issues exactly MT loads, all before any wait.  Slot i holds tile t0 + i when that is below
+// t1, else a copy of tile t0 whose codes block_compute replaces by zeros (E2M1 code 0 is +0, so the slot adds
+// nothing).  The half tile is read as 16 bytes per lane at 8-byte stride (the last lane's excess bytes fall in the
+// block's scale rows) and block_compute zeroes its groups 90 and 91.  The zeroing happens at the use, so that no
+// wait for the codes is placed before the first barrier.
+NA_DEVICE int slot_tile(int t0, int t1, int i) { return t0 + i < t1 ? t0 + i : t0; }
+
 template <int MT>
-NA_DEVICE void block_load(const uint8_t* blk, int lane, int t0, int t1, BlockRegs<MT>& r) {
-  const int n = lane & 15;
+NA_DEVICE void code_load(const uint8_t* blk, int lane, int t0, int t1, CodeRegs<MT>& r) {
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
-    const int t = t0 + i;
-    if (t < t1) {
-      if (t < kTFull) {
-        r.c[i] = load16(blk + t * 1024 + 16 * lane);
-      } else {
-        const uint2 h = *reinterpret_cast<const uint2*>(blk + kTFull * 1024 + 8 * lane);
-        r.c[i] = make_uint4(h.x, h.y, 0, 0);
-      }
-      r.sc[i] = *reinterpret_cast<const uint32_t*>(blk + kTCodes + n * kTScalePitch + 4 * t);
-    }
+    const int t = slot_tile(t0, t1, i);
+    const int off = t < kTFull ? t * 1024 + 16 * lane : kTFull * 1024 + 8 * lane;
+    r.c[i] = load16<true>(blk + off);
   }
 }
 
-// xs_lds points at this lane's staged x row (token m = lane % 16, clamped to a staged row: rows m >= nt only feed
-// D rows that are never read).
+// Scale rows of NB row blocks (NB = 1 or 2) through registers to LDS: piece p = tid + NTH k of NB x 96 pieces;
+// piece p of block p / 96 is bytes 16 c .. 16 c + 15 of scale row n (p % 96 = 6 n + c).
+template <int NB, int NTH>
+struct ScaleRegs {
+  static constexpr int SP = (NB * kScPieces + NTH - 1) / NTH;
+  uint4 v[SP];
+};
+
+// Branch-free: thread tid handles piece min(tid + NTH k, NB x 96 - 1); the clamped duplicates store the same bytes.
+template <int NB, int NTH>
+NA_DEVICE void scale_load(int tid, const uint8_t* blk0, const uint8_t* blk1, ScaleRegs<NB, NTH>& r) {
+#pragma unroll
+  for (int k = 0; k < ScaleRegs<NB, NTH>::SP; ++k) {
+    const int p = min(tid + NTH * k, NB * kScPieces - 1);
+    const int bi = p >= kScPieces ? 1 : 0, q = p - bi * kScPieces;
+    r.v[k] = load16((bi ? blk1 : blk0) + kTCodes + 16 * q);
+  }
+}
+
+template <int NB, int NTH>
+NA_DEVICE void scale_store(int tid, uint8_t* lds, const ScaleRegs<NB, NTH>& r) {
+#pragma unroll
+  for (int k = 0; k < ScaleRegs<NB, NTH>::SP; ++k) {
+    const int p = min(tid + NTH * k, NB * kScPieces - 1);
+    const int bi = p >= kScPieces ? 1 : 0, q = p - bi * kScPieces, n = q / 6, c = q - 6 * n;
+    *reinterpret_cast<uint4*>(lds + bi * kScLds + n * kScPitch + 16 * c) = r.v[k];
+  }
+}
+
+// xs_lds points at this lane's A row (token m = lane % 16; rows m >= nt only feed D rows that are never read),
+// sc_row at this lane's staged scale row (row n = lane % 16 of the block).
 template <int MT>
-NA_DEVICE void block_compute(const BlockRegs<MT>& r, const uint8_t* xs_lds, int lane, int t0, int t1, f32x4_t& acc) {
+NA_DEVICE void block_compute(const CodeRegs<MT>& r, const uint8_t* sc_row, const uint8_t* xs_lds, int lane, int t0,
+                             int t1, f32x4_t& acc) {
   const int q = lane >> 4;
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
-    const int t = t0 + i;
-    if (t < t1) {
-      const uint32_t w[4] = {r.c[i].x, r.c[i].y, r.c[i].z, r.c[i].w};
-      const int ng = t < kTFull ? 4 : 2;
+    const int t = slot_tile(t0, t1, i);
+    const bool live = t0 + i < t1, full = live && t < kTFull;
+    const uint32_t w[4] = {live ? r.c[i].x : 0u, live ? r.c[i].y : 0u, full ? r.c[i].z : 0u, full ? r.c[i].w : 0u};
+    const uint32_t sc = *reinterpret_cast<const uint32_t*>(sc_row + 4 * t);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j < ng) {
-          const int g = 4 * t + j;
-          const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(xs_lds + (32 * g + 8 * q) * 2);
-          const bf16x8_t b = dequant8(w[j], e8m0_f32((r.sc[i] >> (8 * j)) & 0xff));
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
-        }
-      }
+    for (int j = 0; j < 4; ++j) {
+      const int g = min(4 * t + j, kGK - 1);             // zeroed groups 90, 91 read a finite A row
+      const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(xs_lds + (32 * g + 8 * q) * 2);
+      const bf16x8_t b = dequant8(w[j], e8m0_f32((sc >> (8 * j)) & 0xff));
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
     }
   }
 }
 
-// x rows of up to XT tokens, staged through registers: piece p = tid + NTH * k (k < XP) of 360 * XT 16-byte pieces.
+// Activation rows (x, or h) of up to XT tokens, staged through registers: piece p = tid + NTH * k (k < XP) of
+// 360 * XT 16-byte pieces.
 template <int XT, int NTH>
 struct XRegs {
   static constexpr int XP = (XT * (kH / 8) + NTH - 1) / NTH;
   uint4 v[XP];
 };
 
-template <int XT, int NTH>
-NA_DEVICE void x_load(const uint16_t* base, long long row_stride, const int* rows, int nt, XRegs<XT, NTH>& xr) {
+// Thread tid stages pieces p = tid + NTH k < nt x 360 (a per-lane predicate, no branch), i.e. rows t < nt
+// (1 <= nt <= XT) of the staged block, row t = source row row_of(t).  Staged rows t >= nt are not written: they only
+// feed D rows m >= nt, which are never read (each MFMA output row depends on its own A row only).
+template <int XT, int NTH, typename RowOf>
+NA_DEVICE void x_load(int tid, const uint16_t* base, long long row_stride, RowOf row_of, int nt, XRegs<XT, NTH>& xr) {
 #pragma unroll
   for (int k = 0; k < XRegs<XT, NTH>::XP; ++k) {
-    const int p = threadIdx.x + NTH * k;
+    const int p = tid + NTH * k;
     const int t = p / (kH / 8), pp = p - t * (kH / 8);
-    if (t < XT && t < nt)
-      xr.v[k] = load16(reinterpret_cast<const uint8_t*>(base + (long long)rows[t] * row_stride) + 16 * pp);
+    if (p < nt * (kH / 8))
+      xr.v[k] = load16(reinterpret_cast<const uint8_t*>(base + (long long)row_of(t) * row_stride) + 16 * pp);
   }
 }
 
 template <int XT, int NTH>
-NA_DEVICE void x_store(uint8_t* lds, int nt, const XRegs<XT, NTH>& xr) {
+NA_DEVICE void x_store(int tid, uint8_t* lds, int nt, const XRegs<XT, NTH>& xr) {
 #pragma unroll
   for (int k = 0; k < XRegs<XT, NTH>::XP; ++k) {
-    const int p = threadIdx.x + NTH * k;
+    const int p = tid + NTH * k;
     const int t = p / (kH / 8), pp = p - t * (kH / 8);
-    if (t < XT && t < nt) *reinterpret_cast<uint4*>(lds + t * kXPitch + 16 * pp) = xr.v[k];
+    if (p < nt * (kH / 8)) *reinterpret_cast<uint4*>(lds + t * kXPitch + 16 * pp) = xr.v[k];
   }
+}
+
+// Store the bf16 values v held as D columns n = lane % 16 (16 lanes per D row) as 32-bit pairs: even lanes write
+// (v[n], v[n + 1]) to row_ptr + n.  All lanes must call it (it exchanges values between neighbouring lanes).
+NA_DEVICE void store_row_pairs(uint16_t* row_ptr, uint16_t v, bool ok) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
+  if (ok && !(lane & 1)) *reinterpret_cast<uint32_t*>(row_ptr + (lane & 15)) = (uint32_t)v | (hi << 16);
 }
 
 // Route of a decode batch (same rule as the store-layout kernels): the `item`-th distinct expert in first-appearance
-// order; returns its id (or -1: no such item; 128: an invalid id) and the ascending pair list of its tokens.
-NA_DEVICE int route_t950(const int64_t* ids, int npairs, int item, int& nt, int* pair, int& distinct) {
+// order; returns its id (or -1: no such item; 128: an invalid id), nt = its number of pairs and `users` = the mask
+// of its pairs (bit p = pair p = 4 token + k; pair_at(users, m) is the m-th in ascending order).  `valid` = distinct
+// experts with a valid id (the invalid marker 128 excluded).  Pair lists stay masks in scalar registers: an indexed
+// register array would be placed in scratch memory.
+NA_DEVICE int route_t950(const int64_t* ids, int npairs, int item, int& nt, uint64_t& users, int& distinct,
+                         int& valid) {
   const int lane = threadIdx.x & 63;
   int my = 129;
   if (lane < npairs) {
@@ -266,151 +310,172 @@ NA_DEVICE int route_t950(const int64_t* ids, int npairs, int item, int& nt, int*
   }
   uint64_t fm = __ballot(lane < npairs && !dup);
   distinct = __popcll(fm);
+  valid = __popcll(__ballot(lane < npairs && !dup && my != 128));
+  users = 0;
+  nt = 0;
   if (item >= distinct) return -1;
   for (int i = 0; i < item; ++i) fm &= fm - 1;
   const int e = __builtin_amdgcn_readlane(my, __ffsll((long long)fm) - 1);
-  uint64_t users = __ballot(lane < npairs && my == e);
-  nt = 0;
-#pragma unroll
-  for (int t = 0; t < kMaxTokT; ++t) {
-    pair[t] = 0;
-    if (users) {
-      pair[t] = __ffsll((long long)users) - 1;
-      users &= users - 1;
-      nt = t + 1;
-    }
-  }
+  users = __ballot(lane < npairs && my == e);
+  nt = min(__popcll(users), kMaxTokT);
   return e;
 }
 
-// Kernel templates: KS waves per workgroup split the k-tiles; XT token rows staged (at least the batch size B).
-// Order: route -> x loads -> code and scale loads -> x to LDS, barrier -> MFMA tile by tile (each waits only for
-// its own loads) -> fixed-order sum of the KS partial tiles through LDS -> epilogue in wave 0.
+// The m-th pair (ascending) of a route's mask, 0 <= m < kMaxTokT; the mask is uniform, the walk is scalar.
+NA_DEVICE int pair_at(uint64_t users, int m) {
+  int p = __ffsll((long long)users) - 1;
+  uint64_t u = users;
+#pragma unroll
+  for (int t = 1; t < kMaxTokT; ++t) {
+    u &= u - 1;
+    const int pt = __ffsll((long long)u) - 1;
+    p = (t == m) ? pt : p;
+  }
+  return p;
+}
 
-// gate_up: output block b (rows j = 16b .. 16b + 15 of gate and of up) -> h[pair, j]
+// LDS of one expert-major decode workgroup: staged x (or h) rows, scale rows, the KS partial D tiles.
+template <int KS, int XT>
+struct DecodeLds {
+  __align__(16) uint8_t xs[XT * kXPitch];
+  __align__(16) uint8_t sc[2 * kScLds];
+  f32x4_t red[KS > 1 ? KS : 1][2][64];
+};
+
+// gate_up: output block b (rows j = 16b .. 16b + 15 of gate and of up) of the item-th distinct expert -> h[pair, j].
+// Order: route and slot -> every global load (codes, scales, x, bias) -> x and scales to LDS, barrier -> MFMA tile by
+// tile (each waits only for its own codes) -> fixed-order sum of the KS partial tiles through LDS -> epilogue in wave
+// 0, which reads nothing from global memory.
 template <int KS, int XT>
 __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
     const uint16_t* __restrict__ x, const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool,
     long long slot_bytes, const int64_t* __restrict__ slot_tab, long long expert_base,
     const uint16_t* __restrict__ bias_gu, uint16_t* __restrict__ h, float alpha, float limit) {
   constexpr int MT = (kTTiles + KS - 1) / KS;
-  __shared__ __align__(16) uint8_t xs[XT * kXPitch];
-  __shared__ f32x4_t red[KS > 1 ? KS : 1][2][64];
-  __shared__ int pairs_s[kMaxTokT];
-  int pair[kMaxTokT], nt, distinct;
-  const int e = route_t950(ids, 4 * B, blockIdx.x, nt, pair, distinct);
+  constexpr int NTH = 64 * KS;
+  __shared__ DecodeLds<KS, XT> L;
+  int nt, distinct, valid;
+  uint64_t users;
+  const int e = route_t950(ids, 4 * B, blockIdx.x, nt, users, distinct, valid);
   if (e < 0 || e == 128) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.y;
   const long long gid = expert_base + e;
   const long long slot = slot_tab ? slot_tab[gid] : gid;
-  const uint8_t* sbase = pool + slot * slot_bytes;
-  const int b = blockIdx.y;
+  const uint8_t* gblk = pool + slot * slot_bytes + (long long)b * kTBlock;
+  const uint8_t* ublk = gblk + (long long)kTUpBlock0 * kTBlock;
   int t0, t1;
   ktile_range<KS>(wave, t0, t1);
-  int tok[XT];
-#pragma unroll
-  for (int t = 0; t < XT; ++t) tok[t] = pair[t] >> 2;
-  XRegs<XT, 64 * KS> xr;
-  x_load<XT, 64 * KS>(x, kH, tok, nt, xr);
-  BlockRegs<MT> rg, ru;
-  block_load<MT>(sbase + (long long)b * kTBlock, lane, t0, t1, rg);
-  block_load<MT>(sbase + (long long)(kTUpBlock0 + b) * kTBlock, lane, t0, t1, ru);
-  if (threadIdx.x == 0) {
-#pragma unroll
-    for (int t = 0; t < kMaxTokT; ++t) pairs_s[t] = pair[t];
-  }
-  x_store<XT, 64 * KS>(xs, nt, xr);
+  ScaleRegs<2, NTH> sr;
+  scale_load<2, NTH>(tid, gblk, ublk, sr);
+  XRegs<XT, NTH> xr;
+  x_load<XT, NTH>(tid, x, kH, [users](int t) { return pair_at(users, t) >> 2; }, nt, xr);
+  const int j = 16 * b + (lane & 15);
+  const uint16_t* bg = bias_gu ? bias_gu + gid * kGU : nullptr;
+  // epilogue operands are loaded now and converted at their use, so no wait is placed before the barrier
+  // (unconditional loads: without a bias they read x, in bounds, and the value is not used)
+  const uint16_t* bgs = bg ? bg : x;
+  const uint16_t* bus = bg ? bg + kI : x;
+  const uint16_t bgj = bgs[j], buj = bus[j];
+  CodeRegs<MT> rg, ru;
+  code_load<MT>(gblk, lane, t0, t1, rg);
+  code_load<MT>(ublk, lane, t0, t1, ru);
+  // every load is issued above; the first wait (for x and the scales, issued first) comes below
+  __builtin_amdgcn_sched_barrier(0);
+  x_store<XT, NTH>(tid, L.xs, nt, xr);
+  scale_store<2, NTH>(tid, L.sc, sr);
   __syncthreads();
-  const uint8_t* xrow = xs + min(lane & 15, XT - 1) * kXPitch;
+  const uint8_t* xrow = L.xs + min(lane & 15, XT - 1) * kXPitch;
+  const uint8_t* srow = L.sc + (lane & 15) * kScPitch;
   f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-  block_compute<MT>(rg, xrow, lane, t0, t1, ag);
-  block_compute<MT>(ru, xrow, lane, t0, t1, au);
+  block_compute<MT>(rg, srow, xrow, lane, t0, t1, ag);
+  block_compute<MT>(ru, srow + kScLds, xrow, lane, t0, t1, au);
   if constexpr (KS > 1) {
-    red[wave][0][lane] = ag;
-    red[wave][1][lane] = au;
+    L.red[wave][0][lane] = ag;
+    L.red[wave][1][lane] = au;
     __syncthreads();
     if (wave != 0) return;
-    ag = red[0][0][lane];
-    au = red[0][1][lane];
+    ag = L.red[0][0][lane];
+    au = L.red[0][1][lane];
 #pragma unroll
     for (int w = 1; w < KS; ++w) {
-      ag += red[w][0][lane];
-      au += red[w][1][lane];
+      ag += L.red[w][0][lane];
+      au += L.red[w][1][lane];
     }
   }
-  const int n = lane & 15, j = 16 * b + n;
-  const uint16_t* bg = bias_gu ? bias_gu + gid * kGU : nullptr;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int m = 4 * (lane >> 4) + r;
-    if (m < nt) {
-      float gb = rb(ag[r]), ub = rb(au[r]);
-      if (bg) {
-        gb = rb(gb + bf16_to_f32(bg[j]));
-        ub = rb(ub + bf16_to_f32(bg[kI + j]));
-      }
-      h[(long long)pairs_s[m] * kI + j] = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
+    float gb = rb(ag[r]), ub = rb(au[r]);
+    if (bg) {
+      gb = rb(gb + bf16_to_f32(bgj));
+      ub = rb(ub + bf16_to_f32(buj));
     }
+    const uint16_t hv = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
+    store_row_pairs(h + (long long)pair_at(users, min(m, nt - 1)) * kI + 16 * b, hv, m < nt);
   }
 }
 
-// down: output block b (rows n = 16b .. 16b + 15) from each routed token's own h, + bias, x routing weight -> yw
+// down, expert-major: output block b (rows n = 16b .. 16b + 15) of the item-th distinct expert from each routed
+// token's own h row, + bias, x routing weight -> yw[pair, n].  An invalid id (128) writes +0 for its pairs and reads
+// no weights.  The top-k sum is left to k_combine_t950.  Load order as in the gate_up kernel.
 template <int KS, int XT>
 __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
     const uint16_t* __restrict__ h, const int64_t* __restrict__ ids, const uint16_t* __restrict__ wts, int B,
     const uint8_t* __restrict__ pool, long long slot_bytes, const int64_t* __restrict__ slot_tab,
     long long expert_base, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw) {
   constexpr int MT = (kTTiles + KS - 1) / KS;
-  __shared__ __align__(16) uint8_t xs[XT * kXPitch];
-  __shared__ f32x4_t red[KS > 1 ? KS : 1][64];
-  __shared__ int pairs_s[kMaxTokT];
-  int pair[kMaxTokT], nt, distinct;
-  const int e = route_t950(ids, 4 * B, blockIdx.x, nt, pair, distinct);
+  constexpr int NTH = 64 * KS;
+  __shared__ DecodeLds<KS, XT> L;
+  int nt, distinct, valid;
+  uint64_t users;
+  const int e = route_t950(ids, 4 * B, blockIdx.x, nt, users, distinct, valid);
   if (e < 0) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.y;
-  if (threadIdx.x == 0) {
-#pragma unroll
-    for (int t = 0; t < kMaxTokT; ++t) pairs_s[t] = pair[t];
-  }
   if (e == 128) {                                      // invalid id: its pairs contribute +0
-    __syncthreads();
-    for (int i = threadIdx.x; i < nt * kTRows; i += 64 * KS)
-      yw[(long long)pairs_s[i / kTRows] * kH + 16 * b + (i % kTRows)] = 0;
+    for (int i = 2 * tid; i < nt * kTRows; i += 2 * NTH)
+      *reinterpret_cast<uint32_t*>(yw + (long long)pair_at(users, i / kTRows) * kH + 16 * b + (i % kTRows)) = 0u;
     return;
   }
   const long long gid = expert_base + e;
   const long long slot = slot_tab ? slot_tab[gid] : gid;
-  const uint8_t* sbase = pool + slot * slot_bytes;
+  const uint8_t* blk = pool + slot * slot_bytes + kTDownOff + (long long)b * kTBlock;
   int t0, t1;
   ktile_range<KS>(wave, t0, t1);
-  XRegs<XT, 64 * KS> xr;
-  x_load<XT, 64 * KS>(h, kI, pair, nt, xr);
-  BlockRegs<MT> rd;
-  block_load<MT>(sbase + kTDownOff + (long long)b * kTBlock, lane, t0, t1, rd);
-  x_store<XT, 64 * KS>(xs, nt, xr);
+  ScaleRegs<1, NTH> sr;
+  scale_load<1, NTH>(tid, blk, blk, sr);
+  XRegs<XT, NTH> xr;
+  x_load<XT, NTH>(tid, h, kI, [users](int t) { return pair_at(users, t); }, nt, xr);
+  const int n = 16 * b + (lane & 15);
+  // epilogue operands are loaded now and converted at their use, so no wait is placed before the barrier
+  const uint16_t bdn = (bias_dn ? bias_dn + gid * kH : wts)[bias_dn ? n : 0];   // unconditional load
+  uint16_t wr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) wr[r] = wts[pair_at(users, min(4 * (lane >> 4) + r, nt - 1))];
+  CodeRegs<MT> rd;
+  code_load<MT>(blk, lane, t0, t1, rd);
+  __builtin_amdgcn_sched_barrier(0);
+  x_store<XT, NTH>(tid, L.xs, nt, xr);
+  scale_store<1, NTH>(tid, L.sc, sr);
   __syncthreads();
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  block_compute<MT>(rd, xs + min(lane & 15, XT - 1) * kXPitch, lane, t0, t1, acc);
+  block_compute<MT>(rd, L.sc + (lane & 15) * kScPitch, L.xs + min(lane & 15, XT - 1) * kXPitch, lane, t0, t1, acc);
   if constexpr (KS > 1) {
-    red[wave][lane] = acc;
+    L.red[wave][0][lane] = acc;
     __syncthreads();
     if (wave != 0) return;
-    acc = red[0][lane];
+    acc = L.red[0][0][lane];
 #pragma unroll
-    for (int w = 1; w < KS; ++w) acc += red[w][lane];
+    for (int w = 1; w < KS; ++w) acc += L.red[w][0][lane];
   }
-  const int n = 16 * b + (lane & 15);
-  const uint16_t* bd = bias_dn ? bias_dn + gid * kH : nullptr;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int m = 4 * (lane >> 4) + r;
-    if (m < nt) {
-      float y = rb(acc[r]);
-      if (bd) y = rb(y + bf16_to_f32(bd[n]));
-      const int p = pairs_s[m];
-      yw[(long long)p * kH + n] = f32_to_bf16(y * bf16_to_f32(wts[p]));
-    }
+    const int p = pair_at(users, min(m, nt - 1));
+    float y = rb(acc[r]);
+    if (bias_dn) y = rb(y + bf16_to_f32(bdn));
+    store_row_pairs(yw + (long long)p * kH + 16 * b, f32_to_bf16(y * bf16_to_f32(wr[r])), m < nt);
   }
 }
 
@@ -426,6 +491,93 @@ __global__ __launch_bounds__(256) void k_combine_t950(const uint32_t* __restrict
     a1 += bf16_to_f32((uint16_t)(v >> 16));
   }
   out[i] = (uint32_t)f32_to_bf16(a0) | ((uint32_t)f32_to_bf16(a1) << 16);
+}
+
+// down + combine, row-block-major, for B <= 2 (at most G = 16 / KSD distinct experts): one workgroup of 16 waves per
+// output block b holds every distinct expert of the batch (G groups of KSD waves; group g serves the g-th distinct
+// expert), so the top-k sum needs no third kernel and no cross-workgroup exchange.  All 4B h rows are staged in
+// LDS once; each group runs the expert-major down arithmetic on its pairs' rows; the group leaders leave each pair's
+// bf16 yw row slice in LDS; after a barrier, out[t, 16b + n] = bf16(sum_k yw[4t + k, n]) in top-k order.
+constexpr int kDcWaves = 16;
+
+template <int KSD, int XT>
+struct DownCombLds {
+  static constexpr int G = kDcWaves / KSD;
+  __align__(16) uint8_t hs[4 * XT * kXPitch];           // h rows of all pairs, row p = pair p
+  __align__(16) uint8_t sc[G * kScLds];
+  f32x4_t red[kDcWaves][64];
+  float yw[4 * XT][kTRows];
+};
+
+template <int KSD, int XT>
+__global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
+    const uint16_t* __restrict__ h, const int64_t* __restrict__ ids, const uint16_t* __restrict__ wts, int B,
+    const uint8_t* __restrict__ pool, long long slot_bytes, const int64_t* __restrict__ slot_tab,
+    long long expert_base, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ out) {
+  constexpr int MT = (kTTiles + KSD - 1) / KSD;
+  constexpr int NTH = 64 * kDcWaves;
+  constexpr int GTH = 64 * KSD;
+  __shared__ DownCombLds<KSD, XT> L;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = wave / KSD, kw = wave - g * KSD, gtid = tid - g * GTH;
+  const int b = blockIdx.x;
+  const int npairs = 4 * B;
+  int nt, distinct, valid;
+  uint64_t users;
+  const int e = route_t950(ids, npairs, g, nt, users, distinct, valid);
+  const bool live = e >= 0 && e != 128;
+  const long long gid = expert_base + (live ? e : 0);
+  // groups without a live expert load slot 0's block (valid memory) with every tile slot zeroed, so that the loads
+  // stay unconditional and are all issued before the first wait
+  const long long slot = live ? (slot_tab ? slot_tab[gid] : gid) : 0;
+  const uint8_t* blk = pool + slot * slot_bytes + kTDownOff + (long long)b * kTBlock;
+  int t0, t1;
+  ktile_range<KSD>(kw, t0, t1);
+  ScaleRegs<1, GTH> sr;
+  scale_load<1, GTH>(gtid, blk, blk, sr);
+  XRegs<4 * XT, NTH> xr;                                 // all pairs' h rows: staged row p = pair p
+  x_load<4 * XT, NTH>(tid, h, kI, [](int t) { return t; }, npairs, xr);
+  const int n = 16 * b + (lane & 15);
+  const uint16_t bdn = (bias_dn ? bias_dn + gid * kH : wts)[bias_dn ? n : 0];   // unconditional load
+  uint16_t wr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) wr[r] = wts[live ? pair_at(users, min(4 * (lane >> 4) + r, nt - 1)) : 0];
+  CodeRegs<MT> rd;
+  code_load<MT>(blk, lane, t0, live ? t1 : t0, rd);
+  __builtin_amdgcn_sched_barrier(0);
+  x_store<4 * XT, NTH>(tid, L.hs, npairs, xr);
+  scale_store<1, GTH>(gtid, L.sc + g * kScLds, sr);
+  if (e == 128 && kw == 0) {                             // invalid id: its pairs contribute +0
+    for (int i = lane; i < nt * kTRows; i += 64) L.yw[pair_at(users, i / kTRows)][i % kTRows] = 0.f;
+  }
+  __syncthreads();
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  const int pm = live ? pair_at(users, min(lane & 15, nt - 1)) : 0;   // A row of token slot m = lane % 16
+  if (live)
+    block_compute<MT>(rd, L.sc + g * kScLds + (lane & 15) * kScPitch, L.hs + pm * kXPitch, lane, t0, t1, acc);
+  L.red[wave][lane] = acc;
+  __syncthreads();
+  if (live && kw == 0) {
+#pragma unroll
+    for (int w = 1; w < KSD; ++w) acc += L.red[wave + w][lane];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * (lane >> 4) + r;
+      if (m < nt) {
+        float y = rb(acc[r]);
+        if (bias_dn) y = rb(y + bf16_to_f32(bdn));
+        L.yw[pair_at(users, m)][lane & 15] = rb(y * bf16_to_f32(wr[r]));
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < B * kTRows) {
+    const int t = tid / kTRows, c = tid - t * kTRows;
+    float a = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a += L.yw[4 * t + k][c];
+    out[(long long)t * kH + 16 * b + c] = f32_to_bf16(a);
+  }
 }
 
 template <typename... KArgs, typename... Args>
@@ -496,25 +648,36 @@ int na_repack_from_t950(const void* src, long long src_stride, void* dst, long l
 int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_w, int B, const void* pool,
                        long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
                        const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha, float limit,
-                       int k_split, void* const* events, hipStream_t stream) {
+                       int k_split, int down_mode, void* const* events, hipStream_t stream) {
   if (!x || !topk_ids || !topk_w || !pool || !h_scratch || !yw_scratch || B <= 0) return kErrArgs;
+  if (down_mode != 0 && down_mode != 1) return kErrArgs;
   if (B > 8) return kErrTooLarge;
   if (slot_bytes < kTSlot || (slot_bytes & 15) || (reinterpret_cast<uintptr_t>(pool) & 15)) return kErrArgs;
   if (k_split <= 0) k_split = 4;
   if (k_split != 1 && k_split != 2 && k_split != 4) return kErrArgs;
+  // down_mode 0, B = 1, with an output: gate_up, then down + combine (two launches); else gate_up, down, combine
+  // (at B = 2 the row-block kernel's 16-wave workgroups with two waves per expert measured slower than three launches)
+  const bool two = down_mode == 0 && out != nullptr && B == 1;
   hipEvent_t ev[6] = {};
   if (events)
-    for (int i = 0; i < 6; ++i) ev[i] = (hipEvent_t)events[i];
+    for (int i = 0; i < (two ? 4 : 6); ++i) ev[i] = (hipEvent_t)events[i];
   const int items = 4 * B;
-  const dim3 g1(items, kTDownBlocks), g2(items, kTDownBlocks);
+  const dim3 g1(items, kTDownBlocks);
   const dim3 blk(64 * k_split);
   const int xt = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
-  auto gu = pick_gate_up_t950(k_split, xt);
-  auto dn = pick_down_t950(k_split, xt);
-  launch_t(gu, g1, blk, stream, ev[0], ev[1], (const uint16_t*)x, topk_ids, B, (const uint8_t*)pool, slot_bytes,
-           slot_tab, expert_base, (const uint16_t*)bias_gu, (uint16_t*)h_scratch, alpha, limit);
-  launch_t(dn, g2, blk, stream, ev[2], ev[3], (const uint16_t*)h_scratch, topk_ids, (const uint16_t*)topk_w, B,
-           (const uint8_t*)pool, slot_bytes, slot_tab, expert_base, (const uint16_t*)bias_dn, (uint16_t*)yw_scratch);
+  launch_t(pick_gate_up_t950(k_split, xt), g1, blk, stream, ev[0], ev[1], (const uint16_t*)x, topk_ids, B,
+           (const uint8_t*)pool, slot_bytes, slot_tab, expert_base, (const uint16_t*)bias_gu, (uint16_t*)h_scratch,
+           alpha, limit);
+  if (two) {
+    launch_t(k_moe_down_comb_t950<4, 1>, dim3(kTDownBlocks),
+             dim3(64 * kDcWaves), stream, ev[2], ev[3], (const uint16_t*)h_scratch, topk_ids,
+             (const uint16_t*)topk_w, B, (const uint8_t*)pool, slot_bytes, slot_tab, expert_base,
+             (const uint16_t*)bias_dn, (uint16_t*)out);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+  }
+  launch_t(pick_down_t950(k_split, xt), g1, blk, stream, ev[2], ev[3], (const uint16_t*)h_scratch, topk_ids,
+           (const uint16_t*)topk_w, B, (const uint8_t*)pool, slot_bytes, slot_tab, expert_base,
+           (const uint16_t*)bias_dn, (uint16_t*)yw_scratch);
   if (out)
     launch_t(k_combine_t950, dim3((B * kH / 2 + 255) / 256), dim3(256), stream, ev[4], ev[5],
              (const uint32_t*)yw_scratch, B, (uint32_t*)out);

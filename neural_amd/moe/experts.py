@@ -2,9 +2,10 @@
 routing_weights)`` seam the reference installs per layer (reference neural/moe/gptoss_adapter.py:267-284), backed by
 one HBM slot pool [n_layers * n_experts, slot_bytes] that holds every expert (60.9 GB raw; nothing is offloaded).
 
-Decode (T <= 8 tokens) runs the fused expert body of the reference's b_body (server.py:508-518) as three HIP launches
-(gate_up + bias + clamped SwiGLU; down + bias + routing weight; top-k combine); routing is read on the device, so
-``forward_decode`` never synchronises and can be captured in a hipGraph.
+Decode (T <= 8 tokens) runs the fused expert body of the reference's b_body (server.py:508-518) as HIP launches
+(gate_up + bias + clamped SwiGLU; down + bias + routing weight; top-k combine, which the down kernel does itself for
+T = 1 on the tile layout); routing is read on the device, so ``forward_decode`` never synchronises and can be
+captured in a hipGraph.
 """
 from __future__ import annotations
 
@@ -20,10 +21,10 @@ class ResidentExperts:
     def __init__(self, pool: torch.Tensor, layout: ExpertLayout = GPTOSS_LAYOUT, bias_gu: torch.Tensor | None = None,
                  bias_dn: torch.Tensor | None = None, slot_tab: torch.Tensor | None = None,
                  max_batch: int = MAX_DECODE_TOKENS, gu_pairs_per_wave: int = 4, dn_pairs_per_wave: int = 2,
-                 k_split: int = 4):
+                 k_split: int = 4, combine_in_down: bool = True):
         """pool: uint8 [n, layout.slot_bytes] in the raw, PS4 or t950 (gfx950 tile) layout.  The t950 layout runs the
-        MFMA decode kernels (k_split waves per workgroup split K); the store layouts run the VALU kernels
-        (gu/dn_pairs_per_wave row pairs per wavefront)."""
+        MFMA decode kernels (k_split waves per workgroup split K); with combine_in_down, a single token takes two
+        launches (the down kernel holds every expert of an output block and sums the top-k itself) instead of three.  The store layouts run the VALU kernels (gu/dn_pairs_per_wave row pairs per wavefront)."""
         if layout.weight_repr not in ("mxfp4_g32", "mxfp4_g32_ps4", TILE_REPR):
             raise ValueError(f"ResidentExperts serves the raw, PS4 and t950 slot layouts, not {layout.weight_repr}")
         if k_split not in (1, 2, 4):
@@ -53,6 +54,7 @@ class ResidentExperts:
             raise ValueError("row pairs per wave must be 1, 2 or 4")
         self.gu_pairs, self.dn_pairs = int(gu_pairs_per_wave), int(dn_pairs_per_wave)
         dev = pool.device
+        self.down_mode = 0 if combine_in_down else 1
         self.h = torch.empty(max_batch * layout.top_k, layout.down_k, dtype=torch.bfloat16, device=dev)
         self.yw = torch.empty(max_batch * layout.top_k, layout.down_n, dtype=torch.bfloat16, device=dev)
 
@@ -60,8 +62,8 @@ class ResidentExperts:
                        routing_weights: torch.Tensor, out: torch.Tensor | None = None, events=None) -> torch.Tensor:
         """hidden [B, 2880] bf16, router_indices [B, 4] int64 (expert ids within the layer), routing_weights [B, 4]
         bf16 -> [B, 2880] bf16 = bf16(sum_k bf16(bf16(expert_k(h) + b_dn) * w_k)) in top-k order.
-        events: None, or six recorded timing torch.cuda.Event objects (start/stop of the gate_up, down and combine
-        kernels), timestamped by the dispatches themselves (measurement only; not for graph capture).
+        events: None, or recorded timing torch.cuda.Event objects timestamped by the dispatches themselves
+        (measurement only; not for graph capture): start/stop of each launch, see launches().
         Calls that overlap on one device must use different ResidentExperts objects (they share scratch)."""
         L = self.layout
         B = hidden.shape[0]
@@ -86,7 +88,7 @@ class ResidentExperts:
             N.call("na_moe_decode_t950", hidden.data_ptr(), router_indices.data_ptr(), routing_weights.data_ptr(), B,
                    self.pool.data_ptr(), L.slot_bytes, N.ptr(self.slot_tab), layer * L.n_experts,
                    N.ptr(self.bias_gu), N.ptr(self.bias_dn), self.h.data_ptr(), self.yw.data_ptr(), out.data_ptr(),
-                   float(L.act_alpha), float(L.act_limit), self.k_split, N.events_array(events),
+                   float(L.act_alpha), float(L.act_limit), self.k_split, self.down_mode, N.events_array(events),
                    N.stream(hidden.device))
             return out
         N.call("na_moe_decode", hidden.data_ptr(), router_indices.data_ptr(), routing_weights.data_ptr(), B,
@@ -95,6 +97,13 @@ class ResidentExperts:
                float(L.act_alpha), float(L.act_limit), self.gu_pairs, self.dn_pairs, N.events_array(events),
                N.stream(hidden.device))
         return out
+
+
+    def launches(self, batch: int, with_out: bool = True) -> tuple:
+        """Names of the kernels one forward_decode call launches, in order (two timing events per launch)."""
+        if self.tiled and self.down_mode == 0 and with_out and batch == 1:
+            return ("gate_up", "down_combine")
+        return ("gate_up", "down", "combine") if with_out else ("gate_up", "down")
 
 
 class Router:

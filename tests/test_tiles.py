@@ -215,3 +215,60 @@ def test_moe_decode_t950_graph_replay():
         eager = rt.forward_decode(2, xd, idd, wd)
         torch.cuda.synchronize()
         assert torch.equal(out, eager), rep
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B", [1, 2])
+def test_down_with_combine_matches_expert_major_path(B):
+    """For B = 1 the down kernel holds every expert of an output block and does the top-k combine itself; it splits K
+    exactly as the expert-major kernel with k_split 4 does, so the outputs are bitwise equal, and both match the
+    oracle.  B = 2 takes three launches either way.  Consecutive calls include invalid ids, which contribute +0 and
+    read no weights."""
+    import torch
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
+    dev = _dev()
+    slots, x, ids, w, tab, bgu, bdn = _t950_case(B, 900 + B, True, nslot=8)
+    print(f"case down_with_combine B={B}", flush=True)
+    raw = torch.from_numpy(np.stack(slots)).to(dev)
+    tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
+    tiles.repack_to_t950(raw, tp)
+    tabd, bg, bd = torch.from_numpy(tab).to(dev), bgu.to(dev), bdn.to(dev)
+    two = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=True)
+    three = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=False)
+    assert two.launches(B) == (("gate_up", "down_combine") if B == 1 else ("gate_up", "down", "combine"))
+    assert len(three.launches(B)) == 3
+    rng = np.random.default_rng(B)
+    cache = {}
+    for call in range(3):
+        idc = ids.copy()
+        if call == 1:
+            idc[0, 1] = -1                                    # invalid ids: +0 contributions
+            idc[B - 1, 3] = 200
+        xn = synth.bf16_normal(rng, (B, 2880))
+        xd = xn.to(dev)
+        idd = torch.from_numpy(idc).to(dev)
+        wd = torch.from_numpy(w).to(torch.bfloat16).to(dev)
+        layer = 3 + call
+        a = two.forward_decode(layer, xd, idd, wd).float().cpu().numpy()
+        c = three.forward_decode(layer, xd, idd, wd).float().cpu().numpy()
+        if B == 1:
+            assert np.array_equal(a, c), call
+        for b in range(B):
+            ys = []
+            for k in range(4):
+                e = int(idc[b, k])
+                if not 0 <= e < 128:
+                    ys.append(np.zeros(2880, np.float32))
+                    continue
+                g = layer * 128 + e
+                sl = int(tab[g])
+                if sl not in cache:
+                    cache[sl] = mo.expert_weights(slots[sl])
+                ys.append(mo.expert_forward_bf16(xn[b:b + 1].float().numpy(), None, bgu[g].float().numpy(),
+                                                 bdn[g].float().numpy(), weights=cache[sl])[0])
+            want = mo.combine_bf16(np.stack(ys), w[b])
+            scale = np.abs(want).max()
+            for name, arr in (("two", a[b]), ("three", c[b])):
+                d = np.abs(arr - want)
+                assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale, (name, call, b, d.max(), scale)
