@@ -136,6 +136,81 @@ def cpu_baseline(pool_dev, ids, B, seconds=12.0):
             "gbps": round(4 * SLOT_ALGO_BYTES / t_call / 1e9, 2)}
 
 
+def bench_attention(A):
+    """Configuration 3: GQA decode attention (64 q / 8 KV heads, head_dim 64, bf16 K/V ~ N(0,1), sinks ~ N(0,1)),
+    batch 1 and 4, contexts 1024 / 4096 / 8192, layers alternating full attention and a 128-token sliding window
+    (rolling 128-row cache).  One step = 36 layers (18 full + 18 sliding) captured in one hipGraph; per layer one
+    launch.  Reported per case: us per full and per sliding layer (graph replays; a graph of only full or only
+    sliding layers), and the full layer's algorithmic HBM rate (K + V bytes = 2048 x ctx per sequence and layer)."""
+    import torch
+
+    from neural_amd import attention as AT
+
+    dev = torch.device("cuda", 0)
+    rng = torch.Generator(device=dev)
+    rng.manual_seed(1234)
+    NL = 18
+    cases = []
+    for B in (1, 4):
+        for ctx in (1024, 4096, 8192):
+            kf = [(torch.randn(B, AT.NKV, ctx, AT.HD, device=dev, generator=rng)).to(torch.bfloat16) for _ in range(2)]
+            vf = [(torch.randn(B, AT.NKV, ctx, AT.HD, device=dev, generator=rng)).to(torch.bfloat16) for _ in range(2)]
+            kr = (torch.randn(B, AT.NKV, 128, AT.HD, device=dev, generator=rng)).to(torch.bfloat16)
+            vr = (torch.randn(B, AT.NKV, 128, AT.HD, device=dev, generator=rng)).to(torch.bfloat16)
+            sinks = torch.randn(AT.NQ, device=dev, generator=rng).to(torch.bfloat16)
+            q = torch.randn(B, AT.NQ * AT.HD, device=dev, generator=rng).to(torch.bfloat16)
+            out = torch.empty_like(q)
+            pos = torch.full((B,), ctx - 1, dtype=torch.int64, device=dev)
+            def timed(fn):
+                fn(0)
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for l in range(NL):
+                        fn(l)
+                for _ in range(5):
+                    g.replay()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                R = 50
+                e0.record()
+                for _ in range(R):
+                    g.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                return e0.elapsed_time(e1) * 1e3 / (R * NL)
+
+            res, sweep = {}, {}
+            for ns in sorted({max(1, min(AT.MAX_SPLIT, ctx // c)) for c in (64, 128, 256, 512)}):
+                split = AT.SplitAttn(ns, ctx, dev, batch=B)
+                sweep[ns] = round(timed(lambda l, sp=split: AT.decode_attention_batched(
+                    q, kf[l % 2], vf[l % 2], sinks, pos, out, 0.125, split=sp)), 3)
+            ns = min(sweep, key=sweep.get)
+            res["full"] = sweep[ns]
+            res["sliding"] = timed(lambda l: AT.decode_attention_batched(q, kr, vr, sinks, pos, out, 0.125,
+                                                                         sliding=128, ring=128))
+            full_bytes = B * 2048 * ctx
+            case = {"batch": B, "ctx": ctx, "n_split": ns, "n_split_sweep_us": sweep, "full_us": round(res["full"], 3),
+                    "sliding_us": round(res["sliding"], 3),
+                    "full_hbm_gbps": round(full_bytes / (res["full"] * 1e-6) / 1e9, 1),
+                    "layer_pair_us": round(res["full"] + res["sliding"], 3)}
+            log(f"attention B={B} ctx={ctx} ns={ns}: full {case['full_us']} us ({case['full_hbm_gbps']} GB/s), "
+                f"sliding {case['sliding_us']} us")
+            cases.append(case)
+            del kf, vf, kr, vr
+    worst = max(c["full_us"] for c in cases)
+    res = {"metric": "decode attention us per full layer (config 3, worst case)", "value": worst, "unit": "us",
+           "n_gpus": 1, "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
+           "config": {"workload": "config3: GQA 64q/8kv hd64 decode attention with sinks, batch 1 and 4, ctx 1024/"
+                                  "4096/8192, full layers chunked (SplitAttn), sliding layers on a 128-row ring",
+                      "cases": cases},
+           "roofline": {"bound": "hbm", "achieved": max(c["full_hbm_gbps"] for c in cases), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(max(c["full_hbm_gbps"] for c in cases) / HBM_PEAK_GBS, 4),
+                        "traffic": None, "kernel": "k_decode_attn"},
+           "cpu_baseline": None}
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -154,14 +229,18 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--gu-pairs", type=int, default=4, help="gate_up row pairs per wavefront (1, 2, 4)")
     ap.add_argument("--dn-pairs", type=int, default=2, help="down row pairs per wavefront (1, 2, 4)")
+    ap.add_argument("--workload", choices=("experts", "attention"), default="experts",
+                    help="experts: configuration 1 (the headline); attention: configuration 3 (decode attention)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run one device-to-device copy of this many MB first (a known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
     A = ap.parse_args()
     if A.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {A.gpus} is not supported (the design note on "
-              f"sharding across GPUs is in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU per process and measures one GPU; --gpus {A.gpus} is not "
+              f"supported (sharding across GPUs is designed, not built)", file=sys.stderr)
         sys.exit(2)
+    if A.workload == "attention":
+        return bench_attention(A)
     if not 1 <= A.batch <= 8:
         sys.exit("--batch must be in [1, 8]")
 

@@ -104,6 +104,26 @@ int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
                        const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha, float limit,
                        int k_split, int down_mode, void* const* events, hipStream_t stream);
 
+/* ---- decode attention (GQA 64 query / 8 KV heads, head_dim 64, learned sinks, sliding window, rolling cache) */
+
+/* Floats of workspace na_decode_attention needs for B sequences and n_split chunks (-1 if out of range). */
+long long na_attn_workspace_floats(int B, int n_split);
+
+/* Decode attention of B sequences, one query each.  Replaces fused_core.py:145-208 (k_attn, n_split = 1) and
+ * :211-382 (SplitAttn, k_attn_s1..s4, n_split > 1), entry :385-398 (decode_attention).
+ *   q        bf16 [B, 64 * 64] (RoPE applied); sinks bf16 [64]
+ *   kc, vc   bf16 [B, 8, cache_rows, 64]; key position j in row j, or j % ring when ring > 0 (then cache_rows == ring
+ *            and window > 0, ring >= window)
+ *   pos      int64 [B] on the device: attended keys [lo, pos], lo = max(pos - window + 1, 0) (window = 0: lo = 0)
+ *   out      bf16 [B, 64 * 64]
+ *   n_split  chunks per (sequence, KV head), 1..64; n_split > 1 needs work (na_attn_workspace_floats floats) and
+ *            counters (uint32 [B * 8], zero before the first call; every completed call leaves them zero).  Calls
+ *            sharing work/counters must not overlap.
+ *   events   NULL or 2 hipEvent_t (start/stop of the launch, timestamped by the dispatch) */
+int na_decode_attention(const void* q, const void* kc, const void* vc, long long cache_rows, const void* sinks,
+                        const int64_t* pos, void* out, int B, float scaling, int window, int ring, int n_split,
+                        float* work, unsigned int* counters, void* const* events, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

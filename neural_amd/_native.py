@@ -29,8 +29,10 @@ SIGNATURES = {
     "na_repack_to_t950": [VP, I64, I32, VP, I64, I32, VP],
     "na_repack_from_t950": [VP, I64, VP, I64, I32, I32, VP],
     "na_moe_decode_t950": [VP, VP, VP, I32, VP, I64, VP, I64, VP, VP, VP, VP, VP, F32, F32, I32, I32, VP, VP],
+    "na_attn_workspace_floats": [I32, I32],
+    "na_decode_attention": [VP, VP, VP, I64, VP, VP, VP, I32, F32, I32, I32, I32, VP, VP, VP, VP],
 }
-RESTYPES = {"na_t950_slot_bytes": I64}
+RESTYPES = {"na_t950_slot_bytes": I64, "na_attn_workspace_floats": I64}
 
 ERRORS = {-1: "invalid arguments", -2: "kernel launch failed", -3: "size beyond the kernel's limits"}
 

@@ -203,3 +203,20 @@ def test_product_code_never_touches_the_oracle():
             if f.endswith((".py", ".hip", ".h", ".cpp")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert not re.search(r"\boracle\b", text), f"{f} mentions the oracle"
+
+
+def test_ring_reuse_rule_truth_table():
+    """reference tests/test_attention.py:309-311"""
+    from neural_amd import attention as A
+    rr = [A.ring_reuse_ok(1000, 999, 128), A.ring_reuse_ok(1000, 998, 128), A.ring_reuse_ok(100, 7, 128),
+          A.ring_reuse_ok(1000, 1001, 128), A.ring_reuse_ok(2000, 1200, 1024)]
+    assert rr == [True, False, True, False, True]
+
+
+def test_attention_workspace_and_argument_checks():
+    from neural_amd import _native as N
+    lib = N.lib()
+    assert lib.na_attn_workspace_floats(1, 32) == 1 * 8 * 32 * (8 + 8 + 512)
+    assert lib.na_attn_workspace_floats(1, 65) == -1
+    assert lib.na_decode_attention(None, None, None, 1, None, None, None, 1, ctypes.c_float(0.125), 0, 0, 1,
+                                   None, None, None, None) == -1
