@@ -36,7 +36,10 @@ struct AttnLds {
   __align__(16) uint8_t p[16 * kPPitch];           // P of the sub-chunk, bf16 [row][key] (rows 8..15 unused)
   float mx[4][kRep];                               // per-wave row maxima
   float sm[4][kRep];                               // per-wave row sums
-  float fin[kRep][2];                              // combine: (scale of this chunk, 1 / S) per row
+  float fin[kRep][2];                              // combine: 1 / S per row (index 1)
+  float cm[kAttnMaxSplit][kRep];                   // combine: chunk maxima, sums and weights
+  float cs[kAttnMaxSplit][kRep];
+  float cw[kAttnMaxSplit][kRep];
 };
 
 // Wave-wide max / sum over the 16 lanes of a row group (lanes 16 q .. 16 q + 15).
@@ -237,37 +240,36 @@ __global__ __launch_bounds__(256) void k_decode_attn(
   }
   __syncthreads();
   if (!last) return;
+  // Combine.  One acquire fence (the partials were published with device-coherent stores before the count), then
+  // plain loads, spread over the workgroup so that they are in flight together: chunk maxima and sums to LDS, the
+  // chunk weights exp(m_c - m) and 1 / S per row, then out[row][d] = sum_c acc_c[row][d] w_c[row] in chunk order.
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   const float* pbase = work + (long long)bh * ns * kPartFloats;
-  if (tid < kRep) {                                // per row: global max, chunk weights, 1 / S
+  for (int i = tid; i < ns * kRep; i += 256) {
+    const int cc = i / kRep, row = i - cc * kRep;
+    L.cm[cc][row] = pbase[cc * kPartFloats + row];
+    L.cs[cc][row] = pbase[cc * kPartFloats + kRep + row];
+  }
+  __syncthreads();
+  if (tid < kRep) {
     const int row = tid;
     const float sink = bf16_to_f32(sk[row]);
     float m = sink;
-    for (int cc = 0; cc < ns; ++cc) {
-      const float mc = __hip_atomic_load(pbase + cc * kPartFloats + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      m = fmaxf(m, mc);
-    }
+    for (int cc = 0; cc < ns; ++cc) m = fmaxf(m, L.cm[cc][row]);
     float S = expf(sink - m);
     for (int cc = 0; cc < ns; ++cc) {
-      const float mc = __hip_atomic_load(pbase + cc * kPartFloats + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float sc = __hip_atomic_load(pbase + cc * kPartFloats + kRep + row, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-      if (mc != kNegInf) S += sc * expf(mc - m);
+      const float mc = L.cm[cc][row];
+      const float w = mc == kNegInf ? 0.f : expf(mc - m);
+      L.cw[cc][row] = w;
+      S += L.cs[cc][row] * w;
     }
-    L.fin[row][0] = m;
     L.fin[row][1] = 1.f / S;
   }
   __syncthreads();
-  for (int i = tid; i < kRep * kHD; i += 256) {    // out[row][d] = sum_c acc_c exp(m_c - m) / S, chunk order
+  for (int i = tid; i < kRep * kHD; i += 256) {
     const int row = i / kHD;
-    const float m = L.fin[row][0];
     float o = 0.f;
-    for (int cc = 0; cc < ns; ++cc) {
-      const float mc = __hip_atomic_load(pbase + cc * kPartFloats + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (mc == kNegInf) continue;
-      const float a = __hip_atomic_load(pbase + cc * kPartFloats + 2 * kRep + i, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-      o += a * expf(mc - m);
-    }
+    for (int cc = 0; cc < ns; ++cc) o += pbase[cc * kPartFloats + 2 * kRep + i] * L.cw[cc][row];
     orow[i] = f32_to_bf16(o * L.fin[row][1]);
   }
 }
