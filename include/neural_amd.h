@@ -124,6 +124,40 @@ int na_decode_attention(const void* q, const void* kc, const void* vc, long long
                         const int64_t* pos, void* out, int B, float scaling, int window, int ring, int n_split,
                         float* work, unsigned int* counters, void* const* events, hipStream_t stream);
 
+/* ---- prefill (prompt) products */
+
+/* out[e][m][n] = bf16(sum_k x[m][k] w_e[n][k]) for e < E (weights of slot slots[e]), m < M.  Replaces
+ * neural/q80/mxfp4_kernels.py:202-231 (mxfp4_gemm / mxfp4_gemm_into; any E and M).
+ *   x        bf16 [M, K], K = 2880 (16-byte aligned rows)
+ *   blocks   layout 0 (raw) / 1 (PS4): u8 view [cap, N, 90, 16], slot stride sb_slot; scales [cap, N, 90 | 46] with
+ *            slot stride ss_slot.  layout 2: blocks = the matrix's first t950 row block of slot 0, stride sb_slot.
+ *   out      bf16 [E, M, N], N a multiple of 64 */
+int na_mxfp4_gemm(const void* x, int M, int K, const void* blocks, long long sb_slot, const void* scales,
+                  long long ss_slot, int layout, const int64_t* slots, int E, void* out, int N, hipStream_t stream);
+
+/* One ragged GEMM launch over GroupedGemmPlan tile descriptors.  Replaces mxfp4_kernels.py:242-295 and :385-419.
+ *   tiles    int64 [ntiles][5] = (x address, out address, slot, pair rows M, tile pm): rows [pm * block_m,
+ *            min(M, (pm + 1) * block_m)) of the pair; x rows K = 2880 bf16, out rows N bf16 (16-byte aligned)
+ *   block_m  power of two >= 16 */
+int na_mxfp4_gemm_grouped(const void* blocks, long long sb_slot, const void* scales, long long ss_slot, int layout,
+                          const int64_t* tiles, int ntiles, int block_m, int N, int K, hipStream_t stream);
+
+/* Bytes of workspace na_moe_prefill needs for T tokens (-1 if out of range). */
+long long na_moe_prefill_workspace_bytes(int T);
+
+/* One MoE layer over T prompt tokens, all experts resident.  Replaces server.py:1837-1936 (moe_prefill) with the
+ * expert products of _expert_gemms :1977-2040 for resident experts; five launches: pair counts, stable expert
+ * order + 64-token tiles, gate_up + bias + clamped SwiGLU, down + bias + routing weight, top-k sum.
+ *   x [T, 2880] bf16; topk_ids int64 [T, 4] (ids outside [0, 128) contribute +0); topk_w bf16 [T, 4]
+ *   pool / slot_bytes / slot_tab / expert_base / biases as na_moe_decode; layout 0 raw, 1 PS4, 2 t950
+ *   workspace: na_moe_prefill_workspace_bytes(T) bytes, 16-byte aligned
+ *   out [T, 2880] bf16 = bf16(sum_k fp32(yw[t, k])) in top-k order
+ *   events  NULL or 10 hipEvent_t (start/stop of the five launches) */
+int na_moe_prefill(const void* x, const int64_t* topk_ids, const void* topk_w, int T, const void* pool,
+                   long long slot_bytes, int layout, const int64_t* slot_tab, long long expert_base,
+                   const void* bias_gu, const void* bias_dn, void* workspace, long long ws_bytes, void* out,
+                   float alpha, float limit, void* const* events, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

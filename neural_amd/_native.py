@@ -30,9 +30,13 @@ SIGNATURES = {
     "na_repack_from_t950": [VP, I64, VP, I64, I32, I32, VP],
     "na_moe_decode_t950": [VP, VP, VP, I32, VP, I64, VP, I64, VP, VP, VP, VP, VP, F32, F32, I32, I32, VP, VP],
     "na_attn_workspace_floats": [I32, I32],
+    "na_moe_prefill_workspace_bytes": [I32],
+    "na_moe_prefill": [VP, VP, VP, I32, VP, I64, I32, VP, I64, VP, VP, VP, I64, VP, F32, F32, VP, VP],
+    "na_mxfp4_gemm": [VP, I32, I32, VP, I64, VP, I64, I32, VP, I32, VP, I32, VP],
+    "na_mxfp4_gemm_grouped": [VP, I64, VP, I64, I32, VP, I32, I32, I32, I32, VP],
     "na_decode_attention": [VP, VP, VP, I64, VP, VP, VP, I32, F32, I32, I32, I32, VP, VP, VP, VP],
 }
-RESTYPES = {"na_t950_slot_bytes": I64, "na_attn_workspace_floats": I64}
+RESTYPES = {"na_t950_slot_bytes": I64, "na_attn_workspace_floats": I64, "na_moe_prefill_workspace_bytes": I64}
 
 ERRORS = {-1: "invalid arguments", -2: "kernel launch failed", -3: "size beyond the kernel's limits"}
 

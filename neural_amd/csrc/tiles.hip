@@ -13,22 +13,11 @@
 // E2M1 nibbles unchanged and the scales the store's E8M0 bytes unchanged (PS4 rows are expanded), so the repack is a
 // byte permutation plus padding and round-trips exactly (na_repack_from_t950).
 #include "common.h"
+#include "t950.h"
 
 #include <hip/hip_ext.h>
 
 namespace na {
-
-constexpr int kTRows = 16;
-constexpr int kTFull = 22;
-constexpr int kTTiles = 23;                         // 22 full + 1 half
-constexpr int kTCodes = kTFull * 1024 + 512;        // 23,040
-constexpr int kTScalePitch = 96;
-constexpr int kTBlock = kTCodes + kTRows * kTScalePitch;   // 24,576
-constexpr int kTGateBlocks = kGU / kTRows;          // 360
-constexpr int kTDownBlocks = kH / kTRows;           // 180
-constexpr long long kTSlot = (long long)(kTGateBlocks + kTDownBlocks) * kTBlock;   // 13,271,040
-constexpr long long kTDownOff = (long long)kTGateBlocks * kTBlock;
-constexpr int kTUpBlock0 = kI / kTRows;             // first row block of the up half of gate_up (180)
 
 // ------------------------------------------------------------------------------------------------- repack
 // Source row r of a slot in the store layout: code row bytes and its E8M0 scale of group g.
@@ -154,19 +143,6 @@ constexpr int kXPitch = kH * 2 + 16;         // LDS bytes per staged token row (
 constexpr int kScPitch = 112;                // LDS bytes per staged scale row: 28 dwords, so 16 rows hit 16 banks
 constexpr int kScLds = kTRows * kScPitch;    // 1,792 LDS bytes per staged row block
 constexpr int kScPieces = kTRows * kTScalePitch / 16;   // 96 16-byte pieces of scales per row block
-
-NA_DEVICE float e8m0_f32(uint32_t s) { return __uint_as_float(s << 23); }
-
-// 8 bf16 B values (one MFMA operand) from one code dword and its scale.
-NA_DEVICE bf16x8_t dequant8(uint32_t w, float scale) {
-  typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4v;
-  u32x4v r;
-  r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0));
-  r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1));
-  r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2));
-  r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3));
-  return __builtin_bit_cast(bf16x8_t, r);
-}
 
 // k-tile range of wave w of KS
 template <int KS>

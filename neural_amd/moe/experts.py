@@ -99,6 +99,46 @@ class ResidentExperts:
         return out
 
 
+    def forward_prefill(self, layer: int, hidden: torch.Tensor, router_indices: torch.Tensor,
+                        routing_weights: torch.Tensor, out: torch.Tensor | None = None, events=None) -> torch.Tensor:
+        """Prompt tokens of one layer (the reference's moe_prefill, server.py:1837-1936, for an all-resident pool):
+        hidden [T, 2880] bf16, router_indices [T, 4] int64, routing_weights [T, 4] bf16 -> [T, 2880] bf16 =
+        per token bf16(sum_k bf16(bf16(expert_k(h) + b_dn) * w_k)) in top-k order, each expert product the
+        reference's GEMM arithmetic.  Five launches on the current stream, no host synchronisation: pair counts per
+        expert, a stable expert-major order of the pairs with its 64-token tiles, gate_up + bias + clamped SwiGLU
+        (activation rows gathered through the order), down + bias + routing weight (scattered back to pair order),
+        and the top-k sum.  The workspace (~ T x 92 KB) is allocated through torch's caching allocator.
+        events: None or ten recorded timing events (start/stop of each launch; measurement only)."""
+        L = self.layout
+        T = hidden.shape[0]
+        if hidden.dtype is not torch.bfloat16 or hidden.ndim != 2 or hidden.shape[1] != L.hidden \
+                or not hidden.is_contiguous():
+            raise ValueError("hidden must be contiguous bf16 [T, hidden]")
+        if T < 1:
+            raise ValueError("prefill needs at least one token")
+        if router_indices.dtype is not torch.int64 or tuple(router_indices.shape) != (T, L.top_k) \
+                or not router_indices.is_contiguous():
+            raise ValueError("router_indices must be contiguous int64 [T, top_k]")
+        if routing_weights.dtype is not torch.bfloat16 or tuple(routing_weights.shape) != (T, L.top_k) \
+                or not routing_weights.is_contiguous():
+            raise ValueError("routing_weights must be contiguous bf16 [T, top_k]")
+        if not 0 <= layer < L.n_layers:
+            raise ValueError(f"layer {layer} outside [0, {L.n_layers})")
+        if out is None:
+            out = torch.empty(T, L.hidden, dtype=torch.bfloat16, device=hidden.device)
+        elif out.dtype is not torch.bfloat16 or tuple(out.shape) != (T, L.hidden) or not out.is_contiguous():
+            raise ValueError("out must be contiguous bf16 [T, hidden]")
+        nbytes = N.lib().na_moe_prefill_workspace_bytes(T)
+        if nbytes < 0:
+            raise ValueError(f"prefill of {T} tokens is beyond the kernel's limits")
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=hidden.device)
+        layout_code = 2 if self.tiled else L.scale_layout_mode
+        N.call("na_moe_prefill", hidden.data_ptr(), router_indices.data_ptr(), routing_weights.data_ptr(), T,
+               self.pool.data_ptr(), L.slot_bytes, layout_code, N.ptr(self.slot_tab), layer * L.n_experts,
+               N.ptr(self.bias_gu), N.ptr(self.bias_dn), ws.data_ptr(), nbytes, out.data_ptr(), float(L.act_alpha),
+               float(L.act_limit), N.events_array(events), N.stream(hidden.device))
+        return out
+
     def launches(self, batch: int, with_out: bool = True) -> tuple:
         """Names of the kernels one forward_decode call launches, in order (two timing events per launch)."""
         if self.tiled and self.down_mode == 0 and with_out and batch == 1:

@@ -198,3 +198,100 @@ class GroupedGemmPlan:
         if tiles:
             self.metadata_host.copy_(torch.tensor(tiles, dtype=torch.int64))
         self.metadata = (self.metadata_host.to(self.device, non_blocking=True) if on_gpu else self.metadata_host)
+
+
+# ------------------------------------------------------------------------------------------ prefill products
+def _gemm_views(x, blocks, scales, packed):
+    if blocks.ndim != 4 or blocks.shape[-1] != 16 or blocks.dtype is not torch.uint8:
+        raise ValueError("blocks must be a uint8 [cap, N, GK, 16] view")
+    cap, n, gk, _ = blocks.shape
+    if tuple(blocks.stride()[1:]) != (gk * 16, 16, 1):
+        raise ValueError("blocks rows must be contiguous")
+    if scales.dtype is not torch.uint8 or scales.ndim != 3 or tuple(scales.shape[:2]) != (cap, n):
+        raise ValueError("scales must be a uint8 [cap, N, w] view matching blocks")
+    if gk != GK_SUPPORTED:
+        raise ValueError(f"GK={gk}: these kernels are built for K = {GK_SUPPORTED * 32} (GPT-OSS-120B)")
+    if n % 64:
+        raise ValueError(f"N={n}: the GEMM tiles 64 weight rows per workgroup")
+    for t, nm in ((blocks, "blocks"), (scales, "scales")):
+        if t.device != x.device or t.device.type != "cuda":
+            raise ValueError(f"{nm} must be on the input's CUDA device")
+    return cap, n, gk, _scale_layout(scales, gk, packed)
+
+
+def _native_gemm(x, blocks, scales, slots, out, E, M, n, pk):
+    N.call("na_mxfp4_gemm", x.data_ptr(), M, x.shape[1], blocks.data_ptr(), blocks.stride(0), scales.data_ptr(),
+           scales.stride(0), int(pk), slots.data_ptr(), E, out.data_ptr(), n, N.stream(x.device))
+
+
+def _gemm_args(x, blocks, scales, slots, packed):
+    if x.dtype is not torch.bfloat16 or x.ndim != 2 or not x.is_contiguous():
+        raise ValueError("x must be a contiguous bf16 [M, K] tensor")
+    cap, n, gk, pk = _gemm_views(x, blocks, scales, packed)
+    M, K = x.shape
+    if K != gk * 32:
+        raise AssertionError(f"x has K={K}, the pool {gk * 32}")
+    if slots.dtype is not torch.int64 or not slots.is_contiguous() or slots.device != x.device:
+        raise ValueError("slots must be a contiguous int64 tensor on the input's device")
+    return slots.numel(), M, n, pk
+
+
+def mxfp4_gemm(x: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor, slots: torch.Tensor, *,
+               block_n: int = 128, block_m: int = 16, packed: bool | None = None) -> torch.Tensor:
+    """x [M, K] bf16; blocks/scales = slot-pool u8 views; slots int64 [E].  Returns [E, M, N] bf16 with
+    out[e, m, n] = bf16(sum_k x[m, k] w_slot[e][n, k]) (reference mxfp4_kernels.py:202-216; any E and M here).
+    block_n / block_m are accepted for interface compatibility: the kernel tiles 64 x 64."""
+    E, M, n, pk = _gemm_args(x, blocks, scales, slots, packed)
+    out = torch.empty(E, M, n, dtype=torch.bfloat16, device=x.device)
+    if E and M:
+        _native_gemm(x, blocks, scales, slots, out, E, M, n, pk)
+    return out
+
+
+def mxfp4_gemm_into(x: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor, slots: torch.Tensor,
+                    out: torch.Tensor, *, block_n: int = 128, block_m: int = 16,
+                    packed: bool | None = None) -> torch.Tensor:
+    """mxfp4_gemm writing into a caller-provided contiguous bf16 ``out`` of E*M*N elements (reference
+    mxfp4_kernels.py:218-231): same kernel and arithmetic; the caller owns the stream ordering of ``out``."""
+    E, M, n, pk = _gemm_args(x, blocks, scales, slots, packed)
+    if out.dtype is not torch.bfloat16 or out.numel() != E * M * n or not out.is_contiguous():
+        raise AssertionError("out must be contiguous bf16 with E*M*N elements")
+    if out.device != x.device:
+        raise ValueError("out must be on the input's device")
+    if E and M:
+        _native_gemm(x, blocks, scales, slots, out, E, M, n, pk)
+    return out
+
+
+def mxfp4_gemm_grouped_into(pairs_or_plan, blocks: torch.Tensor, scales: torch.Tensor, *, block_n=128, block_m=64,
+                            packed=None):
+    """One ragged GEMM launch writing each pair's own output slice (reference mxfp4_kernels.py:385-419).  Returns the
+    GroupedGemmPlan so a caller can reuse it.  Each output row gets exactly mxfp4_gemm's arithmetic."""
+    plan = (pairs_or_plan if isinstance(pairs_or_plan, GroupedGemmPlan)
+            else GroupedGemmPlan(pairs_or_plan, block_m=block_m))
+    if plan.block_m != block_m:
+        raise ValueError("plan block_m differs from the requested launch")
+    if not plan.ntiles:
+        return plan
+    if blocks.ndim != 4 or blocks.shape[-1] != 16:
+        raise ValueError("grouped blocks must have shape [capacity,N,GK,16]")
+    cap, n, gk, _ = blocks.shape
+    if plan.K != gk * 32 or plan.N != n or max(plan.slots) >= cap:
+        raise ValueError("grouped plan dimensions or slots do not match the pool")
+    if (plan.device != blocks.device or scales.device != blocks.device or blocks.device.type != "cuda"):
+        raise ValueError("grouped launch needs plan, blocks and scales on the same CUDA device")
+    if blocks.dtype is not torch.uint8 or scales.dtype is not torch.uint8:
+        raise ValueError("grouped blocks and scales must be uint8")
+    if tuple(blocks.stride()[1:]) != (gk * 16, 16, 1) or scales.shape[:2] != (cap, n):
+        raise ValueError("grouped pool matrix rows must be contiguous and scales must match")
+    block_n = operator.index(block_n)
+    if block_n < 16 or block_n & (block_n - 1):
+        raise ValueError("block_n must be a power of two >= 16")
+    if gk != GK_SUPPORTED or n % 64:
+        raise ValueError(f"these kernels serve K = {GK_SUPPORTED * 32} and N a multiple of 64")
+    if not plan.aligned:
+        raise ValueError("pair rows must be 16-byte aligned (x and out addresses and row pitches)")
+    pk = _scale_layout(scales, gk, packed)
+    N.call("na_mxfp4_gemm_grouped", blocks.data_ptr(), blocks.stride(0), scales.data_ptr(), scales.stride(0), int(pk),
+           plan.metadata.data_ptr(), plan.ntiles, plan.block_m, n, gk * 32, N.stream(blocks.device))
+    return plan

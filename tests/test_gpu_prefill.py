@@ -1,0 +1,175 @@
+"""Prefill products on the GPU against the CPU oracle (reference behaviour: neural/q80/mxfp4_kernels.py:87-419,
+server.py:1837-1936).
+
+Bars: GEMM outputs within 2e-2 + 1e-2 * max|want| of the fp64 product of the exactly dequantised weights (the
+reference's own GEMV-vs-dequant bar is rel < 2e-2, tools/scale_pack_gpu_test.py:179-189) plus a mean-error bar;
+raw and PS4 pools give bit-identical outputs (tools/scale_pack_gpu_test.py); the grouped launch equals per-pair
+mxfp4_gemm bit for bit at block_m 16 and 64 over the reference's ragged M set [0, 1, 63, 64, 65, 129]
+(tools/grouped_gemm_ab.py:5-6); the fused prefill layer matches the oracle's expert forward and top-k combine per
+token, with invalid ids contributing +0.
+"""
+import numpy as np
+import pytest
+
+from oracle import mxfp4_oracle as mo
+from oracle.bf16 import rb
+from neural_amd import synth, tiles
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev():
+    import torch
+    return torch.device("cuda", 0)
+
+
+def _close(got, want, tag):
+    d = np.abs(got - want)
+    scale = np.abs(want).max()
+    assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale + 1e-6, (tag, d.max(), d.mean(), scale)
+
+
+def _pool(slots, packed, dev):
+    import torch
+    arr = np.stack([mo.ps4_pack_slot(s) if packed else s for s in slots])
+    return torch.from_numpy(arr).to(dev)
+
+
+@pytest.mark.parametrize("which", ["gate", "down"])
+def test_mxfp4_gemm_matches_oracle_raw_equals_ps4(which):
+    import torch
+    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4, mxfp4_pool_views
+    from neural_amd.q80 import mxfp4_kernels as mk
+    dev = _dev()
+    rng = np.random.default_rng(41 if which == "gate" else 42)
+    slots = [synth.slot_raw(rng) for _ in range(3)]
+    raw, ps4 = _pool(slots, False, dev), _pool(slots, True, dev)
+    gb, db, gs, ds = mxfp4_pool_views(raw, GPTOSS_LAYOUT)
+    gb4, db4, gs4, ds4 = mxfp4_pool_views(ps4, GPTOSS_LAYOUT_PS4)
+    blocks, scales = (gb, gs) if which == "gate" else (db, ds)
+    blocks4, scales4 = (gb4, gs4) if which == "gate" else (db4, ds4)
+    sl = torch.tensor([2, 0], dtype=torch.int64, device=dev)
+    W = [mo.expert_weights(s)[0 if which == "gate" else 1] for s in slots]
+    for M in (1, 5, 64, 100):
+        print(f"case mxfp4_gemm {which} M={M}", flush=True)
+        x = synth.bf16_normal(rng, (M, 2880))
+        xd = x.to(dev)
+        got = mk.mxfp4_gemm(xd, blocks, scales, sl)
+        got4 = mk.mxfp4_gemm(xd, blocks4, scales4, sl)
+        assert torch.equal(got, got4), "raw and PS4 pools must give identical outputs"
+        into = torch.empty_like(got)
+        mk.mxfp4_gemm_into(xd, blocks, scales, sl, into)
+        assert torch.equal(got, into)
+        g = got.float().cpu().numpy()
+        xf = x.float().numpy()
+        for e, s in enumerate((2, 0)):
+            _close(g[e], mo.gemv_f64(xf, W[s]), f"{which} M={M} e={e}")
+
+
+@pytest.mark.parametrize("block_m", [16, 64])
+def test_grouped_equals_per_pair_gemm(block_m):
+    import torch
+    from neural_amd.moe.layout import GPTOSS_LAYOUT_PS4, mxfp4_pool_views
+    from neural_amd.q80 import mxfp4_kernels as mk
+    dev = _dev()
+    rng = np.random.default_rng(7)
+    slots = [synth.slot_raw(rng) for _ in range(4)]
+    pool = _pool(slots, True, dev)
+    gb, db, gs, ds = mxfp4_pool_views(pool, GPTOSS_LAYOUT_PS4)
+    ms = [0, 1, 63, 64, 65, 129]
+    xs = [synth.bf16_normal(rng, (m, 2880)).to(dev) for m in ms]
+    for blocks, scales, n in ((gb, gs, 5760), (db, ds, 2880)):
+        print(f"case grouped N={n} block_m={block_m}", flush=True)
+        outs = [torch.full((m, n), 7.0, dtype=torch.bfloat16, device=dev) for m in ms]
+        pairs = [(x, i % 4, o) for i, (x, o) in enumerate(zip(xs, outs))]
+        plan = mk.mxfp4_gemm_grouped_into(pairs, blocks, scales, block_m=block_m)
+        assert plan.ntiles == sum(-(-m // block_m) for m in ms)
+        for i, (x, o) in enumerate(zip(xs, outs)):
+            if x.shape[0] == 0:
+                continue
+            want = mk.mxfp4_gemm(x, blocks, scales, torch.tensor([i % 4], dtype=torch.int64, device=dev))[0]
+            assert torch.equal(o, want), (n, block_m, i)
+        # the plan is reusable: a second launch writes the same values
+        for o in outs:
+            o.fill_(3.0)
+        mk.mxfp4_gemm_grouped_into(plan, blocks, scales, block_m=block_m)
+        want0 = mk.mxfp4_gemm(xs[-1], blocks, scales, torch.tensor([(len(ms) - 1) % 4], dtype=torch.int64,
+                                                                      device=dev))[0]
+        assert torch.equal(outs[-1], want0)
+
+
+def _routing(rng, T, nexp=128, invalid=True):
+    ranks = rng.permutation(nexp)
+    p = 1.0 / np.arange(1, nexp + 1) ** 1.1
+    p /= p.sum()
+    ids = np.stack([ranks[rng.choice(nexp, 4, replace=False, p=p)] for _ in range(T)]).astype(np.int64)
+    if invalid:
+        ids[3, 2] = -1
+        ids[T - 1, 0] = 300
+    w = mo.rb(rng.dirichlet(np.ones(4), size=T).astype(np.float32))
+    return ids, w
+
+
+@pytest.mark.parametrize("layout", ["raw", "ps4", "t950"])
+def test_forward_prefill_matches_oracle(layout):
+    import torch
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4, GPTOSS_LAYOUT_T950
+    dev = _dev()
+    rng = np.random.default_rng(2024)
+    nslot = 6
+    slots = [synth.slot_raw(rng) for _ in range(nslot)]
+    T = 96
+    x = synth.bf16_normal(rng, (T, 2880))
+    ids, w = _routing(rng, T)
+    n = 36 * 128
+    tab = (np.arange(n) % nslot).astype(np.int64)
+    bgu = synth.bf16_normal(rng, (n, 5760), 0.02)
+    bdn = synth.bf16_normal(rng, (n, 2880), 0.02)
+    if layout == "t950":
+        raw = _pool(slots, False, dev)
+        pool = torch.empty((nslot, tiles.SLOT_T950), dtype=torch.uint8, device=dev)
+        tiles.repack_to_t950(raw, pool)
+        L = GPTOSS_LAYOUT_T950
+    else:
+        pool = _pool(slots, layout == "ps4", dev)
+        L = GPTOSS_LAYOUT_PS4 if layout == "ps4" else GPTOSS_LAYOUT
+    rx = ResidentExperts(pool, L, bgu.to(dev), bdn.to(dev), torch.from_numpy(tab).to(dev))
+    layer = 5
+    print(f"case forward_prefill layout={layout} T={T}", flush=True)
+    got = rx.forward_prefill(layer, x.to(dev), torch.from_numpy(ids).to(dev),
+                             torch.from_numpy(w).to(torch.bfloat16).to(dev)).float().cpu().numpy()
+    cache = {}
+    for t in list(range(0, T, 9)) + [3, T - 1]:
+        ys = []
+        for k in range(4):
+            e = int(ids[t, k])
+            if not 0 <= e < 128:
+                ys.append(np.zeros(2880, np.float32))
+                continue
+            g = layer * 128 + e
+            s = int(tab[g])
+            if s not in cache:
+                cache[s] = mo.expert_weights(slots[s])
+            ys.append(mo.expert_forward_bf16(x[t:t + 1].float().numpy(), None, bgu[g].float().numpy(),
+                                             bdn[g].float().numpy(), weights=cache[s])[0])
+        _close(got[t], mo.combine_bf16(np.stack(ys), w[t]), f"{layout} token {t}")
+
+
+def test_prefill_raw_equals_ps4_bitwise():
+    import torch
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4
+    dev = _dev()
+    rng = np.random.default_rng(77)
+    slots = [synth.slot_raw(rng) for _ in range(5)]
+    T = 200
+    x = synth.bf16_normal(rng, (T, 2880)).to(dev)
+    ids, w = _routing(rng, T)
+    idd, wd = torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(torch.bfloat16).to(dev)
+    tab = torch.from_numpy((np.arange(36 * 128) % 5).astype(np.int64)).to(dev)
+    outs = []
+    for packed, L in ((False, GPTOSS_LAYOUT), (True, GPTOSS_LAYOUT_PS4)):
+        rx = ResidentExperts(_pool(slots, packed, dev), L, None, None, tab)
+        outs.append(rx.forward_prefill(11, x, idd, wd))
+    assert torch.equal(outs[0], outs[1])
