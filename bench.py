@@ -136,6 +136,112 @@ def cpu_baseline(pool_dev, ids, B, seconds=12.0):
             "gbps": round(4 * SLOT_ALGO_BYTES / t_call / 1e9, 2)}
 
 
+def zipf_routing(rng, T, n_exp=128, s=1.1):
+    """Per token 4 distinct experts drawn without replacement with probability ~ Zipf(s) over a fixed random rank
+    permutation of the experts; softmax weights of random logits (configuration 2)."""
+    ranks = rng.permutation(n_exp)
+    p = 1.0 / np.arange(1, n_exp + 1) ** s
+    p /= p.sum()
+    ids = np.stack([ranks[rng.choice(n_exp, TOPK, replace=False, p=p)] for _ in range(T)]).astype(np.int64)
+    lg = rng.standard_normal((T, TOPK)).astype(np.float32)
+    e = np.exp(lg - lg.max(-1, keepdims=True))
+    return ids, (e / e.sum(-1, keepdims=True)).astype(np.float32)
+
+
+def bench_prefill(A):
+    """Configuration 2: one MoE layer over T = 2048 prompt tokens (hidden 2880, 128 experts, top-4, Zipf(1.1) expert
+    popularity), weights MXFP4 as configuration 0 in the t950 pool, x bf16 N(0,1), zero biases.  One step = the fused
+    prefill layer (five launches), captured in a hipGraph.  Reported: tokens/s, the layer's TFLOP/s on the bf16
+    MFMA path, and the roofline fraction max(flop / 2.5 PF bf16, bytes / 8 TB/s) / measured time."""
+    import torch
+
+    from neural_amd import synth, tiles
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_T950
+
+    dev = torch.device("cuda", 0)
+    T = A.tokens
+    L = GPTOSS_LAYOUT_T950
+    pool = torch.empty(N_EXPERTS, L.slot_bytes, dtype=torch.uint8, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    raw = torch.empty((N_EXPERTS, GPTOSS_LAYOUT.slot_bytes), dtype=torch.uint8, device=dev)
+    cb = synth.CODE_BYTES
+    raw[:, :cb].random_(0, 256, generator=g)
+    raw[:, cb:].random_(synth.SCALE_LO, synth.SCALE_HI + 1, generator=g)
+    tiles.repack_to_t950(raw, pool)
+    del raw
+    tab = torch.arange(N_LAYERS * N_EXPERTS, dtype=torch.int64, device=dev) % N_EXPERTS
+    rx = ResidentExperts(pool, L, None, None, tab)
+    rng = np.random.default_rng(2048)
+    ids_np, w_np = zipf_routing(rng, T)
+    counts = np.bincount(ids_np.reshape(-1), minlength=N_EXPERTS)
+    ids = torch.from_numpy(ids_np).to(dev)
+    wts = torch.from_numpy(w_np).to(torch.bfloat16).to(dev)
+    x = synth.bf16_normal(rng, (T, H)).to(dev)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    rx.forward_prefill(0, x, ids, wts, out=out)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        rx.forward_prefill(0, x, ids, wts, out=out)
+    torch.cuda.current_stream().wait_stream(cs)
+    with torch.cuda.graph(gr):
+        rx.forward_prefill(0, x, ids, wts, out=out)
+    for _ in range(max(A.warmup // 4, 3)):
+        gr.replay()
+    torch.cuda.synchronize()
+    steps = max(A.steps // 10, 10)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        gr.replay()
+    torch.cuda.synchronize()
+    el = (time.perf_counter() - t0) / steps
+    # per-launch times (eager, dispatch-timestamped events)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(10)]
+    for e in ev:
+        e.record()
+    torch.cuda.synchronize()
+    names = ("count", "order", "gate_up", "down", "combine")
+    per = {nm: 0.0 for nm in names}
+    R = 5
+    for _ in range(R):
+        rx.forward_prefill(0, x, ids, wts, out=out, events=ev)
+        torch.cuda.synchronize()
+        for i, nm in enumerate(names):
+            per[nm] += ev[2 * i].elapsed_time(ev[2 * i + 1]) * 1e3 / R
+    P = int(counts.sum())
+    flop = 2.0 * P * (5760 * 2880 + 2880 * 2880)
+    touched = int((counts > 0).sum())
+    wbytes = touched * SLOT_ALGO_BYTES
+    abytes = T * H * 2 + P * 2880 * 2 * 2 + P * H * 2 * 2 + T * H * 2
+    t_roof = max(flop / 2.5e15, (wbytes + abytes) / (HBM_PEAK_GBS * 1e9))
+    log(f"prefill T={T}: {el * 1e6:.1f} us/layer ({T / el:.0f} tok/s), {flop / el / 1e12:.1f} TFLOP/s; launches "
+        + ", ".join(f"{nm} {v:.1f} us" for nm, v in per.items()))
+    gu_flop = 2.0 * P * 5760 * 2880
+    res = {"metric": "prefill MoE layer tokens/s (config 2)", "value": round(T / el, 1), "unit": "tok/s", "n_gpus": 1,
+           "steps": steps, "ms_per_step": round(el * 1e3, 4), "higher_is_better": True, "dtype": "bf16",
+           "data": "synthetic",
+           "config": {"workload": f"config2: one MoE layer, {T} tokens, 128 experts top-4 Zipf(1.1), t950 pool, "
+                                  "bf16 MFMA with in-register FP4 dequant", "tokens": T, "pairs": P,
+                      "experts_touched": touched, "max_expert_tokens": int(counts.max()),
+                      "min_expert_tokens": int(counts[counts > 0].min()),
+                      "launch_us": {k: round(v, 2) for k, v in per.items()},
+                      "layer_tflops": round(flop / el / 1e12, 2),
+                      "gate_up_tflops": round(gu_flop / (per["gate_up"] * 1e-6) / 1e12, 2),
+                      "roofline_time_us": round(t_roof * 1e6, 1),
+                      "roofline_fraction": round(t_roof / el, 4)},
+           "roofline": {"bound": "hbm" if (wbytes + abytes) / (HBM_PEAK_GBS * 1e9) >= flop / 2.5e15 else "mfma",
+                        "achieved": round((wbytes + abytes) / el / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round((wbytes + abytes) / el / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                        "kernel": "k_prefill_gate_up + k_prefill_down",
+                        "mfma_bf16_frac": round(flop / el / 2.5e15, 4)},
+           "cpu_baseline": None}
+    print(json.dumps(res), flush=True)
+
+
 def bench_attention(A):
     """Configuration 3: GQA decode attention (64 q / 8 KV heads, head_dim 64, bf16 K/V ~ N(0,1), sinks ~ N(0,1)),
     batch 1 and 4, contexts 1024 / 4096 / 8192, layers alternating full attention and a 128-token sliding window
@@ -229,8 +335,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--gu-pairs", type=int, default=4, help="gate_up row pairs per wavefront (1, 2, 4)")
     ap.add_argument("--dn-pairs", type=int, default=2, help="down row pairs per wavefront (1, 2, 4)")
-    ap.add_argument("--workload", choices=("experts", "attention"), default="experts",
-                    help="experts: configuration 1 (the headline); attention: configuration 3 (decode attention)")
+    ap.add_argument("--workload", choices=("experts", "attention", "prefill"), default="experts",
+                    help="experts: configuration 1 (the headline); prefill: configuration 2 (grouped GEMM layer); "
+                         "attention: configuration 3 (decode attention)")
+    ap.add_argument("--tokens", type=int, default=2048, help="prefill: prompt tokens")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run one device-to-device copy of this many MB first (a known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
@@ -241,6 +349,8 @@ def main():
         sys.exit(2)
     if A.workload == "attention":
         return bench_attention(A)
+    if A.workload == "prefill":
+        return bench_prefill(A)
     if not 1 <= A.batch <= 8:
         sys.exit("--batch must be in [1, 8]")
 

@@ -131,14 +131,14 @@ int na_decode_attention(const void* q, const void* kc, const void* vc, long long
  *   x        bf16 [M, K], K = 2880 (16-byte aligned rows)
  *   blocks   layout 0 (raw) / 1 (PS4): u8 view [cap, N, 90, 16], slot stride sb_slot; scales [cap, N, 90 | 46] with
  *            slot stride ss_slot.  layout 2: blocks = the matrix's first t950 row block of slot 0, stride sb_slot.
- *   out      bf16 [E, M, N], N a multiple of 64 */
+ *   out      bf16 [E, M, N], N a multiple of 192 */
 int na_mxfp4_gemm(const void* x, int M, int K, const void* blocks, long long sb_slot, const void* scales,
                   long long ss_slot, int layout, const int64_t* slots, int E, void* out, int N, hipStream_t stream);
 
 /* One ragged GEMM launch over GroupedGemmPlan tile descriptors.  Replaces mxfp4_kernels.py:242-295 and :385-419.
  *   tiles    int64 [ntiles][5] = (x address, out address, slot, pair rows M, tile pm): rows [pm * block_m,
  *            min(M, (pm + 1) * block_m)) of the pair; x rows K = 2880 bf16, out rows N bf16 (16-byte aligned)
- *   block_m  power of two >= 16 */
+ *   block_m  power of two >= 16; N a multiple of 192 */
 int na_mxfp4_gemm_grouped(const void* blocks, long long sb_slot, const void* scales, long long ss_slot, int layout,
                           const int64_t* tiles, int ntiles, int block_m, int N, int K, hipStream_t stream);
 

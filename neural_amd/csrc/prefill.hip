@@ -3,11 +3,11 @@
 // each output; reference neural/q80/mxfp4_kernels.py:87-126, 242-295) on v_mfma_f32_16x16x32_bf16, and the fused
 // MoE prefill layer built on it (reference server.py:1837-1936, _expert_gemms :1977-2040).
 //
-// Workgroup tile: 64 tokens x 64 weight rows (4 waves, wave w owns the 16-row block w), K walked in k-tiles of 4
-// groups (128 elements).  Per k-tile the workgroup stages the 64 x 128 activation tile in LDS (double buffered,
-// gathered through a row map: token-permuted rows for the MoE path), each wave loads its block's codes and scales
-// (next k-tile in flight while the current one computes), dequantises them in registers with
-// v_cvt_scalef32_pk_bf16_fp4 and runs 16 MFMAs (4 token tiles x 4 groups).  The activations stay bf16: an FP4 or
+// Workgroup tile: 64 tokens x (4 waves x NB row blocks of 16 weight rows; NB = 3, or 4 in the SwiGLU gate_up
+// kernel), K walked in k-tiles of 4 groups (128 elements).  Per k-tile the workgroup stages the 64 x 128 activation
+// tile in LDS (double buffered, gathered through a row map: token-permuted rows for the MoE path), each wave loads
+// its blocks' codes and scales (next k-tile in flight while the current one computes), reads its 16 A fragments
+// once, dequantises each block's codes in registers with v_cvt_scalef32_pk_bf16_fp4 and runs 16 NB MFMAs.  The activations stay bf16: an FP4 or
 // FP8 MFMA would need quantised activations and would no longer give the reference's results.
 //
 // Weight layouts (template W): the store's raw and PS4 slots (row r: 1,440 code bytes, then a raw 90-byte or PS4
@@ -98,45 +98,65 @@ NA_DEVICE void a_store(uint8_t* lds, int tid, const AStage& a) {
   }
 }
 
-// acc[tt] = D of token tile tt (tokens 16 tt .. 16 tt + 15) x the wave's 16 rows: lane (q, n) holds tokens
-// 16 tt + 4 q + r, r = 0..3, row n.  All 256 threads must call it (barriers inside).
-template <int W, typename RowPtr>
-NA_DEVICE void gemm_tile(const WSrc& src, int rblk, RowPtr row_ptr, uint8_t* lds_a /* 2 x 64 x kPApitch */,
-                         f32x4_t acc[4]) {
+// acc[tt][nb] = D of token tile tt (tokens 16 tt .. 16 tt + 15) x row block blk[nb] of this wave: lane (q, n)
+// holds tokens 16 tt + 4 q + r, r = 0..3, row n of the block.  Per k-tile the wave reads its 16 A fragments from LDS
+// once and feeds each to NB MFMAs per group (one per row block), so LDS traffic per MFMA falls as 1 / NB.  A wave
+// without work (live = false) still stages activations and meets every barrier; its loads use block blk[0] (valid
+// memory) and it runs no MFMA.  All 256 threads must call it (barriers inside).
+template <int W, int NB, typename RowPtr>
+NA_DEVICE void gemm_tile(const WSrc& src, const int (&blk)[NB], bool live, RowPtr row_ptr,
+                         uint8_t* lds_a /* 2 x 64 x kPApitch */, f32x4_t (&acc)[4][NB]) {
   const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, n = lane & 15;
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) acc[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[tt][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   AStage an;
-  uint4 cn;
-  uint32_t sn;
+  uint4 cn[NB];
+  uint32_t sn[NB];
   a_load(row_ptr, 0, tid, an);
-  w_load<W>(src, rblk, 0, lane, cn, sn);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) w_load<W>(src, blk[nb], 0, lane, cn[nb], sn[nb]);
   a_store(lds_a, tid, an);
   __syncthreads();
   for (int t = 0; t < kPTiles; ++t) {
-    const uint4 c = cn;
-    const uint32_t sc = sn;
-    uint8_t* cur = lds_a + (t & 1) * (kPBM * kPApitch);
+    uint4 c[NB];
+    uint32_t sc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      c[nb] = cn[nb];
+      sc[nb] = sn[nb];
+    }
+    const uint8_t* cur = lds_a + (t & 1) * (kPBM * kPApitch);
     if (t + 1 < kPTiles) {                           // next k-tile in flight during this one's MFMAs
       a_load(row_ptr, t + 1, tid, an);
-      w_load<W>(src, rblk, t + 1, lane, cn, sn);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) w_load<W>(src, blk[nb], t + 1, lane, cn[nb], sn[nb]);
     }
-    bf16x8_t b[4];
+    bf16x8_t a[4][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = w_operand<W>(c, sc, t, j, lane);
+    for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const uint8_t* arow = cur + (16 * tt + n) * kPApitch;
+      for (int j = 0; j < 4; ++j)
+        a[tt][j] = *reinterpret_cast<const bf16x8_t*>(cur + (16 * tt + n) * kPApitch + a_offset<W>(j, q));
+    if (live) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(arow + a_offset<W>(j, q));
-        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[j], acc[tt], 0, 0, 0);
-      }
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8_t b = w_operand<W>(c[nb], sc[nb], t, j, lane);
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+            acc[tt][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tt][j], b, acc[tt][nb], 0, 0, 0);
+        }
     }
     if (t + 1 < kPTiles) a_store(lds_a + ((t + 1) & 1) * (kPBM * kPApitch), tid, an);
     __syncthreads();
   }
 }
+
+constexpr int kPNB = 3;                  // row blocks per wave in the plain, grouped and down kernels
+constexpr int kPRows = 4 * kPNB * 16;    // 192 weight rows per workgroup
 
 template <int W>
 NA_DEVICE WSrc w_src(const uint8_t* blocks, long long sb_slot, const uint8_t* scales, long long ss_slot,
@@ -145,7 +165,25 @@ NA_DEVICE WSrc w_src(const uint8_t* blocks, long long sb_slot, const uint8_t* sc
 }
 
 // ------------------------------------------------------------------------------- plain GEMM (mxfp4_gemm)
-// out[e][m][n] = bf16(sum_k x[m][k] w_e[n][k]); grid (E * ceil(M / 64), N / 64).
+// out[e][m][n] = bf16(sum_k x[m][k] w_e[n][k]); grid (E * ceil(M / 64), N / 192); wave w: row blocks
+// 12 y + 3 w + i.
+NA_DEVICE void store_tile(uint16_t* out_row0, long long pitch, const f32x4_t (&acc)[4][kPNB], const int (&blk)[kPNB],
+                          int m_limit) {
+  const int lane = threadIdx.x & 63, q = lane >> 4, n = lane & 15;
+#pragma unroll
+  for (int nb = 0; nb < kPNB; ++nb)
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * tt + 4 * q + r;
+        const uint16_t v = f32_to_bf16(acc[tt][nb][r]);
+        const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
+        if (m < m_limit && !(n & 1))
+          *reinterpret_cast<uint32_t*>(out_row0 + (long long)m * pitch + 16 * blk[nb] + n) = (uint32_t)v | (hi << 16);
+      }
+}
+
 template <int W>
 __global__ __launch_bounds__(256) void k_mxfp4_gemm(const uint16_t* __restrict__ x, int M,
                                                     const uint8_t* __restrict__ blocks, long long sb_slot,
@@ -155,27 +193,19 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemm(const uint16_t* __restrict__
   __shared__ __align__(16) uint8_t lds_a[2 * kPBM * kPApitch];
   const int mt = (M + kPBM - 1) / kPBM;
   const int e = blockIdx.x / mt, m0 = (blockIdx.x - e * mt) * kPBM;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q = lane >> 4, n = lane & 15;
-  const int rblk = blockIdx.y * 4 + wave;
+  const int wave = threadIdx.x >> 6;
+  int blk[kPNB];
+#pragma unroll
+  for (int i = 0; i < kPNB; ++i) blk[i] = blockIdx.y * (4 * kPNB) + kPNB * wave + i;
   const WSrc src = w_src<W>(blocks, sb_slot, scales, ss_slot, slots[e]);
-  f32x4_t acc[4];
-  gemm_tile<W>(src, rblk, [=](int row) { return x + (long long)min(m0 + row, M - 1) * kH; }, lds_a, acc);
-  uint16_t* ob = out + (long long)e * M * N + 16 * rblk;
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = m0 + 16 * tt + 4 * q + r;
-      const uint16_t v = f32_to_bf16(acc[tt][r]);
-      const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
-      if (m < M && !(n & 1))
-        *reinterpret_cast<uint32_t*>(ob + (long long)m * N + n) = (uint32_t)v | (hi << 16);
-    }
+  f32x4_t acc[4][kPNB];
+  gemm_tile<W, kPNB>(src, blk, true, [=](int row) { return x + (long long)min(m0 + row, M - 1) * kH; }, lds_a, acc);
+  store_tile(out + ((long long)e * M + m0) * N, N, acc, blk, M - m0);
 }
 
 // --------------------------------------------------------------- grouped GEMM (GroupedGemmPlan descriptors)
 // tiles int64 [ntiles][5] = (x address, out address, slot, pair M, pm); rows [pm * block_m, min(M, pm * block_m +
-// block_m)) of the pair, walked in 64-row sub-tiles (block_m <= 64: one).  grid (ntiles, N / 64).
+// block_m)) of the pair, walked in 64-row sub-tiles (block_m <= 64: one).  grid (ntiles, N / 192).
 template <int W>
 __global__ __launch_bounds__(256) void k_mxfp4_gemm_grouped(const uint8_t* __restrict__ blocks, long long sb_slot,
                                                             const uint8_t* __restrict__ scales, long long ss_slot,
@@ -186,23 +216,17 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemm_grouped(const uint8_t* __res
   uint16_t* out = reinterpret_cast<uint16_t*>(d[1]);
   const long long slot = d[2];
   const int M = (int)d[3], pm = (int)d[4];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q = lane >> 4, n = lane & 15;
-  const int rblk = blockIdx.y * 4 + wave;
+  const int wave = threadIdx.x >> 6;
+  int blk[kPNB];
+#pragma unroll
+  for (int i = 0; i < kPNB; ++i) blk[i] = blockIdx.y * (4 * kPNB) + kPNB * wave + i;
   const WSrc src = w_src<W>(blocks, sb_slot, scales, ss_slot, slot);
   const int r0 = pm * block_m, r1 = min(M, r0 + block_m);
   for (int m0 = r0; m0 < r1; m0 += kPBM) {
-    f32x4_t acc[4];
-    gemm_tile<W>(src, rblk, [=](int row) { return x + (long long)min(m0 + row, r1 - 1) * kH; }, lds_a, acc);
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + 16 * tt + 4 * q + r;
-        const uint16_t v = f32_to_bf16(acc[tt][r]);
-        const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
-        if (m < r1 && !(n & 1))
-          *reinterpret_cast<uint32_t*>(out + (long long)m * N + 16 * rblk + n) = (uint32_t)v | (hi << 16);
-      }
+    f32x4_t acc[4][kPNB];
+    gemm_tile<W, kPNB>(src, blk, true, [=](int row) { return x + (long long)min(m0 + row, r1 - 1) * kH; }, lds_a,
+                       acc);
+    store_tile(out + (long long)m0 * N, N, acc, blk, r1 - m0);
   }
 }
 
@@ -267,9 +291,10 @@ __global__ __launch_bounds__(256) void k_prefill_order(const int64_t* __restrict
   }
 }
 
-// gate_up + bias + clamped SwiGLU: tile i, column block a (intermediate columns 32a .. 32a + 31).  Waves 0, 1 hold
-// the gate rows (blocks 2a, 2a + 1), waves 2, 3 the up rows (blocks 180 + 2a, 181 + 2a); h rows are in sorted pair
-// order: h[p0 + m][j].  grid (max tiles, 90).
+// gate_up + bias + clamped SwiGLU: tile i, column group a.  Wave w owns intermediate blocks jb, jb + 1
+// (jb = 8 a + 2 w; columns 16 jb .. 16 jb + 31) and reads their gate rows (blocks jb, jb + 1) and up rows (blocks
+// 180 + jb, 181 + jb), so the SwiGLU pairs registers of one lane.  h rows are in sorted pair order: h[p0 + m][j].
+// grid (max tiles, 23); in the last column group waves 2 and 3 have no blocks.
 template <int W>
 __global__ __launch_bounds__(256) void k_prefill_gate_up(
     const uint16_t* __restrict__ x, const int* __restrict__ order, const PTile* __restrict__ tiles,
@@ -277,53 +302,48 @@ __global__ __launch_bounds__(256) void k_prefill_gate_up(
     const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ bias_gu,
     uint16_t* __restrict__ h, float alpha, float limit) {
   __shared__ __align__(16) uint8_t lds_a[2 * kPBM * kPApitch];
-  __shared__ float ups[2][kPBM][16 + 1];
   if ((int)blockIdx.x >= *ntiles) return;
   const PTile tl = tiles[blockIdx.x];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q = lane >> 4, n = lane & 15;
-  const int a = blockIdx.y;
-  const int half = wave >> 1;                          // 0: gate, 1: up
-  const int rblk = (half ? kTUpBlock0 : 0) + 2 * a + (wave & 1);
+  const int jb = 8 * blockIdx.y + 2 * wave;
+  const bool live = jb < kTUpBlock0;
+  const int jl = live ? jb : 0;
+  const int blk[4] = {jl, jl + 1, kTUpBlock0 + jl, kTUpBlock0 + jl + 1};
   const long long gid = expert_base + tl.e;
   const long long slot = slot_tab ? slot_tab[gid] : gid;
   const uint8_t* sb = pool + slot * slot_bytes;
   const WSrc src = W == kWT950 ? WSrc{sb, nullptr} : WSrc{sb, sb + kOffGateScales};
-  f32x4_t acc[4];
-  gemm_tile<W>(src, rblk, [=](int row) { return x + (long long)(order[tl.p0 + min(row, tl.cnt - 1)] >> 2) * kH; },
-               lds_a, acc);
-  // gu = bf16(acc) + bias (bf16 rounding of each op, as the reference's torch ops); up half through LDS
-  const int j = 32 * a + 16 * (wave & 1) + n;
+  f32x4_t acc[4][4];
+  gemm_tile<W, 4>(src, blk, live,
+                  [=](int row) { return x + (long long)(order[tl.p0 + min(row, tl.cnt - 1)] >> 2) * kH; }, lds_a,
+                  acc);
+  if (!live) return;
+  // gu = bf16(acc) + bias (bf16 rounding of each op, as the reference's torch ops), then the clamped SwiGLU
   const uint16_t* bg = bias_gu ? bias_gu + gid * kGU : nullptr;
-  if (half) {
-    const float bu = bg ? bf16_to_f32(bg[kI + j]) : 0.f;
+#pragma unroll
+  for (int hb = 0; hb < 2; ++hb) {
+    const int j = 16 * (jl + hb) + n;
+    const float bgv = bg ? bf16_to_f32(bg[j]) : 0.f, buv = bg ? bf16_to_f32(bg[kI + j]) : 0.f;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float u = rb(acc[tt][r]);
-        if (bg) u = rb(u + bu);
-        ups[wave & 1][16 * tt + 4 * q + r][n] = u;
+        const int m = 16 * tt + 4 * q + r;
+        float g = rb(acc[tt][hb][r]), u = rb(acc[tt][2 + hb][r]);
+        if (bg) {
+          g = rb(g + bgv);
+          u = rb(u + buv);
+        }
+        const uint16_t hv = f32_to_bf16(swiglu_clamp_bf16(g, u, alpha, limit));
+        const uint32_t hi = (uint32_t)__shfl_xor((int)hv, 1) & 0xffff;
+        if (m < tl.cnt && !(n & 1))
+          *reinterpret_cast<uint32_t*>(h + (long long)(tl.p0 + m) * kI + j) = (uint32_t)hv | (hi << 16);
       }
   }
-  __syncthreads();
-  if (half) return;
-  const float bgv = bg ? bf16_to_f32(bg[j]) : 0.f;
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 16 * tt + 4 * q + r;
-      float g = rb(acc[tt][r]);
-      if (bg) g = rb(g + bgv);
-      const uint16_t hv = f32_to_bf16(swiglu_clamp_bf16(g, ups[wave & 1][m][n], alpha, limit));
-      const uint32_t hi = (uint32_t)__shfl_xor((int)hv, 1) & 0xffff;
-      if (m < tl.cnt && !(n & 1))
-        *reinterpret_cast<uint32_t*>(h + (long long)(tl.p0 + m) * kI + j) = (uint32_t)hv | (hi << 16);
-    }
 }
 
 // down + bias, x routing weight, scattered back to pair order: ys[p][n] = bf16(bf16(bf16(y) + b) * w[p]) with p the
-// pair of sorted position p0 + m.  grid (max tiles, 45).
+// pair of sorted position p0 + m.  grid (max tiles, 15); wave w: row blocks 12 y + 3 w + i.
 template <int W>
 __global__ __launch_bounds__(256) void k_prefill_down(
     const uint16_t* __restrict__ h, const int* __restrict__ order, const PTile* __restrict__ tiles,
@@ -334,29 +354,40 @@ __global__ __launch_bounds__(256) void k_prefill_down(
   if ((int)blockIdx.x >= *ntiles) return;
   const PTile tl = tiles[blockIdx.x];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q = lane >> 4, n = lane & 15;
-  const int rblk = blockIdx.y * 4 + wave;
+  int blk[kPNB];
+#pragma unroll
+  for (int i = 0; i < kPNB; ++i) blk[i] = blockIdx.y * (4 * kPNB) + kPNB * wave + i;
   const long long gid = expert_base + tl.e;
   const long long slot = slot_tab ? slot_tab[gid] : gid;
   const uint8_t* sb = pool + slot * slot_bytes;
   const WSrc src = W == kWT950 ? WSrc{sb + kTDownOff, nullptr}
                                : WSrc{sb + kOffDownCodes, sb + kOffGateScales + (long long)kGU * (W == kWRaw ? kGK : kPs4Row)};
-  f32x4_t acc[4];
-  gemm_tile<W>(src, rblk, [=](int row) { return h + (long long)(tl.p0 + min(row, tl.cnt - 1)) * kI; }, lds_a, acc);
-  const int col = 16 * rblk + n;
-  const float bd = bias_dn ? bf16_to_f32(bias_dn[gid * kH + col]) : 0.f;
+  f32x4_t acc[4][kPNB];
+  gemm_tile<W, kPNB>(src, blk, true, [=](int row) { return h + (long long)(tl.p0 + min(row, tl.cnt - 1)) * kI; },
+                     lds_a, acc);
+  int pr[4][4];                                       // pair of each of the lane's 16 tokens
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 16 * tt + 4 * q + r;
-      const int p = order[tl.p0 + min(m, tl.cnt - 1)];
-      float y = rb(acc[tt][r]);
-      if (bias_dn) y = rb(y + bd);
-      const uint16_t v = f32_to_bf16(y * bf16_to_f32(wts[p]));
-      const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
-      if (m < tl.cnt && !(n & 1))
-        *reinterpret_cast<uint32_t*>(ys + (long long)p * kH + 16 * rblk + n) = (uint32_t)v | (hi << 16);
-    }
+    for (int r = 0; r < 4; ++r) pr[tt][r] = order[tl.p0 + min(16 * tt + 4 * q + r, tl.cnt - 1)];
+#pragma unroll
+  for (int nb = 0; nb < kPNB; ++nb) {
+    const int col = 16 * blk[nb] + n;
+    const float bd = bias_dn ? bf16_to_f32(bias_dn[gid * kH + col]) : 0.f;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * tt + 4 * q + r;
+        const int p = pr[tt][r];
+        float y = rb(acc[tt][nb][r]);
+        if (bias_dn) y = rb(y + bd);
+        const uint16_t v = f32_to_bf16(y * bf16_to_f32(wts[p]));
+        const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
+        if (m < tl.cnt && !(n & 1))
+          *reinterpret_cast<uint32_t*>(ys + (long long)p * kH + 16 * blk[nb] + n) = (uint32_t)v | (hi << 16);
+      }
+  }
 }
 
 // out[t][n] = bf16(sum_k ys[4 t + k][n]) over the valid ranks k, fp32 sum in top-k order (server.py:2340-2341).
@@ -445,7 +476,7 @@ int na_moe_prefill(const void* x, const int64_t* topk_ids, const void* topk_w, i
   launch_p(k_prefill_count, dim3(128), dim3(256), stream, ev[0], ev[1], topk_ids, P, counts);
   launch_p(k_prefill_order, dim3(128), dim3(256), stream, ev[2], ev[3], topk_ids, P, (const int*)counts, order, tiles,
            ntiles);
-  const dim3 gg(w.max_tiles, kI / 32), gd(w.max_tiles, kH / 64), blk(256);
+  const dim3 gg(w.max_tiles, (kTUpBlock0 + 7) / 8), gd(w.max_tiles, kH / kPRows), blk(256);
 #define NA_PREFILL_GEMMS(W)                                                                                          \
   launch_p(k_prefill_gate_up<W>, gg, blk, stream, ev[4], ev[5], (const uint16_t*)x, (const int*)order,                \
            (const PTile*)tiles, (const int*)ntiles, (const uint8_t*)pool, slot_bytes, slot_tab, expert_base,          \
@@ -470,11 +501,11 @@ int na_moe_prefill(const void* x, const int64_t* topk_ids, const void* topk_w, i
 int na_mxfp4_gemm(const void* x, int M, int K, const void* blocks, long long sb_slot, const void* scales,
                   long long ss_slot, int layout, const int64_t* slots, int E, void* out, int N, hipStream_t stream) {
   if (!x || !blocks || !slots || !out || M <= 0 || E <= 0 || N <= 0) return kErrArgs;
-  if (K != kH || N % 64 || layout < kWRaw || layout > kWT950 || (layout != kWT950 && !scales)) return kErrArgs;
+  if (K != kH || N % kPRows || layout < kWRaw || layout > kWT950 || (layout != kWT950 && !scales)) return kErrArgs;
   if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) & 15) return kErrArgs;
   const long long mt = (M + kPBM - 1) / kPBM;
   if (mt * E > 0x7fffffff) return kErrTooLarge;
-  const dim3 grid((unsigned)(mt * E), N / 64), blk(256);
+  const dim3 grid((unsigned)(mt * E), N / kPRows), blk(256);
   auto kern = layout == kWT950 ? k_mxfp4_gemm<kWT950> : layout == kWPs4 ? k_mxfp4_gemm<kWPs4> : k_mxfp4_gemm<kWRaw>;
   hipLaunchKernelGGL(kern, grid, blk, 0, stream, (const uint16_t*)x, M, (const uint8_t*)blocks, sb_slot,
                      (const uint8_t*)scales, ss_slot, slots, (uint16_t*)out, N);
@@ -484,10 +515,10 @@ int na_mxfp4_gemm(const void* x, int M, int K, const void* blocks, long long sb_
 int na_mxfp4_gemm_grouped(const void* blocks, long long sb_slot, const void* scales, long long ss_slot, int layout,
                           const int64_t* tiles, int ntiles, int block_m, int N, int K, hipStream_t stream) {
   if (!blocks || !tiles || ntiles < 0 || N <= 0) return kErrArgs;
-  if (K != kH || N % 64 || layout < kWRaw || layout > kWT950 || (layout != kWT950 && !scales)) return kErrArgs;
+  if (K != kH || N % kPRows || layout < kWRaw || layout > kWT950 || (layout != kWT950 && !scales)) return kErrArgs;
   if (block_m < 16 || (block_m & (block_m - 1)) || block_m > 4096) return kErrArgs;
   if (ntiles == 0) return kOk;
-  const dim3 grid(ntiles, N / 64), blk(256);
+  const dim3 grid(ntiles, N / kPRows), blk(256);
   auto kern = layout == kWT950 ? k_mxfp4_gemm_grouped<kWT950>
             : layout == kWPs4 ? k_mxfp4_gemm_grouped<kWPs4> : k_mxfp4_gemm_grouped<kWRaw>;
   hipLaunchKernelGGL(kern, grid, blk, 0, stream, (const uint8_t*)blocks, sb_slot, (const uint8_t*)scales, ss_slot,

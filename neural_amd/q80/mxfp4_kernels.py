@@ -211,8 +211,8 @@ def _gemm_views(x, blocks, scales, packed):
         raise ValueError("scales must be a uint8 [cap, N, w] view matching blocks")
     if gk != GK_SUPPORTED:
         raise ValueError(f"GK={gk}: these kernels are built for K = {GK_SUPPORTED * 32} (GPT-OSS-120B)")
-    if n % 64:
-        raise ValueError(f"N={n}: the GEMM tiles 64 weight rows per workgroup")
+    if n % 192:
+        raise ValueError(f"N={n}: the GEMM tiles 192 weight rows per workgroup")
     for t, nm in ((blocks, "blocks"), (scales, "scales")):
         if t.device != x.device or t.device.type != "cuda":
             raise ValueError(f"{nm} must be on the input's CUDA device")
@@ -240,7 +240,7 @@ def mxfp4_gemm(x: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor, slot
                block_n: int = 128, block_m: int = 16, packed: bool | None = None) -> torch.Tensor:
     """x [M, K] bf16; blocks/scales = slot-pool u8 views; slots int64 [E].  Returns [E, M, N] bf16 with
     out[e, m, n] = bf16(sum_k x[m, k] w_slot[e][n, k]) (reference mxfp4_kernels.py:202-216; any E and M here).
-    block_n / block_m are accepted for interface compatibility: the kernel tiles 64 x 64."""
+    block_n / block_m are accepted for interface compatibility: the kernel tiles 64 tokens x 192 rows."""
     E, M, n, pk = _gemm_args(x, blocks, scales, slots, packed)
     out = torch.empty(E, M, n, dtype=torch.bfloat16, device=x.device)
     if E and M:
@@ -287,8 +287,8 @@ def mxfp4_gemm_grouped_into(pairs_or_plan, blocks: torch.Tensor, scales: torch.T
     block_n = operator.index(block_n)
     if block_n < 16 or block_n & (block_n - 1):
         raise ValueError("block_n must be a power of two >= 16")
-    if gk != GK_SUPPORTED or n % 64:
-        raise ValueError(f"these kernels serve K = {GK_SUPPORTED * 32} and N a multiple of 64")
+    if gk != GK_SUPPORTED or n % 192:
+        raise ValueError(f"these kernels serve K = {GK_SUPPORTED * 32} and N a multiple of 192")
     if not plan.aligned:
         raise ValueError("pair rows must be 16-byte aligned (x and out addresses and row pitches)")
     pk = _scale_layout(scales, gk, packed)
