@@ -158,6 +158,53 @@ int na_moe_prefill(const void* x, const int64_t* topk_ids, const void* topk_w, i
                    const void* bias_gu, const void* bias_dn, void* workspace, long long ws_bytes, void* out,
                    float alpha, float limit, void* const* events, hipStream_t stream);
 
+/* ---- dense decode core of one token (bf16 weights; rounding points of the reference's eager core,
+ *      neural/moe/gptoss_core_graphs.py:55-109, and of its fused twin fused_core.py) */
+
+/* mid = embed[seq[*pos]] (seq[0] when pos is NULL); the position is clamped into [0, seq_len), the id into
+ * [0, vocab).  Replaces the embedding lookup ahead of the layer loop (gptoss_core_graphs.py:113-140 embeds on the
+ * host; here the id stays on the device).
+ *   emb bf16 [vocab, 2880]; seq int64 [seq_len]; pos int64 [1] or NULL; mid bf16 [2880] */
+int na_core_embed(const void* emb, long long vocab, const int64_t* seq, long long seq_len, const int64_t* pos,
+                  void* mid, hipStream_t stream);
+
+/* Residual combine + input RMSNorm + fused Q|K|V GEMV + bias + YaRN RoPE + K/V cache write.  Replaces
+ * fused_core.py:72-142 (_combine, k_qkv).
+ *   x = mid (g NULL: first layer) or bf16(mid + bf16(g + bf16(c))) (c fp32 [2880] or NULL = 0; g bf16 [2880]);
+ *   xbuf bf16 [2880] <- x; in_w bf16 [2880]; W bf16 [5120, 2880] (q 4096 | k 512 | v 512 rows); bias bf16 [5120];
+ *   pos int64 [1]; inv_freq fp32 [32]; kc, vc bf16 [8, cache_rows, 64]: position pos in row pos, or pos % ring when
+ *   ring > 0 (then cache_rows == ring); a row outside [0, cache_rows) is not written; q bf16 [4096] <- RoPE'd
+ *   query */
+int na_core_qkv(const void* mid, const void* g, const float* c, void* xbuf, const void* in_w, const void* W,
+                const void* bias, const int64_t* pos, const float* inv_freq, void* kc, void* vc, long long cache_rows,
+                int ring, void* q, float eps, float att_scale, hipStream_t stream);
+
+/* mid = bf16(xbuf + bf16(att . Wo^T + bo)).  Replaces fused_core.py:401-414 (k_oproj).
+ *   att bf16 [4096]; Wo bf16 [2880, 4096]; bo, xbuf, mid bf16 [2880] */
+int na_core_oproj(const void* att, const void* Wo, const void* bo, const void* xbuf, void* mid, hipStream_t stream);
+
+/* Post-attention RMSNorm + router GEMV + top-4 + softmax, one launch.  Replaces fused_core.py:417-441 (k_router) and
+ * :460-502 (k_topk, without the host residency lookup: every expert is resident).
+ *   mid bf16 [2880]; post_w bf16 [2880]; Wr bf16 [128, 2880]; br bf16 [128]; hn bf16 [2880] <- normed mid
+ *   logits fp32 [128] scratch; counter uint32 [1], zero before the first call (every completed call leaves it zero)
+ *   ids int64 [4], wts bf16 [4] <- top-4 by repeated argmax (lowest index on ties), bf16(exp(v - v0) / sum) */
+int na_core_router(const void* mid, const void* post_w, float eps, const void* Wr, const void* br, void* hn,
+                   float* logits, unsigned int* counter, int64_t* ids, void* wts, hipStream_t stream);
+
+/* Workgroup partials na_core_lm_tail needs for a vocabulary (-1 if vocab <= 0). */
+long long na_core_lm_partials(int vocab);
+
+/* Decode tail: residual combine + final RMSNorm, lm_head GEMV, argmax (first index of the maximum).  Replaces
+ * server.py:521-525 (t_body).
+ *   mid, g, c as na_core_qkv; final_w bf16 [2880]; Wl bf16 [vocab, 2880]; hn bf16 [2880] scratch;
+ *   logits_out bf16 [vocab] or NULL; part uint64 [na_core_lm_partials(vocab)] scratch; tok int64 [1] <- argmax
+ *   pos int64 [1] (p = *pos): pred[p + 1] <- tok (pred int64 [seq_len] or NULL); seq[p + 1] <- tok unless
+ *   p + 1 < *n_forced (n_forced int64 [1] or NULL); *pos <- p + 1 when step_pos.  Needs pos for seq/pred/step_pos. */
+int na_core_lm_tail(const void* mid, const void* g, const float* c, const void* final_w, float eps, const void* Wl,
+                    int vocab, void* hn, void* logits_out, unsigned long long* part, int64_t* tok, int64_t* pos,
+                    int step_pos, int64_t* seq, const int64_t* n_forced, int64_t* pred, long long seq_len,
+                    hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,8 +35,15 @@ SIGNATURES = {
     "na_mxfp4_gemm": [VP, I32, I32, VP, I64, VP, I64, I32, VP, I32, VP, I32, VP],
     "na_mxfp4_gemm_grouped": [VP, I64, VP, I64, I32, VP, I32, I32, I32, I32, VP],
     "na_decode_attention": [VP, VP, VP, I64, VP, VP, VP, I32, F32, I32, I32, I32, VP, VP, VP, VP],
+    "na_core_embed": [VP, I64, VP, I64, VP, VP, VP],
+    "na_core_qkv": [VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, I64, I32, VP, F32, F32, VP],
+    "na_core_oproj": [VP, VP, VP, VP, VP, VP],
+    "na_core_router": [VP, VP, F32, VP, VP, VP, VP, VP, VP, VP, VP],
+    "na_core_lm_partials": [I32],
+    "na_core_lm_tail": [VP, VP, VP, VP, F32, VP, I32, VP, VP, VP, VP, VP, I32, VP, VP, VP, I64, VP],
 }
-RESTYPES = {"na_t950_slot_bytes": I64, "na_attn_workspace_floats": I64, "na_moe_prefill_workspace_bytes": I64}
+RESTYPES = {"na_t950_slot_bytes": I64, "na_attn_workspace_floats": I64, "na_moe_prefill_workspace_bytes": I64,
+            "na_core_lm_partials": I64}
 
 ERRORS = {-1: "invalid arguments", -2: "kernel launch failed", -3: "size beyond the kernel's limits"}
 

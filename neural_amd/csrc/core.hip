@@ -1,0 +1,446 @@
+// Dense decode core of GPT-OSS-120B on gfx950 (one token per step): per layer the fused residual + input RMSNorm +
+// QKV GEMV + bias + RoPE + K/V cache write (reference fused_core.py:72-142, k_qkv), o_proj + bias + residual
+// (:401-414, k_oproj), post-attention RMSNorm + router GEMV + top-4 + softmax (:417-502, k_router / k_topk), and the
+// tail: residual + final RMSNorm, lm_head GEMV and argmax (server.py:521-525, t_body); plus the embedding lookup.
+//
+// Rounding points (the reference's): the residual x = bf16(mid + g) (g = the previous layer's expert output); the
+// RMSNorm factor r = rsqrt(sum x^2 / H + eps) in fp32; the normed activation hc = bf16(w * (x * r)); GEMV rows
+// bf16(fp32 dot + bias); RoPE cos/sin = bf16(cos(inv_freq[d] pos) * att_scale), o1 = bf16(bf16(ya cs) - bf16(yb sn)),
+// o2 = bf16(bf16(yb cs) + bf16(ya sn)); o_proj mid = bf16(x + bf16(dot + bo)); router logits bf16(dot + br), top-4 by
+// repeated argmax (lowest index on ties), weights bf16(exp(v_j - v_0) / sum); logits of the tail bf16(dot), argmax
+// = the first index of the maximum.
+//
+// GEMV layout: a workgroup of 256 threads computes 16 weight rows; thread (r = tid / 16, j = tid % 16) streams row
+// r's 16-byte chunks j, j + 16, ... (all issued before the first use) against the normed activation staged in LDS,
+// and the 16 lanes of a row group sum with xor shuffles.
+#include "common.h"
+
+#include <hip/hip_ext.h>
+
+namespace na {
+
+constexpr int kHq = 64 * 64;             // query width (NQ x HD)
+constexpr int kQkvRows = (64 + 2 * 8) * 64;   // 5120
+constexpr int kNE = 128;
+
+// Sum over the 16 lanes of a row group.
+NA_DEVICE float sum16(float v) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// dot of 8 bf16 weights with 8 bf16 activations, fp32 accumulation
+NA_DEVICE float dot8(uint4 w, uint4 x, float a) {
+  a = dot2_bf16(w.x, x.x, a);
+  a = dot2_bf16(w.y, x.y, a);
+  a = dot2_bf16(w.z, x.z, a);
+  return dot2_bf16(w.w, x.w, a);
+}
+
+// One weight row's 16-byte chunks j, j + 16, ... held in registers: issued before the activation is ready so that the
+// weight stream overlaps the normalisation; dot() then sums them against the LDS-staged activation hc and every lane
+// of the 16-lane row group returns the row's total.
+template <int K>
+struct RowChunks {
+  static constexpr int NCH = K / 8, IT = (NCH + 15) / 16;
+  uint4 w[IT];
+  NA_DEVICE void load(const uint16_t* __restrict__ wrow, int j) {
+#pragma unroll
+    for (int i = 0; i < IT; ++i) w[i] = load16<true>(wrow + 8 * min(j + 16 * i, NCH - 1));
+  }
+  NA_DEVICE float dot(const uint16_t* hc, int j) const {
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      const int c = j + 16 * i;
+      if (c < NCH) a = dot8(w[i], *reinterpret_cast<const uint4*>(hc + 8 * c), a);
+    }
+    return sum16(a);
+  }
+};
+
+// Inputs of the residual + RMSNorm stage, loaded first (before a kernel's weight stream, so that waiting for them
+// does not wait for the weights): thread t holds chunks t and t + 256 (8 values each) of mid, of the expert outputs
+// g (bf16) and c (fp32, optional: the experts computed elsewhere, reference fused_core.py:72-79) and of the norm
+// weight.
+struct NormIn {
+  uint4 m[2], g[2], w[2], c[2][2];
+  NA_DEVICE void load(const uint16_t* __restrict__ mid, const uint16_t* __restrict__ gp, const float* __restrict__ cp,
+                      const uint16_t* __restrict__ wp) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int ch = min((int)threadIdx.x + 256 * i, kH / 8 - 1);
+      m[i] = *reinterpret_cast<const uint4*>(mid + 8 * ch);
+      w[i] = *reinterpret_cast<const uint4*>(wp + 8 * ch);
+      // absent inputs read mid's chunk (a valid address) and are replaced by zero at use
+      g[i] = *reinterpret_cast<const uint4*>((gp ? gp : mid) + 8 * ch);
+      const float* cc = cp ? cp + 8 * ch : reinterpret_cast<const float*>(mid);
+      c[i][0] = *reinterpret_cast<const uint4*>(cc);
+      c[i][1] = *reinterpret_cast<const uint4*>(cc + 4);
+    }
+  }
+};
+
+NA_DEVICE float half_at(const uint4& v, int e) {
+  const uint32_t wd = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+  return bf16_to_f32((uint16_t)(wd >> (16 * (e & 1))));
+}
+
+NA_DEVICE float float_at(const uint4 (&v)[2], int e) {
+  const uint4& q = v[e >> 2];
+  const int k = e & 3;
+  return __uint_as_float(k == 0 ? q.x : k == 1 ? q.y : k == 2 ? q.z : q.w);
+}
+
+// x = mid, or bf16(mid + bf16(g + bf16(c))) when g is given; r = rsqrt(sum x^2 / H + eps); hc = bf16(w * (x * r)) into
+// LDS (all H values); workgroup 0 also writes x to xbuf when given.  All 256 threads call it; ends with a barrier.
+NA_DEVICE void norm_finish(const NormIn& in, bool has_g, bool has_c, float eps, uint16_t* hc,
+                           uint16_t* __restrict__ xbuf) {
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  float xv[2][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x = half_at(in.m[i], e);
+      if (has_g) {
+        const float c = has_c ? rb(float_at(in.c[i], e)) : 0.f;
+        x = rb(x + rb(half_at(in.g[i], e) + c));
+      }
+      xv[i][e] = x;
+      if (tid + 256 * i < kH / 8) ss += x * x;
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float var = ((red[0] + red[1]) + (red[2] + red[3])) * (1.0f / kH);
+  const float r = rsqrtf(var + eps);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int ch = tid + 256 * i;
+    if (ch < kH / 8) {
+      uint32_t o[4], xo[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        o[e >> 1] = (uint32_t)f32_to_bf16(half_at(in.w[i], e) * (xv[i][e] * r)) |
+                    ((uint32_t)f32_to_bf16(half_at(in.w[i], e + 1) * (xv[i][e + 1] * r)) << 16);
+        xo[e >> 1] = (uint32_t)f32_to_bf16(xv[i][e]) | ((uint32_t)f32_to_bf16(xv[i][e + 1]) << 16);
+      }
+      *reinterpret_cast<uint4*>(hc + 8 * ch) = make_uint4(o[0], o[1], o[2], o[3]);
+      if (xbuf && blockIdx.x == 0) *reinterpret_cast<uint4*>(xbuf + 8 * ch) = make_uint4(xo[0], xo[1], xo[2], xo[3]);
+    }
+  }
+  __syncthreads();
+}
+
+// A bf16 vector of N values (N / 8 chunks, at most 512) copied to LDS: load() first, store() after the weights.
+template <int N>
+struct VecIn {
+  static constexpr int NCH = N / 8;
+  uint4 v[2];
+  NA_DEVICE void load(const uint16_t* __restrict__ p) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) v[i] = *reinterpret_cast<const uint4*>(p + 8 * min((int)threadIdx.x + 256 * i, NCH - 1));
+  }
+  NA_DEVICE void store(uint16_t* lds) const {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if ((int)threadIdx.x + 256 * i < NCH) *reinterpret_cast<uint4*>(lds + 8 * (threadIdx.x + 256 * i)) = v[i];
+    __syncthreads();
+  }
+};
+
+// mid = embed[tok], tok = seq[*pos] (seq[0] without pos); the position is clamped into [0, seq_len) and the id into
+// [0, vocab) so that bad device state cannot read out of bounds (one workgroup).
+__global__ __launch_bounds__(256) void k_embed(const uint16_t* __restrict__ emb, long long vocab,
+                                               const int64_t* __restrict__ seq, long long seq_len,
+                                               const int64_t* __restrict__ pos, uint16_t* __restrict__ mid) {
+  long long p = pos ? *pos : 0;
+  p = p < 0 ? 0 : p >= seq_len ? seq_len - 1 : p;
+  long long t = seq[p];
+  t = t < 0 ? 0 : t >= vocab ? vocab - 1 : t;
+  for (int ch = threadIdx.x; ch < kH / 8; ch += 256)
+    *reinterpret_cast<uint4*>(mid + 8 * ch) = *reinterpret_cast<const uint4*>(emb + t * kH + 8 * ch);
+}
+
+// QKV: grid 320 = 80 heads x 4; workgroup (head, c) computes the rows of dims d = 8c .. 8c + 7 (row groups 0..7) and
+// of their RoPE partners d + 32 (row groups 8..15) of head `head` (0..63 q, 64..71 k, 72..79 v).
+__global__ __launch_bounds__(256) void k_qkv(const uint16_t* __restrict__ mid, const uint16_t* __restrict__ g,
+                                             const float* __restrict__ cext, uint16_t* __restrict__ xbuf,
+                                             const uint16_t* __restrict__ in_w, const uint16_t* __restrict__ W,
+                                             const uint16_t* __restrict__ bias, const int64_t* __restrict__ pos_p,
+                                             const float* __restrict__ inv_freq, uint16_t* __restrict__ kc,
+                                             uint16_t* __restrict__ vc, long long rows, int ring,
+                                             uint16_t* __restrict__ qout, float eps, float att_scale) {
+  __shared__ __align__(16) uint16_t hc[kH];
+  __shared__ float ys[16];
+  const int tid = threadIdx.x, r = tid >> 4, j = tid & 15;
+  const int head = blockIdx.x >> 2, c = blockIdx.x & 3;
+  const int d = 8 * c + (r & 7);
+  const int row = head * 64 + 32 * (r >> 3) + d;
+  NormIn ni;
+  ni.load(mid, g, cext, in_w);
+  const uint16_t bv = bias[row];
+  __builtin_amdgcn_sched_barrier(0);
+  RowChunks<kH> rw;
+  rw.load(W + (long long)row * kH, j);
+  __builtin_amdgcn_sched_barrier(0);
+  norm_finish(ni, g != nullptr, cext != nullptr, eps, hc, xbuf);
+  const float s = rw.dot(hc, j);
+  if (j == 0) ys[r] = rb(s + bf16_to_f32(bv));
+  __syncthreads();
+  if (tid >= 8 * 16 || j != 0) return;              // row group r < 8 writes dims d and d + 32
+  const long long pos = *pos_p;
+  const float ya = ys[r], yb = ys[r + 8];
+  float o1 = ya, o2 = yb;
+  if (head < 64 + 8) {                               // q and k heads: RoPE
+    const float fr = inv_freq[d] * (float)pos;
+    const float cs = rb(cosf(fr) * att_scale), sn = rb(sinf(fr) * att_scale);
+    o1 = rb(rb(ya * cs) - rb(yb * sn));
+    o2 = rb(rb(yb * cs) + rb(ya * sn));
+  }
+  if (head < 64) {
+    qout[head * 64 + d] = f32_to_bf16(o1);
+    qout[head * 64 + 32 + d] = f32_to_bf16(o2);
+  } else {
+    const long long slot = ring > 0 ? pos % ring : pos;
+    if (slot < 0 || slot >= rows) return;           // a position outside the cache is stored nowhere
+    uint16_t* cache = head < 72 ? kc + (long long)(head - 64) * rows * 64 : vc + (long long)(head - 72) * rows * 64;
+    cache[slot * 64 + d] = f32_to_bf16(o1);
+    cache[slot * 64 + 32 + d] = f32_to_bf16(o2);
+  }
+}
+
+// o_proj + residual: grid 180 (16 rows each): mid[n] = bf16(xbuf[n] + bf16(att . Wo[n] + bo[n])).
+__global__ __launch_bounds__(256) void k_oproj(const uint16_t* __restrict__ att, const uint16_t* __restrict__ Wo,
+                                               const uint16_t* __restrict__ bo, const uint16_t* __restrict__ xbuf,
+                                               uint16_t* __restrict__ mid) {
+  __shared__ __align__(16) uint16_t hc[kHq];
+  const int tid = threadIdx.x, r = tid >> 4, j = tid & 15;
+  const int row = 16 * blockIdx.x + r;
+  VecIn<kHq> a;
+  a.load(att);
+  const uint16_t bv = bo[row], xv = xbuf[row];
+  __builtin_amdgcn_sched_barrier(0);
+  RowChunks<kHq> rw;
+  rw.load(Wo + (long long)row * kHq, j);
+  __builtin_amdgcn_sched_barrier(0);
+  a.store(hc);
+  const float s = rw.dot(hc, j);
+  if (j == 0) mid[row] = f32_to_bf16(bf16_to_f32(xv) + rb(s + bf16_to_f32(bv)));
+}
+
+// post-attention RMSNorm + router + top-4: grid 8 (16 experts each).  Workgroup 0 writes hn (the experts' input);
+// every workgroup publishes its 16 logits (device-coherent stores, then a count); the last one selects the top 4,
+// writes ids / weights and resets the count.
+__global__ __launch_bounds__(256) void k_router_norm(const uint16_t* __restrict__ mid, const uint16_t* __restrict__ post_w,
+                                                     float eps, const uint16_t* __restrict__ Wr,
+                                                     const uint16_t* __restrict__ br, uint16_t* __restrict__ hn,
+                                                     float* __restrict__ logits, uint32_t* __restrict__ counter,
+                                                     int64_t* __restrict__ ids, uint16_t* __restrict__ wts) {
+  __shared__ __align__(16) uint16_t hc[kH];
+  __shared__ uint32_t last;
+  const int tid = threadIdx.x, r = tid >> 4, j = tid & 15;
+  const int e = 16 * blockIdx.x + r;
+  NormIn ni;
+  ni.load(mid, nullptr, nullptr, post_w);
+  const uint16_t bv = br[e];
+  __builtin_amdgcn_sched_barrier(0);
+  RowChunks<kH> rw;
+  rw.load(Wr + (long long)e * kH, j);
+  __builtin_amdgcn_sched_barrier(0);
+  norm_finish(ni, false, false, eps, hc, nullptr);
+  if (blockIdx.x == 0)
+    for (int i = tid; i < kH / 8; i += 256)
+      *reinterpret_cast<uint4*>(hn + 8 * i) = *reinterpret_cast<const uint4*>(hc + 8 * i);
+  const float s = rw.dot(hc, j);
+  if (j == 0) __hip_atomic_store(logits + e, rb(s + bf16_to_f32(bv)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last || tid >= 64) return;
+  const int lane = tid;
+  float v0 = __hip_atomic_load(logits + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float v1 = __hip_atomic_load(logits + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float tv[4];
+  int ti[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {                      // repeated argmax, lowest index on ties
+    float bvv = v0;
+    int bi = lane;
+    if (v1 > bvv) { bvv = v1; bi = lane + 64; }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bvv, off);
+      const int oi = __shfl_xor(bi, off);
+      if (ov > bvv || (ov == bvv && oi < bi)) { bvv = ov; bi = oi; }
+    }
+    tv[k] = bvv;
+    ti[k] = bi;
+    if (bi == lane) v0 = -__builtin_inff();
+    if (bi == lane + 64) v1 = -__builtin_inff();
+  }
+  if (lane < 4) {
+    float ex[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ex[k] = expf(tv[k] - tv[0]);
+    const float sum = ((ex[0] + ex[1]) + ex[2]) + ex[3];
+    const float mine = lane == 0 ? ex[0] : lane == 1 ? ex[1] : lane == 2 ? ex[2] : ex[3];
+    ids[lane] = lane == 0 ? ti[0] : lane == 1 ? ti[1] : lane == 2 ? ti[2] : ti[3];
+    wts[lane] = f32_to_bf16(mine / sum);
+  }
+}
+
+// Tail 1: x = bf16(mid + bf16(g + bf16(c))); hn = bf16(w * (x * r)) (one workgroup).
+__global__ __launch_bounds__(256) void k_final_norm(const uint16_t* __restrict__ mid, const uint16_t* __restrict__ g,
+                                                    const float* __restrict__ cext, const uint16_t* __restrict__ w,
+                                                    float eps, uint16_t* __restrict__ hn) {
+  __shared__ __align__(16) uint16_t hc[kH];
+  NormIn ni;
+  ni.load(mid, g, cext, w);
+  norm_finish(ni, g != nullptr, cext != nullptr, eps, hc, nullptr);
+  for (int i = threadIdx.x; i < kH / 8; i += 256)
+    *reinterpret_cast<uint4*>(hn + 8 * i) = *reinterpret_cast<const uint4*>(hc + 8 * i);
+}
+
+// Monotone map of bf16 bit patterns to unsigned order (-0 equal to +0; NaN patterns above +inf).
+NA_DEVICE uint32_t bf16_order_key(uint16_t b) {
+  if (b == 0x8000) b = 0;
+  return (b & 0x8000) ? (uint32_t)(~b & 0xffff) : (uint32_t)(b | 0x8000);
+}
+
+// Tail 2: logits = bf16(hn . lm_head[v]) for 16 rows per workgroup; the workgroup's best as a 64-bit key
+// (order key of the logit << 32 | ~index: a larger key is a larger logit, then a smaller index) -> part[wg];
+// optionally the logits themselves.
+__global__ __launch_bounds__(256) void k_lmhead(const uint16_t* __restrict__ hn, const uint16_t* __restrict__ Wl,
+                                                int vocab, uint16_t* __restrict__ logits_out,
+                                                uint64_t* __restrict__ part) {
+  __shared__ __align__(16) uint16_t hc[kH];
+  __shared__ uint64_t best[16];
+  const int tid = threadIdx.x, r = tid >> 4, j = tid & 15;
+  const int v = 16 * blockIdx.x + r;
+  VecIn<kH> a;
+  a.load(hn);
+  __builtin_amdgcn_sched_barrier(0);
+  RowChunks<kH> rw;
+  rw.load(Wl + (long long)min(v, vocab - 1) * kH, j);
+  __builtin_amdgcn_sched_barrier(0);
+  a.store(hc);
+  const float s = rw.dot(hc, j);
+  const uint16_t lb = f32_to_bf16(s);
+  if (j == 0) {
+    if (logits_out && v < vocab) logits_out[v] = lb;
+    best[r] = v < vocab ? ((uint64_t)bf16_order_key(lb) << 32) | (uint64_t)(0xffffffffu - (uint32_t)v) : 0ull;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t b = best[0];
+    for (int i = 1; i < 16; ++i) b = best[i] > b ? best[i] : b;
+    part[blockIdx.x] = b;
+  }
+}
+
+// Tail 3: argmax over the workgroup keys -> tok.  With pos (p = *pos, the position of this step's input token):
+// pred[p + 1] = tok when pred is given; seq[p + 1] = tok unless position p + 1 is forced (p + 1 < *n_forced, a prompt
+// token); pos = p + 1 when step_pos.  Writes stay below seq_len.
+__global__ __launch_bounds__(1024) void k_argmax(const uint64_t* __restrict__ part, int n, int64_t* __restrict__ tok,
+                                                 int64_t* __restrict__ pos, int step_pos, int64_t* __restrict__ seq,
+                                                 const int64_t* __restrict__ n_forced, int64_t* __restrict__ pred,
+                                                 long long seq_len) {
+  __shared__ uint64_t red[16];
+  uint64_t b = 0;
+  for (int i = threadIdx.x; i < n; i += 1024) b = part[i] > b ? part[i] : b;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint64_t ob = ((uint64_t)(uint32_t)__shfl_xor((int)(b >> 32), o) << 32) | (uint32_t)__shfl_xor((int)b, o);
+    b = ob > b ? ob : b;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = b;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 16; ++i) b = red[i] > b ? red[i] : b;
+    const int64_t t = (int64_t)(0xffffffffu - (uint32_t)(b & 0xffffffffu));
+    *tok = t;
+    if (pos) {
+      const long long p = *pos, nx = p + 1;
+      if (nx < seq_len && nx >= 0) {
+        if (pred) pred[nx] = t;
+        if (seq && !(n_forced && nx < *n_forced)) seq[nx] = t;
+      }
+      if (step_pos) *pos = nx;
+    }
+  }
+}
+
+}  // namespace na
+
+using namespace na;
+
+extern "C" {
+
+int na_core_embed(const void* emb, long long vocab, const int64_t* seq, long long seq_len, const int64_t* pos,
+                  void* mid, hipStream_t stream) {
+  if (!emb || vocab <= 0 || !seq || seq_len <= 0 || !mid) return kErrArgs;
+  hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, stream, (const uint16_t*)emb, vocab, seq, seq_len, pos,
+                     (uint16_t*)mid);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int na_core_qkv(const void* mid, const void* g, const float* c, void* xbuf, const void* in_w, const void* W,
+                const void* bias, const int64_t* pos, const float* inv_freq, void* kc, void* vc, long long cache_rows,
+                int ring, void* q, float eps, float att_scale, hipStream_t stream) {
+  if (!mid || !xbuf || !in_w || !W || !bias || !pos || !inv_freq || !kc || !vc || !q || cache_rows <= 0 || ring < 0)
+    return kErrArgs;
+  if (c && !g) return kErrArgs;
+  if (ring > 0 && cache_rows != ring) return kErrArgs;
+  hipLaunchKernelGGL(k_qkv, dim3(kQkvRows / 16), dim3(256), 0, stream, (const uint16_t*)mid, (const uint16_t*)g, c,
+                     (uint16_t*)xbuf, (const uint16_t*)in_w, (const uint16_t*)W, (const uint16_t*)bias, pos, inv_freq,
+                     (uint16_t*)kc, (uint16_t*)vc, cache_rows, ring, (uint16_t*)q, eps, att_scale);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int na_core_oproj(const void* att, const void* Wo, const void* bo, const void* xbuf, void* mid, hipStream_t stream) {
+  if (!att || !Wo || !bo || !xbuf || !mid) return kErrArgs;
+  hipLaunchKernelGGL(k_oproj, dim3(kH / 16), dim3(256), 0, stream, (const uint16_t*)att, (const uint16_t*)Wo,
+                     (const uint16_t*)bo, (const uint16_t*)xbuf, (uint16_t*)mid);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int na_core_router(const void* mid, const void* post_w, float eps, const void* Wr, const void* br, void* hn,
+                   float* logits, unsigned int* counter, int64_t* ids, void* wts, hipStream_t stream) {
+  if (!mid || !post_w || !Wr || !br || !hn || !logits || !counter || !ids || !wts) return kErrArgs;
+  hipLaunchKernelGGL(k_router_norm, dim3(kNE / 16), dim3(256), 0, stream, (const uint16_t*)mid,
+                     (const uint16_t*)post_w, eps, (const uint16_t*)Wr, (const uint16_t*)br, (uint16_t*)hn, logits,
+                     (uint32_t*)counter, ids, (uint16_t*)wts);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+long long na_core_lm_partials(int vocab) { return vocab > 0 ? (vocab + 15) / 16 : -1; }
+
+int na_core_lm_tail(const void* mid, const void* g, const float* c, const void* final_w, float eps, const void* Wl,
+                    int vocab, void* hn, void* logits_out, unsigned long long* part, int64_t* tok, int64_t* pos,
+                    int step_pos, int64_t* seq, const int64_t* n_forced, int64_t* pred, long long seq_len,
+                    hipStream_t stream) {
+  if (!mid || !final_w || !Wl || vocab <= 0 || !hn || !part || !tok) return kErrArgs;
+  if ((step_pos || seq || pred) && !pos) return kErrArgs;
+  if ((seq || pred) && seq_len <= 0) return kErrArgs;
+  if (c && !g) return kErrArgs;
+  const int nwg = (vocab + 15) / 16;
+  hipLaunchKernelGGL(k_final_norm, dim3(1), dim3(256), 0, stream, (const uint16_t*)mid, (const uint16_t*)g, c,
+                     (const uint16_t*)final_w, eps, (uint16_t*)hn);
+  hipLaunchKernelGGL(k_lmhead, dim3(nwg), dim3(256), 0, stream, (const uint16_t*)hn, (const uint16_t*)Wl, vocab,
+                     (uint16_t*)logits_out, (uint64_t*)part);
+  hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, stream, (const uint64_t*)part, nwg, tok, pos, step_pos, seq,
+                     n_forced, pred, seq_len);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // extern "C"

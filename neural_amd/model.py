@@ -1,0 +1,283 @@
+"""GPT-OSS-120B single-sequence greedy decode on one MI355X: the per-token decode loop of the reference server
+(server.py:453-545: embed -> 36 x [core layer, expert body] -> tail), with every launch a HIP kernel of this package
+and the whole step capturable in one hipGraph.
+
+Per layer (reference fused_core.py:581-629, FusedCore.run, plus the expert body server.py:508-518):
+    na_core_qkv        residual combine + input RMSNorm + Q|K|V GEMV + bias + YaRN RoPE + K/V cache write
+    na_decode_attention   GQA sink attention (sliding layers: 128-key window over a rolling cache)
+    na_core_oproj      o_proj + bias + residual -> mid
+    na_core_router     post RMSNorm -> hn, router GEMV + top-4 + softmax -> ids / weights
+    ResidentExperts    gate_up + bias + clamped SwiGLU, down + bias + weight, top-4 combine -> g
+and the tail (server.py:521-525): combine + final RMSNorm + lm_head + argmax, which also advances the position and
+appends the token to the device-side sequence.  The input token of each step is read on the device from that
+sequence at the current position, so replaying a captured step graph runs greedy decode with no host involvement;
+positions below ``n_forced`` keep their preset tokens (a prompt read token by token, or a teacher-forced sequence).
+
+Shapes (reference neural/moe/layout.py and the model config): hidden 2880, 64 query / 8 KV heads of 64, q|k|v rows
+5120, o_proj [2880, 4096], router [128, 2880], vocab 201088, RMSNorm eps 1e-5, layers alternate sliding (even, window
+128) and full attention, YaRN RoPE (theta 150000, factor 32, beta_fast 32, beta_slow 1, original context 4096).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _native as N
+from .moe.experts import ResidentExperts
+
+H, NQ, NKV, HD, NE, TOP_K = 2880, 64, 8, 64, 128, 4
+HQ = NQ * HD                      # 4096
+QKV_ROWS = (NQ + 2 * NKV) * HD    # 5120
+N_LAYERS, VOCAB, EPS, WINDOW = 36, 201088, 1e-5, 128
+ROPE_THETA = 150000.0
+YARN = dict(factor=32.0, beta_fast=32.0, beta_slow=1.0, original_max_position_embeddings=4096, truncate=False)
+
+
+def yarn_inv_freq(head_dim: int = HD, theta: float = ROPE_THETA, factor: float = 32.0, beta_fast: float = 32.0,
+                  beta_slow: float = 1.0, original_max_position_embeddings: int = 4096, truncate: bool = False):
+    """YaRN rotary frequencies (Peng et al. 2023, "YaRN: Efficient Context Window Extension of Large Language Models",
+    sections 3.2-3.4) as the model's rotary embedding computes them in fp32: dimension pair i has the base frequency
+    theta^(-2i/d); pairs that complete fewer than beta_slow rotations over the original context are interpolated
+    (frequency / factor), pairs that complete more than beta_fast keep it, with a linear ramp over the pair index in
+    between.  Returns (inv_freq fp32 [head_dim / 2] on the CPU, attention factor 0.1 ln(factor) + 1 that scales cos and
+    sin).  The reference reads the same table from the checkpoint's rotary module (gptoss_core_graphs.py:126-127)."""
+    d = head_dim
+
+    def corr_dim(n_rot):               # pair index at which a pair makes n_rot full turns over the original context
+        return (d * math.log(original_max_position_embeddings / (n_rot * 2 * math.pi))) / (2 * math.log(theta))
+
+    lo, hi = corr_dim(beta_fast), corr_dim(beta_slow)
+    if truncate:
+        lo, hi = math.floor(lo), math.ceil(hi)
+    lo, hi = max(lo, 0), min(hi, d - 1)
+    if lo == hi:
+        hi += 0.001
+    pos_freqs = theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d)
+    extrap = 1.0 / pos_freqs
+    interp = 1.0 / (factor * pos_freqs)
+    ramp = torch.clamp((torch.arange(d // 2, dtype=torch.float32) - lo) / (hi - lo), 0, 1)
+    keep = 1 - ramp                    # 1: keep the base frequency, 0: interpolate
+    inv_freq = interp * (1 - keep) + extrap * keep
+    return inv_freq, 0.1 * math.log(factor) + 1.0
+
+
+@dataclass
+class LayerWeights:
+    in_w: torch.Tensor        # [2880] input RMSNorm
+    Wqkv: torch.Tensor        # [5120, 2880]  q | k | v rows
+    bqkv: torch.Tensor        # [5120]
+    Wo: torch.Tensor          # [2880, 4096]
+    bo: torch.Tensor          # [2880]
+    sinks: torch.Tensor       # [64]
+    post_w: torch.Tensor      # [2880] post-attention RMSNorm
+    Wr: torch.Tensor          # [128, 2880] router
+    br: torch.Tensor          # [128]
+    sliding: int              # window (0: full attention)
+
+    def to(self, dev):
+        kw = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in self.__dict__.items()}
+        return LayerWeights(**kw)
+
+
+@dataclass
+class DecodeWeights:
+    embed: torch.Tensor       # [vocab, 2880]
+    layers: list = field(default_factory=list)
+    final_w: torch.Tensor = None
+    lm_head: torch.Tensor = None  # [vocab, 2880]
+
+    @property
+    def vocab(self) -> int:
+        return self.embed.shape[0]
+
+    def to(self, dev):
+        return DecodeWeights(self.embed.to(dev), [ly.to(dev) for ly in self.layers], self.final_w.to(dev),
+                             self.lm_head.to(dev))
+
+
+def random_weights(n_layers: int = N_LAYERS, vocab: int = VOCAB, device="cpu", seed: int = 0, std: float = 0.02,
+                   bias_std: float = 0.02, norm_std: float = 0.02, sink_std: float = 1.0,
+                   window: int = WINDOW) -> DecodeWeights:
+    """Random-init weights of the model's shapes, bf16: matrices and embeddings N(0, std), biases N(0, bias_std), norm
+    weights 1 + N(0, norm_std), sinks N(0, sink_std).  Layer L is a sliding-window layer when L is even.  Drawn with a
+    torch generator on ``device`` (a function of the seed on a given device type)."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    bf = torch.bfloat16
+
+    def rn(*shape, s=std, mean=0.0):
+        t = torch.randn(*shape, generator=g, device=device, dtype=torch.float32)
+        return (t * s + mean).to(bf)
+
+    layers = []
+    for li in range(n_layers):
+        layers.append(LayerWeights(
+            in_w=rn(H, s=norm_std, mean=1.0), Wqkv=rn(QKV_ROWS, H), bqkv=rn(QKV_ROWS, s=bias_std),
+            Wo=rn(H, HQ), bo=rn(H, s=bias_std), sinks=rn(NQ, s=sink_std), post_w=rn(H, s=norm_std, mean=1.0),
+            Wr=rn(NE, H), br=rn(NE, s=bias_std), sliding=window if li % 2 == 0 else 0))
+    return DecodeWeights(rn(vocab, H), layers, rn(H, s=norm_std, mean=1.0), rn(vocab, H))
+
+
+class DecodeModel:
+    """Greedy single-sequence decode over ``weights`` (a DecodeWeights on the device) and ``experts`` (a
+    ResidentExperts over the same number of layers or more).
+
+    smax:       positions the full-attention K/V caches hold (the sequence buffer holds smax tokens)
+    n_split:    key chunks of full-attention layers (1..64); sliding layers use ``sliding_split``
+    ring:       rows of a sliding layer's rolling K/V cache (>= its window; 0: linear caches of smax rows)
+
+    The step reads its input token from ``seq[pos]`` and writes the argmax to ``pred[pos + 1]`` and, unless
+    ``pos + 1 < n_forced``, to ``seq[pos + 1]``; it then advances ``pos``.  All of that state lives on the device."""
+
+    def __init__(self, weights: DecodeWeights, experts: ResidentExperts, smax: int, n_split: int = 32,
+                 sliding_split: int = 1, ring: int | None = None, keep_logits: bool = False):
+        dev = weights.embed.device
+        if dev.type != "cuda":
+            raise ValueError("weights must be on a CUDA device")
+        self.w, self.rx, self.dev = weights, experts, dev
+        self.n_layers = len(weights.layers)
+        if self.n_layers > experts.layout.n_layers:
+            raise ValueError("the expert pool holds fewer layers than the model")
+        self._check_weights()
+        self.smax = int(smax)
+        self.n_split, self.sliding_split = int(n_split), int(sliding_split)
+        windows = {ly.sliding for ly in weights.layers if ly.sliding}
+        self.ring = (max(windows) if windows else 0) if ring is None else int(ring)
+        for win in windows:
+            if self.ring and self.ring < win:
+                raise ValueError(f"ring {self.ring} is smaller than a sliding window {win}")
+        bf = torch.bfloat16
+        z = lambda *s, dt=bf: torch.zeros(*s, dtype=dt, device=dev)  # noqa: E731
+        self.kc, self.vc = [], []
+        for ly in weights.layers:
+            rows = self.ring if (ly.sliding and self.ring) else self.smax
+            self.kc.append(z(1, NKV, rows, HD))
+            self.vc.append(z(1, NKV, rows, HD))
+        inv, self.att_scale = yarn_inv_freq()
+        self.inv_freq = inv.to(dev)
+        self.scaling = HD ** -0.5
+        self.seq = z(self.smax, dt=torch.int64)
+        self.pred = z(self.smax, dt=torch.int64)
+        self.pos = z(1, dt=torch.int64)
+        self.n_forced = z(1, dt=torch.int64)
+        self.tok = z(1, dt=torch.int64)
+        self.mid, self.xbuf, self.hn, self.g = z(1, H), z(1, H), z(1, H), z(1, H)
+        self.q, self.att = z(HQ), z(HQ)
+        self.r_logits = z(NE, dt=torch.float32)
+        self.r_counter = z(1, dt=torch.int32)
+        self.ids = z(1, TOP_K, dt=torch.int64)
+        self.wts = z(1, TOP_K)
+        self.part = z(N.lib().na_core_lm_partials(weights.vocab), dt=torch.int64)
+        self.logits = z(weights.vocab) if keep_logits else None
+        ns_max = max(self.n_split, self.sliding_split)
+        if not 1 <= self.n_split <= 64 or not 1 <= self.sliding_split <= 64:
+            raise ValueError("n_split and sliding_split must be in [1, 64]")
+        self.attn_work = z(max(N.lib().na_attn_workspace_floats(1, ns_max), 1), dt=torch.float32)
+        self.attn_counters = z(NKV, dt=torch.int32)
+        self.graph = None
+
+    def _check_weights(self):
+        w = self.w
+        shapes = dict(in_w=(H,), Wqkv=(QKV_ROWS, H), bqkv=(QKV_ROWS,), Wo=(H, HQ), bo=(H,), sinks=(NQ,), post_w=(H,),
+                      Wr=(NE, H), br=(NE,))
+        for li, ly in enumerate(w.layers):
+            for nm, shp in shapes.items():
+                t = getattr(ly, nm)
+                if t.dtype is not torch.bfloat16 or tuple(t.shape) != shp or not t.is_contiguous() \
+                        or t.device != self.dev:
+                    raise ValueError(f"layer {li} {nm} must be contiguous bf16 {shp} on {self.dev}")
+        for nm, shp in (("embed", (w.vocab, H)), ("lm_head", (w.vocab, H)), ("final_w", (H,))):
+            t = getattr(w, nm)
+            if t.dtype is not torch.bfloat16 or tuple(t.shape) != shp or not t.is_contiguous() or t.device != self.dev:
+                raise ValueError(f"{nm} must be contiguous bf16 {shp} on {self.dev}")
+
+    # ------------------------------------------------------------------------------------------------ host state
+    def reset(self, tokens, n_forced: int | None = None, pos: int = 0) -> None:
+        """Load a token sequence (its first ``n_forced`` tokens are kept, default all of them), zero the K/V caches
+        and set the position.  Synchronous host -> device copies; not for use under capture."""
+        t = torch.as_tensor(tokens, dtype=torch.int64).reshape(-1)
+        if t.numel() > self.smax:
+            raise ValueError(f"{t.numel()} tokens exceed smax {self.smax}")
+        if t.numel() and (int(t.min()) < 0 or int(t.max()) >= self.w.vocab):
+            raise ValueError("token ids outside the vocabulary")
+        self.seq.zero_()
+        self.seq[:t.numel()] = t.to(self.dev)
+        self.pred.fill_(-1)
+        self.n_forced.fill_(t.numel() if n_forced is None else int(n_forced))
+        self.pos.fill_(int(pos))
+        for c in self.kc + self.vc:
+            c.zero_()
+
+    # ------------------------------------------------------------------------------------------------ launches
+    def layer(self, li: int) -> None:
+        """One layer's launches on the current stream (no host synchronisation, capturable)."""
+        ly = self.w.layers[li]
+        s = N.stream(self.dev)
+        kc, vc = self.kc[li], self.vc[li]
+        ring = self.ring if ly.sliding else 0
+        rows = kc.shape[2]
+        N.call("na_core_qkv", self.mid.data_ptr(), self.g.data_ptr() if li else None, None, self.xbuf.data_ptr(),
+               ly.in_w.data_ptr(), ly.Wqkv.data_ptr(), ly.bqkv.data_ptr(), self.pos.data_ptr(),
+               self.inv_freq.data_ptr(), kc.data_ptr(), vc.data_ptr(), rows, ring, self.q.data_ptr(), EPS,
+               float(self.att_scale), s)
+        ns = self.sliding_split if ly.sliding else self.n_split
+        N.call("na_decode_attention", self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), rows, ly.sinks.data_ptr(),
+               self.pos.data_ptr(), self.att.data_ptr(), 1, float(self.scaling), int(ly.sliding), ring, ns,
+               self.attn_work.data_ptr(), self.attn_counters.data_ptr(), None, s)
+        N.call("na_core_oproj", self.att.data_ptr(), ly.Wo.data_ptr(), ly.bo.data_ptr(), self.xbuf.data_ptr(),
+               self.mid.data_ptr(), s)
+        N.call("na_core_router", self.mid.data_ptr(), ly.post_w.data_ptr(), EPS, ly.Wr.data_ptr(), ly.br.data_ptr(),
+               self.hn.data_ptr(), self.r_logits.data_ptr(), self.r_counter.data_ptr(), self.ids.data_ptr(),
+               self.wts.data_ptr(), s)
+        self.rx.forward_decode(li, self.hn, self.ids, self.wts, out=self.g)
+
+    def embed(self) -> None:
+        N.call("na_core_embed", self.w.embed.data_ptr(), self.w.vocab, self.seq.data_ptr(), self.smax,
+               self.pos.data_ptr(), self.mid.data_ptr(), N.stream(self.dev))
+
+    def tail(self, step_pos: bool = True) -> None:
+        N.call("na_core_lm_tail", self.mid.data_ptr(), self.g.data_ptr() if self.n_layers else None, None,
+               self.w.final_w.data_ptr(), EPS, self.w.lm_head.data_ptr(), self.w.vocab, self.hn.data_ptr(),
+               N.ptr(self.logits), self.part.data_ptr(), self.tok.data_ptr(), self.pos.data_ptr(), int(step_pos),
+               self.seq.data_ptr(), self.n_forced.data_ptr(), self.pred.data_ptr(), self.smax, N.stream(self.dev))
+
+    def step(self) -> None:
+        """One decode step (embed, every layer, tail) on the current stream."""
+        self.embed()
+        for li in range(self.n_layers):
+            self.layer(li)
+        self.tail()
+
+    # ------------------------------------------------------------------------------------------------ graphs
+    def capture(self) -> torch.cuda.CUDAGraph:
+        """Capture one step as a hipGraph (replay = one greedy step at the device-side position).  The capture itself
+        runs nothing; state is untouched."""
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step()
+        self.graph = g
+        return g
+
+    def run(self, n_steps: int, graph: bool = True) -> None:
+        """n_steps decode steps from the current device state (graph replays when a graph was captured)."""
+        if graph:
+            if self.graph is None:
+                self.capture()
+            for _ in range(n_steps):
+                self.graph.replay()
+        else:
+            for _ in range(n_steps):
+                self.step()
+
+    def generate(self, prompt, n_new: int, graph: bool = True):
+        """Greedy decode: read the prompt token by token (its K/V written by decode steps), then ``n_new`` new
+        tokens.  Returns the full sequence (prompt + new tokens) as a CPU int64 tensor."""
+        p = torch.as_tensor(prompt, dtype=torch.int64).reshape(-1)
+        if p.numel() < 1 or p.numel() + n_new > self.smax:
+            raise ValueError("prompt must be non-empty and prompt + n_new must fit smax")
+        self.reset(p)
+        self.run(p.numel() - 1 + n_new, graph)
+        torch.cuda.synchronize(self.dev)
+        return self.seq[:p.numel() + n_new].cpu()

@@ -1,0 +1,181 @@
+"""GPT-OSS decode step restated on the CPU in numpy (test infrastructure; see oracle/__init__.py).
+
+The eager decode core of the reference (neural/moe/gptoss_core_graphs.py:55-109, an op-for-op copy of transformers'
+gpt-oss forward in bf16) with its fused twin's residual combine (fused_core.py:72-79), the expert body (server.py:
+508-518, through mxfp4_oracle) and the decode tail (server.py:521-525).  Every bf16 rounding point is reproduced;
+dot products are summed in fp64 and rounded once (the reference's fp32 summation order is not reproducible).
+
+Weights are passed as numpy arrays of bf16 values held in fp32 (the dense matrices are widened to fp64 once).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .attention_oracle import attn_bf16
+from .bf16 import rb
+from .mxfp4_oracle import combine_bf16, expert_forward_bf16, expert_weights, router_logits_bf16, router_top4
+
+H, NQ, NKV, HD, NE = 2880, 64, 8, 64, 128
+HQ = NQ * HD
+
+
+def rms_bf16(x, w, eps):
+    """RMSNorm at the reference's rounding points (gptoss_core_graphs.py:48-53; fused_core.py:95-109):
+    r = rsqrt(mean(x^2) + eps) in fp32, out = bf16(w * (x * r)).  x, w: bf16 values."""
+    x = np.asarray(x, np.float32)
+    var = np.float32(np.sum(x.astype(np.float64) ** 2) / x.shape[-1])
+    r = np.float32(1.0 / np.sqrt(np.float64(var + np.float32(eps))))
+    return rb(np.asarray(w, np.float32) * (x * r))
+
+
+def linear_bf16(x, W64, b=None):
+    """F.linear in bf16: bf16(x . W^T (+ b)), one rounding (fp64 sum here)."""
+    y = np.asarray(W64 @ np.asarray(x, np.float64))
+    if b is not None:
+        y = y + np.asarray(b, np.float64)
+    return rb(y.astype(np.float32))
+
+
+def rope_tables(pos: int, inv_freq, att_scale):
+    """cos/sin of one position (gptoss_core_graphs.py:68-73): freqs = inv_freq * pos in fp32; bf16(cos(f) * s),
+    bf16(sin(f) * s)."""
+    f = (np.asarray(inv_freq, np.float32) * np.float32(pos)).astype(np.float32)
+    cs = rb((np.cos(f.astype(np.float64)).astype(np.float32) * np.float32(att_scale)).astype(np.float32))
+    sn = rb((np.sin(f.astype(np.float64)).astype(np.float32) * np.float32(att_scale)).astype(np.float32))
+    return cs, sn
+
+
+def rope_bf16(y, cs, sn):
+    """Rotate-half RoPE in bf16 ops (gptoss_core_graphs.py:74-77): [y1 cs - y2 sn, y2 cs + y1 sn] with every product
+    and sum rounded.  y [..., 64]."""
+    y = np.asarray(y, np.float32)
+    y1, y2 = y[..., :HD // 2], y[..., HD // 2:]
+    return np.concatenate([rb(rb(y1 * cs) - rb(y2 * sn)), rb(rb(y2 * cs) + rb(y1 * sn))], axis=-1)
+
+
+def residual(mid, g=None, c=None):
+    """x = mid, or bf16(mid + bf16(g + bf16(c))) (fused_core.py:72-79; server.py:522 for the tail)."""
+    mid = np.asarray(mid, np.float32)
+    if g is None:
+        return mid
+    cc = rb(np.asarray(c, np.float32)) if c is not None else np.float32(0.0)
+    return rb(mid + rb(np.asarray(g, np.float32) + cc))
+
+
+class DecodeOracle:
+    """Greedy decode of one sequence.  ``layers``: list of dicts with bf16-valued numpy arrays in_w, Wqkv, bqkv, Wo,
+    bo, sinks, post_w, Wr, br and int ``sliding``; ``experts(li, e)`` -> (raw slot bytes, bias_gu, bias_dn) of expert
+    e of layer li.  K/V caches are linear (position j in row j)."""
+
+    def __init__(self, embed, layers, final_w, lm_head, experts, inv_freq, att_scale, eps=1e-5, smax=256):
+        f32 = lambda a: np.asarray(a, np.float32)  # noqa: E731
+        self.embed = f32(embed)
+        self.layers = []
+        for ly in layers:
+            d = {k: f32(ly[k]) for k in ("in_w", "bqkv", "bo", "sinks", "post_w", "br")}
+            d["Wqkv"] = np.asarray(ly["Wqkv"], np.float64)
+            d["Wo"] = np.asarray(ly["Wo"], np.float64)
+            d["Wr"] = f32(ly["Wr"])
+            d["sliding"] = int(ly["sliding"])
+            self.layers.append(d)
+        self.final_w = f32(final_w)
+        self.lm_head = np.asarray(lm_head, np.float64)
+        self.experts = experts
+        self.inv_freq, self.att_scale, self.eps = f32(inv_freq), float(att_scale), float(eps)
+        self.kc = [np.zeros((NKV, smax, HD), np.float32) for _ in layers]
+        self.vc = [np.zeros((NKV, smax, HD), np.float32) for _ in layers]
+        self._wcache = {}
+
+    def _expert(self, li, e):
+        slot, bgu, bdn = self.experts(li, e)
+        key = id(slot)
+        w = self._wcache.get(key)
+        if w is None:
+            wg, wd = expert_weights(slot)
+            w = (np.asarray(wg, np.float64), np.asarray(wd, np.float64))
+            self._wcache[key] = w
+        return w, bgu, bdn
+
+    # -- the stages of one layer (each restates one kernel of the reference's fused core)
+    def qkv(self, li, x, pos):
+        """Input RMSNorm + Q|K|V + bias + RoPE (fused_core.py:82-142): returns q [4096], k [512], v [512]."""
+        ly = self.layers[li]
+        h = rms_bf16(x, ly["in_w"], self.eps)
+        y = linear_bf16(h, ly["Wqkv"], ly["bqkv"])
+        q = y[:HQ].reshape(NQ, HD)
+        k = y[HQ:HQ + NKV * HD].reshape(NKV, HD)
+        v = y[HQ + NKV * HD:].reshape(NKV, HD)
+        cs, sn = rope_tables(pos, self.inv_freq, self.att_scale)
+        return rope_bf16(q, cs, sn).reshape(-1), rope_bf16(k, cs, sn).reshape(-1), v.reshape(-1)
+
+    def attend(self, li, q, k, v, pos):
+        """Store K/V at pos, then sink attention over the layer's key range (fused_core.py:145-208)."""
+        ly = self.layers[li]
+        self.kc[li][:, pos] = np.asarray(k, np.float32).reshape(NKV, HD)
+        self.vc[li][:, pos] = np.asarray(v, np.float32).reshape(NKV, HD)
+        return attn_bf16(q, self.kc[li], self.vc[li], ly["sinks"], pos, HD ** -0.5, ly["sliding"])
+
+    def oproj(self, li, att, x):
+        """mid = bf16(x + bf16(att . Wo^T + bo)) (fused_core.py:401-414)."""
+        ly = self.layers[li]
+        return rb(np.asarray(x, np.float32) + linear_bf16(att, ly["Wo"], ly["bo"]))
+
+    def route(self, li, mid):
+        """Post-attention RMSNorm, router logits, top-4 and their softmax (fused_core.py:417-502)."""
+        ly = self.layers[li]
+        hn = rms_bf16(mid, ly["post_w"], self.eps)
+        logits = router_logits_bf16(hn, ly["Wr"], ly["br"])[0]
+        ids, wts = router_top4(logits)
+        return hn, logits, ids, wts
+
+    def moe(self, li, hn, ids, wts):
+        """Expert body of one token: the top-4 experts and their weighted sum (server.py:508-518)."""
+        ys = []
+        for e in ids:
+            (wg, wd), bgu, bdn = self._expert(li, int(e))
+            ys.append(expert_forward_bf16(hn, None, bgu, bdn, weights=(wg, wd))[0])
+        return combine_bf16(np.stack(ys), wts)
+
+    def layer(self, li, mid, g, pos, trace=None):
+        """One layer at position pos: returns (mid, g) for the next layer.  trace: optional dict filled with the
+        layer's intermediates (x, q, k, v, att, mid, hn, logits, ids, wts, g)."""
+        x = residual(mid, g)
+        q, k, v = self.qkv(li, x, pos)
+        att = self.attend(li, q, k, v, pos)
+        mid = self.oproj(li, att, x)
+        hn, logits, ids, wts = self.route(li, mid)
+        gout = self.moe(li, hn, ids, wts)
+        if trace is not None:
+            trace.update(x=x, q=q, k=k, v=v, att=att, mid=mid, hn=hn, logits=logits, ids=ids, wts=wts, g=gout)
+        return mid, gout
+
+    def tail(self, mid, g):
+        """Final norm + lm_head: bf16 logits [vocab] (server.py:521-525)."""
+        h = residual(mid, g)
+        hn = rms_bf16(h, self.final_w, self.eps)
+        return linear_bf16(hn, self.lm_head)
+
+    def step(self, tok, pos, trace=None):
+        """One decode step: token tok at position pos -> bf16 logits of the next token."""
+        mid = rb(self.embed[int(tok)])
+        g = None
+        for li in range(len(self.layers)):
+            t = {} if trace is not None else None
+            mid, g = self.layer(li, mid, g, pos, t)
+            if trace is not None:
+                trace.append(t)
+        return self.tail(mid, g)
+
+
+def argmax_first(logits) -> int:
+    """First index of the maximum (torch.argmax's documented tie rule; server.py:525)."""
+    return int(np.argmax(np.asarray(logits, np.float32)))
+
+
+def near_tie(logits, a: int, b: int, ulps: float = 2.0) -> bool:
+    """Whether tokens a and b are within ``ulps`` bf16 units (at the larger logit's magnitude) of each other: the rule
+    for accepting a different greedy choice between two implementations whose fp32 sums differ in order."""
+    la, lb = float(logits[a]), float(logits[b])
+    m = max(abs(la), abs(lb), 1e-30)
+    ulp = 2.0 ** (np.floor(np.log2(m)) - 7)
+    return abs(la - lb) <= ulps * ulp
