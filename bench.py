@@ -242,6 +242,140 @@ def bench_prefill(A):
     print(json.dumps(res), flush=True)
 
 
+def build_t950_pool(dev, seed):
+    """All 36 x 128 experts resident in the t950 layout: raw store slots (uniform E2M1 code bytes, E8M0 exponents
+    uniform in [119, 125]) generated on the device 128 at a time and repacked, the way a store is loaded."""
+    import torch
+
+    from neural_amd import synth, tiles
+    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_T950
+
+    n_slots = N_LAYERS * N_EXPERTS
+    pool = torch.empty((n_slots, GPTOSS_LAYOUT_T950.slot_bytes), dtype=torch.uint8, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    chunk = torch.empty((N_EXPERTS, GPTOSS_LAYOUT.slot_bytes), dtype=torch.uint8, device=dev)
+    cb = synth.CODE_BYTES
+    for c0 in range(0, n_slots, N_EXPERTS):
+        chunk[:, :cb].random_(0, 256, generator=g)
+        chunk[:, cb:].random_(synth.SCALE_LO, synth.SCALE_HI + 1, generator=g)
+        tiles.repack_to_t950(chunk, pool[c0:c0 + N_EXPERTS])
+    torch.cuda.synchronize()
+    del chunk
+    return pool
+
+
+def bench_model(A):
+    """Configuration 4: full 36-layer GPT-OSS-120B-shaped greedy decode on one GPU.  Random-init weights (attention,
+    router, embedding and lm_head bf16 N(0, 0.02), norms 1 + N(0, 0.02), sinks N(0, 1), vocab 201088), all 36 x 128
+    MXFP4 experts resident (t950 layout, 61.2 GB), a context of 4096 random token ids read through the decode step
+    (its K/V written by the same kernels), then greedy decode with one hipGraph per step (embed, 36 x [QKV + RoPE +
+    cache write, attention, o_proj, router + top-4, experts], final norm + lm_head + argmax; the next step reads its
+    token on the device).  Timed: exactly --steps greedy steps from the end of the context; the warm-up steps run
+    from the same context snapshot and are rolled back.  value = tokens / s.  The roofline is the expert gate_up
+    kernel's (the step's largest share), from dispatch-timestamped events over one eager step."""
+    import torch
+
+    from neural_amd.model import DecodeModel, random_weights
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
+
+    dev = torch.device("cuda", 0)
+    ctx, n_new = A.context, A.steps
+    log(f"model: building the expert pool ({N_LAYERS * N_EXPERTS} slots, t950)")
+    pool = build_t950_pool(dev, 4242)
+    L = GPTOSS_LAYOUT_T950
+    rx = ResidentExperts(pool, L, None, None, max_batch=1, k_split=A.k_split, combine_in_down=A.down == "combine")
+    log("model: random-init dense weights")
+    w = random_weights(device=dev, seed=77)
+    smax = ctx + max(n_new, A.warmup) + 1
+    model = DecodeModel(w, rx, smax=smax, n_split=A.attn_split, sliding_split=A.sliding_split)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(4096)
+    prompt = rng.integers(0, w.vocab, ctx)
+    model.reset(prompt)
+    model.capture()
+    t0 = time.perf_counter()
+    model.run(ctx - 1)                                   # the context, token by token (graph replays)
+    torch.cuda.synchronize()
+    t_ctx = time.perf_counter() - t0
+    log(f"model: context of {ctx} tokens read in {t_ctx:.2f} s ({(ctx - 1) / t_ctx:.0f} steps/s)")
+    model.n_forced.fill_(ctx)
+    snap = model.snapshot()
+    model.run(A.warmup)
+    torch.cuda.synchronize()
+    model.restore(snap)
+    torch.cuda.synchronize()
+    # ------------------------------------------------------------------ timed region
+    t0 = time.perf_counter()
+    model.run(n_new)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    toks = model.seq[ctx:ctx + n_new].cpu().numpy()
+    tok_s = n_new / el
+    log(f"model: {n_new} greedy tokens in {el * 1e3:.1f} ms: {el / n_new * 1e3:.3f} ms/token, {tok_s:.1f} tok/s")
+    # determinism: the same steps again from the same snapshot give the same tokens
+    model.restore(snap)
+    model.run(n_new)
+    torch.cuda.synchronize()
+    same = bool(np.array_equal(model.seq[ctx:ctx + n_new].cpu().numpy(), toks))
+    # ------------------------------------------------------------------ per-kernel events (one eager step)
+    model.restore(snap)
+    names = rx.launches(1)
+    ev = []
+    for _ in range(N_LAYERS):
+        d = {"attn": [torch.cuda.Event(enable_timing=True) for _ in range(2)],
+             "experts": [torch.cuda.Event(enable_timing=True) for _ in range(2 * len(names))]}
+        for e in d["attn"] + d["experts"]:
+            e.record()
+        ev.append(d)
+    torch.cuda.synchronize()
+    R = max(1, A.roofline_steps // 4)
+    acc = {nm: 0.0 for nm in names}
+    att_full = att_slide = 0.0
+    for _ in range(R):
+        model.step(events=ev)
+        torch.cuda.synchronize()
+        for li in range(N_LAYERS):
+            for k, nm in enumerate(names):
+                acc[nm] += ev[li]["experts"][2 * k].elapsed_time(ev[li]["experts"][2 * k + 1]) * 1e3
+            a = ev[li]["attn"][0].elapsed_time(ev[li]["attn"][1]) * 1e3
+            if li % 2 == 0:
+                att_slide += a
+            else:
+                att_full += a
+    n_l = R * N_LAYERS
+    avg = {nm: acc[nm] / n_l for nm in names}
+    gu_bytes = TOPK * GATE_UP_BYTES
+    gu_gbps = gu_bytes / (avg["gate_up"] * 1e-6) / 1e9
+    log("model: per launch " + ", ".join(f"{nm} {v:.2f} us" for nm, v in avg.items())
+        + f", attention full {att_full / (n_l / 2):.2f} us, sliding {att_slide / (n_l / 2):.2f} us")
+    traffic, why = measured_traffic("k_moe_gate_up_t950", "t950", 1, A.k_split)
+    dense = N_LAYERS * 2 * (5120 * 2880 + 2880 * 4096 + 128 * 2880) + 2 * 201088 * 2880
+    experts = N_LAYERS * TOPK * SLOT_ALGO_BYTES
+    kv = 2 * 2 * 8 * 64 * (18 * (ctx + n_new / 2) + 18 * 128)
+    step_bytes = dense + experts + kv
+    res = {"metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": n_new,
+           "warmup": A.warmup, "ms_per_step": round(el / n_new * 1e3, 4), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+           "config": {"workload": f"config4: full 36-layer GPT-OSS-120B-shaped greedy decode, random-init weights, "
+                                  f"{ctx}-token context, {n_new} tokens, one hipGraph per step, experts t950 resident",
+                      "context": ctx, "tokens": n_new, "vocab": int(w.vocab), "attn_split_full": A.attn_split,
+                      "attn_split_sliding": A.sliding_split, "deterministic_tokens": same,
+                      "first_tokens": [int(t) for t in toks[:8]],
+                      "step_algorithmic_gb": round(step_bytes / 1e9, 3),
+                      "step_hbm_gbps": round(step_bytes / (el / n_new) / 1e9, 1),
+                      "launch_us": {**{nm: round(v, 2) for nm, v in avg.items()},
+                                    "attention_full": round(att_full / (n_l / 2), 2),
+                                    "attention_sliding": round(att_slide / (n_l / 2), 2)},
+                      "context_steps_per_s": round((ctx - 1) / t_ctx, 1)},
+           "roofline": {"bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gu_gbps / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_moe_gate_up_t950",
+                        "avg_launch_us": round(avg["gate_up"], 3), "algorithmic_bytes_per_launch": gu_bytes},
+           "cpu_baseline": None}
+    print(json.dumps(res), flush=True)
+
+
 def bench_attention(A):
     """Configuration 3: GQA decode attention (64 q / 8 KV heads, head_dim 64, bf16 K/V ~ N(0,1), sinks ~ N(0,1)),
     batch 1 and 4, contexts 1024 / 4096 / 8192, layers alternating full attention and a 128-token sliding window
@@ -320,7 +454,7 @@ def bench_attention(A):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 200; model: 256 tokens)")
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--layout", choices=("t950", "raw", "ps4"), default="t950",
@@ -335,14 +469,19 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--gu-pairs", type=int, default=4, help="gate_up row pairs per wavefront (1, 2, 4)")
     ap.add_argument("--dn-pairs", type=int, default=2, help="down row pairs per wavefront (1, 2, 4)")
-    ap.add_argument("--workload", choices=("experts", "attention", "prefill"), default="experts",
+    ap.add_argument("--workload", choices=("experts", "attention", "prefill", "model"), default="experts",
                     help="experts: configuration 1 (the headline); prefill: configuration 2 (grouped GEMM layer); "
-                         "attention: configuration 3 (decode attention)")
+                         "attention: configuration 3 (decode attention); model: configuration 4 (full decode)")
     ap.add_argument("--tokens", type=int, default=2048, help="prefill: prompt tokens")
+    ap.add_argument("--context", type=int, default=4096, help="model: context tokens before the timed decode")
+    ap.add_argument("--attn-split", type=int, default=32, help="model: key chunks of full-attention layers")
+    ap.add_argument("--sliding-split", type=int, default=1, help="model: key chunks of sliding-window layers")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="run one device-to-device copy of this many MB first (a known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
     A = ap.parse_args()
+    if A.steps is None:
+        A.steps = 256 if A.workload == "model" else 200
     if A.gpus != 1:
         print(f"bench.py: this build runs on one GPU per process and measures one GPU; --gpus {A.gpus} is not "
               f"supported (sharding across GPUs is designed, not built)", file=sys.stderr)
@@ -351,6 +490,8 @@ def main():
         return bench_attention(A)
     if A.workload == "prefill":
         return bench_prefill(A)
+    if A.workload == "model":
+        return bench_model(A)
     if not 1 <= A.batch <= 8:
         sys.exit("--batch must be in [1, 8]")
 

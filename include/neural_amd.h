@@ -72,6 +72,10 @@ int na_moe_decode(const void* x, const int64_t* topk_ids, const void* topk_w, in
 int na_router_topk(const void* xn, int B, const void* w_router, const void* b_router, int n_exp, float* logits,
                    unsigned int* counter, int64_t* ids_out, void* w_out, hipStream_t stream);
 
+/* Device self-check of the fp32 -> bf16 rounding the kernels use (gfx950 v_cvt_pk_bf16_f32, single and paired)
+ * against an integer round-to-nearest-even: n floats in, three uint16 [n] outputs (hardware, hardware pair, integer). */
+int na_selftest_bf16(const float* in, void* out_hw, void* out_pk, void* out_int, long long n, hipStream_t stream);
+
 /* Device self-check of the MFMA operand layout the tile kernels use: d [16, 16] fp32 = a [16, 32] x b [32, 16] bf16. */
 int na_selftest_mfma(const void* a, const void* b, float* d, hipStream_t stream);
 

@@ -25,6 +25,7 @@ SIGNATURES = {
     "na_moe_decode": [VP, VP, VP, I32, VP, I64, I32, VP, I64, VP, VP, VP, VP, VP, F32, F32, I32, I32, VP, VP],
     "na_router_topk": [VP, I32, VP, VP, I32, VP, VP, VP, VP, VP],
     "na_selftest_mfma": [VP, VP, VP, VP],
+    "na_selftest_bf16": [VP, VP, VP, VP, I64, VP],
     "na_t950_slot_bytes": [],
     "na_repack_to_t950": [VP, I64, I32, VP, I64, I32, VP],
     "na_repack_from_t950": [VP, I64, VP, I64, I32, I32, VP],

@@ -30,6 +30,24 @@ __global__ void k_selftest_mfma(const uint16_t* a_in, const uint16_t* b_in, floa
   for (int r = 0; r < 4; ++r) d_out[(4 * q + r) * 16 + m] = c[r];
 }
 
+// out_hw[i] = bf16 bits of in[i] through the kernels' conversion (f32_to_bf16, and pack_bf16x2 for the pair
+// (in[i & ~1], in[i | 1])); out_int[i] = the integer round-to-nearest-even reference.
+__global__ void k_selftest_bf16(const float* __restrict__ in, uint16_t* __restrict__ out_hw,
+                                uint16_t* __restrict__ out_pk, uint16_t* __restrict__ out_int, long long n) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float f = in[i];
+  out_hw[i] = f32_to_bf16(f);
+  out_int[i] = f32_to_bf16_int(f);
+  const long long p = i & ~1ll;
+  if (p + 1 < n) {
+    const uint32_t w = pack_bf16x2(in[p], in[p + 1]);
+    out_pk[i] = (uint16_t)(i & 1 ? w >> 16 : w & 0xffff);
+  } else {
+    out_pk[i] = f32_to_bf16(f);
+  }
+}
+
 }  // namespace na
 
 extern "C" {
@@ -48,6 +66,16 @@ int na_selftest_fp4(void* out, hipStream_t stream) {
 int na_selftest_mfma(const void* a, const void* b, float* d, hipStream_t stream) {
   if (!a || !b || !d) return na::kErrArgs;
   hipLaunchKernelGGL(na::k_selftest_mfma, dim3(1), dim3(64), 0, stream, (const uint16_t*)a, (const uint16_t*)b, d);
+  return hipGetLastError() == hipSuccess ? na::kOk : na::kErrLaunch;
+}
+
+// Conversion self-check: n floats -> three uint16 arrays (hardware single, hardware pair, integer reference).
+int na_selftest_bf16(const float* in, void* out_hw, void* out_pk, void* out_int, long long n, hipStream_t stream) {
+  if (!in || !out_hw || !out_pk || !out_int || n <= 0) return na::kErrArgs;
+  const long long blocks = (n + 255) / 256;
+  if (blocks > 0x7fffffffll) return na::kErrTooLarge;
+  hipLaunchKernelGGL(na::k_selftest_bf16, dim3((unsigned)blocks), dim3(256), 0, stream, in, (uint16_t*)out_hw,
+                     (uint16_t*)out_pk, (uint16_t*)out_int, n);
   return hipGetLastError() == hipSuccess ? na::kOk : na::kErrLaunch;
 }
 

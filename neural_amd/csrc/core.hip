@@ -23,10 +23,11 @@ constexpr int kHq = 64 * 64;             // query width (NQ x HD)
 constexpr int kQkvRows = (64 + 2 * 8) * 64;   // 5120
 constexpr int kNE = 128;
 
-// Sum over the 16 lanes of a row group.
-NA_DEVICE float sum16(float v) {
+// Sum over the TPR lanes of a row group (TPR a power of two <= 64, groups aligned to TPR lanes).
+template <int TPR>
+NA_DEVICE float sum_group(float v) {
 #pragma unroll
-  for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o);
+  for (int o = 1; o < TPR; o <<= 1) v += __shfl_xor(v, o);
   return v;
 }
 
@@ -38,27 +39,42 @@ NA_DEVICE float dot8(uint4 w, uint4 x, float a) {
   return dot2_bf16(w.w, x.w, a);
 }
 
-// One weight row's 16-byte chunks j, j + 16, ... held in registers: issued before the activation is ready so that the
-// weight stream overlaps the normalisation; dot() then sums them against the LDS-staged activation hc and every lane
-// of the 16-lane row group returns the row's total.
-template <int K>
+// One weight row's 16-byte chunks j, j + TPR, ... (thread j of the row's TPR threads) held in registers: issued before
+// the activation is ready so that the weight stream overlaps the normalisation; dot() then sums them against the
+// LDS-staged activation hc and every lane of the row group returns the row's total.
+template <int K, int TPR>
 struct RowChunks {
-  static constexpr int NCH = K / 8, IT = (NCH + 15) / 16;
+  static constexpr int NCH = K / 8, IT = (NCH + TPR - 1) / TPR;
   uint4 w[IT];
   NA_DEVICE void load(const uint16_t* __restrict__ wrow, int j) {
 #pragma unroll
-    for (int i = 0; i < IT; ++i) w[i] = load16<true>(wrow + 8 * min(j + 16 * i, NCH - 1));
+    for (int i = 0; i < IT; ++i) w[i] = load16<true>(wrow + 8 * min(j + TPR * i, NCH - 1));
   }
   NA_DEVICE float dot(const uint16_t* hc, int j) const {
     float a = 0.f;
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
-      const int c = j + 16 * i;
+      const int c = j + TPR * i;
       if (c < NCH) a = dot8(w[i], *reinterpret_cast<const uint4*>(hc + 8 * c), a);
     }
-    return sum16(a);
+    return sum_group<TPR>(a);
   }
 };
+
+// Threads per weight row of each GEMV (256 / TPR rows per workgroup).
+#ifndef NA_QKV_TPR
+#define NA_QKV_TPR 32
+#endif
+#ifndef NA_OPROJ_TPR
+#define NA_OPROJ_TPR 64
+#endif
+#ifndef NA_ROUTER_TPR
+#define NA_ROUTER_TPR 64
+#endif
+#ifndef NA_LM_TPR
+#define NA_LM_TPR 16
+#endif
+constexpr int kQkvTpr = NA_QKV_TPR, kOprojTpr = NA_OPROJ_TPR, kRouterTpr = NA_ROUTER_TPR, kLmTpr = NA_LM_TPR;
 
 // Inputs of the residual + RMSNorm stage, loaded first (before a kernel's weight stream, so that waiting for them
 // does not wait for the weights): thread t holds chunks t and t + 256 (8 values each) of mid, of the expert outputs
@@ -126,9 +142,8 @@ NA_DEVICE void norm_finish(const NormIn& in, bool has_g, bool has_c, float eps, 
       uint32_t o[4], xo[4];
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
-        o[e >> 1] = (uint32_t)f32_to_bf16(half_at(in.w[i], e) * (xv[i][e] * r)) |
-                    ((uint32_t)f32_to_bf16(half_at(in.w[i], e + 1) * (xv[i][e + 1] * r)) << 16);
-        xo[e >> 1] = (uint32_t)f32_to_bf16(xv[i][e]) | ((uint32_t)f32_to_bf16(xv[i][e + 1]) << 16);
+        o[e >> 1] = pack_bf16x2(half_at(in.w[i], e) * (xv[i][e] * r), half_at(in.w[i], e + 1) * (xv[i][e + 1] * r));
+        xo[e >> 1] = pack_bf16x2(xv[i][e], xv[i][e + 1]);
       }
       *reinterpret_cast<uint4*>(hc + 8 * ch) = make_uint4(o[0], o[1], o[2], o[3]);
       if (xbuf && blockIdx.x == 0) *reinterpret_cast<uint4*>(xbuf + 8 * ch) = make_uint4(xo[0], xo[1], xo[2], xo[3]);
@@ -167,8 +182,10 @@ __global__ __launch_bounds__(256) void k_embed(const uint16_t* __restrict__ emb,
     *reinterpret_cast<uint4*>(mid + 8 * ch) = *reinterpret_cast<const uint4*>(emb + t * kH + 8 * ch);
 }
 
-// QKV: grid 320 = 80 heads x 4; workgroup (head, c) computes the rows of dims d = 8c .. 8c + 7 (row groups 0..7) and
-// of their RoPE partners d + 32 (row groups 8..15) of head `head` (0..63 q, 64..71 k, 72..79 v).
+// QKV: ROWS = 256 / TPR rows per workgroup, grid 5120 / ROWS; workgroup (head, c) computes the rows of dims
+// d = c * ROWS/2 + (0 .. ROWS/2 - 1) (row groups 0 .. ROWS/2 - 1) and of their RoPE partners d + 32 (the other row
+// groups) of head `head` (0..63 q, 64..71 k, 72..79 v).
+template <int TPR>
 __global__ __launch_bounds__(256) void k_qkv(const uint16_t* __restrict__ mid, const uint16_t* __restrict__ g,
                                              const float* __restrict__ cext, uint16_t* __restrict__ xbuf,
                                              const uint16_t* __restrict__ in_w, const uint16_t* __restrict__ W,
@@ -176,57 +193,62 @@ __global__ __launch_bounds__(256) void k_qkv(const uint16_t* __restrict__ mid, c
                                              const float* __restrict__ inv_freq, uint16_t* __restrict__ kc,
                                              uint16_t* __restrict__ vc, long long rows, int ring,
                                              uint16_t* __restrict__ qout, float eps, float att_scale) {
+  constexpr int ROWS = 256 / TPR, HALF = ROWS / 2, PER_HEAD = 64 / ROWS;
   __shared__ __align__(16) uint16_t hc[kH];
-  __shared__ float ys[16];
-  const int tid = threadIdx.x, r = tid >> 4, j = tid & 15;
-  const int head = blockIdx.x >> 2, c = blockIdx.x & 3;
-  const int d = 8 * c + (r & 7);
-  const int row = head * 64 + 32 * (r >> 3) + d;
+  __shared__ float ys[ROWS];
+  const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
+  const int head = blockIdx.x / PER_HEAD, c = blockIdx.x % PER_HEAD;
+  const int d = HALF * c + (r % HALF);
+  const int row = head * 64 + 32 * (r / HALF) + d;
   NormIn ni;
   ni.load(mid, g, cext, in_w);
   const uint16_t bv = bias[row];
+  const long long pos = *pos_p;
+  const float freq = inv_freq[HALF * c + (tid % HALF)];
   __builtin_amdgcn_sched_barrier(0);
-  RowChunks<kH> rw;
+  RowChunks<kH, TPR> rw;
   rw.load(W + (long long)row * kH, j);
   __builtin_amdgcn_sched_barrier(0);
   norm_finish(ni, g != nullptr, cext != nullptr, eps, hc, xbuf);
   const float s = rw.dot(hc, j);
   if (j == 0) ys[r] = rb(s + bf16_to_f32(bv));
   __syncthreads();
-  if (tid >= 8 * 16 || j != 0) return;              // row group r < 8 writes dims d and d + 32
-  const long long pos = *pos_p;
-  const float ya = ys[r], yb = ys[r + 8];
+  if (tid >= HALF) return;                           // thread t < HALF writes dims 32c' + t and its partner
+  const int dd = HALF * c + tid;
+  const float ya = ys[tid], yb = ys[tid + HALF];
   float o1 = ya, o2 = yb;
   if (head < 64 + 8) {                               // q and k heads: RoPE
-    const float fr = inv_freq[d] * (float)pos;
+    const float fr = freq * (float)pos;
     const float cs = rb(cosf(fr) * att_scale), sn = rb(sinf(fr) * att_scale);
     o1 = rb(rb(ya * cs) - rb(yb * sn));
     o2 = rb(rb(yb * cs) + rb(ya * sn));
   }
   if (head < 64) {
-    qout[head * 64 + d] = f32_to_bf16(o1);
-    qout[head * 64 + 32 + d] = f32_to_bf16(o2);
+    qout[head * 64 + dd] = f32_to_bf16(o1);
+    qout[head * 64 + 32 + dd] = f32_to_bf16(o2);
   } else {
     const long long slot = ring > 0 ? pos % ring : pos;
     if (slot < 0 || slot >= rows) return;           // a position outside the cache is stored nowhere
     uint16_t* cache = head < 72 ? kc + (long long)(head - 64) * rows * 64 : vc + (long long)(head - 72) * rows * 64;
-    cache[slot * 64 + d] = f32_to_bf16(o1);
-    cache[slot * 64 + 32 + d] = f32_to_bf16(o2);
+    cache[slot * 64 + dd] = f32_to_bf16(o1);
+    cache[slot * 64 + 32 + dd] = f32_to_bf16(o2);
   }
 }
 
-// o_proj + residual: grid 180 (16 rows each): mid[n] = bf16(xbuf[n] + bf16(att . Wo[n] + bo[n])).
+// o_proj + residual: 256 / TPR rows per workgroup: mid[n] = bf16(xbuf[n] + bf16(att . Wo[n] + bo[n])).
+template <int TPR>
 __global__ __launch_bounds__(256) void k_oproj(const uint16_t* __restrict__ att, const uint16_t* __restrict__ Wo,
                                                const uint16_t* __restrict__ bo, const uint16_t* __restrict__ xbuf,
                                                uint16_t* __restrict__ mid) {
+  constexpr int ROWS = 256 / TPR;
   __shared__ __align__(16) uint16_t hc[kHq];
-  const int tid = threadIdx.x, r = tid >> 4, j = tid & 15;
-  const int row = 16 * blockIdx.x + r;
+  const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
+  const int row = ROWS * blockIdx.x + r;
   VecIn<kHq> a;
   a.load(att);
   const uint16_t bv = bo[row], xv = xbuf[row];
   __builtin_amdgcn_sched_barrier(0);
-  RowChunks<kHq> rw;
+  RowChunks<kHq, TPR> rw;
   rw.load(Wo + (long long)row * kHq, j);
   __builtin_amdgcn_sched_barrier(0);
   a.store(hc);
@@ -234,9 +256,10 @@ __global__ __launch_bounds__(256) void k_oproj(const uint16_t* __restrict__ att,
   if (j == 0) mid[row] = f32_to_bf16(bf16_to_f32(xv) + rb(s + bf16_to_f32(bv)));
 }
 
-// post-attention RMSNorm + router + top-4: grid 8 (16 experts each).  Workgroup 0 writes hn (the experts' input);
+// post-attention RMSNorm + router + top-4: 256 / TPR experts per workgroup, grid 128 / (256 / TPR).  Workgroup 0 writes hn (the experts' input);
 // every workgroup publishes its 16 logits (device-coherent stores, then a count); the last one selects the top 4,
 // writes ids / weights and resets the count.
+template <int TPR>
 __global__ __launch_bounds__(256) void k_router_norm(const uint16_t* __restrict__ mid, const uint16_t* __restrict__ post_w,
                                                      float eps, const uint16_t* __restrict__ Wr,
                                                      const uint16_t* __restrict__ br, uint16_t* __restrict__ hn,
@@ -244,13 +267,14 @@ __global__ __launch_bounds__(256) void k_router_norm(const uint16_t* __restrict_
                                                      int64_t* __restrict__ ids, uint16_t* __restrict__ wts) {
   __shared__ __align__(16) uint16_t hc[kH];
   __shared__ uint32_t last;
-  const int tid = threadIdx.x, r = tid >> 4, j = tid & 15;
-  const int e = 16 * blockIdx.x + r;
+  constexpr int ROWS = 256 / TPR;
+  const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
+  const int e = ROWS * blockIdx.x + r;
   NormIn ni;
   ni.load(mid, nullptr, nullptr, post_w);
   const uint16_t bv = br[e];
   __builtin_amdgcn_sched_barrier(0);
-  RowChunks<kH> rw;
+  RowChunks<kH, TPR> rw;
   rw.load(Wr + (long long)e * kH, j);
   __builtin_amdgcn_sched_barrier(0);
   norm_finish(ni, false, false, eps, hc, nullptr);
@@ -320,17 +344,19 @@ NA_DEVICE uint32_t bf16_order_key(uint16_t b) {
 // Tail 2: logits = bf16(hn . lm_head[v]) for 16 rows per workgroup; the workgroup's best as a 64-bit key
 // (order key of the logit << 32 | ~index: a larger key is a larger logit, then a smaller index) -> part[wg];
 // optionally the logits themselves.
+template <int TPR>
 __global__ __launch_bounds__(256) void k_lmhead(const uint16_t* __restrict__ hn, const uint16_t* __restrict__ Wl,
                                                 int vocab, uint16_t* __restrict__ logits_out,
                                                 uint64_t* __restrict__ part) {
   __shared__ __align__(16) uint16_t hc[kH];
-  __shared__ uint64_t best[16];
-  const int tid = threadIdx.x, r = tid >> 4, j = tid & 15;
-  const int v = 16 * blockIdx.x + r;
+  constexpr int ROWS = 256 / TPR;
+  __shared__ uint64_t best[ROWS];
+  const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
+  const int v = ROWS * blockIdx.x + r;
   VecIn<kH> a;
   a.load(hn);
   __builtin_amdgcn_sched_barrier(0);
-  RowChunks<kH> rw;
+  RowChunks<kH, TPR> rw;
   rw.load(Wl + (long long)min(v, vocab - 1) * kH, j);
   __builtin_amdgcn_sched_barrier(0);
   a.store(hc);
@@ -343,7 +369,7 @@ __global__ __launch_bounds__(256) void k_lmhead(const uint16_t* __restrict__ hn,
   __syncthreads();
   if (tid == 0) {
     uint64_t b = best[0];
-    for (int i = 1; i < 16; ++i) b = best[i] > b ? best[i] : b;
+    for (int i = 1; i < ROWS; ++i) b = best[i] > b ? best[i] : b;
     part[blockIdx.x] = b;
   }
 }
@@ -401,7 +427,7 @@ int na_core_qkv(const void* mid, const void* g, const float* c, void* xbuf, cons
     return kErrArgs;
   if (c && !g) return kErrArgs;
   if (ring > 0 && cache_rows != ring) return kErrArgs;
-  hipLaunchKernelGGL(k_qkv, dim3(kQkvRows / 16), dim3(256), 0, stream, (const uint16_t*)mid, (const uint16_t*)g, c,
+  hipLaunchKernelGGL(k_qkv<kQkvTpr>, dim3(kQkvRows / (256 / kQkvTpr)), dim3(256), 0, stream, (const uint16_t*)mid, (const uint16_t*)g, c,
                      (uint16_t*)xbuf, (const uint16_t*)in_w, (const uint16_t*)W, (const uint16_t*)bias, pos, inv_freq,
                      (uint16_t*)kc, (uint16_t*)vc, cache_rows, ring, (uint16_t*)q, eps, att_scale);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
@@ -409,7 +435,7 @@ int na_core_qkv(const void* mid, const void* g, const float* c, void* xbuf, cons
 
 int na_core_oproj(const void* att, const void* Wo, const void* bo, const void* xbuf, void* mid, hipStream_t stream) {
   if (!att || !Wo || !bo || !xbuf || !mid) return kErrArgs;
-  hipLaunchKernelGGL(k_oproj, dim3(kH / 16), dim3(256), 0, stream, (const uint16_t*)att, (const uint16_t*)Wo,
+  hipLaunchKernelGGL(k_oproj<kOprojTpr>, dim3(kH / (256 / kOprojTpr)), dim3(256), 0, stream, (const uint16_t*)att, (const uint16_t*)Wo,
                      (const uint16_t*)bo, (const uint16_t*)xbuf, (uint16_t*)mid);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
@@ -417,13 +443,13 @@ int na_core_oproj(const void* att, const void* Wo, const void* bo, const void* x
 int na_core_router(const void* mid, const void* post_w, float eps, const void* Wr, const void* br, void* hn,
                    float* logits, unsigned int* counter, int64_t* ids, void* wts, hipStream_t stream) {
   if (!mid || !post_w || !Wr || !br || !hn || !logits || !counter || !ids || !wts) return kErrArgs;
-  hipLaunchKernelGGL(k_router_norm, dim3(kNE / 16), dim3(256), 0, stream, (const uint16_t*)mid,
+  hipLaunchKernelGGL(k_router_norm<kRouterTpr>, dim3(kNE / (256 / kRouterTpr)), dim3(256), 0, stream, (const uint16_t*)mid,
                      (const uint16_t*)post_w, eps, (const uint16_t*)Wr, (const uint16_t*)br, (uint16_t*)hn, logits,
                      (uint32_t*)counter, ids, (uint16_t*)wts);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
-long long na_core_lm_partials(int vocab) { return vocab > 0 ? (vocab + 15) / 16 : -1; }
+long long na_core_lm_partials(int vocab) { return vocab > 0 ? (vocab + 256 / kLmTpr - 1) / (256 / kLmTpr) : -1; }
 
 int na_core_lm_tail(const void* mid, const void* g, const float* c, const void* final_w, float eps, const void* Wl,
                     int vocab, void* hn, void* logits_out, unsigned long long* part, int64_t* tok, int64_t* pos,
@@ -433,10 +459,10 @@ int na_core_lm_tail(const void* mid, const void* g, const float* c, const void* 
   if ((step_pos || seq || pred) && !pos) return kErrArgs;
   if ((seq || pred) && seq_len <= 0) return kErrArgs;
   if (c && !g) return kErrArgs;
-  const int nwg = (vocab + 15) / 16;
+  const int nwg = (int)na_core_lm_partials(vocab);
   hipLaunchKernelGGL(k_final_norm, dim3(1), dim3(256), 0, stream, (const uint16_t*)mid, (const uint16_t*)g, c,
                      (const uint16_t*)final_w, eps, (uint16_t*)hn);
-  hipLaunchKernelGGL(k_lmhead, dim3(nwg), dim3(256), 0, stream, (const uint16_t*)hn, (const uint16_t*)Wl, vocab,
+  hipLaunchKernelGGL(k_lmhead<kLmTpr>, dim3(nwg), dim3(256), 0, stream, (const uint16_t*)hn, (const uint16_t*)Wl, vocab,
                      (uint16_t*)logits_out, (uint64_t*)part);
   hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, stream, (const uint64_t*)part, nwg, tok, pos, step_pos, seq,
                      n_forced, pred, seq_len);

@@ -211,8 +211,10 @@ class DecodeModel:
             c.zero_()
 
     # ------------------------------------------------------------------------------------------------ launches
-    def layer(self, li: int) -> None:
-        """One layer's launches on the current stream (no host synchronisation, capturable)."""
+    def layer(self, li: int, events: dict | None = None) -> None:
+        """One layer's launches on the current stream (no host synchronisation, capturable).  events: None, or a dict
+        with "attn" (2 timing events) and/or "experts" (the expert launches' events, ResidentExperts.launches(1)) for
+        dispatch-timestamped timing of an eager call (measurement only)."""
         ly = self.w.layers[li]
         s = N.stream(self.dev)
         kc, vc = self.kc[li], self.vc[li]
@@ -225,13 +227,15 @@ class DecodeModel:
         ns = self.sliding_split if ly.sliding else self.n_split
         N.call("na_decode_attention", self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), rows, ly.sinks.data_ptr(),
                self.pos.data_ptr(), self.att.data_ptr(), 1, float(self.scaling), int(ly.sliding), ring, ns,
-               self.attn_work.data_ptr(), self.attn_counters.data_ptr(), None, s)
+               self.attn_work.data_ptr(), self.attn_counters.data_ptr(),
+               N.events_array(events.get("attn")) if events else None, s)
         N.call("na_core_oproj", self.att.data_ptr(), ly.Wo.data_ptr(), ly.bo.data_ptr(), self.xbuf.data_ptr(),
                self.mid.data_ptr(), s)
         N.call("na_core_router", self.mid.data_ptr(), ly.post_w.data_ptr(), EPS, ly.Wr.data_ptr(), ly.br.data_ptr(),
                self.hn.data_ptr(), self.r_logits.data_ptr(), self.r_counter.data_ptr(), self.ids.data_ptr(),
                self.wts.data_ptr(), s)
-        self.rx.forward_decode(li, self.hn, self.ids, self.wts, out=self.g)
+        self.rx.forward_decode(li, self.hn, self.ids, self.wts, out=self.g,
+                               events=events.get("experts") if events else None)
 
     def embed(self) -> None:
         N.call("na_core_embed", self.w.embed.data_ptr(), self.w.vocab, self.seq.data_ptr(), self.smax,
@@ -243,12 +247,28 @@ class DecodeModel:
                N.ptr(self.logits), self.part.data_ptr(), self.tok.data_ptr(), self.pos.data_ptr(), int(step_pos),
                self.seq.data_ptr(), self.n_forced.data_ptr(), self.pred.data_ptr(), self.smax, N.stream(self.dev))
 
-    def step(self) -> None:
-        """One decode step (embed, every layer, tail) on the current stream."""
+    def step(self, events=None) -> None:
+        """One decode step (embed, every layer, tail) on the current stream.  events: None or one dict per layer (see
+        layer())."""
         self.embed()
         for li in range(self.n_layers):
-            self.layer(li)
+            self.layer(li, None if events is None else events[li])
         self.tail()
+
+    def snapshot(self):
+        """Copy of the decode state a later restore() returns to: position, sequence and every K/V cache (use it to
+        rerun the same steps from the same context)."""
+        return (self.pos.clone(), self.seq.clone(), self.n_forced.clone(), [c.clone() for c in self.kc],
+                [c.clone() for c in self.vc])
+
+    def restore(self, snap) -> None:
+        """In-place restore of a snapshot (buffer addresses unchanged, so captured graphs stay valid)."""
+        pos, seq, nf, kc, vc = snap
+        self.pos.copy_(pos)
+        self.seq.copy_(seq)
+        self.n_forced.copy_(nf)
+        for d, s_ in zip(self.kc + self.vc, kc + vc):
+            d.copy_(s_)
 
     # ------------------------------------------------------------------------------------------------ graphs
     def capture(self) -> torch.cuda.CUDAGraph:
