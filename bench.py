@@ -285,7 +285,8 @@ def bench_model(A):
     log(f"model: building the expert pool ({N_LAYERS * N_EXPERTS} slots, t950)")
     pool = build_t950_pool(dev, 4242)
     L = GPTOSS_LAYOUT_T950
-    rx = ResidentExperts(pool, L, None, None, max_batch=1, k_split=A.k_split, combine_in_down=A.down == "combine")
+    rx = ResidentExperts(pool, L, None, None, max_batch=1, k_split=A.k_split, combine_in_down=A.down != "expert",
+                         single_launch=A.down == "layer")
     log("model: random-init dense weights")
     w = random_weights(device=dev, seed=77)
     smax = ctx + max(n_new, A.warmup) + 1
@@ -346,11 +347,13 @@ def bench_model(A):
                 att_full += a
     n_l = R * N_LAYERS
     avg = {nm: acc[nm] / n_l for nm in names}
-    gu_bytes = TOPK * GATE_UP_BYTES
-    gu_gbps = gu_bytes / (avg["gate_up"] * 1e-6) / 1e9
+    dom = names[0]
+    gu_bytes = TOPK * (GATE_UP_BYTES + DOWN_BYTES if dom == "layer" else GATE_UP_BYTES)
+    gu_gbps = gu_bytes / (avg[dom] * 1e-6) / 1e9
+    kname = "k_moe_layer_t950" if dom == "layer" else "k_moe_gate_up_t950"
     log("model: per launch " + ", ".join(f"{nm} {v:.2f} us" for nm, v in avg.items())
         + f", attention full {att_full / (n_l / 2):.2f} us, sliding {att_slide / (n_l / 2):.2f} us")
-    traffic, why = measured_traffic("k_moe_gate_up_t950", "t950", 1, A.k_split)
+    traffic, why = measured_traffic(kname, "t950", 1, A.k_split)
     dense = N_LAYERS * 2 * (5120 * 2880 + 2880 * 4096 + 128 * 2880) + 2 * 201088 * 2880
     experts = N_LAYERS * TOPK * SLOT_ALGO_BYTES
     kv = 2 * 2 * 8 * 64 * (18 * (ctx + n_new / 2) + 18 * 128)
@@ -370,8 +373,8 @@ def bench_model(A):
                                     "attention_sliding": round(att_slide / (n_l / 2), 2)},
                       "context_steps_per_s": round((ctx - 1) / t_ctx, 1)},
            "roofline": {"bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(gu_gbps / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_moe_gate_up_t950",
-                        "avg_launch_us": round(avg["gate_up"], 3), "algorithmic_bytes_per_launch": gu_bytes},
+                        "frac": round(gu_gbps / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kname,
+                        "avg_launch_us": round(avg[dom], 3), "algorithmic_bytes_per_launch": gu_bytes},
            "cpu_baseline": None}
     print(json.dumps(res), flush=True)
 
@@ -460,9 +463,9 @@ def main():
     ap.add_argument("--layout", choices=("t950", "raw", "ps4"), default="t950",
                     help="resident slot layout: gfx950 tiles (MFMA kernels) or the store layouts (VALU kernels)")
     ap.add_argument("--k-split", type=int, default=4, help="t950: waves per workgroup splitting K (1, 2, 4)")
-    ap.add_argument("--down", choices=("combine", "expert"), default="combine",
-                    help="t950, batch <= 2: down kernel that also does the top-k combine (default), or expert-major "
-                         "down + combine kernel")
+    ap.add_argument("--down", choices=("combine", "layer", "expert"), default="combine",
+                    help="t950, batch 1: gate_up then down + combine (two launches, default), both in one launch with "
+                         "a grid barrier (layer), or expert-major down + a combine kernel (expert)")
     ap.add_argument("--sets", type=int, default=16, help="routing sets (graphs) cycled over the steps")
     ap.add_argument("--roofline-steps", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
@@ -545,7 +548,7 @@ def main():
     bias_gu = torch.zeros(n_slots, L.gate_up_n, dtype=torch.bfloat16, device=dev)
     bias_dn = torch.zeros(n_slots, L.down_n, dtype=torch.bfloat16, device=dev)
     rx = ResidentExperts(pool, L, bias_gu, bias_dn, gu_pairs_per_wave=A.gu_pairs, dn_pairs_per_wave=A.dn_pairs,
-                         k_split=A.k_split, combine_in_down=A.down == "combine")
+                         k_split=A.k_split, combine_in_down=A.down != "expert", single_launch=A.down == "layer")
     launches = rx.launches(A.batch)
     per_layer = len(launches)
 
@@ -597,7 +600,8 @@ def main():
         f"{step_bytes / (ms_step * 1e-3) / 1e9:.0f} GB/s whole-step")
 
     # ------------------------------------------------------------------ roofline pass (per-kernel events)
-    per_kernel_bytes = {"gate_up": GATE_UP_BYTES, "down": DOWN_BYTES, "down_combine": DOWN_BYTES, "combine": 0}
+    per_kernel_bytes = {"gate_up": GATE_UP_BYTES, "down": DOWN_BYTES, "down_combine": DOWN_BYTES, "combine": 0,
+                        "layer": GATE_UP_BYTES + DOWN_BYTES}
     kernels = tuple((nm, per_kernel_bytes[nm]) for nm in launches)
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * len(kernels))] for _ in range(N_LAYERS)]
     for row in ev:
@@ -623,7 +627,8 @@ def main():
     dom = kernels[0][0]
     top = kern[dom]
     per_launch = tot[dom][1] / tot[dom][2]
-    kname = "k_moe_gate_up_t950" if A.layout == "t950" else "k_moe_gate_up"
+    kname = ("k_moe_layer_t950" if dom == "layer" else "k_moe_gate_up_t950") if A.layout == "t950" \
+        else "k_moe_gate_up"
     traffic, why = measured_traffic(kname, A.layout, B, A.k_split)
     log(f"traffic: {traffic} ({why})")
     roofline = {"bound": "hbm", "achieved": round(top["gbps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

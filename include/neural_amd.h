@@ -98,7 +98,7 @@ int na_repack_from_t950(const void* src, long long src_stride, void* dst, long l
 
 /* na_moe_decode over a t950 pool (slot_bytes >= 13,271,040, 16-byte aligned): the same contract and results as
  * na_moe_decode (server.py:508-518), computed with v_mfma_f32_16x16x32_bf16 on in-register dequantised codes.
- * k_split = waves per workgroup splitting K in the expert-major kernels (1, 2 or 4; <= 0: 4).
+ * k_split = waves per workgroup splitting K in the expert-major kernels (1, 2, 4 or 8; <= 0: 4).
  * down_mode 0: for B = 1 with an output, two launches: gate_up, then one down workgroup per 16 output rows that
  *   holds every distinct expert of the token and sums the top-k outputs itself (events = 4: gate_up, down);
  *   otherwise as down_mode 1.
@@ -107,6 +107,19 @@ int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
                        long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
                        const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha, float limit,
                        int k_split, int down_mode, void* const* events, hipStream_t stream);
+
+/* na_moe_decode_t950 for one token (B = 1, with an output) in ONE launch: gate_up + bias + clamped SwiGLU, a
+ * grid-wide barrier, then down + bias + routing weight and the top-4 sum; results identical to down_mode 0.  Same
+ * reference interface (server.py:508-518).  180 workgroups of 1024 threads that must all be resident at once: the
+ * occupancy is checked once per device (kErrTooLarge if they do not fit).
+ *   h_scratch  16-byte aligned, >= 4 x 2880 bf16 (the 4 pairs' activations)
+ *   sync       uint32 [3], zero before the first call; a completed call leaves [0] and [1] zero.  [2] is set if a
+ *              barrier wait gave up (outputs undefined); the caller clears it.  Calls sharing sync must not overlap.
+ *   events     NULL or 2 hipEvent_t (start/stop of the launch) */
+int na_moe_layer_t950(const void* x, const int64_t* topk_ids, const void* topk_w, const void* pool,
+                      long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
+                      const void* bias_dn, void* h_scratch, unsigned int* sync, void* out, float alpha, float limit,
+                      void* const* events, hipStream_t stream);
 
 /* ---- decode attention (GQA 64 query / 8 KV heads, head_dim 64, learned sinks, sliding window, rolling cache) */
 

@@ -101,6 +101,15 @@ NA_DEVICE float group_dot(const uint4 c, const uint32_t* x) {
   return a0 + a1;
 }
 
+// Pairs are (token b, rank k) flattened as p = 4b + k, one bit each in a 64-bit mask.  Of each token's pairs in
+// mask x, keep the lowest (the first of its ranks routed to the same expert): a token that lists one expert twice
+// is computed once and its result written to every duplicate pair.
+NA_DEVICE uint64_t first_per_token(uint64_t x) {
+  const uint64_t b1 = (x << 1) & 0xEEEEEEEEEEEEEEEEull, b2 = (x << 2) & 0xCCCCCCCCCCCCCCCCull,
+                 b3 = (x << 3) & 0x8888888888888888ull;
+  return x & ~(b1 | b2 | b3);
+}
+
 // E8M0 exponent applied exactly: v * 2^(s-127)  (s = 255 -> inf for v != 0, as exp2(128) in fp32).
 NA_DEVICE float e8m0_scale(float v, int s) {
   return s == 255 ? v * __builtin_inff() : __builtin_amdgcn_ldexpf(v, s - 127);

@@ -134,14 +134,20 @@ NA_DEVICE void load_xreg_global(const LaneMap& m, const uint16_t* const* xsrc, u
 // ----------------------------------------------------------------------------- routing of a decode batch
 // Pairs are (token b, rank k) flattened as p = 4b + k.  Work item w of a launch is the w-th distinct expert of the
 // batch in first-appearance order.  Expert ids outside [0, 128) are gathered into one item with status kBadExpert.
+// An item's rows are its tokens (the first pair of each token routed to it); a token that lists the expert twice
+// gets the result written to each of those pairs.
 enum RouteStatus { kNoItem = 0, kItem = 1, kBadExpert = 2 };
 
 struct Route {
   int expert;            // expert id within the layer
   int nt;                // tokens routed to it
   int distinct;          // distinct experts in the batch (= work items with status != kNoItem)
-  int pair[kMaxTok];     // their pair indices, ascending (0 past nt)
+  int pair[kMaxTok];     // the first pair of each of those tokens, ascending (0 past nt)
+  uint64_t all;          // every pair routed to it
 };
+
+// The ranks k of pair p's token that `all` routes to the same expert, as a 4-bit mask.
+NA_DEVICE uint32_t token_dup_mask(uint64_t all, int p) { return (uint32_t)(all >> (p & ~3)) & 0xFu; }
 
 NA_DEVICE int route_item(const int64_t* ids, int npairs, int item, Route& r) {
   const int lane = threadIdx.x & 63;
@@ -163,7 +169,8 @@ NA_DEVICE int route_item(const int64_t* ids, int npairs, int item, Route& r) {
   for (int i = 0; i < item; ++i) fm &= fm - 1;         // drop the lowest `item` set bits
   const int leader = __ffsll((long long)fm) - 1;
   r.expert = __builtin_amdgcn_readlane(my, leader);
-  uint64_t users = __ballot(lane < npairs && my == r.expert);
+  r.all = __ballot(lane < npairs && my == r.expert);
+  uint64_t users = first_per_token(r.all);
   r.nt = 0;
 #pragma unroll
   for (int t = 0; t < kMaxTok; ++t) {
@@ -281,7 +288,10 @@ __global__ __launch_bounds__(kThreads) void k_moe_gate_up(
             gb = rb(gb + bf16_to_f32(bg[j]));
             ub = rb(ub + bf16_to_f32(bg[kI + j]));
           }
-          h[(long long)r.pair[t] * kI + j] = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
+          const uint16_t hv = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
+          const uint32_t dm = token_dup_mask(r.all, r.pair[t]);
+          for (int k = 0; k < 4; ++k)
+            if ((dm >> k) & 1) h[(long long)((r.pair[t] & ~3) + k) * kI + j] = hv;
         }
       }
     }
@@ -304,12 +314,11 @@ __global__ __launch_bounds__(kThreads) void k_moe_down(
   const int pb0 = blockIdx.y * (kWaves * R);             // first row pair of this workgroup
   const int p0 = pb0 + wave * R;
   const int nt = min(r.nt, NT);
-  if (st == kBadExpert) {                                // its pairs contribute +0; no weights are read
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-      if (t < nt)
+  if (st == kBadExpert) {                                // each of its pairs contributes +0; no weights are read
+    for (int q = 0; q < 4 * B; ++q)
+      if ((r.all >> q) & 1)
         for (int n = 2 * pb0 + threadIdx.x; n < min(2 * (pb0 + kWaves * R), kH); n += kThreads)
-          yw[(long long)r.pair[t] * kH + n] = 0;
+          yw[(long long)q * kH + n] = 0;
     return;
   }
   const LaneMap m = lane_map(lane);
@@ -340,6 +349,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_down(
   float wt[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) wt[t] = bf16_to_f32(wts[r.pair[t]]);
+  const bool dups = r.all != first_per_token(r.all);    // uniform: some token lists this expert twice
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int na = 2 * (p0 + i);
@@ -356,8 +366,17 @@ __global__ __launch_bounds__(kThreads) void k_moe_down(
             ya = rb(ya + bf16_to_f32(bd[na]));
             yb = rb(yb + bf16_to_f32(bd[na + 1]));
           }
-          const uint32_t packed = (uint32_t)f32_to_bf16(ya * wt[t]) | ((uint32_t)f32_to_bf16(yb * wt[t]) << 16);
-          *reinterpret_cast<uint32_t*>(yw + (long long)r.pair[t] * kH + na) = packed;
+          if (!dups) {
+            *reinterpret_cast<uint32_t*>(yw + (long long)r.pair[t] * kH + na) = pack_bf16x2(ya * wt[t], yb * wt[t]);
+          } else {
+            const uint32_t dm = token_dup_mask(r.all, r.pair[t]);
+            for (int k = 0; k < 4; ++k)
+              if ((dm >> k) & 1) {
+                const int q = (r.pair[t] & ~3) + k;
+                const float wq = bf16_to_f32(wts[q]);
+                *reinterpret_cast<uint32_t*>(yw + (long long)q * kH + na) = pack_bf16x2(ya * wq, yb * wq);
+              }
+          }
         }
       }
     }

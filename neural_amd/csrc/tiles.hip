@@ -266,12 +266,14 @@ NA_DEVICE void store_row_pairs(uint16_t* row_ptr, uint16_t v, bool ok) {
 }
 
 // Route of a decode batch (same rule as the store-layout kernels): the `item`-th distinct expert in first-appearance
-// order; returns its id (or -1: no such item; 128: an invalid id), nt = its number of pairs and `users` = the mask
-// of its pairs (bit p = pair p = 4 token + k; pair_at(users, m) is the m-th in ascending order).  `valid` = distinct
-// experts with a valid id (the invalid marker 128 excluded).  Pair lists stay masks in scalar registers: an indexed
-// register array would be placed in scratch memory.
-NA_DEVICE int route_t950(const int64_t* ids, int npairs, int item, int& nt, uint64_t& users, int& distinct,
-                         int& valid) {
+// order; returns its id (or -1: no such item; 128: an invalid id), `all` = the mask of its pairs (bit p = pair
+// p = 4 token + k), `users` = the first of them per token (first_per_token) and nt = their number (the tokens routed
+// to the expert, <= B); pair_at(users, m) is the m-th user in ascending order.  The MFMA rows are the users; each
+// result is written to every pair of its token in `all`.  `valid` = distinct experts with a valid id (the invalid
+// marker 128 excluded).  Pair lists stay masks in scalar registers: an indexed register array would be placed in
+// scratch memory.
+NA_DEVICE int route_t950(const int64_t* ids, int npairs, int item, int& nt, uint64_t& users, uint64_t& all,
+                         int& distinct, int& valid) {
   const int lane = threadIdx.x & 63;
   int my = 129;
   if (lane < npairs) {
@@ -288,14 +290,19 @@ NA_DEVICE int route_t950(const int64_t* ids, int npairs, int item, int& nt, uint
   distinct = __popcll(fm);
   valid = __popcll(__ballot(lane < npairs && !dup && my != 128));
   users = 0;
+  all = 0;
   nt = 0;
   if (item >= distinct) return -1;
   for (int i = 0; i < item; ++i) fm &= fm - 1;
   const int e = __builtin_amdgcn_readlane(my, __ffsll((long long)fm) - 1);
-  users = __ballot(lane < npairs && my == e);
+  all = __ballot(lane < npairs && my == e);
+  users = first_per_token(all);
   nt = min(__popcll(users), kMaxTokT);
   return e;
 }
+
+// The pairs of user pair p's token that `all` routes to the same expert, as a 4-bit mask over the ranks k.
+NA_DEVICE uint32_t token_dups(uint64_t all, int p) { return (uint32_t)(all >> (p & ~3)) & 0xFu; }
 
 // The m-th pair (ascending) of a route's mask, 0 <= m < kMaxTokT; the mask is uniform, the walk is scalar.
 NA_DEVICE int pair_at(uint64_t users, int m) {
@@ -308,6 +315,41 @@ NA_DEVICE int pair_at(uint64_t users, int m) {
     p = (t == m) ? pt : p;
   }
   return p;
+}
+
+// The duplicate pairs' rows: for D row m < nt (user pair p), the same values v[r] also go to every other pair of
+// p's token that `all` routes to the expert (row stride `stride` elements, columns 16b .. 16b + 15).  All lanes call
+// it.  Kept out of line of the common path, which stores only the users' rows.
+__device__ __noinline__ void dup_rows_store(uint16_t* base, int stride, uint64_t users, uint64_t all, int nt, int b,
+                                            uint16_t v0, uint16_t v1, uint16_t v2, uint16_t v3) {
+  const int lane = threadIdx.x & 63;
+  const uint16_t v[4] = {v0, v1, v2, v3};
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * (lane >> 4) + r;
+    const int p = pair_at(users, min(m, nt - 1));
+    const uint32_t dm = token_dups(all, p) & ~(1u << (p & 3));
+    for (int k = 0; k < 4; ++k)
+      store_row_pairs(base + (long long)((p & ~3) + k) * stride + 16 * b, v[r], m < nt && ((dm >> k) & 1));
+  }
+}
+
+// As dup_rows_store for the down outputs: pair q gets bf16(y[r] x w[q]) with its own routing weight.
+__device__ __noinline__ void dup_rows_store_w(uint16_t* yw, uint64_t users, uint64_t all, int nt, int b, float y0,
+                                              float y1, float y2, float y3, const uint16_t* wts) {
+  const int lane = threadIdx.x & 63;
+  const float y[4] = {y0, y1, y2, y3};
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * (lane >> 4) + r;
+    const int p = pair_at(users, min(m, nt - 1));
+    const uint32_t dm = token_dups(all, p) & ~(1u << (p & 3));
+    for (int k = 0; k < 4; ++k) {
+      const int q = (p & ~3) + k;
+      store_row_pairs(yw + (long long)q * kH + 16 * b, f32_to_bf16(y[r] * bf16_to_f32(wts[q])),
+                      m < nt && ((dm >> k) & 1));
+    }
+  }
 }
 
 // LDS of one expert-major decode workgroup: staged x (or h) rows, scale rows, the KS partial D tiles.
@@ -331,8 +373,8 @@ __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
   constexpr int NTH = 64 * KS;
   __shared__ DecodeLds<KS, XT> L;
   int nt, distinct, valid;
-  uint64_t users;
-  const int e = route_t950(ids, 4 * B, blockIdx.x, nt, users, distinct, valid);
+  uint64_t users, all;
+  const int e = route_t950(ids, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
   if (e < 0 || e == 128) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.y;
@@ -379,6 +421,7 @@ __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
       au += L.red[w][1][lane];
     }
   }
+  uint16_t hv[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int m = 4 * (lane >> 4) + r;
@@ -387,9 +430,10 @@ __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
       gb = rb(gb + bf16_to_f32(bgj));
       ub = rb(ub + bf16_to_f32(buj));
     }
-    const uint16_t hv = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
-    store_row_pairs(h + (long long)pair_at(users, min(m, nt - 1)) * kI + 16 * b, hv, m < nt);
+    hv[r] = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
+    store_row_pairs(h + (long long)pair_at(users, min(m, nt - 1)) * kI + 16 * b, hv[r], m < nt);
   }
+  if (all != users) dup_rows_store(h, kI, users, all, nt, b, hv[0], hv[1], hv[2], hv[3]);   // uniform, rare
 }
 
 // down, expert-major: output block b (rows n = 16b .. 16b + 15) of the item-th distinct expert from each routed
@@ -404,14 +448,16 @@ __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
   constexpr int NTH = 64 * KS;
   __shared__ DecodeLds<KS, XT> L;
   int nt, distinct, valid;
-  uint64_t users;
-  const int e = route_t950(ids, 4 * B, blockIdx.x, nt, users, distinct, valid);
+  uint64_t users, all;
+  const int e = route_t950(ids, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
   if (e < 0) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.y;
-  if (e == 128) {                                      // invalid id: its pairs contribute +0
-    for (int i = 2 * tid; i < nt * kTRows; i += 2 * NTH)
-      *reinterpret_cast<uint32_t*>(yw + (long long)pair_at(users, i / kTRows) * kH + 16 * b + (i % kTRows)) = 0u;
+  if (e == 128) {                                      // invalid ids: each of their pairs contributes +0
+    for (int i = tid; i < 4 * B * (kTRows / 2); i += NTH) {
+      const int q = i / (kTRows / 2), c = i - q * (kTRows / 2);
+      if ((all >> q) & 1) *reinterpret_cast<uint32_t*>(yw + (long long)q * kH + 16 * b + 2 * c) = 0u;
+    }
     return;
   }
   const long long gid = expert_base + e;
@@ -445,14 +491,17 @@ __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
 #pragma unroll
     for (int w = 1; w < KS; ++w) acc += L.red[w][0][lane];
   }
+  float yb[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int m = 4 * (lane >> 4) + r;
-    const int p = pair_at(users, min(m, nt - 1));
     float y = rb(acc[r]);
     if (bias_dn) y = rb(y + bf16_to_f32(bdn));
-    store_row_pairs(yw + (long long)p * kH + 16 * b, f32_to_bf16(y * bf16_to_f32(wr[r])), m < nt);
+    yb[r] = y;
+    store_row_pairs(yw + (long long)pair_at(users, min(m, nt - 1)) * kH + 16 * b,
+                    f32_to_bf16(y * bf16_to_f32(wr[r])), m < nt);
   }
+  if (all != users) dup_rows_store_w(yw, users, all, nt, b, yb[0], yb[1], yb[2], yb[3], wts);   // uniform, rare
 }
 
 __global__ __launch_bounds__(256) void k_combine_t950(const uint32_t* __restrict__ yw, int B, uint32_t* __restrict__ out) {
@@ -499,8 +548,8 @@ __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
   const int b = blockIdx.x;
   const int npairs = 4 * B;
   int nt, distinct, valid;
-  uint64_t users;
-  const int e = route_t950(ids, npairs, g, nt, users, distinct, valid);
+  uint64_t users, all;
+  const int e = route_t950(ids, npairs, g, nt, users, all, distinct, valid);
   const bool live = e >= 0 && e != 128;
   const long long gid = expert_base + (live ? e : 0);
   // groups without a live expert load slot 0's block (valid memory) with every tile slot zeroed, so that the loads
@@ -523,8 +572,9 @@ __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
   __builtin_amdgcn_sched_barrier(0);
   x_store<4 * XT, NTH>(tid, L.hs, npairs, xr);
   scale_store<1, GTH>(gtid, L.sc + g * kScLds, sr);
-  if (e == 128 && kw == 0) {                             // invalid id: its pairs contribute +0
-    for (int i = lane; i < nt * kTRows; i += 64) L.yw[pair_at(users, i / kTRows)][i % kTRows] = 0.f;
+  if (e == 128 && kw == 0) {                             // invalid ids: each of their pairs contributes +0
+    for (int i = lane; i < npairs * kTRows; i += 64)
+      if ((all >> (i / kTRows)) & 1) L.yw[i / kTRows][i % kTRows] = 0.f;
   }
   __syncthreads();
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -542,7 +592,14 @@ __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
       if (m < nt) {
         float y = rb(acc[r]);
         if (bias_dn) y = rb(y + bf16_to_f32(bdn));
-        L.yw[pair_at(users, m)][lane & 15] = rb(y * bf16_to_f32(wr[r]));
+        const int p = pair_at(users, m);
+        if (all == users) {                              // uniform: no token lists this expert twice
+          L.yw[p][lane & 15] = rb(y * bf16_to_f32(wr[r]));
+        } else {
+          const uint32_t dm = token_dups(all, p);
+          for (int k = 0; k < 4; ++k)
+            if ((dm >> k) & 1) L.yw[(p & ~3) + k][lane & 15] = rb(y * bf16_to_f32(wts[(p & ~3) + k]));
+        }
       }
     }
   }
@@ -553,6 +610,171 @@ __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
 #pragma unroll
     for (int k = 0; k < 4; ++k) a += L.yw[4 * t + k][c];
     out[(long long)t * kH + 16 * b + c] = f32_to_bf16(a);
+  }
+}
+
+// ------------------------------------------------------------------------- one launch per layer (one token)
+// gate_up and down + combine of one token's top-4 experts in a single launch: 180 workgroups, one per 16-row output
+// block b, of 16 waves = 4 subgroups of 4 waves; subgroup s serves pair s (the token's s-th routed expert) and its
+// waves split K as in the expert-major kernels.  Phase 1: gate_up rows j = 16b .. 16b + 15 (gate block b, up block
+// b + 180) -> h[s][j] with device-coherent stores.  The workgroup then arrives at a grid-wide barrier, and before
+// waiting it issues the loads of its down block's codes and scales, so that the down weights stream while the last
+// workgroups finish phase 1.  Phase 2: down rows n = 16b .. 16b + 15 of each pair from its h row (device-coherent
+// loads), + bias, x routing weight, and the top-4 sum in pair order -> out[n].  The arithmetic is the two-launch
+// path's (k_moe_gate_up_t950 + k_moe_down_comb_t950) step for step, so the results are identical.
+// The barrier needs all 180 workgroups resident at once (the host checks the occupancy before launching).  Its wait
+// is bounded: past spin_limit polls a workgroup sets sync[2] and goes on (the outputs are then undefined; the kernel
+// still ends).  The last workgroup to leave resets sync[0] and sync[1], so a completed launch leaves them zero.
+constexpr int kLwWaves = 16, kLwKS = 4;
+constexpr int kLwHWords = 4 * kI / 2;                  // h of the 4 pairs as bf16 pairs
+
+union LayerLds {
+  struct {
+    __align__(16) uint8_t xs[kXPitch];
+    __align__(16) uint8_t sc[4][2 * kScLds];
+    f32x4_t red[kLwWaves][2][64];
+  } p1;
+  struct {
+    __align__(16) uint8_t hs[4 * kXPitch];
+    __align__(16) uint8_t sc[4][kScLds];
+    f32x4_t red[kLwWaves][64];
+    float yw[4][kTRows];
+  } p2;
+};
+
+__global__ __launch_bounds__(64 * kLwWaves) void k_moe_layer_t950(
+    const uint16_t* __restrict__ x, const int64_t* __restrict__ ids, const uint16_t* __restrict__ wts,
+    const uint8_t* __restrict__ pool, long long slot_bytes, const int64_t* __restrict__ slot_tab,
+    long long expert_base, const uint16_t* __restrict__ bias_gu, const uint16_t* __restrict__ bias_dn,
+    uint32_t* __restrict__ hbuf, uint32_t* __restrict__ sync, int spin_limit, uint16_t* __restrict__ out,
+    float alpha, float limit) {
+  constexpr int MT = (kTTiles + kLwKS - 1) / kLwKS;
+  constexpr int NTH = 64 * kLwWaves, STH = 64 * kLwKS;
+  constexpr int HP = (kLwHWords + NTH - 1) / NTH;
+  __shared__ LayerLds L;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int s = wave / kLwKS, kw = wave - s * kLwKS, stid = tid - s * STH;
+  const int b = blockIdx.x;
+  const long long v = ids[s];
+  const bool live = v >= 0 && v < 128;
+  const long long gid = expert_base + (live ? v : 0);
+  // a dead pair (invalid id) loads slot 0's blocks (valid memory) with every tile slot zeroed and computes nothing
+  const long long slot = live ? (slot_tab ? slot_tab[gid] : gid) : 0;
+  const uint8_t* sbase = pool + slot * slot_bytes;
+  const uint8_t* gblk = sbase + (long long)b * kTBlock;
+  const uint8_t* ublk = gblk + (long long)kTUpBlock0 * kTBlock;
+  const uint8_t* dblk = sbase + kTDownOff + (long long)b * kTBlock;
+  int t0, t1;
+  ktile_range<kLwKS>(kw, t0, t1);
+  const int t1l = live ? t1 : t0;
+
+  // ---- phase 1: gate_up + bias + clamped SwiGLU of pair s, rows 16b .. 16b + 15
+  ScaleRegs<2, STH> sr;
+  scale_load<2, STH>(stid, gblk, ublk, sr);
+  XRegs<1, NTH> xr;
+  x_load<1, NTH>(tid, x, kH, [](int) { return 0; }, 1, xr);
+  const int j = 16 * b + (lane & 15);
+  const uint16_t* bgs = bias_gu ? bias_gu + gid * kGU : x;         // unconditional loads (x when there is no bias)
+  const uint16_t bgj = bgs[bias_gu ? j : 0], buj = bgs[bias_gu ? kI + j : 0];
+  CodeRegs<MT> rg, ru;
+  code_load<MT>(gblk, lane, t0, t1l, rg);
+  code_load<MT>(ublk, lane, t0, t1l, ru);
+  __builtin_amdgcn_sched_barrier(0);
+  x_store<1, NTH>(tid, L.p1.xs, 1, xr);
+  scale_store<2, STH>(stid, L.p1.sc[s], sr);
+  __syncthreads();
+  f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+  if (live) {
+    const uint8_t* srow = L.p1.sc[s] + (lane & 15) * kScPitch;
+    block_compute<MT>(rg, srow, L.p1.xs, lane, t0, t1, ag);
+    block_compute<MT>(ru, srow + kScLds, L.p1.xs, lane, t0, t1, au);
+  }
+  L.p1.red[wave][0][lane] = ag;
+  L.p1.red[wave][1][lane] = au;
+  __syncthreads();
+  if (kw == 0) {                                         // wave-uniform: the subgroup's first wave
+    ag = L.p1.red[wave][0][lane];
+    au = L.p1.red[wave][1][lane];
+#pragma unroll
+    for (int w = 1; w < kLwKS; ++w) {
+      ag += L.p1.red[wave + w][0][lane];
+      au += L.p1.red[wave + w][1][lane];
+    }
+    float gb = rb(ag[0]), ub = rb(au[0]);                // lanes 0..15: D row 0 (the token), column lane
+    if (bias_gu) {
+      gb = rb(gb + bf16_to_f32(bgj));
+      ub = rb(ub + bf16_to_f32(buj));
+    }
+    const uint16_t hv = live ? f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit)) : (uint16_t)0;
+    const uint32_t hi = (uint32_t)__shfl_xor((int)hv, 1) & 0xffff;
+    if (lane < 16 && !(lane & 1))
+      __hip_atomic_store(hbuf + s * (kI / 2) + (16 * b + lane) / 2, (uint32_t)hv | (hi << 16), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);                         // this wave's h stores are complete
+  __syncthreads();                                       // (and phase 1's LDS is free for phase 2)
+  if (tid == 0) __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // ---- the down block's weights, issued before the wait
+  ScaleRegs<1, STH> sd;
+  scale_load<1, STH>(stid, dblk, dblk, sd);
+  const int n = 16 * b + (lane & 15);
+  const uint16_t bdn = (bias_dn ? bias_dn + gid * kH : wts)[bias_dn ? n : 0];   // unconditional load
+  const uint16_t wv = wts[s];
+  CodeRegs<MT> rd;
+  code_load<MT>(dblk, lane, t0, t1l, rd);
+  __builtin_amdgcn_sched_barrier(0);
+  if (tid == 0) {
+    int it = 0;
+    while (__hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gridDim.x) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++it > spin_limit) {
+        __hip_atomic_store(sync + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2: every pair's h row (device-coherent loads, all issued before the LDS stores), down, combine
+  uint32_t hw[HP];
+#pragma unroll
+  for (int k = 0; k < HP; ++k)
+    hw[k] = __hip_atomic_load(hbuf + min(tid + NTH * k, kLwHWords - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int k = 0; k < HP; ++k) {
+    const int i = tid + NTH * k;
+    if (i < kLwHWords) {
+      const int p = i / (kI / 2), c = i - p * (kI / 2);
+      *reinterpret_cast<uint32_t*>(L.p2.hs + p * kXPitch + 4 * c) = hw[k];
+    }
+  }
+  scale_store<1, STH>(stid, L.p2.sc[s], sd);
+  __syncthreads();
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  if (live) block_compute<MT>(rd, L.p2.sc[s] + (lane & 15) * kScPitch, L.p2.hs + s * kXPitch, lane, t0, t1, acc);
+  L.p2.red[wave][lane] = acc;
+  __syncthreads();
+  if (kw == 0 && lane < 16) {
+#pragma unroll
+    for (int w = 1; w < kLwKS; ++w) acc += L.p2.red[wave + w][lane];
+    float y = rb(acc[0]);
+    if (bias_dn) y = rb(y + bf16_to_f32(bdn));
+    L.p2.yw[s][lane] = live ? rb(y * bf16_to_f32(wv)) : 0.f;
+  }
+  __syncthreads();
+  if (tid < kTRows) {
+    float a = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a += L.p2.yw[k][tid];
+    out[16 * b + tid] = f32_to_bf16(a);
+  }
+  if (tid == 0) {
+    const uint32_t done = __hip_atomic_fetch_add(sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == gridDim.x - 1) {
+      __hip_atomic_store(sync, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(sync + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -576,7 +798,8 @@ static GateUpT gate_up_t950_xt(int xt) {
        : xt == 4 ? k_moe_gate_up_t950<KS, 4> : k_moe_gate_up_t950<KS, 8>;
 }
 static GateUpT pick_gate_up_t950(int ks, int xt) {
-  return ks == 1 ? gate_up_t950_xt<1>(xt) : ks == 2 ? gate_up_t950_xt<2>(xt) : gate_up_t950_xt<4>(xt);
+  return ks == 1 ? gate_up_t950_xt<1>(xt) : ks == 2 ? gate_up_t950_xt<2>(xt)
+       : ks == 4 ? gate_up_t950_xt<4>(xt) : gate_up_t950_xt<8>(xt);
 }
 template <int KS>
 static DownT down_t950_xt(int xt) {
@@ -584,7 +807,8 @@ static DownT down_t950_xt(int xt) {
        : xt == 4 ? k_moe_down_t950<KS, 4> : k_moe_down_t950<KS, 8>;
 }
 static DownT pick_down_t950(int ks, int xt) {
-  return ks == 1 ? down_t950_xt<1>(xt) : ks == 2 ? down_t950_xt<2>(xt) : down_t950_xt<4>(xt);
+  return ks == 1 ? down_t950_xt<1>(xt) : ks == 2 ? down_t950_xt<2>(xt)
+       : ks == 4 ? down_t950_xt<4>(xt) : down_t950_xt<8>(xt);
 }
 
 }  // namespace na
@@ -630,7 +854,7 @@ int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
   if (B > 8) return kErrTooLarge;
   if (slot_bytes < kTSlot || (slot_bytes & 15) || (reinterpret_cast<uintptr_t>(pool) & 15)) return kErrArgs;
   if (k_split <= 0) k_split = 4;
-  if (k_split != 1 && k_split != 2 && k_split != 4) return kErrArgs;
+  if (k_split != 1 && k_split != 2 && k_split != 4 && k_split != 8) return kErrArgs;
   // down_mode 0, B = 1, with an output: gate_up, then down + combine (two launches); else gate_up, down, combine
   // (at B = 2 the row-block kernel's 16-wave workgroups with two waves per expert measured slower than three launches)
   const bool two = down_mode == 0 && out != nullptr && B == 1;
@@ -657,6 +881,34 @@ int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
   if (out)
     launch_t(k_combine_t950, dim3((B * kH / 2 + 255) / 256), dim3(256), stream, ev[4], ev[5],
              (const uint32_t*)yw_scratch, B, (uint32_t*)out);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+// Single-launch decode layer for one token (k_moe_layer_t950).  Needs every one of its 180 workgroups resident at
+// once: the occupancy is checked once per device; a device that cannot hold them gets kErrTooLarge.
+int na_moe_layer_t950(const void* x, const int64_t* topk_ids, const void* topk_w, const void* pool,
+                      long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
+                      const void* bias_dn, void* h_scratch, unsigned int* sync, void* out, float alpha, float limit,
+                      void* const* events, hipStream_t stream) {
+  if (!x || !topk_ids || !topk_w || !pool || !h_scratch || !sync || !out) return kErrArgs;
+  if (slot_bytes < kTSlot || (slot_bytes & 15) || (reinterpret_cast<uintptr_t>(pool) & 15)) return kErrArgs;
+  if (reinterpret_cast<uintptr_t>(h_scratch) & 15) return kErrArgs;
+  static int fits[64];                                   // per device: 0 unknown, 1 fits, -1 does not
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kErrArgs;
+  if (fits[dev] == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_layer_t950, 64 * kLwWaves, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return kErrLaunch;
+    fits[dev] = (long long)per_cu * cus >= kTDownBlocks ? 1 : -1;
+  }
+  if (fits[dev] < 0) return kErrTooLarge;
+  hipEvent_t e0 = events ? (hipEvent_t)events[0] : nullptr, e1 = events ? (hipEvent_t)events[1] : nullptr;
+  launch_t(k_moe_layer_t950, dim3(kTDownBlocks), dim3(64 * kLwWaves), stream, e0, e1, (const uint16_t*)x,
+           topk_ids, (const uint16_t*)topk_w, (const uint8_t*)pool, slot_bytes, slot_tab, expert_base,
+           (const uint16_t*)bias_gu, (const uint16_t*)bias_dn, (uint32_t*)h_scratch, (uint32_t*)sync, 1 << 22,
+           (uint16_t*)out, alpha, limit);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

@@ -234,8 +234,10 @@ def test_down_with_combine_matches_expert_major_path(B):
     tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
     tiles.repack_to_t950(raw, tp)
     tabd, bg, bd = torch.from_numpy(tab).to(dev), bgu.to(dev), bdn.to(dev)
-    two = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=True)
-    three = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=False)
+    two = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=True,
+                          single_launch=False)
+    three = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=False,
+                            single_launch=False)
     assert two.launches(B) == (("gate_up", "down_combine") if B == 1 else ("gate_up", "down", "combine"))
     assert len(three.launches(B)) == 3
     rng = np.random.default_rng(B)
@@ -272,3 +274,137 @@ def test_down_with_combine_matches_expert_major_path(B):
             for name, arr in (("two", a[b]), ("three", c[b])):
                 d = np.abs(arr - want)
                 assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale, (name, call, b, d.max(), scale)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_single_launch_layer_matches_two_launch_path(with_bias):
+    """One token's layer in one launch (gate_up, a grid-wide barrier, down + combine) gives the two-launch path's
+    output bit for bit, over consecutive calls (the barrier words are left at zero), invalid ids (+0 contributions),
+    duplicate ids, and graph replays; and it matches the oracle."""
+    import torch
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
+    dev = _dev()
+    slots, x, ids, w, tab, bgu, bdn = _t950_case(1, 950 + int(with_bias), True, nslot=8)
+    print(f"case single-launch layer bias={with_bias}", flush=True)
+    raw = torch.from_numpy(np.stack(slots)).to(dev)
+    tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
+    tiles.repack_to_t950(raw, tp)
+    tabd = torch.from_numpy(tab).to(dev)
+    bg, bd = (bgu.to(dev), bdn.to(dev)) if with_bias else (None, None)
+    one = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, single_launch=True)
+    two = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd)
+    assert one.launches(1) == ("layer",) and two.launches(1) == ("gate_up", "down_combine")
+    rng = np.random.default_rng(17)
+    cache = {}
+    for call in range(4):
+        idc = ids.copy()
+        if call == 1:
+            idc[0, 1] = -1
+            idc[0, 3] = 200
+        if call == 2:
+            idc[0, 2] = idc[0, 0]                            # the same expert twice
+        xn = synth.bf16_normal(rng, (1, 2880))
+        xd, idd = xn.to(dev), torch.from_numpy(idc).to(dev)
+        wd = torch.from_numpy(w).to(torch.bfloat16).to(dev)
+        layer = 2 + call
+        a = one.forward_decode(layer, xd, idd, wd)
+        c = two.forward_decode(layer, xd, idd, wd)
+        torch.cuda.synchronize()
+        diff = (a.float() - c.float()).abs()
+        assert torch.equal(a, c), (call, int((diff > 0).sum()), float(diff.max()), idc.tolist(),
+                                   torch.nonzero(diff[0] > 0)[:8].flatten().tolist())
+        assert int(one.sync[:3].abs().sum()) == 0, one.sync
+        ys = []
+        for k in range(4):
+            e = int(idc[0, k])
+            if not 0 <= e < 128:
+                ys.append(np.zeros(2880, np.float32))
+                continue
+            g = layer * 128 + e
+            sl = int(tab[g])
+            if sl not in cache:
+                cache[sl] = mo.expert_weights(slots[sl])
+            bgv = bgu[g].float().numpy() if with_bias else np.zeros(5760, np.float32)
+            bdv = bdn[g].float().numpy() if with_bias else np.zeros(2880, np.float32)
+            ys.append(mo.expert_forward_bf16(xn.float().numpy(), None, bgv, bdv, weights=cache[sl])[0])
+        want = mo.combine_bf16(np.stack(ys), w[0])
+        got = a.float().cpu().numpy()[0]
+        d = np.abs(got - want)
+        assert d.max() <= 2e-2 + 1e-2 * np.abs(want).max(), (call, d.max())
+    # graph replays with the routing changed on the device between them
+    xd = synth.bf16_normal(rng, (1, 2880)).to(dev)
+    idd = torch.from_numpy(ids.copy()).to(dev)
+    wd = torch.from_numpy(w).to(torch.bfloat16).to(dev)
+    out = torch.empty(1, 2880, dtype=torch.bfloat16, device=dev)
+    one.forward_decode(5, xd, idd, wd, out=out)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        one.forward_decode(5, xd, idd, wd, out=out)
+    for rep in range(3):
+        idd.copy_(torch.from_numpy(np.roll(ids, rep, axis=1).copy()))
+        gr.replay()
+        torch.cuda.synchronize()
+        want = two.forward_decode(5, xd, idd, wd)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), rep
+    assert int(one.sync[:3].abs().sum()) == 0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B", [1, 2, 8])
+def test_duplicate_ids_in_a_token(B):
+    """A token whose top-4 list names one expert more than once (and an invalid id twice): each pair is that expert's
+    output times its own weight, as the reference's per-pair GEMV computes it.  Every decode path (t950 single
+    launch, two launches, expert-major three launches; store layout) against the oracle, and the t950 paths against
+    each other bit for bit."""
+    import torch
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_T950
+    dev = _dev()
+    slots, x, ids, w, tab, bgu, bdn = _t950_case(B, 1200 + B, True, nslot=8)
+    print(f"case duplicate ids B={B}", flush=True)
+    ids = ids.copy()
+    ids[0, 2] = ids[0, 0]
+    if B >= 2:
+        ids[1, :] = ids[1, 1]                                # one expert four times
+    if B >= 8:
+        ids[7] = [200, ids[7, 1], 200, ids[7, 1]]          # an invalid id twice and a valid one twice
+    raw = torch.from_numpy(np.stack(slots)).to(dev)
+    tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
+    tiles.repack_to_t950(raw, tp)
+    tabd, bg, bd = torch.from_numpy(tab).to(dev), bgu.to(dev), bdn.to(dev)
+    paths = {"single": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, single_launch=True),
+             "two": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd),
+             "three": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, combine_in_down=False),
+             "store": ResidentExperts(raw, GPTOSS_LAYOUT, bg, bd, tabd)}
+    xd, idd = x.to(dev), torch.from_numpy(ids).to(dev)
+    wd = torch.from_numpy(w).to(torch.bfloat16).to(dev)
+    layer = 4
+    got = {nm: rx.forward_decode(layer, xd, idd, wd).float().cpu().numpy() for nm, rx in paths.items()}
+    torch.cuda.synchronize()
+    if B == 1:
+        assert np.array_equal(got["single"], got["two"]) and np.array_equal(got["two"], got["three"])
+    else:
+        assert np.array_equal(got["single"], got["three"])
+    cache = {}
+    for b in range(B):
+        ys = []
+        for k in range(4):
+            e = int(ids[b, k])
+            if not 0 <= e < 128:
+                ys.append(np.zeros(2880, np.float32))
+                continue
+            g = layer * 128 + e
+            s = int(tab[g])
+            if s not in cache:
+                cache[s] = mo.expert_weights(slots[s])
+            ys.append(mo.expert_forward_bf16(x[b:b + 1].float().numpy(), None, bgu[g].float().numpy(),
+                                             bdn[g].float().numpy(), weights=cache[s])[0])
+        want = mo.combine_bf16(np.stack(ys), w[b])
+        scale = np.abs(want).max()
+        for nm, arr in got.items():
+            d = np.abs(arr[b] - want)
+            assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale, (nm, b, d.max(), scale)
