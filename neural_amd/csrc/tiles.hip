@@ -408,6 +408,36 @@ __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
   f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
   block_compute<MT>(rg, srow, xrow, lane, t0, t1, ag);
   block_compute<MT>(ru, srow + kScLds, xrow, lane, t0, t1, au);
+  if constexpr (XT == 1) {
+    // one token: only D row 0 (element 0 of lanes 0..15) is used; the same sums in the same order as below
+    if constexpr (KS > 1) {
+      float* red = reinterpret_cast<float*>(&L.red[0][0][0]);    // [KS][2][16]
+      if (lane < 16) {
+        red[(2 * wave) * 16 + lane] = ag[0];
+        red[(2 * wave + 1) * 16 + lane] = au[0];
+      }
+      __syncthreads();
+      if (wave != 0) return;
+      const int l = lane & 15;
+      float g = red[l], u = red[16 + l];
+#pragma unroll
+      for (int w = 1; w < KS; ++w) {
+        g += red[(2 * w) * 16 + l];
+        u += red[(2 * w + 1) * 16 + l];
+      }
+      ag[0] = g;
+      au[0] = u;
+    }
+    float gb = rb(ag[0]), ub = rb(au[0]);
+    if (bg) {
+      gb = rb(gb + bf16_to_f32(bgj));
+      ub = rb(ub + bf16_to_f32(buj));
+    }
+    const uint16_t hv0 = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
+    store_row_pairs(h + (long long)pair_at(users, 0) * kI + 16 * b, hv0, lane < 16);
+    if (all != users) dup_rows_store(h, kI, users, all, nt, b, hv0, hv0, hv0, hv0);   // uniform, rare
+    return;
+  }
   if constexpr (KS > 1) {
     L.red[wave][0][lane] = ag;
     L.red[wave][1][lane] = au;
@@ -581,24 +611,45 @@ __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
   const int pm = live ? pair_at(users, min(lane & 15, nt - 1)) : 0;   // A row of token slot m = lane % 16
   if (live)
     block_compute<MT>(rd, L.sc + g * kScLds + (lane & 15) * kScPitch, L.hs + pm * kXPitch, lane, t0, t1, acc);
-  L.red[wave][lane] = acc;
-  __syncthreads();
-  if (live && kw == 0) {
+  if constexpr (XT == 1) {
+    // one token: nt <= 1, only D row 0 (element 0 of lanes 0..15) is used; the same sums in the same order
+    float* red = reinterpret_cast<float*>(&L.red[0][0]);   // [kDcWaves][16]
+    if (lane < 16) red[wave * 16 + lane] = acc[0];
+    __syncthreads();
+    if (live && kw == 0 && lane < 16) {
 #pragma unroll
-    for (int w = 1; w < KSD; ++w) acc += L.red[wave + w][lane];
+      for (int w = 1; w < KSD; ++w) acc[0] += red[(wave + w) * 16 + lane];
+      float y = rb(acc[0]);
+      if (bias_dn) y = rb(y + bf16_to_f32(bdn));
+      const int p = pair_at(users, 0);
+      if (all == users) {                                // uniform: no token lists this expert twice
+        L.yw[p][lane] = rb(y * bf16_to_f32(wr[0]));
+      } else {
+        const uint32_t dm = token_dups(all, p);
+        for (int k = 0; k < 4; ++k)
+          if ((dm >> k) & 1) L.yw[(p & ~3) + k][lane] = rb(y * bf16_to_f32(wts[(p & ~3) + k]));
+      }
+    }
+  } else {
+    L.red[wave][lane] = acc;
+    __syncthreads();
+    if (live && kw == 0) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 4 * (lane >> 4) + r;
-      if (m < nt) {
-        float y = rb(acc[r]);
-        if (bias_dn) y = rb(y + bf16_to_f32(bdn));
-        const int p = pair_at(users, m);
-        if (all == users) {                              // uniform: no token lists this expert twice
-          L.yw[p][lane & 15] = rb(y * bf16_to_f32(wr[r]));
-        } else {
-          const uint32_t dm = token_dups(all, p);
-          for (int k = 0; k < 4; ++k)
-            if ((dm >> k) & 1) L.yw[(p & ~3) + k][lane & 15] = rb(y * bf16_to_f32(wts[(p & ~3) + k]));
+      for (int w = 1; w < KSD; ++w) acc += L.red[wave + w][lane];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 4 * (lane >> 4) + r;
+        if (m < nt) {
+          float y = rb(acc[r]);
+          if (bias_dn) y = rb(y + bf16_to_f32(bdn));
+          const int p = pair_at(users, m);
+          if (all == users) {                              // uniform: no token lists this expert twice
+            L.yw[p][lane & 15] = rb(y * bf16_to_f32(wr[r]));
+          } else {
+            const uint32_t dm = token_dups(all, p);
+            for (int k = 0; k < 4; ++k)
+              if ((dm >> k) & 1) L.yw[(p & ~3) + k][lane & 15] = rb(y * bf16_to_f32(wts[(p & ~3) + k]));
+          }
         }
       }
     }
