@@ -189,11 +189,14 @@ __global__ __launch_bounds__(256) void k_decode_attn(
       m_run[r] = m_new[r];
       acc[r] *= alpha[r];
     }
+    const int nks = (min(kSub, c1 - k0) + 31) / 32;     // 32-key steps holding live keys (P is 0 past c1)
 #pragma unroll
     for (int ks = 0; ks < kSub / 32; ++ks) {
-      const uint4 pa = *reinterpret_cast<const uint4*>(L.p + n * kPPitch + 2 * (32 * ks + 8 * g));
-      const uint4 vb = *reinterpret_cast<const uint4*>(L.vt + (16 * wave + n) * kVtPitch + 2 * (32 * ks + 8 * g));
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pa), as_bf16x8(vb), acc, 0, 0, 0);
+      if (ks < nks) {                                  // uniform
+        const uint4 pa = *reinterpret_cast<const uint4*>(L.p + n * kPPitch + 2 * (32 * ks + 8 * g));
+        const uint4 vb = *reinterpret_cast<const uint4*>(L.vt + (16 * wave + n) * kVtPitch + 2 * (32 * ks + 8 * g));
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pa), as_bf16x8(vb), acc, 0, 0, 0);
+      }
     }
     __syncthreads();                               // LDS is rewritten by the next sub-chunk
   }
