@@ -141,6 +141,28 @@ int na_decode_attention(const void* q, const void* kc, const void* vc, long long
                         const int64_t* pos, void* out, int B, float scaling, int window, int ring, int n_split,
                         float* work, unsigned int* counters, void* const* events, hipStream_t stream);
 
+/* Prompt attention of T tokens at positions p0 .. p0+T-1 (causal, sliding window when window > 0, learned sinks).
+ * Replaces fused_core.py:684-759 (k_prefill_attn), entry :762-784 (prefill_attention).
+ *   q        bf16 [T, 64, 64] (RoPE applied), contiguous; out bf16 [T, 64, 64]; sinks bf16 [64]
+ *   ring = 0 kc, vc bf16 [8, cache_rows, 64] already holding positions < p0 + T (p0 + T <= cache_rows); k_new/v_new
+ *            unused
+ *   ring > 0 (window > 0, ring >= window, cache_rows == ring) kc, vc are the rolling cache holding positions
+ *            p0-ring .. p0-1 in rows j % ring; k_new, v_new bf16 [T, 8, 64] with element strides (sk_t, sk_h) and
+ *            (sv_t, sv_h), multiples of 8, last dimension contiguous, are the block's own K / V.  The ring is not
+ *            updated: call na_ring_write after the attention.
+ *   events   NULL or 2 hipEvent_t (start/stop of the launch)
+ * Ring and linear mode give bit-identical outputs for the same key values.  T = 0 launches nothing and returns 0
+ * (the pointers of an empty prompt may be NULL). */
+int na_prefill_attention(const void* q, const void* kc, const void* vc, long long cache_rows, const void* k_new,
+                         const void* v_new, long long sk_t, long long sk_h, long long sv_t, long long sv_h,
+                         const void* sinks, void* out, long long p0, int T, float scaling, int window, int ring,
+                         void* const* events, hipStream_t stream);
+
+/* The last min(T, ring) positions of a block (K / V rows [T, 8, 64] with element strides as above) into their ring
+ * slots position % ring of kc, vc [8, ring, 64].  Replaces fused_core.py:787-800 (ring_write). */
+int na_ring_write(void* kc, void* vc, int ring, const void* k_new, const void* v_new, long long sk_t, long long sk_h,
+                  long long sv_t, long long sv_h, long long p0, int T, hipStream_t stream);
+
 /* ---- prefill (prompt) products */
 
 /* out[e][m][n] = bf16(sum_k x[m][k] w_e[n][k]) for e < E (weights of slot slots[e]), m < M.  Replaces

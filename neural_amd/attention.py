@@ -1,6 +1,7 @@
-"""GQA decode attention with learned sinks on MI355X: the call surface of the reference's fused_core.py attention
-helpers (decode_attention, SplitAttn, ring_write, ring_reuse_ok; reference fused_core.py:63, 336-398, 787-820), backed
-by the HIP kernel of neural_amd/csrc/attention.hip through the C ABI.
+"""GQA attention with learned sinks on MI355X: the call surface of the reference's fused_core.py attention helpers
+(decode_attention, SplitAttn, prefill_attention, ring_write, ring_reuse_ok; reference fused_core.py:63, 336-398,
+684-820), backed by the HIP kernels of neural_amd/csrc/attention.hip (decode) and neural_amd/csrc/prefill_attn.hip
+(prompt attention, ring write) through the C ABI.
 
 Shapes (reference fused_core.py:63): NQ = 64 query heads, NKV = 8 KV heads, HD = 64, REP = 8.  One decode query per
 sequence: q [NQ*HD] bf16 (RoPE applied), K/V caches [1, NKV, S, HD] bf16 (S = smax, or the ring size on sliding
@@ -110,20 +111,81 @@ def decode_attention_batched(q, kc, vc, sinks, pos_dev, out, scaling, sliding=0,
     return out
 
 
+def _rows_ok(t):
+    """[T, NKV, HD] bf16 on CUDA with a contiguous last dimension, 16-byte aligned rows and element strides that are
+    multiples of 8 (what the kernels' 16-byte row loads need)."""
+    return (t.dtype is torch.bfloat16 and t.dim() == 3 and t.shape[1:] == (NKV, HD) and t.stride(-1) == 1
+            and t.stride(0) % 8 == 0 and t.stride(1) % 8 == 0 and t.data_ptr() % 16 == 0)
+
+
+def _as_rows(t):
+    return t if _rows_ok(t) else t.contiguous()
+
+
+def prefill_attention(q, kc, vc, sinks, p0, scaling, sliding, smax, BM=64, BN=64, k_new=None, v_new=None, ring=0,
+                      out=None, events=None):
+    """Prompt attention (reference fused_core.py:684-784): q [T, NQ, HD] bf16 (contiguous, RoPE applied) for positions
+    p0 .. p0+T-1 -> o [T, NQ, HD] bf16.  Causal, sliding window when ``sliding`` > 0, learned sinks.
+
+    ring = 0: kc / vc are the linear cache [1, NKV, smax, HD] ALREADY holding the block's K / V at p0 .. p0+T-1
+              (k_new / v_new ignored).
+    ring = R: sliding layers only; kc / vc are the rolling cache [1, NKV, R, HD] holding positions p0-R .. p0-1 (those
+              that exist) and k_new / v_new [T, NKV, HD] (last dim contiguous) are the block's own K / V.  T may exceed
+              R.  The ring is not updated here: call ring_write(kc, vc, k_new, v_new, p0, R) after the attention.
+    Ring and linear mode give bit-identical outputs for the same key values.  ``BM`` / ``BN`` (the reference's Triton
+    tiling) are accepted and have no effect: the kernel's tiling is fixed (32 queries x 8 heads per workgroup, 64-key
+    tiles).  One launch on the current stream, no allocation beyond ``out`` (allocated when None), no host sync."""
+    bf = torch.bfloat16
+    T = q.shape[0]
+    if q.dtype is not bf or q.dim() != 3 or q.shape[1:] != (NQ, HD) or not q.is_contiguous():
+        raise AssertionError(f"q must be contiguous bf16 [T, {NQ}, {HD}]")
+    for t, nm in ((kc, "kc"), (vc, "vc"), (sinks, "sinks")):
+        if t.dtype is not bf or not t.is_contiguous() or t.device != q.device:
+            raise AssertionError(f"{nm} must be contiguous bf16 on the query's device")
+    if sinks.numel() != NQ:
+        raise AssertionError(f"sinks must hold {NQ} values")
+    rows = int(ring) if ring else int(smax)
+    if kc.shape != (1, NKV, rows, HD) or vc.shape != kc.shape:
+        raise AssertionError(f"kc/vc must be [1, {NKV}, {rows}, {HD}] (shape {tuple(kc.shape)})")
+    p0 = int(p0)
+    if ring:
+        if not sliding or int(ring) < int(sliding):
+            raise AssertionError(f"a ring cache needs a sliding layer and ring >= window ({sliding}, {ring})")
+        if k_new is None or v_new is None or k_new.shape != (T, NKV, HD) or v_new.shape != (T, NKV, HD):
+            raise AssertionError(f"k_new/v_new must be [{T}, {NKV}, {HD}]")
+        if k_new.stride(-1) != 1 or v_new.stride(-1) != 1:
+            raise AssertionError("k_new/v_new need a contiguous last dimension")
+        kn, vn = _as_rows(k_new), _as_rows(v_new)
+        st = (kn.stride(0), kn.stride(1), vn.stride(0), vn.stride(1))
+        kp, vp = kn.data_ptr(), vn.data_ptr()
+    else:
+        if p0 + T > int(smax):
+            raise AssertionError(f"positions up to {p0 + T} exceed the cache's {smax} rows")
+        st, kp, vp = (0, 0, 0, 0), None, None
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.dtype is not bf or out.shape != q.shape or not out.is_contiguous():
+        raise AssertionError("out must be contiguous bf16 shaped like q")
+    N.call("na_prefill_attention", q.data_ptr(), kc.data_ptr(), vc.data_ptr(), rows, kp, vp, *st, sinks.data_ptr(),
+           out.data_ptr(), p0, T, float(scaling), int(sliding or 0), int(ring or 0), N.events_array(events),
+           N.stream(q.device))
+    return out
+
+
 def ring_write(kc, vc, k_new, v_new, p0, ring):
     """Store the last min(T, ring) positions of a block (positions p0 .. p0+T-1, K/V [T, NKV, HD]) into their ring
-    slots (slot = position % ring), as reference fused_core.py:787-800: at most two contiguous slice copies on the
-    device, no allocation, no host synchronisation."""
+    slots (slot = position % ring) of kc / vc [1, NKV, ring, HD], as reference fused_core.py:787-800.  One launch on
+    the current stream, no host synchronisation; call it after the block's attention."""
     T = k_new.shape[0]
-    n = min(T, ring)
-    a = T - n
-    s0 = (p0 + a) % ring
-    first = min(n, ring - s0)
-    kc[0, :, s0:s0 + first] = k_new[a:a + first].transpose(0, 1)
-    vc[0, :, s0:s0 + first] = v_new[a:a + first].transpose(0, 1)
-    if first < n:
-        kc[0, :, :n - first] = k_new[a + first:].transpose(0, 1)
-        vc[0, :, :n - first] = v_new[a + first:].transpose(0, 1)
+    if kc.shape != (1, NKV, int(ring), HD) or vc.shape != kc.shape or not kc.is_contiguous() or not vc.is_contiguous():
+        raise AssertionError(f"kc/vc must be contiguous [1, {NKV}, {ring}, {HD}]")
+    if kc.dtype is not torch.bfloat16 or vc.dtype is not torch.bfloat16:
+        raise AssertionError("kc/vc must be bf16")
+    if k_new.shape != (T, NKV, HD) or v_new.shape != (T, NKV, HD):
+        raise AssertionError(f"k_new/v_new must be [{T}, {NKV}, {HD}]")
+    kn, vn = _as_rows(k_new), _as_rows(v_new)
+    N.call("na_ring_write", kc.data_ptr(), vc.data_ptr(), int(ring), kn.data_ptr(), vn.data_ptr(), kn.stride(0),
+           kn.stride(1), vn.stride(0), vn.stride(1), int(p0), T, N.stream(kc.device))
 
 
 def ring_reuse_ok(n_written, c, ring, window=128):

@@ -1,0 +1,316 @@
+// Prompt-processing (prefill) attention with learned sinks, causal + optional sliding window, GQA 64 query / 8 KV
+// heads of 64, on gfx950.  The computation of reference fused_core.py:684-759 (k_prefill_attn): per query head and
+// query position qp = p0 + t, keys j <= qp (and j > qp - window on sliding layers) of the cache; scores
+// s = (q . k) * scaling in fp32; online softmax whose running state starts at (m = sink, l = 1), so the sink joins
+// the denominator; P is rounded to bf16 for the P V product, the row sums use the unrounded P; o = bf16(acc / l).
+//
+// Work layout: one workgroup of 8 waves per (32-token query block, KV head h); wave w is query head 8 h + w, so the
+// eight query heads that share a KV head read each K / V tile from LDS, where it is staged once.  Tiles of 64 keys
+// walk [lo, hi) with lo = max(first query - window + 1, 0) rounded down to 64 (0 on full layers) and hi = one past
+// the block's last query; the next tile's global loads are in flight while the current tile is computed (two LDS
+// buffers, one barrier per tile).  Both products run on v_mfma_f32_16x16x32_bf16 with the queries as the columns:
+//   S^T [key][query] = K [key][d] . Q^T [d][query]      (A = K rows from LDS, B = Q held in registers)
+//   O^T [d][query]  += V^T [d][key] . P^T [key][query]   (A = V^T from LDS, B = P^T straight from the S^T registers)
+// A lane then owns one query column in every tile, so the softmax state of that query (running max, the alpha
+// rescale of O^T) stays in the lane; the only cross-lane steps are the max over the 4 lanes that share a column and
+// the final row sum.  The k index of the P V product is a permutation of the 32 keys of a step (lane group g holds
+// keys 4g..4g+3 and 16+4g..16+4g+3), the same permutation on both operands.
+//
+// Key sources: linear cache [NKV][cache_rows][64] holding every position below p0 + T, or (ring > 0, sliding
+// layers) a rolling cache [NKV][ring][64] for keys j < p0 (row j % ring) plus the block's own K / V rows
+// [T][NKV][64] (strided) for j >= p0.  Both modes run the same tiles in the same order with the same arithmetic, so
+// their outputs are bit-identical when the caches hold the same values.  Keys past hi - 1 in the last tile are read
+// from row hi - 1 and masked; a ring slot holding a position that no query can see is masked (its contents must be
+// finite, as in the reference).
+#include "common.h"
+
+#include <hip/hip_ext.h>
+
+namespace na {
+
+namespace pfa {
+
+constexpr int kNQ = 64, kNKV = 8, kHD = 64, kRep = 8;
+constexpr int kKeys = 64;                  // keys per tile
+constexpr int kKPitch = kHD * 2 + 16;      // LDS bytes per K row: 144 (16-byte reads of 8 rows hit distinct banks)
+constexpr int kVPitch = kKeys * 2 + 8;     // LDS bytes per V^T row: 136 (8-byte reads of 16 rows hit distinct banks)
+constexpr int kThreads = 512;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+struct Lds {
+  __align__(16) uint8_t k[2][kKeys * kKPitch];
+  __align__(16) uint8_t vt[2][kHD * kVPitch];
+};
+
+NA_DEVICE bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+struct KeySrc {
+  const uint16_t* kc;
+  const uint16_t* vc;
+  const uint16_t* kn;
+  const uint16_t* vn;
+  long long cache_rows, sk_t, sk_h, sv_t, sv_h, p0;
+  int ring, h;
+
+  // Row of key position j (0 <= j < p0 + T) for head h.
+  NA_DEVICE const uint16_t* krow(long long j) const {
+    if (ring > 0) {
+      if (j < p0) return kc + ((long long)h * cache_rows + j % ring) * kHD;
+      return kn + (j - p0) * sk_t + (long long)h * sk_h;
+    }
+    return kc + ((long long)h * cache_rows + j) * kHD;
+  }
+  NA_DEVICE const uint16_t* vrow(long long j) const {
+    if (ring > 0) {
+      if (j < p0) return vc + ((long long)h * cache_rows + j % ring) * kHD;
+      return vn + (j - p0) * sv_t + (long long)h * sv_h;
+    }
+    return vc + ((long long)h * cache_rows + j) * kHD;
+  }
+};
+
+// QT query tiles of 16 per wave: 16 * QT tokens per workgroup.
+template <int QT>
+__global__ __launch_bounds__(kThreads) void k_prefill_attn(
+    const uint16_t* __restrict__ q, KeySrc src, const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out,
+    int T, float scaling, int window) {
+  constexpr int kQB = 16 * QT;
+  __shared__ Lds L;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, n = lane & 15;
+  const int nqb = (T + kQB - 1) / kQB;
+  const int h = blockIdx.x % kNKV;                    // consecutive workgroups: consecutive heads
+  const int qb = nqb - 1 - (int)(blockIdx.x / kNKV);  // longest key ranges first
+  src.h = h;
+  const int hq = h * kRep + wave;
+  const int q0 = qb * kQB;                            // block-relative first token
+  const long long p0 = src.p0;
+  const long long qpos0 = p0 + q0;
+  const long long hi = p0 + min(q0 + kQB, T);         // one past the last key any query of the block sees
+  long long lo = window > 0 ? qpos0 - window + 1 : 0;
+  lo = lo < 0 ? 0 : (lo / kKeys) * kKeys;
+  const int nt = (int)((hi - lo + kKeys - 1) / kKeys);
+
+  // Q^T as the B operand: lane (n, g) holds query q0 + 16 qt + n, dims 8g.. (step 0) and 32 + 8g.. (step 1).
+  uint4 qf[QT][2];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int t = min(q0 + 16 * qt + n, T - 1);
+    const uint16_t* qr = q + ((long long)t * kNQ + hq) * kHD;
+    qf[qt][0] = *reinterpret_cast<const uint4*>(qr + 8 * g);
+    qf[qt][1] = *reinterpret_cast<const uint4*>(qr + 32 + 8 * g);
+  }
+  const float sl2 = scaling * kLog2e;                 // scores in the log2 domain: exp(s - m) = exp2(s' - m')
+  const float sink2 = bf16_to_f32(sinks[hq]) * kLog2e;
+  float m[QT], l[QT];
+  f32x4_t acc[4][QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m[qt] = sink2;
+    l[qt] = g == 0 ? 1.f : 0.f;                       // the sink's exp(sink - m) = 1, counted once per column
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc[dt][qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // Staging: K row key tid / 8, dims 8 (tid % 8) (a wave reads 8 whole rows); V key tid % 64, dims 8 (tid / 64),
+  // written transposed (a wave writes 64 consecutive keys of 8 V^T rows).
+  const int kk = tid >> 3, kd = tid & 7;
+  const int vk = tid & 63, vd = tid >> 6;
+  uint4 kreg, vreg;
+  auto load_tile = [&](long long s0) {
+    const long long jk = s0 + kk < hi ? s0 + kk : hi - 1, jv = s0 + vk < hi ? s0 + vk : hi - 1;
+    kreg = *reinterpret_cast<const uint4*>(src.krow(jk) + 8 * kd);
+    vreg = *reinterpret_cast<const uint4*>(src.vrow(jv) + 8 * vd);
+  };
+  auto store_tile = [&](int buf) {
+    *reinterpret_cast<uint4*>(L.k[buf] + kk * kKPitch + 16 * kd) = kreg;
+    const uint32_t w4[4] = {vreg.x, vreg.y, vreg.z, vreg.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      *reinterpret_cast<uint16_t*>(L.vt[buf] + (8 * vd + i) * kVPitch + 2 * vk) =
+          (uint16_t)((i & 1) ? (w4[i >> 1] >> 16) : (w4[i >> 1] & 0xffff));
+  };
+
+  load_tile(lo);
+  store_tile(0);
+  __syncthreads();
+  for (int it = 0; it < nt; ++it) {
+    const int buf = it & 1;
+    const long long s0 = lo + (long long)it * kKeys;
+    if (it + 1 < nt) load_tile(s0 + kKeys);
+    // ---- S^T = K Q^T: tile (kt, qt), lane holds keys s0 + 16 kt + 4 g + r of query column n
+    float s[4][QT][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      const uint8_t* kr = L.k[buf] + (16 * kt + n) * kKPitch + 16 * g;
+      const uint4 ka0 = *reinterpret_cast<const uint4*>(kr);
+      const uint4 ka1 = *reinterpret_cast<const uint4*>(kr + 64);
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka0), as_bf16x8(qf[qt][0]), d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka1), as_bf16x8(qf[qt][1]), d, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[kt][qt][r] = d[r];
+      }
+    }
+    // ---- mask, online softmax (per query column), P^T fragments
+    uint4 pf[2][QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const long long qp = qpos0 + 16 * qt + n;
+      float mx = kNegInf;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const long long j = s0 + 16 * kt + 4 * g + r;
+          bool ok = j <= qp && j < hi;
+          if (window > 0) ok = ok && j > qp - window;
+          const float v = ok ? s[kt][qt][r] * sl2 : kNegInf;
+          s[kt][qt][r] = v;
+          mx = fmaxf(mx, v);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m[qt], mx);           // finite: m starts at the sink
+      const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_new);
+      m[qt] = m_new;
+      float ls = l[qt] * alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) acc[dt][qt] *= alpha;
+      uint32_t pk[4][2];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        float e[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          e[r] = __builtin_amdgcn_exp2f(s[kt][qt][r] - m_new);   // exp2(-inf) = +0 for masked keys
+          ls += e[r];
+        }
+        pk[kt][0] = pack_bf16x2(e[0], e[1]);
+        pk[kt][1] = pack_bf16x2(e[2], e[3]);
+      }
+      l[qt] = ls;
+      pf[0][qt] = make_uint4(pk[0][0], pk[0][1], pk[1][0], pk[1][1]);   // keys 4g.., 16+4g.. of step 0
+      pf[1][qt] = make_uint4(pk[2][0], pk[2][1], pk[3][0], pk[3][1]);   // the same of step 1 (+32)
+    }
+    // ---- O^T += V^T P^T over two 32-key steps
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint8_t* vr = L.vt[buf] + (16 * dt + n) * kVPitch + 2 * (32 * ks + 4 * g);
+        const uint2 a0 = *reinterpret_cast<const uint2*>(vr);
+        const uint2 a1 = *reinterpret_cast<const uint2*>(vr + 32);
+        const uint4 va = make_uint4(a0.x, a0.y, a1.x, a1.y);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+          acc[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va), as_bf16x8(pf[ks][qt]), acc[dt][qt], 0,
+                                                                 0, 0);
+      }
+    }
+    if (it + 1 < nt) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- o = acc / l; lane holds dims 16 dt + 4 g + r of query column n
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    float lt = l[qt];
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
+    const int t = q0 + 16 * qt + n;
+    if (t < T) {
+      const float inv = 1.f / lt;
+      uint16_t* orow = out + ((long long)t * kNQ + hq) * kHD;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint2 o = make_uint2(pack_bf16x2(acc[dt][qt][0] * inv, acc[dt][qt][1] * inv),
+                                   pack_bf16x2(acc[dt][qt][2] * inv, acc[dt][qt][3] * inv));
+        *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = o;
+      }
+    }
+  }
+}
+
+// Ring write (reference fused_core.py:787-800): the last min(T, ring) positions of a block, K / V rows [T][NKV][64]
+// with strides, into ring slots position % ring of [NKV][ring][64].  One thread per 16 bytes.
+__global__ __launch_bounds__(256) void k_ring_write(uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int ring,
+                                                    const uint16_t* __restrict__ kn, const uint16_t* __restrict__ vn,
+                                                    long long sk_t, long long sk_h, long long sv_t, long long sv_h,
+                                                    long long p0, int T) {
+  const int n = min(T, ring);
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;   // over n x NKV x 8 pieces
+  if (i >= (long long)n * kNKV * 8) return;
+  const int piece = (int)(i & 7);
+  const int hh = (int)((i >> 3) % kNKV);
+  const int r = (int)(i / (8 * kNKV));
+  const int t = T - n + r;                            // block-relative position
+  const long long slot = (p0 + t) % ring;
+  const long long dst = ((long long)hh * ring + slot) * kHD + 8 * piece;
+  *reinterpret_cast<uint4*>(kc + dst) = *reinterpret_cast<const uint4*>(kn + t * sk_t + hh * sk_h + 8 * piece);
+  *reinterpret_cast<uint4*>(vc + dst) = *reinterpret_cast<const uint4*>(vn + t * sv_t + hh * sv_h + 8 * piece);
+}
+
+}  // namespace pfa
+
+}  // namespace na
+
+using namespace na;
+using namespace na::pfa;
+
+extern "C" {
+
+int na_prefill_attention(const void* q, const void* kc, const void* vc, long long cache_rows, const void* k_new,
+                         const void* v_new, long long sk_t, long long sk_h, long long sv_t, long long sv_h,
+                         const void* sinks, void* out, long long p0, int T, float scaling, int window, int ring,
+                         void* const* events, hipStream_t stream) {
+  if (T < 0 || p0 < 0 || window < 0 || ring < 0 || cache_rows <= 0) return kErrArgs;
+  if (T == 0) return kOk;                             // an empty prompt: nothing to read or write
+  if (!q || !kc || !vc || !sinks || !out) return kErrArgs;
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc)) & 15)
+    return kErrArgs;
+  if (reinterpret_cast<uintptr_t>(out) & 7) return kErrArgs;
+  if (ring > 0) {
+    if (window <= 0 || ring < window || cache_rows != ring || !k_new || !v_new) return kErrArgs;
+    if ((reinterpret_cast<uintptr_t>(k_new) | reinterpret_cast<uintptr_t>(v_new)) & 15) return kErrArgs;
+    if (sk_t < 0 || sk_h < 0 || sv_t < 0 || sv_h < 0 || ((sk_t | sk_h | sv_t | sv_h) & 7)) return kErrArgs;
+  } else if (p0 + T > cache_rows) {
+    return kErrArgs;
+  }
+  KeySrc src{(const uint16_t*)kc, (const uint16_t*)vc, (const uint16_t*)k_new, (const uint16_t*)v_new,
+             cache_rows, sk_t, sk_h, sv_t, sv_h, p0, ring, 0};
+  constexpr int QT = 2;                               // 32 tokens per workgroup (163 VGPRs: no spills)
+  const int qb = 16 * QT;
+  const dim3 grid((unsigned)(((long long)T + qb - 1) / qb * kNKV)), block(kThreads);
+  hipEvent_t e0 = events ? (hipEvent_t)events[0] : nullptr, e1 = events ? (hipEvent_t)events[1] : nullptr;
+  auto kern = k_prefill_attn<QT>;
+  if (e0 || e1)
+    hipExtLaunchKernelGGL(kern, grid, block, 0, stream, e0, e1, 0, (const uint16_t*)q, src, (const uint16_t*)sinks,
+                          (uint16_t*)out, T, scaling, window);
+  else
+    hipLaunchKernelGGL(kern, grid, block, 0, stream, (const uint16_t*)q, src, (const uint16_t*)sinks, (uint16_t*)out,
+                       T, scaling, window);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int na_ring_write(void* kc, void* vc, int ring, const void* k_new, const void* v_new, long long sk_t, long long sk_h,
+                  long long sv_t, long long sv_h, long long p0, int T, hipStream_t stream) {
+  if (ring <= 0 || T < 0 || p0 < 0) return kErrArgs;
+  if (T == 0) return kOk;
+  if (!kc || !vc || !k_new || !v_new) return kErrArgs;
+  if ((reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc) | reinterpret_cast<uintptr_t>(k_new) |
+       reinterpret_cast<uintptr_t>(v_new)) & 15)
+    return kErrArgs;
+  if (sk_t < 0 || sk_h < 0 || sv_t < 0 || sv_h < 0 || ((sk_t | sk_h | sv_t | sv_h) & 7)) return kErrArgs;
+  const long long pieces = (long long)(T < ring ? T : ring) * kNKV * 8;
+  hipLaunchKernelGGL(k_ring_write, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream, (uint16_t*)kc,
+                     (uint16_t*)vc, ring, (const uint16_t*)k_new, (const uint16_t*)v_new, sk_t, sk_h, sv_t, sv_h, p0,
+                     T);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // extern "C"

@@ -60,3 +60,70 @@ def attn_bf16(q, kc, vc, sinks, pos, scaling, sliding=0, ring=0):
     p = rb((e / S).astype(np.float32)).astype(np.float64)
     out = np.einsum("hrn,hnd->hrd", p, v)
     return rb(out.astype(np.float32)).reshape(-1)
+
+
+# ------------------------------------------------------------------------------------------ prompt (prefill) attention
+def prefill_ref64(q, K, V, sinks, p0, scaling, sliding=0):
+    """Exact-math fp64 sink attention of T prompt queries at positions p0 .. p0+T-1 over a linear cache: each query is
+    the decode closed form ``ref64`` at its own position (keys [lo(qp), qp]).  q [T, NQ, HD]; K, V [NKV, S, HD] with
+    S >= p0 + T; returns [T, NQ, HD] fp64."""
+    q = np.asarray(q, np.float64)
+    T = q.shape[0]
+    return np.stack([ref64(q[t].reshape(-1), K, V, sinks, p0 + t, scaling, sliding).reshape(NQ, HD)
+                     for t in range(T)]) if T else np.zeros((0, NQ, HD))
+
+
+def prefill_attn_tiled(q, K, V, sinks, p0, scaling, sliding=0, BM=64, BN=64, sink=True, causal_shift=0,
+                       window_shift=0):
+    """k_prefill_attn's algorithm (reference fused_core.py:684-759), fp32, over a linear cache K, V [NKV, S, HD]:
+    query blocks of BM rows; per block keys walk [lo, hi) in tiles of BN, lo = max(first query - sliding + 1, 0)
+    rounded down to BN (0 on full layers), hi = one past the block's last query; per tile s = (q . k) * scaling,
+    masked to -inf outside j <= qp (and j > qp - sliding); m_new = max(m, max s); alpha = exp(m - m_new);
+    p = exp(s - m_new); l = l alpha + sum p; acc = acc alpha + bf16(p) . v; the running state starts at m = sink,
+    l = 1.  Output bf16(acc / l) [T, NQ, HD] (fp32 values on the bf16 grid).
+
+    ``sink``, ``causal_shift`` and ``window_shift`` exist only to plant mistakes in tests (drop the sink, attend one
+    key past the diagonal, widen the window by one); the defaults are the reference's algorithm."""
+    q = np.asarray(q, np.float32)
+    T = q.shape[0]
+    K = np.asarray(K, np.float32)
+    V = np.asarray(V, np.float32)
+    kvh = np.arange(NQ) // REP
+    sk = np.asarray(sinks, np.float32)
+    out = np.zeros((T, NQ, HD), np.float32)
+    sc = np.float32(scaling)
+    for mb in range((T + BM - 1) // BM):
+        offs = mb * BM + np.arange(BM)
+        mm = offs < T
+        qpos = p0 + offs
+        qb = np.where(mm[:, None, None], q[np.minimum(offs, T - 1)], 0).astype(np.float32)   # [BM, NQ, HD]
+        qh = qb.transpose(1, 0, 2)                                                           # [NQ, BM, HD]
+        m = np.broadcast_to(sk[:, None] if sink else np.float32(-np.inf), (NQ, BM)).astype(np.float32).copy()
+        lsum = np.full((NQ, BM), 1.0 if sink else 0.0, np.float32)
+        acc = np.zeros((NQ, BM, HD), np.float32)
+        hi = min(p0 + mb * BM + BM, p0 + T)
+        lo = max(p0 + mb * BM - sliding + 1, 0) if sliding else 0
+        lo = (lo // BN) * BN
+        for s0 in range(lo, hi, BN):
+            j = s0 + np.arange(BN)
+            jm = j < hi
+            rows = np.minimum(j, hi - 1)
+            k = np.where(jm[None, :, None], K[:, rows], 0)[kvh]                                # [NQ, BN, HD]
+            v = np.where(jm[None, :, None], V[:, rows], 0)[kvh]
+            s = np.matmul(qh, k.transpose(0, 2, 1)) * sc                                      # [NQ, BM, BN]
+            ok = (j[None, :] <= qpos[:, None] + causal_shift) & jm[None, :]
+            if sliding:
+                ok &= j[None, :] > qpos[:, None] - sliding - window_shift
+            s = np.where(ok[None], s, -np.inf).astype(np.float32)
+            m_new = np.maximum(m, s.max(-1))
+            with np.errstate(invalid="ignore"):
+                alpha = np.where(m == m_new, 1.0, np.exp(m - m_new)).astype(np.float32)
+                p = np.exp(s - m_new[..., None]).astype(np.float32)
+            p = np.where(np.isneginf(m_new)[..., None], 0, p).astype(np.float32)
+            lsum = lsum * alpha + p.sum(-1, dtype=np.float32)
+            acc = acc * alpha[..., None] + np.matmul(rb(p), v).astype(np.float32)
+            m = m_new
+        with np.errstate(invalid="ignore", divide="ignore"):
+            o = acc / lsum[..., None]
+        out[offs[mm]] = rb(o.transpose(1, 0, 2)[mm].astype(np.float32))
+    return out

@@ -220,3 +220,25 @@ def test_attention_workspace_and_argument_checks():
     assert lib.na_attn_workspace_floats(1, 65) == -1
     assert lib.na_decode_attention(None, None, None, 1, None, None, None, 1, ctypes.c_float(0.125), 0, 0, 1,
                                    None, None, None, None) == -1
+
+
+def test_prefill_attention_argument_checks():
+    """Host-side validation of na_prefill_attention / na_ring_write (no launch happens on any of these)."""
+    from neural_amd import _native as N
+    lib = N.lib()
+    f = ctypes.c_float(0.125)
+    a = 1 << 20                                   # an aligned non-null stand-in; never dereferenced here
+    # missing pointers; ring without a window; ring != cache_rows; positions beyond the cache; negative T
+    assert lib.na_prefill_attention(None, a, a, 64, None, None, 0, 0, 0, 0, a, a, 0, 4, f, 0, 0, None, None) == -1
+    assert lib.na_prefill_attention(a, a, a, 128, a, a, 512, 64, 512, 64, a, a, 0, 4, f, 0, 128, None, None) == -1
+    assert lib.na_prefill_attention(a, a, a, 64, a, a, 512, 64, 512, 64, a, a, 0, 4, f, 128, 128, None, None) == -1
+    assert lib.na_prefill_attention(a, a, a, 64, None, None, 0, 0, 0, 0, a, a, 62, 4, f, 0, 0, None, None) == -1
+    assert lib.na_prefill_attention(a, a, a, 64, None, None, 0, 0, 0, 0, a, a, 0, -1, f, 0, 0, None, None) == -1
+    # strides not a multiple of 8 elements in ring mode; misaligned q
+    assert lib.na_prefill_attention(a, a, a, 128, a, a, 510, 64, 512, 64, a, a, 0, 4, f, 128, 128, None, None) == -1
+    assert lib.na_prefill_attention(a + 2, a, a, 64, None, None, 0, 0, 0, 0, a, a, 0, 4, f, 0, 0, None, None) == -1
+    # T = 0 is a valid empty call and launches nothing
+    assert lib.na_prefill_attention(a, a, a, 64, None, None, 0, 0, 0, 0, a, a, 0, 0, f, 0, 0, None, None) == 0
+    assert lib.na_prefill_attention(None, a, a, 64, None, None, 0, 0, 0, 0, a, a, 0, 0, f, 0, 0, None, None) == 0
+    assert lib.na_ring_write(a, a, 0, a, a, 512, 64, 512, 64, 0, 4, None) == -1
+    assert lib.na_ring_write(a, a, 128, a, a, 512, 64, 512, 64, 0, 0, None) == 0
