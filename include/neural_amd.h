@@ -244,6 +244,28 @@ int na_core_lm_tail(const void* mid, const void* g, const float* c, const void* 
                     int step_pos, int64_t* seq, const int64_t* n_forced, int64_t* pred, long long seq_len,
                     hipStream_t stream);
 
+/* ---- dense core over T prompt tokens (prefill), one row per workgroup; the GEMMs between them are plain bf16
+ *      library GEMMs (hipBLASLt), as the reference's F.linear calls.  Replace the row-wise parts of server.py:2357-2418
+ *      (_rope_tables, _rope, _attn_router, _prefill_block) and of neural/moe/gptoss_core_graphs.py:48-53 (_rms). */
+
+/* x [T, 2880] <- embed[ids[t]] (ids int64 [T], clamped into [0, vocab)); the reference's EMB_ROWS(ids). */
+int na_rows_embed(const void* emb, long long vocab, const int64_t* ids, int T, void* x, hipStream_t stream);
+
+/* Residual + RMSNorm per row: when add is not NULL, x[t] <- bf16(x[t] + add[t]) in place; hn[t] <- bf16(w * (x[t] *
+ * rsqrt(mean(x[t]^2) + eps))).  x, add, hn bf16 [T, 2880]; w bf16 [2880]; 16-byte aligned. */
+int na_rows_norm(void* x, const void* add, int T, const void* w, float eps, void* hn, hipStream_t stream);
+
+/* RoPE of qkv [T, 5120] (= F.linear(hn, Wqkv, bqkv)) at positions p0 .. p0+T-1 with cos/sin =
+ * bf16(cos(inv_freq[d] pos) * att_scale) (server.py:2357-2364): q [T, 64, 64] <- rotated q heads; the rotated k
+ * heads to k_dst + t kt + h kh and the v heads to v_dst + t vt + h vh (element strides: the linear cache rows at p0,
+ * or [T, 8, 64] buffers of the block for a rolling cache). */
+int na_rows_rope(const void* qkv, int T, long long p0, const float* inv_freq, float att_scale, void* q, void* k_dst,
+                 long long kt, long long kh, void* v_dst, long long vt, long long vh, hipStream_t stream);
+
+/* Router selection per row: logits bf16 [T, 128] (= F.linear(hn, Wr, br)) -> ids int64 [T, 4] (top 4 by repeated
+ * argmax, lowest index on ties) and wts bf16 [T, 4] (softmax over the four; server.py:2400-2401). */
+int na_rows_topk(const void* logits, int T, int64_t* ids, void* wts, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -259,6 +259,39 @@ __global__ __launch_bounds__(256) void k_oproj(const uint16_t* __restrict__ att,
 // post-attention RMSNorm + router + top-4: 256 / TPR experts per workgroup, grid 128 / (256 / TPR).  Workgroup 0 writes hn (the experts' input);
 // every workgroup publishes its 16 logits (device-coherent stores, then a count); the last one selects the top 4,
 // writes ids / weights and resets the count.
+// Top 4 of 128 logits held by one wave (lane l: logits l and l + 64) by repeated argmax, lowest index on ties; lanes
+// 0..3 write ids[k] and the weights bf16(exp(v_k - v_0) / sum_k exp(v_k - v_0)) (the reference's softmax over the
+// four, fused_core.py:486-502).
+NA_DEVICE void top4_softmax(float v0, float v1, int lane, int64_t* __restrict__ ids, uint16_t* __restrict__ wts) {
+  float tv[4];
+  int ti[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float bvv = v0;
+    int bi = lane;
+    if (v1 > bvv) { bvv = v1; bi = lane + 64; }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bvv, off);
+      const int oi = __shfl_xor(bi, off);
+      if (ov > bvv || (ov == bvv && oi < bi)) { bvv = ov; bi = oi; }
+    }
+    tv[k] = bvv;
+    ti[k] = bi;
+    if (bi == lane) v0 = -__builtin_inff();
+    if (bi == lane + 64) v1 = -__builtin_inff();
+  }
+  if (lane < 4) {
+    float ex[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ex[k] = expf(tv[k] - tv[0]);
+    const float sum = ((ex[0] + ex[1]) + ex[2]) + ex[3];
+    const float mine = lane == 0 ? ex[0] : lane == 1 ? ex[1] : lane == 2 ? ex[2] : ex[3];
+    ids[lane] = lane == 0 ? ti[0] : lane == 1 ? ti[1] : lane == 2 ? ti[2] : ti[3];
+    wts[lane] = f32_to_bf16(mine / sum);
+  }
+}
+
 template <int TPR>
 __global__ __launch_bounds__(256) void k_router_norm(const uint16_t* __restrict__ mid, const uint16_t* __restrict__ post_w,
                                                      float eps, const uint16_t* __restrict__ Wr,
@@ -291,36 +324,8 @@ __global__ __launch_bounds__(256) void k_router_norm(const uint16_t* __restrict_
   }
   __syncthreads();
   if (!last || tid >= 64) return;
-  const int lane = tid;
-  float v0 = __hip_atomic_load(logits + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  float v1 = __hip_atomic_load(logits + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  float tv[4];
-  int ti[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {                      // repeated argmax, lowest index on ties
-    float bvv = v0;
-    int bi = lane;
-    if (v1 > bvv) { bvv = v1; bi = lane + 64; }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bvv, off);
-      const int oi = __shfl_xor(bi, off);
-      if (ov > bvv || (ov == bvv && oi < bi)) { bvv = ov; bi = oi; }
-    }
-    tv[k] = bvv;
-    ti[k] = bi;
-    if (bi == lane) v0 = -__builtin_inff();
-    if (bi == lane + 64) v1 = -__builtin_inff();
-  }
-  if (lane < 4) {
-    float ex[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) ex[k] = expf(tv[k] - tv[0]);
-    const float sum = ((ex[0] + ex[1]) + ex[2]) + ex[3];
-    const float mine = lane == 0 ? ex[0] : lane == 1 ? ex[1] : lane == 2 ? ex[2] : ex[3];
-    ids[lane] = lane == 0 ? ti[0] : lane == 1 ? ti[1] : lane == 2 ? ti[2] : ti[3];
-    wts[lane] = f32_to_bf16(mine / sum);
-  }
+  top4_softmax(__hip_atomic_load(logits + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+               __hip_atomic_load(logits + tid + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), tid, ids, wts);
 }
 
 // Tail 1: x = bf16(mid + bf16(g + bf16(c))); hn = bf16(w * (x * r)) (one workgroup).
@@ -406,6 +411,117 @@ __global__ __launch_bounds__(1024) void k_argmax(const uint64_t* __restrict__ pa
   }
 }
 
+// ---- prompt rows (prefill of T tokens; reference server.py:2357-2403 _rope_tables / _attn_router and
+//      _prefill_block :2406-2418): the same rounding points as the decode kernels above, one row per workgroup.
+
+// x[t] = embed[ids[t]] (ids clamped into [0, vocab)).
+__global__ __launch_bounds__(256) void k_rows_embed(const uint16_t* __restrict__ emb, long long vocab,
+                                                    const int64_t* __restrict__ ids, uint16_t* __restrict__ x) {
+  const long long t = blockIdx.x;
+  long long id = ids[t];
+  id = id < 0 ? 0 : id >= vocab ? vocab - 1 : id;
+  for (int ch = threadIdx.x; ch < kH / 8; ch += 256)
+    *reinterpret_cast<uint4*>(x + t * kH + 8 * ch) = *reinterpret_cast<const uint4*>(emb + id * kH + 8 * ch);
+}
+
+// Residual + RMSNorm of row t: x[t] = bf16(x[t] + add[t]) in place when add is given; hn[t] = bf16(w * (x * r)),
+// r = rsqrt(sum x^2 / H + eps) with the decode kernels' summation order.
+__global__ __launch_bounds__(256) void k_rows_norm(uint16_t* __restrict__ x, const uint16_t* __restrict__ add,
+                                                   const uint16_t* __restrict__ w, float eps,
+                                                   uint16_t* __restrict__ hn) {
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const long long base = (long long)blockIdx.x * kH;
+  uint4 xv4[2], av4[2], wv4[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int ch = min(tid + 256 * i, kH / 8 - 1);
+    xv4[i] = *reinterpret_cast<const uint4*>(x + base + 8 * ch);
+    av4[i] = *reinterpret_cast<const uint4*>((add ? add : x) + base + 8 * ch);
+    wv4[i] = *reinterpret_cast<const uint4*>(w + 8 * ch);
+  }
+  float xv[2][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = half_at(xv4[i], e);
+      if (add) v = rb(v + half_at(av4[i], e));
+      xv[i][e] = v;
+      if (tid + 256 * i < kH / 8) ss += v * v;
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float r = rsqrtf(((red[0] + red[1]) + (red[2] + red[3])) * (1.0f / kH) + eps);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int ch = tid + 256 * i;
+    if (ch < kH / 8) {
+      uint32_t o[4], xo[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        o[e >> 1] = pack_bf16x2(half_at(wv4[i], e) * (xv[i][e] * r), half_at(wv4[i], e + 1) * (xv[i][e + 1] * r));
+        xo[e >> 1] = pack_bf16x2(xv[i][e], xv[i][e + 1]);
+      }
+      *reinterpret_cast<uint4*>(hn + base + 8 * ch) = make_uint4(o[0], o[1], o[2], o[3]);
+      if (add) *reinterpret_cast<uint4*>(x + base + 8 * ch) = make_uint4(xo[0], xo[1], xo[2], xo[3]);
+    }
+  }
+}
+
+// RoPE of row t of qkv [T, 5120] (q heads 0..63, k heads 64..71, v heads 72..79) at position p0 + t:
+// q -> q_out [T, 64, 64]; k -> k_dst + t kt + h kh; v (no rotation) -> v_dst + t vt + h vh.
+__global__ __launch_bounds__(256) void k_rows_rope(const uint16_t* __restrict__ qkv, long long p0,
+                                                   const float* __restrict__ inv_freq, float att_scale,
+                                                   uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_dst,
+                                                   long long kt, long long kh, uint16_t* __restrict__ v_dst,
+                                                   long long vt, long long vh) {
+  __shared__ float cs[32], sn[32];
+  const int tid = threadIdx.x;
+  const long long t = blockIdx.x;
+  const uint16_t* row = qkv + t * kQkvRows;
+  if (tid < 32) {
+    const float fr = inv_freq[tid] * (float)(p0 + t);
+    cs[tid] = rb(cosf(fr) * att_scale);
+    sn[tid] = rb(sinf(fr) * att_scale);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 9; ++i) {                      // pairs 0..2047: q heads; 2048..2303: k heads
+    const int P = tid + 256 * i;
+    const int head = P >> 5, d = P & 31;
+    const float ya = bf16_to_f32(row[head * 64 + d]), yb = bf16_to_f32(row[head * 64 + 32 + d]);
+    const uint16_t o1 = f32_to_bf16(rb(ya * cs[d]) - rb(yb * sn[d]));
+    const uint16_t o2 = f32_to_bf16(rb(yb * cs[d]) + rb(ya * sn[d]));
+    if (head < 64) {
+      q_out[t * kHq + head * 64 + d] = o1;
+      q_out[t * kHq + head * 64 + 32 + d] = o2;
+    } else {
+      uint16_t* kr = k_dst + t * kt + (long long)(head - 64) * kh;
+      kr[d] = o1;
+      kr[32 + d] = o2;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int e = tid + 256 * i;                     // v values 0..511
+    v_dst[t * vt + (long long)(e >> 6) * vh + (e & 63)] = row[kHq + 512 + e];
+  }
+}
+
+// Top 4 of each row of router logits [T, 128] (bf16), softmax over the four: one wave per row.
+__global__ __launch_bounds__(256) void k_rows_topk(const uint16_t* __restrict__ logits, int T,
+                                                   int64_t* __restrict__ ids, uint16_t* __restrict__ wts) {
+  const int lane = threadIdx.x & 63;
+  const long long t = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const uint16_t* lr = logits + t * kNE;
+  top4_softmax(bf16_to_f32(lr[lane]), bf16_to_f32(lr[lane + 64]), lane, ids + 4 * t, wts + 4 * t);
+}
+
 }  // namespace na
 
 using namespace na;
@@ -466,6 +582,45 @@ int na_core_lm_tail(const void* mid, const void* g, const float* c, const void* 
                      (uint16_t*)logits_out, (uint64_t*)part);
   hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, stream, (const uint64_t*)part, nwg, tok, pos, step_pos, seq,
                      n_forced, pred, seq_len);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int na_rows_embed(const void* emb, long long vocab, const int64_t* ids, int T, void* x, hipStream_t stream) {
+  if (T < 0 || vocab <= 0) return kErrArgs;
+  if (T == 0) return kOk;
+  if (!emb || !ids || !x) return kErrArgs;
+  hipLaunchKernelGGL(k_rows_embed, dim3(T), dim3(256), 0, stream, (const uint16_t*)emb, vocab, ids, (uint16_t*)x);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int na_rows_norm(void* x, const void* add, int T, const void* w, float eps, void* hn, hipStream_t stream) {
+  if (T < 0) return kErrArgs;
+  if (T == 0) return kOk;
+  if (!x || !w || !hn) return kErrArgs;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(add) | reinterpret_cast<uintptr_t>(w) |
+       reinterpret_cast<uintptr_t>(hn)) & 15)
+    return kErrArgs;
+  hipLaunchKernelGGL(k_rows_norm, dim3(T), dim3(256), 0, stream, (uint16_t*)x, (const uint16_t*)add,
+                     (const uint16_t*)w, eps, (uint16_t*)hn);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int na_rows_rope(const void* qkv, int T, long long p0, const float* inv_freq, float att_scale, void* q, void* k_dst,
+                 long long kt, long long kh, void* v_dst, long long vt, long long vh, hipStream_t stream) {
+  if (T < 0 || p0 < 0) return kErrArgs;
+  if (T == 0) return kOk;
+  if (!qkv || !inv_freq || !q || !k_dst || !v_dst || kt < 0 || kh < 0 || vt < 0 || vh < 0) return kErrArgs;
+  hipLaunchKernelGGL(k_rows_rope, dim3(T), dim3(256), 0, stream, (const uint16_t*)qkv, p0, inv_freq, att_scale,
+                     (uint16_t*)q, (uint16_t*)k_dst, kt, kh, (uint16_t*)v_dst, vt, vh);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int na_rows_topk(const void* logits, int T, int64_t* ids, void* wts, hipStream_t stream) {
+  if (T < 0) return kErrArgs;
+  if (T == 0) return kOk;
+  if (!logits || !ids || !wts) return kErrArgs;
+  hipLaunchKernelGGL(k_rows_topk, dim3((T + 3) / 4), dim3(256), 0, stream, (const uint16_t*)logits, T, ids,
+                     (uint16_t*)wts);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

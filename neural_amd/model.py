@@ -25,6 +25,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _native as N
+from .attention import prefill_attention, ring_write
 from .moe.experts import ResidentExperts
 
 H, NQ, NKV, HD, NE, TOP_K = 2880, 64, 8, 64, 128, 4
@@ -269,6 +270,85 @@ class DecodeModel:
         self.n_forced.copy_(nf)
         for d, s_ in zip(self.kc + self.vc, kc + vc):
             d.copy_(s_)
+
+    # ------------------------------------------------------------------------------------------------ prompt
+    def prefill(self, tokens, chunk: int = 4096, trace: list | None = None) -> None:
+        """Prompt processing (reference server.py:2406-2418 _prefill_block, entry prefill :2446): load ``tokens``
+        (as reset()), run them through every layer in blocks of ``chunk`` tokens (each block through all layers, its
+        K/V written into the caches, so later blocks attend to earlier ones), then the tail of the last prompt token:
+        its greedy successor goes to seq[T] (unless T < n_forced) and pos becomes T, where decode steps continue.
+
+        Per layer and block: residual + input RMSNorm (na_rows_norm), Q|K|V = F.linear (a bf16 library GEMM, as the
+        reference), RoPE + K/V store (na_rows_rope: straight into the linear cache, or into block buffers that
+        na_ring_write copies into a rolling cache after the attention), prompt attention (na_prefill_attention),
+        o_proj = F.linear, residual + post-attention RMSNorm, router logits = F.linear and top-4 (na_rows_topk), the
+        experts (ResidentExperts.forward_prefill).  Host-driven launches on the current stream; not capturable (the
+        block size sets the shapes).  trace: optional list that receives one dict of device tensors per (block,
+        layer) with the stage inputs and outputs (for parity tests)."""
+        t = torch.as_tensor(tokens, dtype=torch.int64).reshape(-1)
+        T = t.numel()
+        if T < 1 or T >= self.smax:
+            raise ValueError(f"a prompt of 1 .. {self.smax - 1} tokens is needed (got {T})")
+        if chunk < 1:
+            raise ValueError("chunk must be positive")
+        self.reset(t)
+        x = m = None
+        for a in range(0, T, chunk):
+            x, m = self._prefill_block(a, min(chunk, T - a), trace)
+        self.mid.copy_(x[-1:])
+        self.g.copy_(m[-1:]) if m is not None else self.g.zero_()
+        self.pos.fill_(T - 1)
+        self.tail()
+
+    def _prefill_block(self, p0: int, T: int, trace):
+        import torch.nn.functional as F
+
+        dev, s, bf = self.dev, N.stream(self.dev), torch.bfloat16
+        x = torch.empty(T, H, dtype=bf, device=dev)
+        hn = torch.empty(T, H, dtype=bf, device=dev)
+        q = torch.empty(T, NQ, HD, dtype=bf, device=dev)
+        ids = torch.empty(T, TOP_K, dtype=torch.int64, device=dev)
+        wts = torch.empty(T, TOP_K, dtype=bf, device=dev)
+        N.call("na_rows_embed", self.w.embed.data_ptr(), self.w.vocab, self.seq.data_ptr() + 8 * p0, T, x.data_ptr(),
+               s)
+        m = None
+        for li, ly in enumerate(self.w.layers):
+            rec = {"p0": p0, "layer": li, "x_in": x.clone(), "m_in": None if m is None else m} if trace is not None \
+                else None
+            N.call("na_rows_norm", x.data_ptr(), N.ptr(m), T, ly.in_w.data_ptr(), EPS, hn.data_ptr(), s)
+            if rec is not None:
+                rec.update(x=x.clone(), h=hn.clone())
+            qkv = F.linear(hn, ly.Wqkv, ly.bqkv)
+            kc, vc = self.kc[li], self.vc[li]
+            rows = kc.shape[2]
+            ring = self.ring if ly.sliding else 0
+            if ring:
+                kn = torch.empty(T, NKV, HD, dtype=bf, device=dev)
+                vn = torch.empty(T, NKV, HD, dtype=bf, device=dev)
+                N.call("na_rows_rope", qkv.data_ptr(), T, p0, self.inv_freq.data_ptr(), float(self.att_scale),
+                       q.data_ptr(), kn.data_ptr(), NKV * HD, HD, vn.data_ptr(), NKV * HD, HD, s)
+                o = prefill_attention(q, kc, vc, ly.sinks, p0, self.scaling, ly.sliding, self.smax, k_new=kn,
+                                      v_new=vn, ring=ring)
+                ring_write(kc, vc, kn, vn, p0, ring)
+            else:
+                kn = vn = None
+                N.call("na_rows_rope", qkv.data_ptr(), T, p0, self.inv_freq.data_ptr(), float(self.att_scale),
+                       q.data_ptr(), kc.data_ptr() + 2 * p0 * HD, HD, rows * HD, vc.data_ptr() + 2 * p0 * HD, HD,
+                       rows * HD, s)
+                o = prefill_attention(q, kc, vc, ly.sinks, p0, self.scaling, ly.sliding, rows)
+            att = F.linear(o.view(T, HQ), ly.Wo, ly.bo)
+            if rec is not None:
+                rec.update(qkv=qkv, q=q.clone(), k_new=kn, v_new=vn, o=o, att=att)
+            N.call("na_rows_norm", x.data_ptr(), att.data_ptr(), T, ly.post_w.data_ptr(), EPS, hn.data_ptr(), s)
+            logits = F.linear(hn, ly.Wr, ly.br)
+            N.call("na_rows_topk", logits.data_ptr(), T, ids.data_ptr(), wts.data_ptr(), s)
+            m = self.rx.forward_prefill(li, hn, ids, wts)
+            if rec is not None:
+                rec.update(mid=x.clone(), hn=hn.clone(), logits=logits, ids=ids.clone(), wts=wts.clone(), m=m)
+                if not ring:
+                    rec.update(k_cache=kc[0, :, p0:p0 + T].clone(), v_cache=vc[0, :, p0:p0 + T].clone())
+                trace.append(rec)
+        return x, m
 
     # ------------------------------------------------------------------------------------------------ graphs
     def capture(self) -> torch.cuda.CUDAGraph:

@@ -21,25 +21,27 @@ HQ = NQ * HD
 
 def rms_bf16(x, w, eps):
     """RMSNorm at the reference's rounding points (gptoss_core_graphs.py:48-53; fused_core.py:95-109):
-    r = rsqrt(mean(x^2) + eps) in fp32, out = bf16(w * (x * r)).  x, w: bf16 values."""
+    r = rsqrt(mean(x^2) + eps) in fp32, out = bf16(w * (x * r)), over the last axis (one row or [T, H] rows).
+    x, w: bf16 values."""
     x = np.asarray(x, np.float32)
-    var = np.float32(np.sum(x.astype(np.float64) ** 2) / x.shape[-1])
-    r = np.float32(1.0 / np.sqrt(np.float64(var + np.float32(eps))))
+    var = (np.sum(x.astype(np.float64) ** 2, axis=-1, keepdims=True) / x.shape[-1]).astype(np.float32)
+    r = (1.0 / np.sqrt((var + np.float32(eps)).astype(np.float64))).astype(np.float32)
     return rb(np.asarray(w, np.float32) * (x * r))
 
 
 def linear_bf16(x, W64, b=None):
-    """F.linear in bf16: bf16(x . W^T (+ b)), one rounding (fp64 sum here)."""
-    y = np.asarray(W64 @ np.asarray(x, np.float64))
+    """F.linear in bf16: bf16(x . W^T (+ b)), one rounding (fp64 sum here); x one row or [T, K] rows."""
+    y = np.asarray(np.asarray(x, np.float64) @ W64.T)
     if b is not None:
         y = y + np.asarray(b, np.float64)
     return rb(y.astype(np.float32))
 
 
-def rope_tables(pos: int, inv_freq, att_scale):
-    """cos/sin of one position (gptoss_core_graphs.py:68-73): freqs = inv_freq * pos in fp32; bf16(cos(f) * s),
-    bf16(sin(f) * s)."""
-    f = (np.asarray(inv_freq, np.float32) * np.float32(pos)).astype(np.float32)
+def rope_tables(pos, inv_freq, att_scale):
+    """cos/sin of one position, or [T, 32] of an array of positions (gptoss_core_graphs.py:68-73, server.py:2357-2364):
+    freqs = inv_freq * pos in fp32; bf16(cos(f) * s), bf16(sin(f) * s)."""
+    p = np.asarray(pos, np.float32)
+    f = (np.asarray(inv_freq, np.float32) * (p[..., None] if p.ndim else p)).astype(np.float32)
     cs = rb((np.cos(f.astype(np.float64)).astype(np.float32) * np.float32(att_scale)).astype(np.float32))
     sn = rb((np.sin(f.astype(np.float64)).astype(np.float32) * np.float32(att_scale)).astype(np.float32))
     return cs, sn
@@ -148,6 +150,62 @@ class DecodeOracle:
         if trace is not None:
             trace.update(x=x, q=q, k=k, v=v, att=att, mid=mid, hn=hn, logits=logits, ids=ids, wts=wts, g=gout)
         return mid, gout
+
+    def moe_rows(self, li, hn, ids, wts):
+        """Expert layer over prompt rows (server.py:1837-1936 moe_prefill): every (token, rank) pair through its
+        expert, then per token bf16(sum_k fp32(bf16(y_k * w_k))) in top-k order (server.py:2340-2341)."""
+        hn = np.asarray(hn, np.float32)
+        ids = np.asarray(ids, np.int64)
+        T, K = ids.shape
+        y = np.zeros((T, K, H), np.float32)
+        for e in np.unique(ids):
+            tt, kk = np.nonzero(ids == e)
+            (wg, wd), bgu, bdn = self._expert(li, int(e))
+            y[tt, kk] = expert_forward_bf16(hn[tt], None, bgu, bdn, weights=(wg, wd))
+        prod = rb(y * np.asarray(wts, np.float32)[:, :, None])
+        acc = np.zeros((T, H), np.float32)
+        for k in range(K):
+            acc = (acc + prod[:, k]).astype(np.float32)
+        return rb(acc)
+
+    def prefill(self, tokens, p0=0, trace=None):
+        """Prompt processing of ``tokens`` at positions p0 .. p0+T-1 (server.py:2366-2418: _attn_router and the
+        experts, layer by layer over the whole block): x = embed; per layer x = bf16(x + m), h = RMSNorm, Q|K|V =
+        F.linear, RoPE, K/V stored at their positions, prompt attention (attention_oracle.prefill_attn_tiled, the
+        k_prefill_attn algorithm), x = bf16(x + F.linear(o, Wo, bo)), post RMSNorm, router top-4, experts.  Returns the
+        bf16 logits of the last token (the tail).  trace: optional list receiving per layer dict(x (the residual
+        input), h, q, k, v, o, mid, hn, logits, ids, wts, m)."""
+        from .attention_oracle import prefill_attn_tiled
+
+        tok = np.asarray(tokens, np.int64).reshape(-1)
+        T = tok.size
+        x = rb(self.embed[tok])
+        m = None
+        cs, sn = rope_tables(p0 + np.arange(T), self.inv_freq, self.att_scale)      # [T, 32]
+        cs, sn = cs[:, None, :], sn[:, None, :]
+        for li, ly in enumerate(self.layers):
+            if m is not None:
+                x = rb(x + m)
+            x_res = x
+            h = rms_bf16(x, ly["in_w"], self.eps)
+            y = linear_bf16(h, ly["Wqkv"], ly["bqkv"])
+            q = rope_bf16(y[:, :HQ].reshape(T, NQ, HD), cs, sn)
+            k = rope_bf16(y[:, HQ:HQ + NKV * HD].reshape(T, NKV, HD), cs, sn)
+            v = y[:, HQ + NKV * HD:].reshape(T, NKV, HD)
+            self.kc[li][:, p0:p0 + T] = k.transpose(1, 0, 2)
+            self.vc[li][:, p0:p0 + T] = v.transpose(1, 0, 2)
+            o = prefill_attn_tiled(q, self.kc[li], self.vc[li], ly["sinks"], p0, HD ** -0.5, ly["sliding"])
+            x = rb(x + linear_bf16(o.reshape(T, HQ), ly["Wo"], ly["bo"]))
+            hn = rms_bf16(x, ly["post_w"], self.eps)
+            logits = router_logits_bf16(hn, ly["Wr"], ly["br"])
+            sel = [router_top4(r) for r in logits]
+            ids = np.array([a for a, _ in sel], np.int64)
+            wts = np.array([b for _, b in sel], np.float32)
+            m = self.moe_rows(li, hn, ids, wts)
+            if trace is not None:
+                trace.append(dict(x=x_res, h=h, q=q, k=k, v=v, o=o, mid=x, hn=hn, logits=logits, ids=ids, wts=wts,
+                                  m=m))
+        return self.tail(x[-1], m[-1] if m is not None else None)
 
     def tail(self, mid, g):
         """Final norm + lm_head: bf16 logits [vocab] (server.py:521-525)."""
