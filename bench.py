@@ -268,8 +268,10 @@ def build_t950_pool(dev, seed):
 def bench_model(A):
     """Configuration 4: full 36-layer GPT-OSS-120B-shaped greedy decode on one GPU.  Random-init weights (attention,
     router, embedding and lm_head bf16 N(0, 0.02), norms 1 + N(0, 0.02), sinks N(0, 1), vocab 201088), all 36 x 128
-    MXFP4 experts resident (t950 layout, 61.2 GB), a context of 4096 random token ids read through the decode step
-    (its K/V written by the same kernels), then greedy decode with one hipGraph per step (embed, 36 x [QKV + RoPE +
+    MXFP4 experts resident (t950 layout, 61.2 GB), a context of 4096 random token ids prefilled (DecodeModel.prefill:
+    the prompt through every layer at once, its K/V written into the caches and its greedy successor appended; or,
+    with --context-mode decode, read token by token through the decode step), then greedy decode with one hipGraph
+    per step (embed, 36 x [QKV + RoPE +
     cache write, attention, o_proj, router + top-4, experts], final norm + lm_head + argmax; the next step reads its
     token on the device).  Timed: exactly --steps greedy steps from the end of the context; the warm-up steps run
     from the same context snapshot and are rolled back.  value = tokens / s.  The roofline is the expert gate_up
@@ -289,19 +291,29 @@ def bench_model(A):
                          single_launch=A.down == "layer")
     log("model: random-init dense weights")
     w = random_weights(device=dev, seed=77)
-    smax = ctx + max(n_new, A.warmup) + 1
+    smax = ctx + max(n_new, A.warmup) + 2
     model = DecodeModel(w, rx, smax=smax, n_split=A.attn_split, sliding_split=A.sliding_split)
     torch.cuda.synchronize()
     rng = np.random.default_rng(4096)
     prompt = rng.integers(0, w.vocab, ctx)
-    model.reset(prompt)
-    model.capture()
-    t0 = time.perf_counter()
-    model.run(ctx - 1)                                   # the context, token by token (graph replays)
-    torch.cuda.synchronize()
-    t_ctx = time.perf_counter() - t0
-    log(f"model: context of {ctx} tokens read in {t_ctx:.2f} s ({(ctx - 1) / t_ctx:.0f} steps/s)")
-    model.n_forced.fill_(ctx)
+    if A.context_mode == "prefill":
+        model.prefill(prompt[:64])                        # first calls: library GEMM selection, code loading
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.prefill(prompt, chunk=A.prefill_chunk)      # K/V of positions 0..ctx-1, seq[ctx] = its greedy token
+        torch.cuda.synchronize()
+        t_ctx = time.perf_counter() - t0
+        log(f"model: {ctx}-token context prefilled in {t_ctx * 1e3:.1f} ms ({ctx / t_ctx:.0f} tok/s)")
+        model.capture()
+    else:
+        model.reset(prompt)
+        model.capture()
+        t0 = time.perf_counter()
+        model.run(ctx - 1)                               # the context, token by token (graph replays)
+        torch.cuda.synchronize()
+        t_ctx = time.perf_counter() - t0
+        log(f"model: context of {ctx} tokens read in {t_ctx:.2f} s ({(ctx - 1) / t_ctx:.0f} steps/s)")
+        model.n_forced.fill_(ctx)
     snap = model.snapshot()
     model.run(A.warmup)
     torch.cuda.synchronize()
@@ -312,14 +324,15 @@ def bench_model(A):
     model.run(n_new)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    toks = model.seq[ctx:ctx + n_new].cpu().numpy()
+    t_lo = int(model.pos.item()) - n_new                 # position of the first timed step's input token
+    toks = model.seq[t_lo + 1:t_lo + 1 + n_new].cpu().numpy()
     tok_s = n_new / el
     log(f"model: {n_new} greedy tokens in {el * 1e3:.1f} ms: {el / n_new * 1e3:.3f} ms/token, {tok_s:.1f} tok/s")
     # determinism: the same steps again from the same snapshot give the same tokens
     model.restore(snap)
     model.run(n_new)
     torch.cuda.synchronize()
-    same = bool(np.array_equal(model.seq[ctx:ctx + n_new].cpu().numpy(), toks))
+    same = bool(np.array_equal(model.seq[t_lo + 1:t_lo + 1 + n_new].cpu().numpy(), toks))
     # ------------------------------------------------------------------ per-kernel events (one eager step)
     model.restore(snap)
     names = rx.launches(1)
@@ -371,7 +384,10 @@ def bench_model(A):
                       "launch_us": {**{nm: round(v, 2) for nm, v in avg.items()},
                                     "attention_full": round(att_full / (n_l / 2), 2),
                                     "attention_sliding": round(att_slide / (n_l / 2), 2)},
-                      "context_steps_per_s": round((ctx - 1) / t_ctx, 1)},
+                      "context_mode": A.context_mode,
+                      **({"context_prefill_ms": round(t_ctx * 1e3, 1), "prefill_tok_s": round(ctx / t_ctx, 1),
+                          "prefill_chunk": A.prefill_chunk} if A.context_mode == "prefill" else
+                         {"context_steps_per_s": round((ctx - 1) / t_ctx, 1)})},
            "roofline": {"bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(gu_gbps / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kname,
                         "avg_launch_us": round(avg[dom], 3), "algorithmic_bytes_per_launch": gu_bytes},
@@ -477,6 +493,10 @@ def main():
                          "attention: configuration 3 (decode attention); model: configuration 4 (full decode)")
     ap.add_argument("--tokens", type=int, default=2048, help="prefill: prompt tokens")
     ap.add_argument("--context", type=int, default=4096, help="model: context tokens before the timed decode")
+    ap.add_argument("--context-mode", choices=("prefill", "decode"), default="prefill",
+                    help="model: build the context by prompt processing (default) or token by token through the "
+                         "decode step")
+    ap.add_argument("--prefill-chunk", type=int, default=4096, help="model: prompt block size of the prefill")
     ap.add_argument("--attn-split", type=int, default=32, help="model: key chunks of full-attention layers")
     ap.add_argument("--sliding-split", type=int, default=1, help="model: key chunks of sliding-window layers")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
