@@ -244,6 +244,20 @@ int na_core_lm_tail(const void* mid, const void* g, const float* c, const void* 
                     int step_pos, int64_t* seq, const int64_t* n_forced, int64_t* pred, long long seq_len,
                     hipStream_t stream);
 
+/* na_core_lm_tail with sampling (reference server.py:1576-1583, t_body_sample): when *temp > 0 the token is
+ * argmax_v(logit_v / temp + g_v), g_v = -log(-log(clamp(u_v, 1e-12, 1 - 1e-7))) in fp32 (Gumbel-max: a draw from
+ * softmax(logits / temp)), first index on ties; when *temp <= 0 it is the greedy argmax of na_core_lm_tail.
+ *   temp  fp32 [1] on the device
+ *   u     fp32 [vocab] uniform draws in [0, 1) (the reference's u_dev, refreshed by the caller per step), or NULL:
+ *         u_v = top 24 bits of splitmix64(splitmix64(*seed ^ p) ^ v) * 2^-24 with p = *pos (the step's input
+ *         position), so a captured step draws fresh numbers at every position with no host work
+ *   seed  uint64 [1] on the device, or NULL (0) */
+int na_core_lm_tail_sample(const void* mid, const void* g, const float* c, const void* final_w, float eps,
+                           const void* Wl, int vocab, void* hn, void* logits_out, unsigned long long* part,
+                           int64_t* tok, int64_t* pos, int step_pos, int64_t* seq, const int64_t* n_forced,
+                           int64_t* pred, long long seq_len, const float* temp, const float* u,
+                           const unsigned long long* seed, hipStream_t stream);
+
 /* ---- dense core over T prompt tokens (prefill), one row per workgroup; the GEMMs between them are plain bf16
  *      library GEMMs (hipBLASLt), as the reference's F.linear calls.  Replace the row-wise parts of server.py:2357-2418
  *      (_rope_tables, _rope, _attn_router, _prefill_block) and of neural/moe/gptoss_core_graphs.py:48-53 (_rms). */

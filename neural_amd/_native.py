@@ -45,6 +45,8 @@ SIGNATURES = {
     "na_core_lm_tail": [VP, VP, VP, VP, F32, VP, I32, VP, VP, VP, VP, VP, I32, VP, VP, VP, I64, VP],
     "na_prefill_attention": [VP, VP, VP, I64, VP, VP, I64, I64, I64, I64, VP, VP, I64, I32, F32, I32, I32, VP, VP],
     "na_ring_write": [VP, VP, I32, VP, VP, I64, I64, I64, I64, I64, I32, VP],
+    "na_core_lm_tail_sample": [VP, VP, VP, VP, F32, VP, I32, VP, VP, VP, VP, VP, I32, VP, VP, VP, I64, VP, VP, VP,
+                               VP],
     "na_rows_embed": [VP, I64, VP, I32, VP, VP],
     "na_rows_norm": [VP, VP, I32, VP, F32, VP, VP],
     "na_rows_rope": [VP, I32, I64, VP, F32, VP, VP, I64, I64, VP, I64, I64, VP],

@@ -349,15 +349,55 @@ NA_DEVICE uint32_t bf16_order_key(uint16_t b) {
 // Tail 2: logits = bf16(hn . lm_head[v]) for 16 rows per workgroup; the workgroup's best as a 64-bit key
 // (order key of the logit << 32 | ~index: a larger key is a larger logit, then a smaller index) -> part[wg];
 // optionally the logits themselves.
-template <int TPR>
+// Monotone map of fp32 bit patterns to unsigned order (-0 equal to +0).
+NA_DEVICE uint32_t f32_order_key(float f) {
+  uint32_t b = __float_as_uint(f);
+  if (b == 0x80000000u) b = 0;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// SplitMix64 (Steele, Lea and Flood, "Fast splittable pseudorandom number generators", OOPSLA 2014): the output
+// function of its generator, used as a counter-based hash.
+NA_DEVICE uint64_t splitmix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// Uniform draw in [0, 1) on a 2^-24 grid for (seed, position, vocabulary index): the top 24 bits of
+// splitmix64(splitmix64(seed ^ position) ^ index).
+NA_DEVICE float uniform_draw(uint64_t seed, uint64_t p, uint32_t v) {
+  return (float)(splitmix64(splitmix64(seed ^ p) ^ (uint64_t)v) >> 40) * 0x1p-24f;
+}
+
+// Sampling parameters of the tail (reference server.py:1576-1583, t_body_sample): token = argmax(logit / temp +
+// g), g = -log(-log(clamp(u, 1e-12, 1 - 1e-7))), fp32, first index on ties; *temp <= 0 selects greedy argmax.  u
+// from the array (the reference's u_dev, refreshed by the caller) or, without one, uniform_draw(*seed, *pos, v)
+// (seed and pos read on the device, so a captured step draws new numbers at every position).
+struct SampleArgs {
+  const float* temp;
+  const float* u;
+  const int64_t* pos;
+  const uint64_t* seed;
+};
+
+template <int TPR, bool SAMPLE>
 __global__ __launch_bounds__(256) void k_lmhead(const uint16_t* __restrict__ hn, const uint16_t* __restrict__ Wl,
                                                 int vocab, uint16_t* __restrict__ logits_out,
-                                                uint64_t* __restrict__ part) {
+                                                uint64_t* __restrict__ part, SampleArgs sa) {
   __shared__ __align__(16) uint16_t hc[kH];
   constexpr int ROWS = 256 / TPR;
   __shared__ uint64_t best[ROWS];
   const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
   const int v = ROWS * blockIdx.x + r;
+  float temp = 0.f;
+  uint64_t p = 0, seed = 0;
+  if constexpr (SAMPLE) {
+    temp = *sa.temp;
+    p = sa.pos ? (uint64_t)*sa.pos : 0;
+    seed = sa.seed ? *sa.seed : 0;
+  }
   VecIn<kH> a;
   a.load(hn);
   __builtin_amdgcn_sched_barrier(0);
@@ -369,7 +409,16 @@ __global__ __launch_bounds__(256) void k_lmhead(const uint16_t* __restrict__ hn,
   const uint16_t lb = f32_to_bf16(s);
   if (j == 0) {
     if (logits_out && v < vocab) logits_out[v] = lb;
-    best[r] = v < vocab ? ((uint64_t)bf16_order_key(lb) << 32) | (uint64_t)(0xffffffffu - (uint32_t)v) : 0ull;
+    uint32_t key = bf16_order_key(lb);
+    if constexpr (SAMPLE) {
+      if (temp > 0.f && v < vocab) {
+        float u = sa.u ? sa.u[v] : uniform_draw(seed, p, (uint32_t)v);
+        u = fminf(fmaxf(u, 1e-12f), 1.0f - 1e-7f);
+        const float gum = -logf(-logf(u));
+        key = f32_order_key(bf16_to_f32(lb) / temp + gum);
+      }
+    }
+    best[r] = v < vocab ? ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)v) : 0ull;
   }
   __syncthreads();
   if (tid == 0) {
@@ -578,8 +627,28 @@ int na_core_lm_tail(const void* mid, const void* g, const float* c, const void* 
   const int nwg = (int)na_core_lm_partials(vocab);
   hipLaunchKernelGGL(k_final_norm, dim3(1), dim3(256), 0, stream, (const uint16_t*)mid, (const uint16_t*)g, c,
                      (const uint16_t*)final_w, eps, (uint16_t*)hn);
-  hipLaunchKernelGGL(k_lmhead<kLmTpr>, dim3(nwg), dim3(256), 0, stream, (const uint16_t*)hn, (const uint16_t*)Wl, vocab,
-                     (uint16_t*)logits_out, (uint64_t*)part);
+  hipLaunchKernelGGL((k_lmhead<kLmTpr, false>), dim3(nwg), dim3(256), 0, stream, (const uint16_t*)hn,
+                     (const uint16_t*)Wl, vocab, (uint16_t*)logits_out, (uint64_t*)part, SampleArgs{});
+  hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, stream, (const uint64_t*)part, nwg, tok, pos, step_pos, seq,
+                     n_forced, pred, seq_len);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int na_core_lm_tail_sample(const void* mid, const void* g, const float* c, const void* final_w, float eps,
+                           const void* Wl, int vocab, void* hn, void* logits_out, unsigned long long* part,
+                           int64_t* tok, int64_t* pos, int step_pos, int64_t* seq, const int64_t* n_forced,
+                           int64_t* pred, long long seq_len, const float* temp, const float* u,
+                           const unsigned long long* seed, hipStream_t stream) {
+  if (!mid || !final_w || !Wl || vocab <= 0 || !hn || !part || !tok || !temp) return kErrArgs;
+  if ((step_pos || seq || pred) && !pos) return kErrArgs;
+  if ((seq || pred) && seq_len <= 0) return kErrArgs;
+  if (c && !g) return kErrArgs;
+  const int nwg = (int)na_core_lm_partials(vocab);
+  hipLaunchKernelGGL(k_final_norm, dim3(1), dim3(256), 0, stream, (const uint16_t*)mid, (const uint16_t*)g, c,
+                     (const uint16_t*)final_w, eps, (uint16_t*)hn);
+  hipLaunchKernelGGL((k_lmhead<kLmTpr, true>), dim3(nwg), dim3(256), 0, stream, (const uint16_t*)hn,
+                     (const uint16_t*)Wl, vocab, (uint16_t*)logits_out, (uint64_t*)part,
+                     SampleArgs{temp, u, pos, (const uint64_t*)seed});
   hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, stream, (const uint64_t*)part, nwg, tok, pos, step_pos, seq,
                      n_forced, pred, seq_len);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;

@@ -133,7 +133,7 @@ class DecodeModel:
     ``pos + 1 < n_forced``, to ``seq[pos + 1]``; it then advances ``pos``.  All of that state lives on the device."""
 
     def __init__(self, weights: DecodeWeights, experts: ResidentExperts, smax: int, n_split: int = 32,
-                 sliding_split: int = 1, ring: int | None = None, keep_logits: bool = False):
+                 sliding_split: int = 1, ring: int | None = None, keep_logits: bool = False, sample: bool = False):
         dev = weights.embed.device
         if dev.type != "cuda":
             raise ValueError("weights must be on a CUDA device")
@@ -172,6 +172,12 @@ class DecodeModel:
         self.wts = z(1, TOP_K)
         self.part = z(N.lib().na_core_lm_partials(weights.vocab), dt=torch.int64)
         self.logits = z(weights.vocab) if keep_logits else None
+        # sampling tail (sample=True): temperature (<= 0: greedy) and seed live on the device, so a captured step
+        # follows set_sampling() without a new capture; u: optional caller-refreshed uniforms [vocab] fp32
+        self.sample = bool(sample)
+        self.temp = z(1, dt=torch.float32)
+        self.seed = z(1, dt=torch.int64)
+        self.u = None
         ns_max = max(self.n_split, self.sliding_split)
         if not 1 <= self.n_split <= 64 or not 1 <= self.sliding_split <= 64:
             raise ValueError("n_split and sliding_split must be in [1, 64]")
@@ -243,10 +249,30 @@ class DecodeModel:
                self.pos.data_ptr(), self.mid.data_ptr(), N.stream(self.dev))
 
     def tail(self, step_pos: bool = True) -> None:
-        N.call("na_core_lm_tail", self.mid.data_ptr(), self.g.data_ptr() if self.n_layers else None, None,
-               self.w.final_w.data_ptr(), EPS, self.w.lm_head.data_ptr(), self.w.vocab, self.hn.data_ptr(),
-               N.ptr(self.logits), self.part.data_ptr(), self.tok.data_ptr(), self.pos.data_ptr(), int(step_pos),
-               self.seq.data_ptr(), self.n_forced.data_ptr(), self.pred.data_ptr(), self.smax, N.stream(self.dev))
+        args = (self.mid.data_ptr(), self.g.data_ptr() if self.n_layers else None, None, self.w.final_w.data_ptr(),
+                EPS, self.w.lm_head.data_ptr(), self.w.vocab, self.hn.data_ptr(), N.ptr(self.logits),
+                self.part.data_ptr(), self.tok.data_ptr(), self.pos.data_ptr(), int(step_pos), self.seq.data_ptr(),
+                self.n_forced.data_ptr(), self.pred.data_ptr(), self.smax)
+        if self.sample:
+            N.call("na_core_lm_tail_sample", *args, self.temp.data_ptr(), N.ptr(self.u), self.seed.data_ptr(),
+                   N.stream(self.dev))
+        else:
+            N.call("na_core_lm_tail", *args, N.stream(self.dev))
+
+    def set_sampling(self, temperature: float, seed: int = 0, u: torch.Tensor | None = None) -> None:
+        """Sampling tail settings (needs sample=True): temperature > 0 draws from softmax(logits / temperature) by
+        Gumbel-max (reference server.py:1576-1583), 0 is greedy; seed keys the on-device uniforms (one draw per
+        position and vocabulary entry); u, if given, is a [vocab] fp32 tensor of uniforms the caller refreshes
+        before each step instead (the reference's u_dev).  Device writes only: a captured graph picks them up, but
+        switching between u and the seeded draws needs a new capture."""
+        if not self.sample:
+            raise RuntimeError("this DecodeModel was built without the sampling tail (sample=True)")
+        if u is not None and (u.dtype is not torch.float32 or u.numel() != self.w.vocab or u.device != self.dev
+                              or not u.is_contiguous()):
+            raise ValueError(f"u must be contiguous fp32 [{self.w.vocab}] on {self.dev}")
+        self.temp.fill_(float(temperature))
+        self.seed.fill_(int(seed) & 0x7FFFFFFFFFFFFFFF)
+        self.u = u
 
     def step(self, events=None) -> None:
         """One decode step (embed, every layer, tail) on the current stream.  events: None or one dict per layer (see

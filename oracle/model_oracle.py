@@ -225,6 +225,41 @@ class DecodeOracle:
         return self.tail(mid, g)
 
 
+_GAMMA = np.uint64(0x9E3779B97F4A7C15)
+
+
+def splitmix64(z):
+    """SplitMix64's output function (Steele, Lea and Flood, OOPSLA 2014) on uint64 values, wrapping arithmetic."""
+    z = np.asarray(z, np.uint64)
+    with np.errstate(over="ignore"):
+        z = z + _GAMMA
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def uniform_draws(seed: int, pos: int, n: int) -> np.ndarray:
+    """The tail's on-device uniforms for (seed, position): top 24 bits of splitmix64(splitmix64(seed ^ pos) ^ v),
+    times 2^-24, for v < n (fp32, exact)."""
+    z = splitmix64(np.uint64(seed) ^ np.uint64(pos))
+    return (splitmix64(z ^ np.arange(n, dtype=np.uint64)) >> np.uint64(40)).astype(np.float32) * np.float32(2.0 ** -24)
+
+
+def gumbel_scores(logits, temp, u) -> np.ndarray:
+    """The sampling tail's fp32 scores (reference server.py:1576-1583): logits / temp + (-log(-log(clamp(u, 1e-12,
+    1 - 1e-7))))."""
+    uc = np.clip(np.asarray(u, np.float32), np.float32(1e-12), np.float32(1.0 - 1e-7)).astype(np.float32)
+    g = (-np.log(-np.log(uc))).astype(np.float32)
+    return (np.asarray(logits, np.float32) / np.float32(temp)).astype(np.float32) + g
+
+
+def sample_token(logits, temp, u) -> int:
+    """Gumbel-max draw: argmax of gumbel_scores (first index on ties); temp <= 0 is the greedy argmax."""
+    if temp <= 0:
+        return argmax_first(logits)
+    return int(np.argmax(gumbel_scores(logits, temp, u)))
+
+
 def argmax_first(logits) -> int:
     """First index of the maximum (torch.argmax's documented tie rule; server.py:525)."""
     return int(np.argmax(np.asarray(logits, np.float32)))
