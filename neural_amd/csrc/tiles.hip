@@ -352,12 +352,18 @@ __device__ __noinline__ void dup_rows_store_w(uint16_t* yw, uint64_t users, uint
   }
 }
 
-// LDS of one expert-major decode workgroup: staged x (or h) rows, scale rows, the KS partial D tiles.
+// LDS of one expert-major decode workgroup: staged x (or h) rows, scale rows, the KS partial D tiles [KS][2][64].
+// With 4 or more staged rows the partial tiles reuse the rows' space (after a barrier that ends every wave's reads
+// of them), which keeps three workgroups per CU at 8 rows instead of two.
 template <int KS, int XT>
 struct DecodeLds {
+  static constexpr bool kAliasRed = XT >= 4;
+  static constexpr int kRedBytes = (KS > 1 ? KS : 1) * 2 * 64 * 16;
+  static_assert(!kAliasRed || kRedBytes <= XT * kXPitch, "partial tiles must fit in the staged rows");
   __align__(16) uint8_t xs[XT * kXPitch];
   __align__(16) uint8_t sc[2 * kScLds];
-  f32x4_t red[KS > 1 ? KS : 1][2][64];
+  __align__(16) uint8_t red_own[kAliasRed ? 16 : kRedBytes];
+  NA_DEVICE f32x4_t* red() { return reinterpret_cast<f32x4_t*>(kAliasRed ? xs : red_own); }
 };
 
 // gate_up: output block b (rows j = 16b .. 16b + 15 of gate and of up) of the item-th distinct expert -> h[pair, j].
@@ -411,7 +417,7 @@ __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
   if constexpr (XT == 1) {
     // one token: only D row 0 (element 0 of lanes 0..15) is used; the same sums in the same order as below
     if constexpr (KS > 1) {
-      float* red = reinterpret_cast<float*>(&L.red[0][0][0]);    // [KS][2][16]
+      float* red = reinterpret_cast<float*>(L.red());           // [KS][2][16]
       if (lane < 16) {
         red[(2 * wave) * 16 + lane] = ag[0];
         red[(2 * wave + 1) * 16 + lane] = au[0];
@@ -439,16 +445,18 @@ __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
     return;
   }
   if constexpr (KS > 1) {
-    L.red[wave][0][lane] = ag;
-    L.red[wave][1][lane] = au;
+    f32x4_t* red = L.red();
+    if constexpr (DecodeLds<KS, XT>::kAliasRed) __syncthreads();   // every wave is done with the staged rows
+    red[(2 * wave) * 64 + lane] = ag;
+    red[(2 * wave + 1) * 64 + lane] = au;
     __syncthreads();
     if (wave != 0) return;
-    ag = L.red[0][0][lane];
-    au = L.red[0][1][lane];
+    ag = red[lane];
+    au = red[64 + lane];
 #pragma unroll
     for (int w = 1; w < KS; ++w) {
-      ag += L.red[w][0][lane];
-      au += L.red[w][1][lane];
+      ag += red[(2 * w) * 64 + lane];
+      au += red[(2 * w + 1) * 64 + lane];
     }
   }
   uint16_t hv[4];
@@ -514,12 +522,14 @@ __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   block_compute<MT>(rd, L.sc + (lane & 15) * kScPitch, L.xs + min(lane & 15, XT - 1) * kXPitch, lane, t0, t1, acc);
   if constexpr (KS > 1) {
-    L.red[wave][0][lane] = acc;
+    f32x4_t* red = L.red();
+    if constexpr (DecodeLds<KS, XT>::kAliasRed) __syncthreads();   // every wave is done with the staged rows
+    red[(2 * wave) * 64 + lane] = acc;
     __syncthreads();
     if (wave != 0) return;
-    acc = L.red[0][0][lane];
+    acc = red[lane];
 #pragma unroll
-    for (int w = 1; w < KS; ++w) acc += L.red[w][0][lane];
+    for (int w = 1; w < KS; ++w) acc += red[(2 * w) * 64 + lane];
   }
   float yb[4];
 #pragma unroll
