@@ -70,6 +70,11 @@ def measured_traffic(kernel, layout, batch, k_split):
     return None, "workload not in traffic table"
 
 
+def effective_k_split(k_split, batch):
+    """The k_split the library runs for a requested one (0 = automatic, as na_moe_decode_t950 picks it)."""
+    return k_split if k_split > 0 else (8 if batch == 1 else 4)
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -366,7 +371,7 @@ def bench_model(A):
     kname = "k_moe_layer_t950" if dom == "layer" else "k_moe_gate_up_t950"
     log("model: per launch " + ", ".join(f"{nm} {v:.2f} us" for nm, v in avg.items())
         + f", attention full {att_full / (n_l / 2):.2f} us, sliding {att_slide / (n_l / 2):.2f} us")
-    traffic, why = measured_traffic(kname, "t950", 1, A.k_split)
+    traffic, why = measured_traffic(kname, "t950", 1, effective_k_split(A.k_split, 1))
     dense = N_LAYERS * 2 * (5120 * 2880 + 2880 * 4096 + 128 * 2880) + 2 * 201088 * 2880
     experts = N_LAYERS * TOPK * SLOT_ALGO_BYTES
     kv = 2 * 2 * 8 * 64 * (18 * (ctx + n_new / 2) + 18 * 128)
@@ -478,7 +483,8 @@ def main():
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--layout", choices=("t950", "raw", "ps4"), default="t950",
                     help="resident slot layout: gfx950 tiles (MFMA kernels) or the store layouts (VALU kernels)")
-    ap.add_argument("--k-split", type=int, default=4, help="t950: waves per workgroup splitting K (1, 2, 4)")
+    ap.add_argument("--k-split", type=int, default=0,
+                    help="t950 gate_up: waves per workgroup splitting K (1, 2, 4, 8; 0 = automatic: 8 at batch 1, else 4)")
     ap.add_argument("--down", choices=("combine", "layer", "expert"), default="combine",
                     help="t950, batch 1: gate_up then down + combine (two launches, default), both in one launch with "
                          "a grid barrier (layer), or expert-major down + a combine kernel (expert)")
@@ -649,7 +655,7 @@ def main():
     per_launch = tot[dom][1] / tot[dom][2]
     kname = ("k_moe_layer_t950" if dom == "layer" else "k_moe_gate_up_t950") if A.layout == "t950" \
         else "k_moe_gate_up"
-    traffic, why = measured_traffic(kname, A.layout, B, A.k_split)
+    traffic, why = measured_traffic(kname, A.layout, B, effective_k_split(A.k_split, B))
     log(f"traffic: {traffic} ({why})")
     roofline = {"bound": "hbm", "achieved": round(top["gbps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(top["gbps"] / HBM_PEAK_GBS, 4), "traffic": traffic,

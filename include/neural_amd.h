@@ -98,7 +98,7 @@ int na_repack_from_t950(const void* src, long long src_stride, void* dst, long l
 
 /* na_moe_decode over a t950 pool (slot_bytes >= 13,271,040, 16-byte aligned): the same contract and results as
  * na_moe_decode (server.py:508-518), computed with v_mfma_f32_16x16x32_bf16 on in-register dequantised codes.
- * k_split = waves per workgroup splitting K in the expert-major kernels (1, 2, 4 or 8; <= 0: 4).
+ * k_split = waves per workgroup splitting K in the expert-major kernels (1, 2, 4 or 8; <= 0: 8 for B = 1, else 4).
  * down_mode 0: for B = 1 with an output, two launches: gate_up, then one down workgroup per 16 output rows that
  *   holds every distinct expert of the token and sums the top-k outputs itself (events = 4: gate_up, down);
  *   otherwise as down_mode 1.

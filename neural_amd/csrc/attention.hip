@@ -71,6 +71,7 @@ __global__ __launch_bounds__(256) void k_decode_attn(
     uint16_t* __restrict__ out, float scaling, int window, int ring, int ns, float* __restrict__ work,
     uint32_t* __restrict__ counters) {
   __shared__ AttnLds L;
+  args_at_entry(q, kc, vc, cache_rows, sinks, pos_p, out, scaling, window, ring, ns, work, counters);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, n = lane & 15;          // row group (D rows 4g..4g+3) and column of this lane
   const int c = blockIdx.x % ns;

@@ -49,6 +49,18 @@ NA_DEVICE uint4 load16(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Kernel arguments read at entry: an empty asm that takes each argument in scalar registers makes the compiler load
+// them in one batch before the first instruction that depends on memory, instead of with one dependent scalar load
+// (a round trip to the L2) at each first use further down the kernel.
+NA_DEVICE void sgpr_use(const void* v) { asm volatile("" ::"s"(v)); }
+NA_DEVICE void sgpr_use(long long v) { asm volatile("" ::"s"(v)); }
+NA_DEVICE void sgpr_use(int v) { asm volatile("" ::"s"(v)); }
+NA_DEVICE void sgpr_use(float v) { asm volatile("" ::"s"(v)); }
+template <typename... T>
+NA_DEVICE void args_at_entry(T... v) {
+  (sgpr_use(v), ...);
+}
+
 NA_DEVICE float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
 // fp32 -> bf16, round to nearest even, in integer arithmetic (NaN -> quiet NaN).  The reference rounding of the

@@ -174,6 +174,7 @@ struct VecIn {
 __global__ __launch_bounds__(256) void k_embed(const uint16_t* __restrict__ emb, long long vocab,
                                                const int64_t* __restrict__ seq, long long seq_len,
                                                const int64_t* __restrict__ pos, uint16_t* __restrict__ mid) {
+  args_at_entry(emb, vocab, seq, seq_len, pos, mid);
   long long p = pos ? *pos : 0;
   p = p < 0 ? 0 : p >= seq_len ? seq_len - 1 : p;
   long long t = seq[p];

@@ -243,6 +243,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_gate_up(
     const uint16_t* __restrict__ bias_gu, uint16_t* __restrict__ h, float alpha, float limit) {
   constexpr bool XREG = NT <= 2;
   __shared__ uint32_t xs[XREG ? 1 : NT * kXTok];
+  args_at_entry(x, ids, B, pool, slot_bytes, slot_tab, expert_base, bias_gu, h, alpha, limit);
   Route r;
   if (route_item(ids, 4 * B, blockIdx.x, r) != kItem) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -307,6 +308,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_down(
     long long expert_base, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw) {
   constexpr bool XREG = NT <= 2;
   __shared__ uint32_t xs[XREG ? 1 : NT * kXTok];
+  args_at_entry(h, ids, wts, B, pool, slot_bytes, slot_tab, expert_base, bias_dn, yw);
   Route r;
   const int st = route_item(ids, 4 * B, blockIdx.x, r);
   if (st == kNoItem) return;

@@ -272,8 +272,11 @@ NA_DEVICE void store_row_pairs(uint16_t* row_ptr, uint16_t v, bool ok) {
 // result is written to every pair of its token in `all`.  `valid` = distinct experts with a valid id (the invalid
 // marker 128 excluded).  Pair lists stay masks in scalar registers: an indexed register array would be placed in
 // scratch memory.
+// MAXP bounds the pair count (npairs <= MAXP <= 32): the dedupe compares each pair with the MAXP - 1 before it.
+template <int MAXP>
 NA_DEVICE int route_t950(const int64_t* ids, int npairs, int item, int& nt, uint64_t& users, uint64_t& all,
                          int& distinct, int& valid) {
+  static_assert(MAXP >= 1 && MAXP <= 32, "at most 8 tokens x top-4 pairs");
   const int lane = threadIdx.x & 63;
   int my = 129;
   if (lane < npairs) {
@@ -282,7 +285,7 @@ NA_DEVICE int route_t950(const int64_t* ids, int npairs, int item, int& nt, uint
   }
   bool dup = false;
 #pragma unroll
-  for (int j = 0; j < 32; ++j) {
+  for (int j = 0; j < MAXP - 1; ++j) {
     const int o = __builtin_amdgcn_readlane(my, j);
     dup |= (j < lane) && (o == my);
   }
@@ -297,7 +300,8 @@ NA_DEVICE int route_t950(const int64_t* ids, int npairs, int item, int& nt, uint
   const int e = __builtin_amdgcn_readlane(my, __ffsll((long long)fm) - 1);
   all = __ballot(lane < npairs && my == e);
   users = first_per_token(all);
-  nt = min(__popcll(users), kMaxTokT);
+  const int nu = __popcll(users);
+  nt = nu < kMaxTokT ? nu : kMaxTokT;
   return e;
 }
 
@@ -378,9 +382,10 @@ __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
   constexpr int MT = (kTTiles + KS - 1) / KS;
   constexpr int NTH = 64 * KS;
   __shared__ DecodeLds<KS, XT> L;
+  args_at_entry(x, ids, B, pool, slot_bytes, slot_tab, expert_base, bias_gu, h, alpha, limit);
   int nt, distinct, valid;
   uint64_t users, all;
-  const int e = route_t950(ids, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
+  const int e = route_t950<4 * XT>(ids, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
   if (e < 0 || e == 128) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.y;
@@ -485,9 +490,10 @@ __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
   constexpr int MT = (kTTiles + KS - 1) / KS;
   constexpr int NTH = 64 * KS;
   __shared__ DecodeLds<KS, XT> L;
+  args_at_entry(h, ids, wts, B, pool, slot_bytes, slot_tab, expert_base, bias_dn, yw);
   int nt, distinct, valid;
   uint64_t users, all;
-  const int e = route_t950(ids, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
+  const int e = route_t950<4 * XT>(ids, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
   if (e < 0) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.y;
@@ -583,13 +589,14 @@ __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
   constexpr int NTH = 64 * kDcWaves;
   constexpr int GTH = 64 * KSD;
   __shared__ DownCombLds<KSD, XT> L;
+  args_at_entry(h, ids, wts, B, pool, slot_bytes, slot_tab, expert_base, bias_dn, out);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = wave / KSD, kw = wave - g * KSD, gtid = tid - g * GTH;
   const int b = blockIdx.x;
   const int npairs = 4 * B;
   int nt, distinct, valid;
   uint64_t users, all;
-  const int e = route_t950(ids, npairs, g, nt, users, all, distinct, valid);
+  const int e = route_t950<4 * XT>(ids, npairs, g, nt, users, all, distinct, valid);
   const bool live = e >= 0 && e != 128;
   const long long gid = expert_base + (live ? e : 0);
   // groups without a live expert load slot 0's block (valid memory) with every tile slot zeroed, so that the loads
@@ -914,7 +921,7 @@ int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
   if (down_mode != 0 && down_mode != 1) return kErrArgs;
   if (B > 8) return kErrTooLarge;
   if (slot_bytes < kTSlot || (slot_bytes & 15) || (reinterpret_cast<uintptr_t>(pool) & 15)) return kErrArgs;
-  if (k_split <= 0) k_split = 4;
+  if (k_split <= 0) k_split = B == 1 ? 8 : 4;       // automatic: the fastest measured on MI355X per batch size
   if (k_split != 1 && k_split != 2 && k_split != 4 && k_split != 8) return kErrArgs;
   // down_mode 0, B = 1, with an output: gate_up, then down + combine (two launches); else gate_up, down, combine
   // (at B = 2 the row-block kernel's 16-wave workgroups with two waves per expert measured slower than three launches)

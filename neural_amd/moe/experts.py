@@ -21,17 +21,18 @@ class ResidentExperts:
     def __init__(self, pool: torch.Tensor, layout: ExpertLayout = GPTOSS_LAYOUT, bias_gu: torch.Tensor | None = None,
                  bias_dn: torch.Tensor | None = None, slot_tab: torch.Tensor | None = None,
                  max_batch: int = MAX_DECODE_TOKENS, gu_pairs_per_wave: int = 4, dn_pairs_per_wave: int = 2,
-                 k_split: int = 4, combine_in_down: bool = True, single_launch: bool = False):
+                 k_split: int = 0, combine_in_down: bool = True, single_launch: bool = False):
         """pool: uint8 [n, layout.slot_bytes] in the raw, PS4 or t950 (gfx950 tile) layout.  The t950 layout runs the
-        MFMA decode kernels (k_split waves per workgroup split K); with combine_in_down, a single token takes two
-        launches (the down kernel holds every expert of an output block and sums the top-k itself) instead of three,
-        and with single_launch one: gate_up and down + combine in one kernel separated by a grid-wide barrier (the
-        same arithmetic, bit for bit; measured slower than two launches on MI355X, whose cross-XCD barrier costs as
-        much as a kernel boundary).  The store layouts run the VALU kernels (gu/dn_pairs_per_wave row pairs per wavefront)."""
+        MFMA decode kernels (k_split waves per workgroup split K; 0 picks per batch: 8 for one token, else 4); with
+        combine_in_down, a single token takes two launches (the down kernel holds every expert of an output block and
+        sums the top-k itself) instead of three, and with single_launch one: gate_up and down + combine in one kernel
+        separated by a grid-wide barrier (the same arithmetic, bit for bit; measured slower than two launches on
+        MI355X, whose cross-XCD barrier costs as much as a kernel boundary).  The store layouts run the VALU kernels
+        (gu/dn_pairs_per_wave row pairs per wavefront)."""
         if layout.weight_repr not in ("mxfp4_g32", "mxfp4_g32_ps4", TILE_REPR):
             raise ValueError(f"ResidentExperts serves the raw, PS4 and t950 slot layouts, not {layout.weight_repr}")
-        if k_split not in (1, 2, 4, 8):
-            raise ValueError("k_split must be 1, 2, 4 or 8")
+        if k_split not in (0, 1, 2, 4, 8):
+            raise ValueError("k_split must be 0 (automatic), 1, 2, 4 or 8")
         self.k_split = int(k_split)
         self.tiled = layout.weight_repr == TILE_REPR
         if pool.dtype is not torch.uint8 or pool.ndim != 2 or pool.shape[1] != layout.slot_bytes:

@@ -142,8 +142,8 @@ def _t950_case(B, seed, bias, nslot=10):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,k_split,bias", [(1, 4, False), (1, 1, True), (2, 2, True), (4, 4, True), (8, 4, False),
-                                            (8, 2, True)])
+@pytest.mark.parametrize("B,k_split,bias", [(1, 4, False), (1, 8, True), (1, 0, False), (1, 1, True), (2, 2, True),
+                                            (4, 4, True), (8, 4, False), (8, 2, True), (8, 8, True)])
 def test_moe_decode_t950_matches_oracle_and_store_path(B, k_split, bias):
     import torch
     from neural_amd.moe.experts import ResidentExperts
@@ -294,7 +294,7 @@ def test_single_launch_layer_matches_two_launch_path(with_bias):
     tabd = torch.from_numpy(tab).to(dev)
     bg, bd = (bgu.to(dev), bdn.to(dev)) if with_bias else (None, None)
     one = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, single_launch=True)
-    two = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd)
+    two = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4)    # the layer kernel's K split
     assert one.launches(1) == ("layer",) and two.launches(1) == ("gate_up", "down_combine")
     rng = np.random.default_rng(17)
     cache = {}
@@ -377,8 +377,8 @@ def test_duplicate_ids_in_a_token(B):
     tiles.repack_to_t950(raw, tp)
     tabd, bg, bd = torch.from_numpy(tab).to(dev), bgu.to(dev), bdn.to(dev)
     paths = {"single": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, single_launch=True),
-             "two": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd),
-             "three": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, combine_in_down=False),
+             "two": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4),   # the layer kernel's K split
+             "three": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=False),
              "store": ResidentExperts(raw, GPTOSS_LAYOUT, bg, bd, tabd)}
     xd, idd = x.to(dev), torch.from_numpy(ids).to(dev)
     wd = torch.from_numpy(w).to(torch.bfloat16).to(dev)
