@@ -5,7 +5,9 @@
 The library is built in-tree so that it travels with the repository snapshot; nothing is JIT-compiled at import time.
 Every .hip file is compiled as its own object (parallel), then linked.  All device code is built with packed-fp32
 instructions disabled (-target-feature -packed-fp32-ops): hipcc would otherwise form v_pk_{add,mul,fma}_f32 from
-ordinary float code.
+ordinary float code.  The first kernel arguments (up to 14 dwords) are preloaded into scalar registers at wave launch
+(-amdgpu-kernarg-preload-count), so that a kernel's first dependent read is issued without a round trip for its
+pointer; each kernel keeps the compiler's fallback prologue that loads them where the firmware does not preload.
 """
 from __future__ import annotations
 
@@ -23,7 +25,8 @@ LIB_PATH = os.path.join(OUT_DIR, LIB_NAME)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
-         "-packed-fp32-ops", "-Wno-unused-result", f"-I{os.path.join(os.path.dirname(HERE), 'include')}"]
+         "-packed-fp32-ops", "-mllvm", "-amdgpu-kernarg-preload-count=16", "-Wno-unused-result",
+         f"-I{os.path.join(os.path.dirname(HERE), 'include')}"]
 
 
 def sources():

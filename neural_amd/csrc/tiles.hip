@@ -265,6 +265,13 @@ NA_DEVICE void store_row_pairs(uint16_t* row_ptr, uint16_t v, bool ok) {
   if (ok && !(lane & 1)) *reinterpret_cast<uint32_t*>(row_ptr + (lane & 15)) = (uint32_t)v | (hi << 16);
 }
 
+// The id of this lane's pair (lanes past the pairs re-read the last one): the first read of a decode kernel, issued
+// by its first instructions (the id pointer arrives preloaded in scalar registers) so that its round trip overlaps
+// the loads of the remaining kernel arguments.
+NA_DEVICE long long route_ids_load(const int64_t* ids, int npairs) {
+  return ids[min((int)(threadIdx.x & 63), npairs - 1)];
+}
+
 // Route of a decode batch (same rule as the store-layout kernels): the `item`-th distinct expert in first-appearance
 // order; returns its id (or -1: no such item; 128: an invalid id), `all` = the mask of its pairs (bit p = pair
 // p = 4 token + k), `users` = the first of them per token (first_per_token) and nt = their number (the tokens routed
@@ -272,17 +279,14 @@ NA_DEVICE void store_row_pairs(uint16_t* row_ptr, uint16_t v, bool ok) {
 // result is written to every pair of its token in `all`.  `valid` = distinct experts with a valid id (the invalid
 // marker 128 excluded).  Pair lists stay masks in scalar registers: an indexed register array would be placed in
 // scratch memory.
-// MAXP bounds the pair count (npairs <= MAXP <= 32): the dedupe compares each pair with the MAXP - 1 before it.
+// v = the id of this lane's pair, from route_ids_load.  MAXP bounds the pair count (npairs <= MAXP <= 32): the dedupe
+// compares each pair with the MAXP - 1 before it.
 template <int MAXP>
-NA_DEVICE int route_t950(const int64_t* ids, int npairs, int item, int& nt, uint64_t& users, uint64_t& all,
-                         int& distinct, int& valid) {
+NA_DEVICE int route_t950(long long v, int npairs, int item, int& nt, uint64_t& users, uint64_t& all, int& distinct,
+                         int& valid) {
   static_assert(MAXP >= 1 && MAXP <= 32, "at most 8 tokens x top-4 pairs");
   const int lane = threadIdx.x & 63;
-  int my = 129;
-  if (lane < npairs) {
-    const long long v = ids[lane];
-    my = (v >= 0 && v < 128) ? (int)v : 128;
-  }
+  const int my = lane < npairs ? ((v >= 0 && v < 128) ? (int)v : 128) : 129;
   bool dup = false;
 #pragma unroll
   for (int j = 0; j < MAXP - 1; ++j) {
@@ -376,16 +380,17 @@ struct DecodeLds {
 // 0, which reads nothing from global memory.
 template <int KS, int XT>
 __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
-    const uint16_t* __restrict__ x, const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool,
-    long long slot_bytes, const int64_t* __restrict__ slot_tab, long long expert_base,
+    const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
+    const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ x,
     const uint16_t* __restrict__ bias_gu, uint16_t* __restrict__ h, float alpha, float limit) {
   constexpr int MT = (kTTiles + KS - 1) / KS;
   constexpr int NTH = 64 * KS;
   __shared__ DecodeLds<KS, XT> L;
-  args_at_entry(x, ids, B, pool, slot_bytes, slot_tab, expert_base, bias_gu, h, alpha, limit);
+  const long long rid = route_ids_load(ids, 4 * B);
+  args_at_entry(x, bias_gu, h, alpha, limit);          // past the preloaded arguments: fetched while the ids fly
   int nt, distinct, valid;
   uint64_t users, all;
-  const int e = route_t950<4 * XT>(ids, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
+  const int e = route_t950<4 * XT>(rid, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
   if (e < 0 || e == 128) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.y;
@@ -484,16 +489,17 @@ __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
 // no weights.  The top-k sum is left to k_combine_t950.  Load order as in the gate_up kernel.
 template <int KS, int XT>
 __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
-    const uint16_t* __restrict__ h, const int64_t* __restrict__ ids, const uint16_t* __restrict__ wts, int B,
-    const uint8_t* __restrict__ pool, long long slot_bytes, const int64_t* __restrict__ slot_tab,
-    long long expert_base, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw) {
+    const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
+    const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ h,
+    const uint16_t* __restrict__ wts, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw) {
   constexpr int MT = (kTTiles + KS - 1) / KS;
   constexpr int NTH = 64 * KS;
   __shared__ DecodeLds<KS, XT> L;
-  args_at_entry(h, ids, wts, B, pool, slot_bytes, slot_tab, expert_base, bias_dn, yw);
+  const long long rid = route_ids_load(ids, 4 * B);
+  args_at_entry(h, wts, bias_dn, yw);                  // past the preloaded arguments: fetched while the ids fly
   int nt, distinct, valid;
   uint64_t users, all;
-  const int e = route_t950<4 * XT>(ids, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
+  const int e = route_t950<4 * XT>(rid, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
   if (e < 0) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.y;
@@ -582,21 +588,22 @@ struct DownCombLds {
 
 template <int KSD, int XT>
 __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
-    const uint16_t* __restrict__ h, const int64_t* __restrict__ ids, const uint16_t* __restrict__ wts, int B,
-    const uint8_t* __restrict__ pool, long long slot_bytes, const int64_t* __restrict__ slot_tab,
-    long long expert_base, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ out) {
+    const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
+    const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ h,
+    const uint16_t* __restrict__ wts, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ out) {
   constexpr int MT = (kTTiles + KSD - 1) / KSD;
   constexpr int NTH = 64 * kDcWaves;
   constexpr int GTH = 64 * KSD;
   __shared__ DownCombLds<KSD, XT> L;
-  args_at_entry(h, ids, wts, B, pool, slot_bytes, slot_tab, expert_base, bias_dn, out);
+  const long long rid = route_ids_load(ids, 4 * B);
+  args_at_entry(h, wts, bias_dn, out);                 // past the preloaded arguments: fetched while the ids fly
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = wave / KSD, kw = wave - g * KSD, gtid = tid - g * GTH;
   const int b = blockIdx.x;
   const int npairs = 4 * B;
   int nt, distinct, valid;
   uint64_t users, all;
-  const int e = route_t950<4 * XT>(ids, npairs, g, nt, users, all, distinct, valid);
+  const int e = route_t950<4 * XT>(rid, npairs, g, nt, users, all, distinct, valid);
   const bool live = e >= 0 && e != 128;
   const long long gid = expert_base + (live ? e : 0);
   // groups without a live expert load slot 0's block (valid memory) with every tile slot zeroed, so that the loads
@@ -855,10 +862,10 @@ static void launch_t(void (*kern)(KArgs...), dim3 grid, dim3 block, hipStream_t 
     hipLaunchKernelGGL(kern, grid, block, 0, stream, static_cast<KArgs>(args)...);
 }
 
-typedef void (*GateUpT)(const uint16_t*, const int64_t*, int, const uint8_t*, long long, const int64_t*, long long,
+typedef void (*GateUpT)(const int64_t*, int, const uint8_t*, long long, const int64_t*, long long, const uint16_t*,
                         const uint16_t*, uint16_t*, float, float);
-typedef void (*DownT)(const uint16_t*, const int64_t*, const uint16_t*, int, const uint8_t*, long long, const int64_t*,
-                      long long, const uint16_t*, uint16_t*);
+typedef void (*DownT)(const int64_t*, int, const uint8_t*, long long, const int64_t*, long long, const uint16_t*,
+                      const uint16_t*, const uint16_t*, uint16_t*);
 
 template <int KS>
 static GateUpT gate_up_t950_xt(int xt) {
@@ -933,19 +940,18 @@ int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
   const dim3 g1(items, kTDownBlocks);
   const dim3 blk(64 * k_split);
   const int xt = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
-  launch_t(pick_gate_up_t950(k_split, xt), g1, blk, stream, ev[0], ev[1], (const uint16_t*)x, topk_ids, B,
-           (const uint8_t*)pool, slot_bytes, slot_tab, expert_base, (const uint16_t*)bias_gu, (uint16_t*)h_scratch,
+  launch_t(pick_gate_up_t950(k_split, xt), g1, blk, stream, ev[0], ev[1], topk_ids, B, (const uint8_t*)pool,
+           slot_bytes, slot_tab, expert_base, (const uint16_t*)x, (const uint16_t*)bias_gu, (uint16_t*)h_scratch,
            alpha, limit);
   if (two) {
-    launch_t(k_moe_down_comb_t950<4, 1>, dim3(kTDownBlocks),
-             dim3(64 * kDcWaves), stream, ev[2], ev[3], (const uint16_t*)h_scratch, topk_ids,
-             (const uint16_t*)topk_w, B, (const uint8_t*)pool, slot_bytes, slot_tab, expert_base,
-             (const uint16_t*)bias_dn, (uint16_t*)out);
+    launch_t(k_moe_down_comb_t950<4, 1>, dim3(kTDownBlocks), dim3(64 * kDcWaves), stream, ev[2], ev[3], topk_ids, B,
+             (const uint8_t*)pool, slot_bytes, slot_tab, expert_base, (const uint16_t*)h_scratch,
+             (const uint16_t*)topk_w, (const uint16_t*)bias_dn, (uint16_t*)out);
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
   }
-  launch_t(pick_down_t950(k_split, xt), g1, blk, stream, ev[2], ev[3], (const uint16_t*)h_scratch, topk_ids,
-           (const uint16_t*)topk_w, B, (const uint8_t*)pool, slot_bytes, slot_tab, expert_base,
-           (const uint16_t*)bias_dn, (uint16_t*)yw_scratch);
+  launch_t(pick_down_t950(k_split, xt), g1, blk, stream, ev[2], ev[3], topk_ids, B, (const uint8_t*)pool, slot_bytes,
+           slot_tab, expert_base, (const uint16_t*)h_scratch, (const uint16_t*)topk_w, (const uint16_t*)bias_dn,
+           (uint16_t*)yw_scratch);
   if (out)
     launch_t(k_combine_t950, dim3((B * kH / 2 + 255) / 256), dim3(256), stream, ev[4], ev[5],
              (const uint32_t*)yw_scratch, B, (uint32_t*)out);
