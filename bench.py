@@ -72,7 +72,7 @@ def measured_traffic(kernel, layout, batch, k_split):
 
 def effective_k_split(k_split, batch):
     """The k_split the library runs for a requested one (0 = automatic, as na_moe_decode_t950 picks it)."""
-    return k_split if k_split > 0 else (8 if batch == 1 else 4)
+    return k_split if k_split > 0 else 4
 
 
 def log(msg):
@@ -292,8 +292,7 @@ def bench_model(A):
     log(f"model: building the expert pool ({N_LAYERS * N_EXPERTS} slots, t950)")
     pool = build_t950_pool(dev, 4242)
     L = GPTOSS_LAYOUT_T950
-    rx = ResidentExperts(pool, L, None, None, max_batch=1, k_split=A.k_split, combine_in_down=A.down != "expert",
-                         single_launch=A.down == "layer")
+    rx = ResidentExperts(pool, L, None, None, max_batch=1, k_split=A.k_split, combine_in_down=A.down != "expert")
     log("model: random-init dense weights")
     w = random_weights(device=dev, seed=77)
     smax = ctx + max(n_new, A.warmup) + 2
@@ -366,9 +365,9 @@ def bench_model(A):
     n_l = R * N_LAYERS
     avg = {nm: acc[nm] / n_l for nm in names}
     dom = names[0]
-    gu_bytes = TOPK * (GATE_UP_BYTES + DOWN_BYTES if dom == "layer" else GATE_UP_BYTES)
+    gu_bytes = TOPK * GATE_UP_BYTES
     gu_gbps = gu_bytes / (avg[dom] * 1e-6) / 1e9
-    kname = "k_moe_layer_t950" if dom == "layer" else "k_moe_gate_up_t950"
+    kname = "k_moe_gate_up_t950"
     log("model: per launch " + ", ".join(f"{nm} {v:.2f} us" for nm, v in avg.items())
         + f", attention full {att_full / (n_l / 2):.2f} us, sliding {att_slide / (n_l / 2):.2f} us")
     traffic, why = measured_traffic(kname, "t950", 1, effective_k_split(A.k_split, 1))
@@ -484,10 +483,10 @@ def main():
     ap.add_argument("--layout", choices=("t950", "raw", "ps4"), default="t950",
                     help="resident slot layout: gfx950 tiles (MFMA kernels) or the store layouts (VALU kernels)")
     ap.add_argument("--k-split", type=int, default=0,
-                    help="t950 gate_up: waves per workgroup splitting K (1, 2, 4, 8; 0 = automatic: 8 at batch 1, else 4)")
-    ap.add_argument("--down", choices=("combine", "layer", "expert"), default="combine",
-                    help="t950, batch 1: gate_up then down + combine (two launches, default), both in one launch with "
-                         "a grid barrier (layer), or expert-major down + a combine kernel (expert)")
+                    help="t950 gate_up: waves per workgroup splitting K (4, 8; 0 = automatic: 4)")
+    ap.add_argument("--down", choices=("combine", "expert"), default="combine",
+                    help="t950, batch 1: gate_up then down + combine (two launches, default), or expert-major down "
+                         "+ a combine kernel (expert)")
     ap.add_argument("--sets", type=int, default=16, help="routing sets (graphs) cycled over the steps")
     ap.add_argument("--roofline-steps", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
@@ -574,7 +573,7 @@ def main():
     bias_gu = torch.zeros(n_slots, L.gate_up_n, dtype=torch.bfloat16, device=dev)
     bias_dn = torch.zeros(n_slots, L.down_n, dtype=torch.bfloat16, device=dev)
     rx = ResidentExperts(pool, L, bias_gu, bias_dn, gu_pairs_per_wave=A.gu_pairs, dn_pairs_per_wave=A.dn_pairs,
-                         k_split=A.k_split, combine_in_down=A.down != "expert", single_launch=A.down == "layer")
+                         k_split=A.k_split, combine_in_down=A.down != "expert")
     launches = rx.launches(A.batch)
     per_layer = len(launches)
 
@@ -626,8 +625,7 @@ def main():
         f"{step_bytes / (ms_step * 1e-3) / 1e9:.0f} GB/s whole-step")
 
     # ------------------------------------------------------------------ roofline pass (per-kernel events)
-    per_kernel_bytes = {"gate_up": GATE_UP_BYTES, "down": DOWN_BYTES, "down_combine": DOWN_BYTES, "combine": 0,
-                        "layer": GATE_UP_BYTES + DOWN_BYTES}
+    per_kernel_bytes = {"gate_up": GATE_UP_BYTES, "down": DOWN_BYTES, "down_combine": DOWN_BYTES, "combine": 0}
     kernels = tuple((nm, per_kernel_bytes[nm]) for nm in launches)
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * len(kernels))] for _ in range(N_LAYERS)]
     for row in ev:
@@ -653,7 +651,7 @@ def main():
     dom = kernels[0][0]
     top = kern[dom]
     per_launch = tot[dom][1] / tot[dom][2]
-    kname = ("k_moe_layer_t950" if dom == "layer" else "k_moe_gate_up_t950") if A.layout == "t950" \
+    kname = "k_moe_gate_up_t950" if A.layout == "t950" \
         else "k_moe_gate_up"
     traffic, why = measured_traffic(kname, A.layout, B, effective_k_split(A.k_split, B))
     log(f"traffic: {traffic} ({why})")

@@ -79,6 +79,13 @@ int na_selftest_bf16(const float* in, void* out_hw, void* out_pk, void* out_int,
 /* Device self-check of the MFMA operand layout the tile kernels use: d [16, 16] fp32 = a [16, 32] x b [32, 16] bf16. */
 int na_selftest_mfma(const void* a, const void* b, float* d, hipStream_t stream);
 
+/* Device self-checks of the t950 decode kernels' arithmetic (no reference counterpart): the activation quantiser
+ * (rows x 2880 bf16 -> hi, lo E4M3 codes [rows][2880] and E8M0 bytes sc [rows][2][90]) and one block-scaled MFMA
+ * in the kernels' operand order (a: E4M3 [16][128], sa: E8M0 [16][4], tile: one full t950 k-tile of 1024 bytes,
+ * sb: E8M0 [16][4] per output row and group; d: fp32 [16][16]). */
+int na_selftest_x8(const void* in, int rows, void* hi, void* lo, void* sc, hipStream_t stream);
+int na_selftest_mfma8(const void* a, const void* sa, const void* tile, const void* sb, float* d, hipStream_t stream);
+
 /* ---- gfx950 tile layout ("t950", weight_repr "mxfp4_g32_t950").  No counterpart in the reference's store; it is
  * this build's resident layout, a lossless permutation of the reference's slot (neural/moe/layout.py:143-186,
  * tools/scale_pack.py:6-12): 540 blocks of 16 rows, each 22.5 KiB of codes in v_mfma_f32_16x16x32_bf16 B-operand
@@ -96,9 +103,11 @@ int na_repack_to_t950(const void* src, long long src_stride, int src_ps4, void* 
 int na_repack_from_t950(const void* src, long long src_stride, void* dst, long long dst_stride, int dst_ps4,
                         int n_slots, hipStream_t stream);
 
-/* na_moe_decode over a t950 pool (slot_bytes >= 13,271,040, 16-byte aligned): the same contract and results as
- * na_moe_decode (server.py:508-518), computed with v_mfma_f32_16x16x32_bf16 on in-register dequantised codes.
- * k_split = waves per workgroup splitting K in the expert-major kernels (1, 2, 4 or 8; <= 0: 8 for B = 1, else 4).
+/* na_moe_decode over a t950 pool (slot_bytes >= 13,271,040, 16-byte aligned): the same contract as na_moe_decode
+ * (server.py:508-518), computed with the block-scaled v_mfma_scale_f32_16x16x128_f8f6f4: the E2M1 codes and E8M0
+ * scales as stored, the activations as two E4M3 rows (hi + lo) with one E8M0 scale per 32-element block, which hold
+ * every bf16 element exactly down to 2^-13 of its block's largest magnitude (fp32 accumulation as the reference's).
+ * k_split = waves per workgroup splitting K in the expert-major kernels (4 or 8; <= 0: 4).
  * down_mode 0: for B = 1 with an output, two launches: gate_up, then one down workgroup per 16 output rows that
  *   holds every distinct expert of the token and sums the top-k outputs itself (events = 4: gate_up, down);
  *   otherwise as down_mode 1.
@@ -107,19 +116,6 @@ int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
                        long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
                        const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha, float limit,
                        int k_split, int down_mode, void* const* events, hipStream_t stream);
-
-/* na_moe_decode_t950 for one token (B = 1, with an output) in ONE launch: gate_up + bias + clamped SwiGLU, a
- * grid-wide barrier, then down + bias + routing weight and the top-4 sum; results identical to down_mode 0.  Same
- * reference interface (server.py:508-518).  180 workgroups of 1024 threads that must all be resident at once: the
- * occupancy is checked once per device (kErrTooLarge if they do not fit).
- *   h_scratch  16-byte aligned, >= 4 x 2880 bf16 (the 4 pairs' activations)
- *   sync       uint32 [3], zero before the first call; a completed call leaves [0] and [1] zero.  [2] is set if a
- *              barrier wait gave up (outputs undefined); the caller clears it.  Calls sharing sync must not overlap.
- *   events     NULL or 2 hipEvent_t (start/stop of the launch) */
-int na_moe_layer_t950(const void* x, const int64_t* topk_ids, const void* topk_w, const void* pool,
-                      long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
-                      const void* bias_dn, void* h_scratch, unsigned int* sync, void* out, float alpha, float limit,
-                      void* const* events, hipStream_t stream);
 
 /* ---- decode attention (GQA 64 query / 8 KV heads, head_dim 64, learned sinks, sliding window, rolling cache) */
 

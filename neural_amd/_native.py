@@ -26,11 +26,12 @@ SIGNATURES = {
     "na_router_topk": [VP, I32, VP, VP, I32, VP, VP, VP, VP, VP],
     "na_selftest_mfma": [VP, VP, VP, VP],
     "na_selftest_bf16": [VP, VP, VP, VP, I64, VP],
+    "na_selftest_x8": [VP, I32, VP, VP, VP, VP],
+    "na_selftest_mfma8": [VP, VP, VP, VP, VP, VP],
     "na_t950_slot_bytes": [],
     "na_repack_to_t950": [VP, I64, I32, VP, I64, I32, VP],
     "na_repack_from_t950": [VP, I64, VP, I64, I32, I32, VP],
     "na_moe_decode_t950": [VP, VP, VP, I32, VP, I64, VP, I64, VP, VP, VP, VP, VP, F32, F32, I32, I32, VP, VP],
-    "na_moe_layer_t950": [VP, VP, VP, VP, I64, VP, I64, VP, VP, VP, VP, VP, F32, F32, VP, VP],
     "na_attn_workspace_floats": [I32, I32],
     "na_moe_prefill_workspace_bytes": [I32],
     "na_moe_prefill": [VP, VP, VP, I32, VP, I64, I32, VP, I64, VP, VP, VP, I64, VP, F32, F32, VP, VP],

@@ -1,5 +1,6 @@
-// Library identity and device self-checks of the gfx950 conversion builtins the kernels rely on.
+// Library identity and device self-checks of the gfx950 conversion builtins and MFMA operand orders the kernels use.
 #include "common.h"
+#include "t950.h"
 
 namespace na {
 
@@ -48,6 +49,47 @@ __global__ void k_selftest_bf16(const float* __restrict__ in, uint16_t* __restri
   }
 }
 
+// One row of 2880 bf16 per workgroup (384 threads: chunk c = thread, threads past 360 quantise zeros) through the
+// decode kernels' activation quantiser: hi[r][i], lo[r][i] = the E4M3 codes of element i, sc[r][0][b], sc[r][1][b] =
+// the E8M0 bytes of block b for hi and lo.
+__global__ __launch_bounds__(384) void k_selftest_x8(const uint16_t* __restrict__ in, uint8_t* __restrict__ hi,
+                                                     uint8_t* __restrict__ lo, uint8_t* __restrict__ sc) {
+  const int r = blockIdx.x, c = threadIdx.x;
+  const uint4 v =
+      c < kChunks ? *reinterpret_cast<const uint4*>(in + (long long)r * kH + 8 * c) : make_uint4(0, 0, 0, 0);
+  uint2 h, l;
+  uint32_t sh, sl;
+  x8_quant_chunk(v, h, l, sh, sl);
+  if (c < kChunks) {
+    *reinterpret_cast<uint2*>(hi + (long long)r * kH + 8 * c) = h;
+    *reinterpret_cast<uint2*>(lo + (long long)r * kH + 8 * c) = l;
+    if ((c & 3) == 0) {
+      sc[(long long)r * 2 * kGK + (c >> 2)] = (uint8_t)sh;
+      sc[(long long)r * 2 * kGK + kGK + (c >> 2)] = (uint8_t)sl;
+    }
+  }
+}
+
+// One v_mfma_scale_f32_16x16x128_f8f6f4 in the decode kernels' operand order: A = E4M3 codes a[m][k] (16 x 128 bytes)
+// with E8M0 bytes sa[m][kb] (16 x 4); B = one full t950 k-tile (1024 bytes: lane 16 q + n holds bytes 4q .. 4q + 3 of
+// groups 0..3 of row n), rearranged by tile_to_mfma_b, with E8M0 bytes sb[n][kb] (16 x 4).  d[m * 16 + n] = D[m][n].
+__global__ void k_selftest_mfma8(const uint8_t* __restrict__ a, const uint8_t* __restrict__ sa,
+                                 const uint8_t* __restrict__ tile, const uint8_t* __restrict__ sb,
+                                 float* __restrict__ d) {
+  const int l = threadIdx.x, kb = l >> 4, m = l & 15;
+  const uint4 a0 = *reinterpret_cast<const uint4*>(a + m * 128 + 16 * kb);
+  const uint4 a1 = *reinterpret_cast<const uint4*>(a + m * 128 + 64 + 16 * kb);
+  const uint4 c = *reinterpret_cast<const uint4*>(tile + 16 * l);
+  uint32_t w0 = c.x, w1 = c.y, w2 = c.z, w3 = c.w;
+  tile_to_mfma_b(w0, w1, w2, w3);
+  const mfma_i32x8_t A = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+  const mfma_i32x8_t Bv = {(int)w0, (int)w1, (int)w2, (int)w3, 0, 0, 0, 0};
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, Bv, acc, 0, 4, 0, (int)sa[m * 4 + kb], 0,
+                                                        (int)sb[m * 4 + kb]);
+  for (int r = 0; r < 4; ++r) d[(4 * kb + r) * 16 + m] = acc[r];
+}
+
 }  // namespace na
 
 extern "C" {
@@ -76,6 +118,22 @@ int na_selftest_bf16(const float* in, void* out_hw, void* out_pk, void* out_int,
   if (blocks > 0x7fffffffll) return na::kErrTooLarge;
   hipLaunchKernelGGL(na::k_selftest_bf16, dim3((unsigned)blocks), dim3(256), 0, stream, in, (uint16_t*)out_hw,
                      (uint16_t*)out_pk, (uint16_t*)out_int, n);
+  return hipGetLastError() == hipSuccess ? na::kOk : na::kErrLaunch;
+}
+
+// Activation quantiser self-check: rows x 2880 bf16 -> hi, lo (rows x 2880 E4M3 codes), sc (rows x 2 x 90 E8M0).
+int na_selftest_x8(const void* in, int rows, void* hi, void* lo, void* sc, hipStream_t stream) {
+  if (!in || !hi || !lo || !sc || rows <= 0) return na::kErrArgs;
+  hipLaunchKernelGGL(na::k_selftest_x8, dim3(rows), dim3(384), 0, stream, (const uint16_t*)in, (uint8_t*)hi,
+                     (uint8_t*)lo, (uint8_t*)sc);
+  return hipGetLastError() == hipSuccess ? na::kOk : na::kErrLaunch;
+}
+
+// D = A x B through the decode kernels' block-scaled MFMA and t950 operand rearrangement (see k_selftest_mfma8).
+int na_selftest_mfma8(const void* a, const void* sa, const void* tile, const void* sb, float* d, hipStream_t stream) {
+  if (!a || !sa || !tile || !sb || !d) return na::kErrArgs;
+  hipLaunchKernelGGL(na::k_selftest_mfma8, dim3(1), dim3(64), 0, stream, (const uint8_t*)a, (const uint8_t*)sa,
+                     (const uint8_t*)tile, (const uint8_t*)sb, d);
   return hipGetLastError() == hipSuccess ? na::kOk : na::kErrLaunch;
 }
 

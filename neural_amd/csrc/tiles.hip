@@ -17,6 +17,8 @@
 
 #include <hip/hip_ext.h>
 
+#include <cmath>
+
 namespace na {
 
 // ------------------------------------------------------------------------------------------------- repack
@@ -130,17 +132,16 @@ __global__ __launch_bounds__(256) void k_repack_from_t950(const uint8_t* __restr
 }
 
 // ------------------------------------------------------------------------------------ MFMA decode kernels
-// Work item = (distinct expert of the batch, 16-row output block); the KS waves of a workgroup split the 23 k-tiles,
-// each accumulates D[token m][row n] with v_mfma_f32_16x16x32_bf16 (A = x of the expert's tokens, m < nt, else 0;
-// B = codes dequantised in registers by v_cvt_scalef32_pk_bf16_fp4 with the group's E8M0 scale), and the partial D
-// tiles are summed in a fixed order through LDS.  No cross-lane reduction and no per-group scaling pass: the MFMA
-// accumulates over all of K.  Exact dequant: E2M1 x 2^(s-127) is a bf16 for the configured exponent range.
-// Code tiles are read with non-temporal 128-bit loads (each weight byte is used once per step); a row block's 1,536
-// scale bytes are read by the workgroup with coalesced 16-byte loads and staged in LDS, so that each wave reads its
-// scales from LDS instead of issuing one scattered 64-lane load per tile.
-constexpr int kMaxTokT = 16;                 // tokens per expert the MFMA M dimension holds
-constexpr int kXPitch = kH * 2 + 16;         // LDS bytes per staged token row (padded against bank conflicts)
-constexpr int kScPitch = 112;                // LDS bytes per staged scale row: 28 dwords, so 16 rows hit 16 banks
+// Work item = (distinct expert of the batch, 16-row output block); the KS waves of a workgroup split the 23 k-tiles.
+// Each k-tile (16 rows x 128 K) is one v_mfma_scale_f32_16x16x128_f8f6f4: B = the block's E2M1 codes with their E8M0
+// scales, consumed as stored (no dequantisation instruction); A = the activations of the expert's tokens as E4M3 with
+// one E8M0 scale per 32-element block, two A rows per token (hi and lo, see x8_quant_chunk), so that one MFMA serves up
+// to 8 tokens.  The KS partial tiles are summed in a fixed order through LDS.  Code tiles are read with non-temporal
+// 128-bit loads (each weight byte is used once per step) and put into the MFMA's operand order by four lane-swap
+// instructions; a row block's 1,536 scale bytes are read by the workgroup with coalesced 16-byte loads and staged in
+// LDS, so that each wave reads its scales from LDS instead of issuing one scattered 64-lane load per tile.
+constexpr int kMaxTokT = 8;                  // tokens per expert the MFMA M dimension holds (two A rows each)
+constexpr int kScPitch = 112;                // LDS bytes per staged weight scale row: 28 dwords, 16 rows hit 16 banks
 constexpr int kScLds = kTRows * kScPitch;    // 1,792 LDS bytes per staged row block
 constexpr int kScPieces = kTRows * kTScalePitch / 16;   // 96 16-byte pieces of scales per row block
 
@@ -203,58 +204,154 @@ NA_DEVICE void scale_store(int tid, uint8_t* lds, const ScaleRegs<NB, NTH>& r) {
   }
 }
 
-// xs_lds points at this lane's A row (token m = lane % 16; rows m >= nt only feed D rows that are never read),
-// sc_row at this lane's staged scale row (row n = lane % 16 of the block).
-template <int MT>
-NA_DEVICE void block_compute(const CodeRegs<MT>& r, const uint8_t* sc_row, const uint8_t* xs_lds, int lane, int t0,
-                             int t1, f32x4_t& acc) {
-  const int q = lane >> 4;
-#pragma unroll
-  for (int i = 0; i < MT; ++i) {
-    const int t = slot_tile(t0, t1, i);
-    const bool live = t0 + i < t1, full = live && t < kTFull;
-    const uint32_t w[4] = {live ? r.c[i].x : 0u, live ? r.c[i].y : 0u, full ? r.c[i].z : 0u, full ? r.c[i].w : 0u};
-    const uint32_t sc = *reinterpret_cast<const uint32_t*>(sc_row + 4 * t);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int g = min(4 * t + j, kGK - 1);             // zeroed groups 90, 91 read a finite A row
-      const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(xs_lds + (32 * g + 8 * q) * 2);
-      const bf16x8_t b = dequant8(w[j], e8m0_f32((sc >> (8 * j)) & 0xff));
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
-    }
-  }
-}
+template <int NR>
+struct X8Lds {
+  __align__(16) uint8_t row[NR][kX8Pitch];   // row 2u = hi, 2u + 1 = lo of the u-th staged token
+  __align__(16) uint8_t zero[128];           // the A operand of MFMA rows past the staged ones
+  __align__(16) uint8_t sc[NR][kX8ScPitch];
+};
 
 // Activation rows (x, or h) of up to XT tokens, staged through registers: piece p = tid + NTH * k (k < XP) of
-// 360 * XT 16-byte pieces.
+// 360 * XT 16-byte pieces (one chunk of 8 elements each).
 template <int XT, int NTH>
 struct XRegs {
-  static constexpr int XP = (XT * (kH / 8) + NTH - 1) / NTH;
+  static constexpr int XP = (XT * kChunks + NTH - 1) / NTH;
   uint4 v[XP];
 };
 
-// Thread tid stages pieces p = tid + NTH k < nt x 360 (a per-lane predicate, no branch), i.e. rows t < nt
-// (1 <= nt <= XT) of the staged block, row t = source row row_of(t).  Staged rows t >= nt are not written: they only
-// feed D rows m >= nt, which are never read (each MFMA output row depends on its own A row only).
+// Thread tid loads pieces p = tid + NTH k < nt x 360 (a per-lane predicate, no branch), i.e. rows t < nt
+// (1 <= nt <= XT) of the staged block, row t = source row row_of(t); the other pieces are zero.
 template <int XT, int NTH, typename RowOf>
 NA_DEVICE void x_load(int tid, const uint16_t* base, long long row_stride, RowOf row_of, int nt, XRegs<XT, NTH>& xr) {
 #pragma unroll
   for (int k = 0; k < XRegs<XT, NTH>::XP; ++k) {
     const int p = tid + NTH * k;
-    const int t = p / (kH / 8), pp = p - t * (kH / 8);
-    if (p < nt * (kH / 8))
+    const int t = p / kChunks, pp = p - t * kChunks;
+    xr.v[k] = make_uint4(0, 0, 0, 0);
+    if (p < nt * kChunks)
       xr.v[k] = load16(reinterpret_cast<const uint8_t*>(base + (long long)row_of(t) * row_stride) + 16 * pp);
   }
 }
 
-template <int XT, int NTH>
-NA_DEVICE void x_store(int tid, uint8_t* lds, int nt, const XRegs<XT, NTH>& xr) {
+// ---- h between the gate_up and down kernels, as E4M3 with two fixed scales.  The clamped SwiGLU bounds |h| by
+// (limit + 1) x max(limit, 1 / alpha) (gate <= limit, |up + 1| <= limit + 1, and |gate sigma(alpha gate)| < 0.28 /
+// alpha for gate < 0), so s_hi = 2^(e - 7) of that bound (x8_scale_byte) keeps every |h| / s_hi below 256, and the
+// remainder h - hi s_hi (at most 8 s_hi) over s_lo = s_hi / 32 stays at most 256.  hi s_hi + lo s_lo equals h exactly
+// when h's lowest bit lies on lo's grid (s_hi 2^-14; for limit 7, alpha 1.702: every |h| >= 2^-9) and to within half
+// of it below.  Per pair: one row of 2880 hi codes, then one of 2880 lo codes (the bytes of a 2880 x bf16 row).
+constexpr int kH8Row = 2 * kI;               // bytes per pair
+constexpr int kH8Pieces = kH8Row / 16;       // 360 16-byte pieces per pair (= kChunks)
+
+// Both E4M3 codes of one h value (a bf16) under the fixed scale bytes sh, sl.
+NA_DEVICE void h8_codes(uint16_t hv, uint32_t sh, uint32_t sl, uint8_t& hi, uint8_t& lo) {
+  const float f = bf16_to_f32(hv), s_hi = e8m0_f32(sh), s_lo = e8m0_f32(sl);
+  fp8x2_t o = {0, 0};
+  o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o, f, 0.f, s_hi, false);
+  const uint32_t c = __builtin_bit_cast(uint32_t, o) & 0xff;
+  const float r = f - __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(c, s_hi, false)[0];
+  fp8x2_t o2 = {0, 0};
+  o2 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o2, r, 0.f, s_lo, false);
+  hi = (uint8_t)c;
+  lo = (uint8_t)(__builtin_bit_cast(uint32_t, o2) & 0xff);
+}
+
+// h of D column n = lane % 16 (output row 16b + n) of `pair` -> its hi and lo bytes (a byte store each).
+NA_DEVICE void store_h8(uint8_t* h8, int pair, int b, uint16_t hv, uint32_t sh, uint32_t sl, bool ok) {
+  uint8_t hi, lo;
+  h8_codes(hv, sh, sl, hi, lo);
+  uint8_t* row = h8 + (long long)pair * kH8Row + 16 * b + (threadIdx.x & 15);
+  if (ok) {
+    row[0] = hi;
+    row[kI] = lo;
+  }
+}
+
+// The pairs' h8 rows of up to XT staged tokens through registers: piece p = tid + NTH k < nt x 360; piece q = p % 360
+// of token t = p / 360 is bytes 16 (q % 180) .. of its hi (q < 180) or lo row.
+template <int XT, int NTH, typename PairOf>
+NA_DEVICE void h8_load(int tid, const uint8_t* h8, PairOf pair_of, int nt, XRegs<XT, NTH>& xr) {
 #pragma unroll
   for (int k = 0; k < XRegs<XT, NTH>::XP; ++k) {
     const int p = tid + NTH * k;
-    const int t = p / (kH / 8), pp = p - t * (kH / 8);
-    if (p < nt * (kH / 8)) *reinterpret_cast<uint4*>(lds + t * kXPitch + 16 * pp) = xr.v[k];
+    const int t = p / kH8Pieces, q = p - t * kH8Pieces;
+    if (p < nt * kH8Pieces) xr.v[k] = load16(h8 + (long long)pair_of(t) * kH8Row + 16 * q);
   }
+}
+
+// ... into the staged rows 2t (hi) / 2t + 1 (lo), every scale byte of a row set to its fixed value, and the zero strip.
+template <int XT, int NTH>
+NA_DEVICE void h8_store(int tid, X8Lds<2 * XT>& L, int nt, const XRegs<XT, NTH>& xr, uint32_t sh, uint32_t sl) {
+#pragma unroll
+  for (int k = 0; k < XRegs<XT, NTH>::XP; ++k) {
+    const int p = tid + NTH * k;
+    const int t = p / kH8Pieces, q = p - t * kH8Pieces, half = q >= kH8Pieces / 2 ? 1 : 0;
+    if (p < nt * kH8Pieces)
+      *reinterpret_cast<uint4*>(L.row[2 * t + half] + 16 * (q - half * (kH8Pieces / 2))) = xr.v[k];
+  }
+  for (int i = tid; i < 2 * nt * (kX8ScPitch / 4); i += NTH) {
+    const int r = i / (kX8ScPitch / 4), c = i - r * (kX8ScPitch / 4);
+    reinterpret_cast<uint32_t*>(L.sc[r])[c] = ((r & 1) ? sl : sh) * 0x01010101u;
+  }
+  if (tid < 8) reinterpret_cast<uint4*>(L.zero)[tid] = make_uint4(0, 0, 0, 0);
+}
+
+// Quantise the loaded pieces into the E4M3 rows 2t (hi) / 2t + 1 (lo) of staged token t < nt and their scales, and
+// clear the zero strip.  NTH is a multiple of 64 and 360 of 4, so the 4 chunks of a block are 4 lanes of one wave that
+// are all inside or all outside p < nt x 360; rounds with no piece below nt x 360 are skipped (a uniform branch).
+template <int XT, int NTH>
+NA_DEVICE void x8_store(int tid, X8Lds<2 * XT>& L, int nt, const XRegs<XT, NTH>& xr) {
+  static_assert(NTH % 64 == 0, "whole waves");
+#pragma unroll
+  for (int k = 0; k < XRegs<XT, NTH>::XP; ++k) {
+    if (NTH * k >= nt * kChunks) break;
+    const int p = tid + NTH * k;
+    const int t = p / kChunks, c = p - t * kChunks;
+    uint2 hi, lo;
+    uint32_t sh, sl;
+    x8_quant_chunk(xr.v[k], hi, lo, sh, sl);
+    if (p < nt * kChunks) {
+      *reinterpret_cast<uint2*>(L.row[2 * t] + 8 * c) = hi;
+      *reinterpret_cast<uint2*>(L.row[2 * t + 1] + 8 * c) = lo;
+      if ((c & 3) == 0) {
+        L.sc[2 * t][c >> 2] = (uint8_t)sh;
+        L.sc[2 * t + 1][c >> 2] = (uint8_t)sl;
+      }
+    }
+  }
+  if (tid < 8) reinterpret_cast<uint4*>(L.zero)[tid] = make_uint4(0, 0, 0, 0);
+}
+
+// One row block over this wave's k-tiles: D[m][n] += sum_k A[m][k] B[k][n], B = the codes (row n = lane % 16), A row
+// m = lane % 16: `arow` is this lane's staged E4M3 row with scales `asc`, or null past the staged rows (zero strip).
+// A's operand order: lane 16 kb + m holds K = 16 kb .. 16 kb + 15 and 64 + 16 kb .. 64 + 16 kb + 15 of the tile.
+// wsc = the staged scale row of output row n.  The half tile (t = 22) holds groups 88 and 89 in its first 64 K.
+template <int MT>
+NA_DEVICE void block_compute(const CodeRegs<MT>& r, const uint8_t* wsc, const uint8_t* arow, const uint8_t* asc,
+                             const uint8_t* zero, int lane, int t0, int t1, f32x4_t& acc) {
+  const int kb = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int t = slot_tile(t0, t1, i);
+    const bool live = t0 + i < t1, full = live && t < kTFull;
+    uint32_t w0 = live ? r.c[i].x : 0u, w1 = live ? r.c[i].y : 0u, w2 = full ? r.c[i].z : 0u, w3 = full ? r.c[i].w : 0u;
+    tile_to_mfma_b(w0, w1, w2, w3);
+    const int g = 4 * t + kb;                              // B: this lane's group; A: this lane's first K block
+    const int sb = wsc[g];                                 // groups 90, 91: the row's zero padding (codes are 0)
+    const int sa = arow ? asc[min(g, kGK - 1)] : 127;
+    const uint8_t* ap = arow ? arow + 128 * t : zero;
+    const uint4 a0 = *reinterpret_cast<const uint4*>(ap + 16 * kb);
+    const uint4 a1 = t < kTFull ? *reinterpret_cast<const uint4*>(ap + 64 + 16 * kb) : make_uint4(0, 0, 0, 0);
+    const mfma_i32x8_t A = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+    const mfma_i32x8_t Bv = {(int)w0, (int)w1, (int)w2, (int)w3, 0, 0, 0, 0};
+    acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, Bv, acc, 0, 4, 0, sa, 0, sb);
+  }
+}
+
+// D rows 2u, 2u + 1 = hi and lo of token u: lane 16 i + n holds D[4i .. 4i + 3][n], i.e. tokens 2i (elements 0, 1)
+// and 2i + 1 (elements 2, 3).  The two sums of this lane.
+NA_DEVICE void token_sums(const f32x4_t& acc, float& y0, float& y1) {
+  y0 = acc[0] + acc[1];
+  y1 = acc[2] + acc[3];
 }
 
 // Store the bf16 values v held as D columns n = lane % 16 (16 lanes per D row) as 32-bit pairs: even lanes write
@@ -275,7 +372,7 @@ NA_DEVICE long long route_ids_load(const int64_t* ids, int npairs) {
 // Route of a decode batch (same rule as the store-layout kernels): the `item`-th distinct expert in first-appearance
 // order; returns its id (or -1: no such item; 128: an invalid id), `all` = the mask of its pairs (bit p = pair
 // p = 4 token + k), `users` = the first of them per token (first_per_token) and nt = their number (the tokens routed
-// to the expert, <= B); pair_at(users, m) is the m-th user in ascending order.  The MFMA rows are the users; each
+// to the expert, <= B); pair_at(users, u) is the u-th user in ascending order.  The staged tokens are the users; each
 // result is written to every pair of its token in `all`.  `valid` = distinct experts with a valid id (the invalid
 // marker 128 excluded).  Pair lists stay masks in scalar registers: an indexed register array would be placed in
 // scratch memory.
@@ -312,82 +409,93 @@ NA_DEVICE int route_t950(long long v, int npairs, int item, int& nt, uint64_t& u
 // The pairs of user pair p's token that `all` routes to the same expert, as a 4-bit mask over the ranks k.
 NA_DEVICE uint32_t token_dups(uint64_t all, int p) { return (uint32_t)(all >> (p & ~3)) & 0xFu; }
 
-// The m-th pair (ascending) of a route's mask, 0 <= m < kMaxTokT; the mask is uniform, the walk is scalar.
-NA_DEVICE int pair_at(uint64_t users, int m) {
+// The u-th pair (ascending) of a route's mask, 0 <= u < kMaxTokT; the mask is uniform, the walk is scalar.
+NA_DEVICE int pair_at(uint64_t users, int u) {
   int p = __ffsll((long long)users) - 1;
-  uint64_t u = users;
+  uint64_t m = users;
 #pragma unroll
   for (int t = 1; t < kMaxTokT; ++t) {
-    u &= u - 1;
-    const int pt = __ffsll((long long)u) - 1;
-    p = (t == m) ? pt : p;
+    m &= m - 1;
+    const int pt = __ffsll((long long)m) - 1;
+    p = (t == u) ? pt : p;
   }
   return p;
 }
 
-// The duplicate pairs' rows: for D row m < nt (user pair p), the same values v[r] also go to every other pair of
-// p's token that `all` routes to the expert (row stride `stride` elements, columns 16b .. 16b + 15).  All lanes call
-// it.  Kept out of line of the common path, which stores only the users' rows.
-__device__ __noinline__ void dup_rows_store(uint16_t* base, int stride, uint64_t users, uint64_t all, int nt, int b,
-                                            uint16_t v0, uint16_t v1, uint16_t v2, uint16_t v3) {
+// The duplicate pairs' h: for token u = 2 (lane / 16) + e < nt (user pair p), the same value v[e] also goes to every
+// other pair of p's token that `all` routes to the expert (columns 16b .. 16b + 15).  Kept out of line of the common
+// path, which stores only the users' rows.
+__device__ __noinline__ void dup_rows_store_h8(uint8_t* h8, uint64_t users, uint64_t all, int nt, int b, uint16_t v0,
+                                               uint16_t v1, uint32_t sh, uint32_t sl) {
   const int lane = threadIdx.x & 63;
-  const uint16_t v[4] = {v0, v1, v2, v3};
+  const uint16_t v[2] = {v0, v1};
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = 4 * (lane >> 4) + r;
-    const int p = pair_at(users, min(m, nt - 1));
+  for (int e = 0; e < 2; ++e) {
+    const int u = 2 * (lane >> 4) + e;
+    const int p = pair_at(users, min(u, nt - 1));
     const uint32_t dm = token_dups(all, p) & ~(1u << (p & 3));
-    for (int k = 0; k < 4; ++k)
-      store_row_pairs(base + (long long)((p & ~3) + k) * stride + 16 * b, v[r], m < nt && ((dm >> k) & 1));
+    for (int k = 0; k < 4; ++k) store_h8(h8, (p & ~3) + k, b, v[e], sh, sl, u < nt && ((dm >> k) & 1));
   }
 }
 
-// As dup_rows_store for the down outputs: pair q gets bf16(y[r] x w[q]) with its own routing weight.
+// As dup_rows_store for the down outputs: pair q gets bf16(y[e] x w[q]) with its own routing weight.
 __device__ __noinline__ void dup_rows_store_w(uint16_t* yw, uint64_t users, uint64_t all, int nt, int b, float y0,
-                                              float y1, float y2, float y3, const uint16_t* wts) {
+                                              float y1, const uint16_t* wts) {
   const int lane = threadIdx.x & 63;
-  const float y[4] = {y0, y1, y2, y3};
+  const float y[2] = {y0, y1};
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = 4 * (lane >> 4) + r;
-    const int p = pair_at(users, min(m, nt - 1));
+  for (int e = 0; e < 2; ++e) {
+    const int u = 2 * (lane >> 4) + e;
+    const int p = pair_at(users, min(u, nt - 1));
     const uint32_t dm = token_dups(all, p) & ~(1u << (p & 3));
     for (int k = 0; k < 4; ++k) {
       const int q = (p & ~3) + k;
-      store_row_pairs(yw + (long long)q * kH + 16 * b, f32_to_bf16(y[r] * bf16_to_f32(wts[q])),
-                      m < nt && ((dm >> k) & 1));
+      store_row_pairs(yw + (long long)q * kH + 16 * b, f32_to_bf16(y[e] * bf16_to_f32(wts[q])),
+                      u < nt && ((dm >> k) & 1));
     }
   }
 }
 
-// LDS of one expert-major decode workgroup: staged x (or h) rows, scale rows, the KS partial D tiles [KS][2][64].
-// With 4 or more staged rows the partial tiles reuse the rows' space (after a barrier that ends every wave's reads
-// of them), which keeps three workgroups per CU at 8 rows instead of two.
+// This lane's A row: staged row m = lane % 16 while m < 2 nt, else none (the zero strip).
+template <int NR>
+NA_DEVICE const uint8_t* a_row(const X8Lds<NR>& L, int lane, int nt) {
+  const int m = lane & 15;
+  return m < 2 * nt ? L.row[min(m, NR - 1)] : nullptr;
+}
+template <int NR>
+NA_DEVICE const uint8_t* a_scales(const X8Lds<NR>& L, int lane) {
+  return L.sc[min(lane & 15, NR - 1)];
+}
+
+// LDS of one expert-major decode workgroup: the staged E4M3 rows, the weight scale rows, and the KS partial sums
+// [KS][2 matrices][64 lanes][2 tokens].  With 4 or more staged tokens the partial sums reuse the rows' space (after a
+// barrier that ends every wave's reads of them), which keeps three workgroups per CU at 8 tokens.
 template <int KS, int XT>
 struct DecodeLds {
   static constexpr bool kAliasRed = XT >= 4;
-  static constexpr int kRedBytes = (KS > 1 ? KS : 1) * 2 * 64 * 16;
-  static_assert(!kAliasRed || kRedBytes <= XT * kXPitch, "partial tiles must fit in the staged rows");
-  __align__(16) uint8_t xs[XT * kXPitch];
+  static constexpr int kRedBytes = (KS > 1 ? KS : 1) * 2 * 64 * 2 * 4;
+  static_assert(!kAliasRed || kRedBytes <= (int)sizeof(X8Lds<2 * XT>::row), "partial sums must fit in the rows");
+  X8Lds<2 * XT> x;
   __align__(16) uint8_t sc[2 * kScLds];
   __align__(16) uint8_t red_own[kAliasRed ? 16 : kRedBytes];
-  NA_DEVICE f32x4_t* red() { return reinterpret_cast<f32x4_t*>(kAliasRed ? xs : red_own); }
+  NA_DEVICE float* red() { return reinterpret_cast<float*>(kAliasRed ? &x.row[0][0] : red_own); }
 };
 
-// gate_up: output block b (rows j = 16b .. 16b + 15 of gate and of up) of the item-th distinct expert -> h[pair, j].
-// Order: route and slot -> every global load (codes, scales, x, bias) -> x and scales to LDS, barrier -> MFMA tile by
-// tile (each waits only for its own codes) -> fixed-order sum of the KS partial tiles through LDS -> epilogue in wave
-// 0, which reads nothing from global memory.
+// gate_up: output block b (rows j = 16b .. 16b + 15 of gate and of up) of the item-th distinct expert -> h[pair, j]
+// (E4M3, see h8_codes; h8_sc = the two scale bytes, hi | lo << 8).
+// Order: route and slot -> every global load (codes, scales, x, bias) -> x quantised to E4M3 and the scales to LDS,
+// barrier -> one MFMA per tile (each waits only for its own codes) -> fixed-order sum of the KS partial sums through
+// LDS -> epilogue in wave 0, which reads nothing from global memory.
 template <int KS, int XT>
 __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
     const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
     const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ x,
-    const uint16_t* __restrict__ bias_gu, uint16_t* __restrict__ h, float alpha, float limit) {
+    const uint16_t* __restrict__ bias_gu, uint8_t* __restrict__ h8, float alpha, float limit, uint32_t h8_sc) {
   constexpr int MT = (kTTiles + KS - 1) / KS;
   constexpr int NTH = 64 * KS;
   __shared__ DecodeLds<KS, XT> L;
   const long long rid = route_ids_load(ids, 4 * B);
-  args_at_entry(x, bias_gu, h, alpha, limit);          // past the preloaded arguments: fetched while the ids fly
+  args_at_entry(x, bias_gu, h8, alpha, limit, (int)h8_sc);   // past the preloaded arguments: fetched while ids fly
   int nt, distinct, valid;
   uint64_t users, all;
   const int e = route_t950<4 * XT>(rid, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
@@ -416,87 +524,74 @@ __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
   code_load<MT>(ublk, lane, t0, t1, ru);
   // every load is issued above; the first wait (for x and the scales, issued first) comes below
   __builtin_amdgcn_sched_barrier(0);
-  x_store<XT, NTH>(tid, L.xs, nt, xr);
+  x8_store<XT, NTH>(tid, L.x, nt, xr);
   scale_store<2, NTH>(tid, L.sc, sr);
   __syncthreads();
-  const uint8_t* xrow = L.xs + min(lane & 15, XT - 1) * kXPitch;
+  const uint8_t* arow = a_row(L.x, lane, nt);
+  const uint8_t* asc = a_scales(L.x, lane);
   const uint8_t* srow = L.sc + (lane & 15) * kScPitch;
   f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-  block_compute<MT>(rg, srow, xrow, lane, t0, t1, ag);
-  block_compute<MT>(ru, srow + kScLds, xrow, lane, t0, t1, au);
-  if constexpr (XT == 1) {
-    // one token: only D row 0 (element 0 of lanes 0..15) is used; the same sums in the same order as below
-    if constexpr (KS > 1) {
-      float* red = reinterpret_cast<float*>(L.red());           // [KS][2][16]
-      if (lane < 16) {
-        red[(2 * wave) * 16 + lane] = ag[0];
-        red[(2 * wave + 1) * 16 + lane] = au[0];
-      }
-      __syncthreads();
-      if (wave != 0) return;
-      const int l = lane & 15;
-      float g = red[l], u = red[16 + l];
-#pragma unroll
-      for (int w = 1; w < KS; ++w) {
-        g += red[(2 * w) * 16 + l];
-        u += red[(2 * w + 1) * 16 + l];
-      }
-      ag[0] = g;
-      au[0] = u;
-    }
-    float gb = rb(ag[0]), ub = rb(au[0]);
-    if (bg) {
-      gb = rb(gb + bf16_to_f32(bgj));
-      ub = rb(ub + bf16_to_f32(buj));
-    }
-    const uint16_t hv0 = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
-    store_row_pairs(h + (long long)pair_at(users, 0) * kI + 16 * b, hv0, lane < 16);
-    if (all != users) dup_rows_store(h, kI, users, all, nt, b, hv0, hv0, hv0, hv0);   // uniform, rare
-    return;
-  }
+  block_compute<MT>(rg, srow, arow, asc, L.x.zero, lane, t0, t1, ag);
+  block_compute<MT>(ru, srow + kScLds, arow, asc, L.x.zero, lane, t0, t1, au);
+  float g2[2], u2[2];
+  token_sums(ag, g2[0], g2[1]);
+  token_sums(au, u2[0], u2[1]);
   if constexpr (KS > 1) {
-    f32x4_t* red = L.red();
+    float* red = L.red();                                  // [KS][2][64][2]
     if constexpr (DecodeLds<KS, XT>::kAliasRed) __syncthreads();   // every wave is done with the staged rows
-    red[(2 * wave) * 64 + lane] = ag;
-    red[(2 * wave + 1) * 64 + lane] = au;
+    if (XT > 1 || lane < 16) {
+      *reinterpret_cast<float2*>(red + ((2 * wave) * 64 + lane) * 2) = make_float2(g2[0], g2[1]);
+      *reinterpret_cast<float2*>(red + ((2 * wave + 1) * 64 + lane) * 2) = make_float2(u2[0], u2[1]);
+    }
     __syncthreads();
     if (wave != 0) return;
-    ag = red[lane];
-    au = red[64 + lane];
+    if (XT > 1 || lane < 16) {
+      float2 gs = *reinterpret_cast<const float2*>(red + lane * 2);
+      float2 us = *reinterpret_cast<const float2*>(red + (64 + lane) * 2);
 #pragma unroll
-    for (int w = 1; w < KS; ++w) {
-      ag += red[(2 * w) * 64 + lane];
-      au += red[(2 * w + 1) * 64 + lane];
+      for (int w = 1; w < KS; ++w) {
+        const float2 gw = *reinterpret_cast<const float2*>(red + ((2 * w) * 64 + lane) * 2);
+        const float2 uw = *reinterpret_cast<const float2*>(red + ((2 * w + 1) * 64 + lane) * 2);
+        gs.x += gw.x;
+        gs.y += gw.y;
+        us.x += uw.x;
+        us.y += uw.y;
+      }
+      g2[0] = gs.x;
+      g2[1] = gs.y;
+      u2[0] = us.x;
+      u2[1] = us.y;
     }
   }
-  uint16_t hv[4];
+  uint16_t hv[2];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = 4 * (lane >> 4) + r;
-    float gb = rb(ag[r]), ub = rb(au[r]);
+  for (int q = 0; q < 2; ++q) {
+    const int u = 2 * (lane >> 4) + q;
+    float gb = rb(g2[q]), ub = rb(u2[q]);
     if (bg) {
       gb = rb(gb + bf16_to_f32(bgj));
       ub = rb(ub + bf16_to_f32(buj));
     }
-    hv[r] = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
-    store_row_pairs(h + (long long)pair_at(users, min(m, nt - 1)) * kI + 16 * b, hv[r], m < nt);
+    hv[q] = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
+    store_h8(h8, pair_at(users, min(u, nt - 1)), b, hv[q], h8_sc & 0xff, h8_sc >> 8, u < nt);
   }
-  if (all != users) dup_rows_store(h, kI, users, all, nt, b, hv[0], hv[1], hv[2], hv[3]);   // uniform, rare
+  if (all != users) dup_rows_store_h8(h8, users, all, nt, b, hv[0], hv[1], h8_sc & 0xff, h8_sc >> 8);   // rare
 }
 
 // down, expert-major: output block b (rows n = 16b .. 16b + 15) of the item-th distinct expert from each routed
-// token's own h row, + bias, x routing weight -> yw[pair, n].  An invalid id (128) writes +0 for its pairs and reads
-// no weights.  The top-k sum is left to k_combine_t950.  Load order as in the gate_up kernel.
+// token's own h row (E4M3 from the gate_up kernel), + bias, x routing weight -> yw[pair, n].  An invalid id (128)
+// writes +0 for its pairs and reads no weights.  The top-k sum is left to k_combine_t950.  Load order as in the
+// gate_up kernel.
 template <int KS, int XT>
 __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
     const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
-    const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ h,
-    const uint16_t* __restrict__ wts, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw) {
+    const int64_t* __restrict__ slot_tab, long long expert_base, const uint8_t* __restrict__ h8,
+    const uint16_t* __restrict__ wts, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw, uint32_t h8_sc) {
   constexpr int MT = (kTTiles + KS - 1) / KS;
   constexpr int NTH = 64 * KS;
   __shared__ DecodeLds<KS, XT> L;
   const long long rid = route_ids_load(ids, 4 * B);
-  args_at_entry(h, wts, bias_dn, yw);                  // past the preloaded arguments: fetched while the ids fly
+  args_at_entry(h8, wts, bias_dn, yw, (int)h8_sc);    // past the preloaded arguments: fetched while the ids fly
   int nt, distinct, valid;
   uint64_t users, all;
   const int e = route_t950<4 * XT>(rid, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
@@ -518,45 +613,57 @@ __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
   ScaleRegs<1, NTH> sr;
   scale_load<1, NTH>(tid, blk, blk, sr);
   XRegs<XT, NTH> xr;
-  x_load<XT, NTH>(tid, h, kI, [users](int t) { return pair_at(users, t); }, nt, xr);
+  h8_load<XT, NTH>(tid, h8, [users](int t) { return pair_at(users, t); }, nt, xr);
   const int n = 16 * b + (lane & 15);
   // epilogue operands are loaded now and converted at their use, so no wait is placed before the barrier
   const uint16_t bdn = (bias_dn ? bias_dn + gid * kH : wts)[bias_dn ? n : 0];   // unconditional load
-  uint16_t wr[4];
+  uint16_t wr[2];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) wr[r] = wts[pair_at(users, min(4 * (lane >> 4) + r, nt - 1))];
+  for (int q = 0; q < 2; ++q) wr[q] = wts[pair_at(users, min(2 * (lane >> 4) + q, nt - 1))];
   CodeRegs<MT> rd;
   code_load<MT>(blk, lane, t0, t1, rd);
   __builtin_amdgcn_sched_barrier(0);
-  x_store<XT, NTH>(tid, L.xs, nt, xr);
+  h8_store<XT, NTH>(tid, L.x, nt, xr, h8_sc & 0xff, h8_sc >> 8);
   scale_store<1, NTH>(tid, L.sc, sr);
   __syncthreads();
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  block_compute<MT>(rd, L.sc + (lane & 15) * kScPitch, L.xs + min(lane & 15, XT - 1) * kXPitch, lane, t0, t1, acc);
+  block_compute<MT>(rd, L.sc + (lane & 15) * kScPitch, a_row(L.x, lane, nt), a_scales(L.x, lane), L.x.zero, lane, t0,
+                    t1, acc);
+  float y2[2];
+  token_sums(acc, y2[0], y2[1]);
   if constexpr (KS > 1) {
-    f32x4_t* red = L.red();
+    float* red = L.red();                                  // [KS][64][2]
     if constexpr (DecodeLds<KS, XT>::kAliasRed) __syncthreads();   // every wave is done with the staged rows
-    red[(2 * wave) * 64 + lane] = acc;
+    if (XT > 1 || lane < 16) *reinterpret_cast<float2*>(red + (wave * 64 + lane) * 2) = make_float2(y2[0], y2[1]);
     __syncthreads();
     if (wave != 0) return;
-    acc = red[lane];
+    if (XT > 1 || lane < 16) {
+      float2 s = *reinterpret_cast<const float2*>(red + lane * 2);
 #pragma unroll
-    for (int w = 1; w < KS; ++w) acc += red[(2 * w) * 64 + lane];
+      for (int w = 1; w < KS; ++w) {
+        const float2 v = *reinterpret_cast<const float2*>(red + (w * 64 + lane) * 2);
+        s.x += v.x;
+        s.y += v.y;
+      }
+      y2[0] = s.x;
+      y2[1] = s.y;
+    }
   }
-  float yb[4];
+  float yb[2];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = 4 * (lane >> 4) + r;
-    float y = rb(acc[r]);
+  for (int q = 0; q < 2; ++q) {
+    const int u = 2 * (lane >> 4) + q;
+    float y = rb(y2[q]);
     if (bias_dn) y = rb(y + bf16_to_f32(bdn));
-    yb[r] = y;
-    store_row_pairs(yw + (long long)pair_at(users, min(m, nt - 1)) * kH + 16 * b,
-                    f32_to_bf16(y * bf16_to_f32(wr[r])), m < nt);
+    yb[q] = y;
+    store_row_pairs(yw + (long long)pair_at(users, min(u, nt - 1)) * kH + 16 * b,
+                    f32_to_bf16(y * bf16_to_f32(wr[q])), u < nt);
   }
-  if (all != users) dup_rows_store_w(yw, users, all, nt, b, yb[0], yb[1], yb[2], yb[3], wts);   // uniform, rare
+  if (all != users) dup_rows_store_w(yw, users, all, nt, b, yb[0], yb[1], wts);   // uniform, rare
 }
 
-__global__ __launch_bounds__(256) void k_combine_t950(const uint32_t* __restrict__ yw, int B, uint32_t* __restrict__ out) {
+__global__ __launch_bounds__(256) void k_combine_t950(const uint32_t* __restrict__ yw, int B,
+                                                      uint32_t* __restrict__ out) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= B * (kH / 2)) return;
   const int b = i / (kH / 2), n2 = i - b * (kH / 2);
@@ -570,40 +677,37 @@ __global__ __launch_bounds__(256) void k_combine_t950(const uint32_t* __restrict
   out[i] = (uint32_t)f32_to_bf16(a0) | ((uint32_t)f32_to_bf16(a1) << 16);
 }
 
-// down + combine, row-block-major, for B <= 2 (at most G = 16 / KSD distinct experts): one workgroup of 16 waves per
-// output block b holds every distinct expert of the batch (G groups of KSD waves; group g serves the g-th distinct
-// expert), so the top-k sum needs no third kernel and no cross-workgroup exchange.  All 4B h rows are staged in
-// LDS once; each group runs the expert-major down arithmetic on its pairs' rows; the group leaders leave each pair's
-// bf16 yw row slice in LDS; after a barrier, out[t, 16b + n] = bf16(sum_k yw[4t + k, n]) in top-k order.
-constexpr int kDcWaves = 16;
+// down + combine, row-block-major, for one token: one workgroup of 16 waves per output block b holds the token's
+// (up to 4) distinct experts (4 groups of KSD = 4 waves; group g serves the g-th distinct expert), so the top-k sum
+// needs no third kernel and no cross-workgroup exchange.  The 4 pairs' E4M3 h rows are staged in LDS once;
+// each group runs the expert-major down arithmetic on its pair's rows; the group leaders leave each pair's
+// bf16(y x w) slice in LDS; after a barrier, out[16b + n] = bf16(sum_k yw[k][n]) in top-k order.
+constexpr int kDcWaves = 16, kDcKS = 4;
 
-template <int KSD, int XT>
 struct DownCombLds {
-  static constexpr int G = kDcWaves / KSD;
-  __align__(16) uint8_t hs[4 * XT * kXPitch];           // h rows of all pairs, row p = pair p
-  __align__(16) uint8_t sc[G * kScLds];
-  f32x4_t red[kDcWaves][64];
-  float yw[4 * XT][kTRows];
+  X8Lds<8> x;                                          // pair p's h row: E4M3 rows 2p (hi), 2p + 1 (lo)
+  __align__(16) uint8_t sc[kDcWaves / kDcKS][kScLds];
+  float red[kDcWaves][16];
+  float yw[4][kTRows];
 };
 
-template <int KSD, int XT>
 __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
     const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
-    const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ h,
-    const uint16_t* __restrict__ wts, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ out) {
-  constexpr int MT = (kTTiles + KSD - 1) / KSD;
+    const int64_t* __restrict__ slot_tab, long long expert_base, const uint8_t* __restrict__ h8,
+    const uint16_t* __restrict__ wts, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ out,
+    uint32_t h8_sc) {
+  constexpr int MT = (kTTiles + kDcKS - 1) / kDcKS;
   constexpr int NTH = 64 * kDcWaves;
-  constexpr int GTH = 64 * KSD;
-  __shared__ DownCombLds<KSD, XT> L;
-  const long long rid = route_ids_load(ids, 4 * B);
-  args_at_entry(h, wts, bias_dn, out);                 // past the preloaded arguments: fetched while the ids fly
+  constexpr int GTH = 64 * kDcKS;
+  __shared__ DownCombLds L;
+  const long long rid = route_ids_load(ids, 4);
+  args_at_entry(h8, wts, bias_dn, out, (int)h8_sc);   // past the preloaded arguments: fetched while the ids fly
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = wave / KSD, kw = wave - g * KSD, gtid = tid - g * GTH;
+  const int g = wave / kDcKS, kw = wave - g * kDcKS, gtid = tid - g * GTH;
   const int b = blockIdx.x;
-  const int npairs = 4 * B;
   int nt, distinct, valid;
   uint64_t users, all;
-  const int e = route_t950<4 * XT>(rid, npairs, g, nt, users, all, distinct, valid);
+  const int e = route_t950<4>(rid, 4, g, nt, users, all, distinct, valid);
   const bool live = e >= 0 && e != 128;
   const long long gid = expert_base + (live ? e : 0);
   // groups without a live expert load slot 0's block (valid memory) with every tile slot zeroed, so that the loads
@@ -611,245 +715,51 @@ __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
   const long long slot = live ? (slot_tab ? slot_tab[gid] : gid) : 0;
   const uint8_t* blk = pool + slot * slot_bytes + kTDownOff + (long long)b * kTBlock;
   int t0, t1;
-  ktile_range<KSD>(kw, t0, t1);
+  ktile_range<kDcKS>(kw, t0, t1);
   ScaleRegs<1, GTH> sr;
   scale_load<1, GTH>(gtid, blk, blk, sr);
-  XRegs<4 * XT, NTH> xr;                                 // all pairs' h rows: staged row p = pair p
-  x_load<4 * XT, NTH>(tid, h, kI, [](int t) { return t; }, npairs, xr);
+  XRegs<4, NTH> xr;                                    // all 4 pairs' h rows: staged token t = pair t
+  h8_load<4, NTH>(tid, h8, [](int t) { return t; }, 4, xr);
   const int n = 16 * b + (lane & 15);
   const uint16_t bdn = (bias_dn ? bias_dn + gid * kH : wts)[bias_dn ? n : 0];   // unconditional load
-  uint16_t wr[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) wr[r] = wts[live ? pair_at(users, min(4 * (lane >> 4) + r, nt - 1)) : 0];
+  const uint16_t wr = wts[live ? pair_at(users, 0) : 0];
   CodeRegs<MT> rd;
   code_load<MT>(blk, lane, t0, live ? t1 : t0, rd);
   __builtin_amdgcn_sched_barrier(0);
-  x_store<4 * XT, NTH>(tid, L.hs, npairs, xr);
-  scale_store<1, GTH>(gtid, L.sc + g * kScLds, sr);
-  if (e == 128 && kw == 0) {                             // invalid ids: each of their pairs contributes +0
-    for (int i = lane; i < npairs * kTRows; i += 64)
+  h8_store<4, NTH>(tid, L.x, 4, xr, h8_sc & 0xff, h8_sc >> 8);
+  scale_store<1, GTH>(gtid, L.sc[g], sr);
+  if (e == 128 && kw == 0) {                           // invalid ids: each of their pairs contributes +0
+    for (int i = lane; i < 4 * kTRows; i += 64)
       if ((all >> (i / kTRows)) & 1) L.yw[i / kTRows][i % kTRows] = 0.f;
   }
   __syncthreads();
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  const int pm = live ? pair_at(users, min(lane & 15, nt - 1)) : 0;   // A row of token slot m = lane % 16
-  if (live)
-    block_compute<MT>(rd, L.sc + g * kScLds + (lane & 15) * kScPitch, L.hs + pm * kXPitch, lane, t0, t1, acc);
-  if constexpr (XT == 1) {
-    // one token: nt <= 1, only D row 0 (element 0 of lanes 0..15) is used; the same sums in the same order
-    float* red = reinterpret_cast<float*>(&L.red[0][0]);   // [kDcWaves][16]
-    if (lane < 16) red[wave * 16 + lane] = acc[0];
-    __syncthreads();
-    if (live && kw == 0 && lane < 16) {
-#pragma unroll
-      for (int w = 1; w < KSD; ++w) acc[0] += red[(wave + w) * 16 + lane];
-      float y = rb(acc[0]);
-      if (bias_dn) y = rb(y + bf16_to_f32(bdn));
-      const int p = pair_at(users, 0);
-      if (all == users) {                                // uniform: no token lists this expert twice
-        L.yw[p][lane] = rb(y * bf16_to_f32(wr[0]));
-      } else {
-        const uint32_t dm = token_dups(all, p);
-        for (int k = 0; k < 4; ++k)
-          if ((dm >> k) & 1) L.yw[(p & ~3) + k][lane] = rb(y * bf16_to_f32(wts[(p & ~3) + k]));
-      }
-    }
-  } else {
-    L.red[wave][lane] = acc;
-    __syncthreads();
-    if (live && kw == 0) {
-#pragma unroll
-      for (int w = 1; w < KSD; ++w) acc += L.red[wave + w][lane];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = 4 * (lane >> 4) + r;
-        if (m < nt) {
-          float y = rb(acc[r]);
-          if (bias_dn) y = rb(y + bf16_to_f32(bdn));
-          const int p = pair_at(users, m);
-          if (all == users) {                              // uniform: no token lists this expert twice
-            L.yw[p][lane & 15] = rb(y * bf16_to_f32(wr[r]));
-          } else {
-            const uint32_t dm = token_dups(all, p);
-            for (int k = 0; k < 4; ++k)
-              if ((dm >> k) & 1) L.yw[(p & ~3) + k][lane & 15] = rb(y * bf16_to_f32(wts[(p & ~3) + k]));
-          }
-        }
-      }
-    }
-  }
+  const int p = live ? pair_at(users, 0) : 0;          // the pair of this group's expert (one token)
+  const int m = lane & 15;
+  const uint8_t* arow = m < 2 ? L.x.row[2 * p + m] : nullptr;
+  if (live) block_compute<MT>(rd, L.sc[g] + m * kScPitch, arow, L.x.sc[2 * p + (m & 1)], L.x.zero, lane, t0, t1, acc);
+  if (lane < 16) L.red[wave][lane] = acc[0] + acc[1];
   __syncthreads();
-  if (tid < B * kTRows) {
-    const int t = tid / kTRows, c = tid - t * kTRows;
-    float a = 0.f;
+  if (live && kw == 0 && lane < 16) {
+    float s = L.red[wave][lane];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) a += L.yw[4 * t + k][c];
-    out[(long long)t * kH + 16 * b + c] = f32_to_bf16(a);
-  }
-}
-
-// ------------------------------------------------------------------------- one launch per layer (one token)
-// gate_up and down + combine of one token's top-4 experts in a single launch: 180 workgroups, one per 16-row output
-// block b, of 16 waves = 4 subgroups of 4 waves; subgroup s serves pair s (the token's s-th routed expert) and its
-// waves split K as in the expert-major kernels.  Phase 1: gate_up rows j = 16b .. 16b + 15 (gate block b, up block
-// b + 180) -> h[s][j] with device-coherent stores.  The workgroup then arrives at a grid-wide barrier, and before
-// waiting it issues the loads of its down block's codes and scales, so that the down weights stream while the last
-// workgroups finish phase 1.  Phase 2: down rows n = 16b .. 16b + 15 of each pair from its h row (device-coherent
-// loads), + bias, x routing weight, and the top-4 sum in pair order -> out[n].  The arithmetic is the two-launch
-// path's (k_moe_gate_up_t950 + k_moe_down_comb_t950) step for step, so the results are identical.
-// The barrier needs all 180 workgroups resident at once (the host checks the occupancy before launching).  Its wait
-// is bounded: past spin_limit polls a workgroup sets sync[2] and goes on (the outputs are then undefined; the kernel
-// still ends).  The last workgroup to leave resets sync[0] and sync[1], so a completed launch leaves them zero.
-constexpr int kLwWaves = 16, kLwKS = 4;
-constexpr int kLwHWords = 4 * kI / 2;                  // h of the 4 pairs as bf16 pairs
-
-union LayerLds {
-  struct {
-    __align__(16) uint8_t xs[kXPitch];
-    __align__(16) uint8_t sc[4][2 * kScLds];
-    f32x4_t red[kLwWaves][2][64];
-  } p1;
-  struct {
-    __align__(16) uint8_t hs[4 * kXPitch];
-    __align__(16) uint8_t sc[4][kScLds];
-    f32x4_t red[kLwWaves][64];
-    float yw[4][kTRows];
-  } p2;
-};
-
-__global__ __launch_bounds__(64 * kLwWaves) void k_moe_layer_t950(
-    const uint16_t* __restrict__ x, const int64_t* __restrict__ ids, const uint16_t* __restrict__ wts,
-    const uint8_t* __restrict__ pool, long long slot_bytes, const int64_t* __restrict__ slot_tab,
-    long long expert_base, const uint16_t* __restrict__ bias_gu, const uint16_t* __restrict__ bias_dn,
-    uint32_t* __restrict__ hbuf, uint32_t* __restrict__ sync, int spin_limit, uint16_t* __restrict__ out,
-    float alpha, float limit) {
-  constexpr int MT = (kTTiles + kLwKS - 1) / kLwKS;
-  constexpr int NTH = 64 * kLwWaves, STH = 64 * kLwKS;
-  constexpr int HP = (kLwHWords + NTH - 1) / NTH;
-  __shared__ LayerLds L;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int s = wave / kLwKS, kw = wave - s * kLwKS, stid = tid - s * STH;
-  const int b = blockIdx.x;
-  const long long v = ids[s];
-  const bool live = v >= 0 && v < 128;
-  const long long gid = expert_base + (live ? v : 0);
-  // a dead pair (invalid id) loads slot 0's blocks (valid memory) with every tile slot zeroed and computes nothing
-  const long long slot = live ? (slot_tab ? slot_tab[gid] : gid) : 0;
-  const uint8_t* sbase = pool + slot * slot_bytes;
-  const uint8_t* gblk = sbase + (long long)b * kTBlock;
-  const uint8_t* ublk = gblk + (long long)kTUpBlock0 * kTBlock;
-  const uint8_t* dblk = sbase + kTDownOff + (long long)b * kTBlock;
-  int t0, t1;
-  ktile_range<kLwKS>(kw, t0, t1);
-  const int t1l = live ? t1 : t0;
-
-  // ---- phase 1: gate_up + bias + clamped SwiGLU of pair s, rows 16b .. 16b + 15
-  ScaleRegs<2, STH> sr;
-  scale_load<2, STH>(stid, gblk, ublk, sr);
-  XRegs<1, NTH> xr;
-  x_load<1, NTH>(tid, x, kH, [](int) { return 0; }, 1, xr);
-  const int j = 16 * b + (lane & 15);
-  const uint16_t* bgs = bias_gu ? bias_gu + gid * kGU : x;         // unconditional loads (x when there is no bias)
-  const uint16_t bgj = bgs[bias_gu ? j : 0], buj = bgs[bias_gu ? kI + j : 0];
-  CodeRegs<MT> rg, ru;
-  code_load<MT>(gblk, lane, t0, t1l, rg);
-  code_load<MT>(ublk, lane, t0, t1l, ru);
-  __builtin_amdgcn_sched_barrier(0);
-  x_store<1, NTH>(tid, L.p1.xs, 1, xr);
-  scale_store<2, STH>(stid, L.p1.sc[s], sr);
-  __syncthreads();
-  f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-  if (live) {
-    const uint8_t* srow = L.p1.sc[s] + (lane & 15) * kScPitch;
-    block_compute<MT>(rg, srow, L.p1.xs, lane, t0, t1, ag);
-    block_compute<MT>(ru, srow + kScLds, L.p1.xs, lane, t0, t1, au);
-  }
-  L.p1.red[wave][0][lane] = ag;
-  L.p1.red[wave][1][lane] = au;
-  __syncthreads();
-  if (kw == 0) {                                         // wave-uniform: the subgroup's first wave
-    ag = L.p1.red[wave][0][lane];
-    au = L.p1.red[wave][1][lane];
-#pragma unroll
-    for (int w = 1; w < kLwKS; ++w) {
-      ag += L.p1.red[wave + w][0][lane];
-      au += L.p1.red[wave + w][1][lane];
-    }
-    float gb = rb(ag[0]), ub = rb(au[0]);                // lanes 0..15: D row 0 (the token), column lane
-    if (bias_gu) {
-      gb = rb(gb + bf16_to_f32(bgj));
-      ub = rb(ub + bf16_to_f32(buj));
-    }
-    const uint16_t hv = live ? f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit)) : (uint16_t)0;
-    const uint32_t hi = (uint32_t)__shfl_xor((int)hv, 1) & 0xffff;
-    if (lane < 16 && !(lane & 1))
-      __hip_atomic_store(hbuf + s * (kI / 2) + (16 * b + lane) / 2, (uint32_t)hv | (hi << 16), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __builtin_amdgcn_s_waitcnt(0);                         // this wave's h stores are complete
-  __syncthreads();                                       // (and phase 1's LDS is free for phase 2)
-  if (tid == 0) __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-
-  // ---- the down block's weights, issued before the wait
-  ScaleRegs<1, STH> sd;
-  scale_load<1, STH>(stid, dblk, dblk, sd);
-  const int n = 16 * b + (lane & 15);
-  const uint16_t bdn = (bias_dn ? bias_dn + gid * kH : wts)[bias_dn ? n : 0];   // unconditional load
-  const uint16_t wv = wts[s];
-  CodeRegs<MT> rd;
-  code_load<MT>(dblk, lane, t0, t1l, rd);
-  __builtin_amdgcn_sched_barrier(0);
-  if (tid == 0) {
-    int it = 0;
-    while (__hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gridDim.x) {
-      __builtin_amdgcn_s_sleep(1);
-      if (++it > spin_limit) {
-        __hip_atomic_store(sync + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-    }
-  }
-  __syncthreads();
-
-  // ---- phase 2: every pair's h row (device-coherent loads, all issued before the LDS stores), down, combine
-  uint32_t hw[HP];
-#pragma unroll
-  for (int k = 0; k < HP; ++k)
-    hw[k] = __hip_atomic_load(hbuf + min(tid + NTH * k, kLwHWords - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-  for (int k = 0; k < HP; ++k) {
-    const int i = tid + NTH * k;
-    if (i < kLwHWords) {
-      const int p = i / (kI / 2), c = i - p * (kI / 2);
-      *reinterpret_cast<uint32_t*>(L.p2.hs + p * kXPitch + 4 * c) = hw[k];
-    }
-  }
-  scale_store<1, STH>(stid, L.p2.sc[s], sd);
-  __syncthreads();
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  if (live) block_compute<MT>(rd, L.p2.sc[s] + (lane & 15) * kScPitch, L.p2.hs + s * kXPitch, lane, t0, t1, acc);
-  L.p2.red[wave][lane] = acc;
-  __syncthreads();
-  if (kw == 0 && lane < 16) {
-#pragma unroll
-    for (int w = 1; w < kLwKS; ++w) acc += L.p2.red[wave + w][lane];
-    float y = rb(acc[0]);
+    for (int w = 1; w < kDcKS; ++w) s += L.red[wave + w][lane];
+    float y = rb(s);
     if (bias_dn) y = rb(y + bf16_to_f32(bdn));
-    L.p2.yw[s][lane] = live ? rb(y * bf16_to_f32(wv)) : 0.f;
+    if (all == users) {                                // uniform: the token lists this expert once
+      L.yw[p][lane] = rb(y * bf16_to_f32(wr));
+    } else {
+      const uint32_t dm = token_dups(all, p);
+      for (int k = 0; k < 4; ++k)
+        if ((dm >> k) & 1) L.yw[(p & ~3) + k][lane] = rb(y * bf16_to_f32(wts[(p & ~3) + k]));
+    }
   }
   __syncthreads();
   if (tid < kTRows) {
     float a = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) a += L.p2.yw[k][tid];
+    for (int k = 0; k < 4; ++k) a += L.yw[k][tid];
     out[16 * b + tid] = f32_to_bf16(a);
-  }
-  if (tid == 0) {
-    const uint32_t done = __hip_atomic_fetch_add(sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (done == gridDim.x - 1) {
-      __hip_atomic_store(sync, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(sync + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
   }
 }
 
@@ -863,9 +773,21 @@ static void launch_t(void (*kern)(KArgs...), dim3 grid, dim3 block, hipStream_t 
 }
 
 typedef void (*GateUpT)(const int64_t*, int, const uint8_t*, long long, const int64_t*, long long, const uint16_t*,
-                        const uint16_t*, uint16_t*, float, float);
-typedef void (*DownT)(const int64_t*, int, const uint8_t*, long long, const int64_t*, long long, const uint16_t*,
-                      const uint16_t*, const uint16_t*, uint16_t*);
+                        const uint16_t*, uint8_t*, float, float, uint32_t);
+typedef void (*DownT)(const int64_t*, int, const uint8_t*, long long, const int64_t*, long long, const uint8_t*,
+                      const uint16_t*, const uint16_t*, uint16_t*, uint32_t);
+
+// The fixed E8M0 bytes of h (hi | lo << 8, see h8_codes) for the activation's alpha and limit; 0 when the bound
+// (limit + 1) x max(limit, 1 / alpha) is not a positive finite float far enough from the E8M0 range's ends.
+static uint32_t h8_scale_bytes(float alpha, float limit) {
+  if (!(alpha > 0.f) || !(limit > 0.f)) return 0;
+  const double bound = ((double)limit + 1.0) * (limit > 1.0 / alpha ? (double)limit : 1.0 / alpha);
+  if (!(bound < 1e30) || !(bound > 1e-30)) return 0;
+  int e = 0;
+  std::frexp(bound, &e);                               // bound = m 2^e, 0.5 <= m < 1: 2^(e-1) <= bound < 2^e
+  const int hi = (e - 1) - 7 + 127;                    // s_hi = 2^((e - 1) - 7)
+  return (uint32_t)hi | ((uint32_t)(hi - 5) << 8);
+}
 
 template <int KS>
 static GateUpT gate_up_t950_xt(int xt) {
@@ -873,8 +795,7 @@ static GateUpT gate_up_t950_xt(int xt) {
        : xt == 4 ? k_moe_gate_up_t950<KS, 4> : k_moe_gate_up_t950<KS, 8>;
 }
 static GateUpT pick_gate_up_t950(int ks, int xt) {
-  return ks == 1 ? gate_up_t950_xt<1>(xt) : ks == 2 ? gate_up_t950_xt<2>(xt)
-       : ks == 4 ? gate_up_t950_xt<4>(xt) : gate_up_t950_xt<8>(xt);
+  return ks == 4 ? gate_up_t950_xt<4>(xt) : gate_up_t950_xt<8>(xt);
 }
 template <int KS>
 static DownT down_t950_xt(int xt) {
@@ -882,8 +803,7 @@ static DownT down_t950_xt(int xt) {
        : xt == 4 ? k_moe_down_t950<KS, 4> : k_moe_down_t950<KS, 8>;
 }
 static DownT pick_down_t950(int ks, int xt) {
-  return ks == 1 ? down_t950_xt<1>(xt) : ks == 2 ? down_t950_xt<2>(xt)
-       : ks == 4 ? down_t950_xt<4>(xt) : down_t950_xt<8>(xt);
+  return ks == 4 ? down_t950_xt<4>(xt) : down_t950_xt<8>(xt);
 }
 
 }  // namespace na
@@ -928,61 +848,35 @@ int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
   if (down_mode != 0 && down_mode != 1) return kErrArgs;
   if (B > 8) return kErrTooLarge;
   if (slot_bytes < kTSlot || (slot_bytes & 15) || (reinterpret_cast<uintptr_t>(pool) & 15)) return kErrArgs;
-  if (k_split <= 0) k_split = B == 1 ? 8 : 4;       // automatic: the fastest measured on MI355X per batch size
-  if (k_split != 1 && k_split != 2 && k_split != 4 && k_split != 8) return kErrArgs;
+  if (k_split <= 0) k_split = 4;                    // automatic: the fastest measured on MI355X at every batch size
+  if (k_split != 4 && k_split != 8) return kErrArgs;
   // down_mode 0, B = 1, with an output: gate_up, then down + combine (two launches); else gate_up, down, combine
   // (at B = 2 the row-block kernel's 16-wave workgroups with two waves per expert measured slower than three launches)
   const bool two = down_mode == 0 && out != nullptr && B == 1;
   hipEvent_t ev[6] = {};
   if (events)
     for (int i = 0; i < (two ? 4 : 6); ++i) ev[i] = (hipEvent_t)events[i];
+  const uint32_t h8_sc = h8_scale_bytes(alpha, limit);
+  if (!h8_sc) return kErrArgs;
   const int items = 4 * B;
   const dim3 g1(items, kTDownBlocks);
   const dim3 blk(64 * k_split);
   const int xt = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
   launch_t(pick_gate_up_t950(k_split, xt), g1, blk, stream, ev[0], ev[1], topk_ids, B, (const uint8_t*)pool,
-           slot_bytes, slot_tab, expert_base, (const uint16_t*)x, (const uint16_t*)bias_gu, (uint16_t*)h_scratch,
-           alpha, limit);
+           slot_bytes, slot_tab, expert_base, (const uint16_t*)x, (const uint16_t*)bias_gu, (uint8_t*)h_scratch,
+           alpha, limit, h8_sc);
   if (two) {
-    launch_t(k_moe_down_comb_t950<4, 1>, dim3(kTDownBlocks), dim3(64 * kDcWaves), stream, ev[2], ev[3], topk_ids, B,
-             (const uint8_t*)pool, slot_bytes, slot_tab, expert_base, (const uint16_t*)h_scratch,
-             (const uint16_t*)topk_w, (const uint16_t*)bias_dn, (uint16_t*)out);
+    launch_t(k_moe_down_comb_t950, dim3(kTDownBlocks), dim3(64 * kDcWaves), stream, ev[2], ev[3], topk_ids, B,
+             (const uint8_t*)pool, slot_bytes, slot_tab, expert_base, (const uint8_t*)h_scratch,
+             (const uint16_t*)topk_w, (const uint16_t*)bias_dn, (uint16_t*)out, h8_sc);
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
   }
   launch_t(pick_down_t950(k_split, xt), g1, blk, stream, ev[2], ev[3], topk_ids, B, (const uint8_t*)pool, slot_bytes,
-           slot_tab, expert_base, (const uint16_t*)h_scratch, (const uint16_t*)topk_w, (const uint16_t*)bias_dn,
-           (uint16_t*)yw_scratch);
+           slot_tab, expert_base, (const uint8_t*)h_scratch, (const uint16_t*)topk_w, (const uint16_t*)bias_dn,
+           (uint16_t*)yw_scratch, h8_sc);
   if (out)
     launch_t(k_combine_t950, dim3((B * kH / 2 + 255) / 256), dim3(256), stream, ev[4], ev[5],
              (const uint32_t*)yw_scratch, B, (uint32_t*)out);
-  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
-}
-
-// Single-launch decode layer for one token (k_moe_layer_t950).  Needs every one of its 180 workgroups resident at
-// once: the occupancy is checked once per device; a device that cannot hold them gets kErrTooLarge.
-int na_moe_layer_t950(const void* x, const int64_t* topk_ids, const void* topk_w, const void* pool,
-                      long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
-                      const void* bias_dn, void* h_scratch, unsigned int* sync, void* out, float alpha, float limit,
-                      void* const* events, hipStream_t stream) {
-  if (!x || !topk_ids || !topk_w || !pool || !h_scratch || !sync || !out) return kErrArgs;
-  if (slot_bytes < kTSlot || (slot_bytes & 15) || (reinterpret_cast<uintptr_t>(pool) & 15)) return kErrArgs;
-  if (reinterpret_cast<uintptr_t>(h_scratch) & 15) return kErrArgs;
-  static int fits[64];                                   // per device: 0 unknown, 1 fits, -1 does not
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kErrArgs;
-  if (fits[dev] == 0) {
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_layer_t950, 64 * kLwWaves, 0) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-      return kErrLaunch;
-    fits[dev] = (long long)per_cu * cus >= kTDownBlocks ? 1 : -1;
-  }
-  if (fits[dev] < 0) return kErrTooLarge;
-  hipEvent_t e0 = events ? (hipEvent_t)events[0] : nullptr, e1 = events ? (hipEvent_t)events[1] : nullptr;
-  launch_t(k_moe_layer_t950, dim3(kTDownBlocks), dim3(64 * kLwWaves), stream, e0, e1, (const uint16_t*)x,
-           topk_ids, (const uint16_t*)topk_w, (const uint8_t*)pool, slot_bytes, slot_tab, expert_base,
-           (const uint16_t*)bias_gu, (const uint16_t*)bias_dn, (uint32_t*)h_scratch, (uint32_t*)sync, 1 << 22,
-           (uint16_t*)out, alpha, limit);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

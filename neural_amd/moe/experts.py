@@ -21,18 +21,16 @@ class ResidentExperts:
     def __init__(self, pool: torch.Tensor, layout: ExpertLayout = GPTOSS_LAYOUT, bias_gu: torch.Tensor | None = None,
                  bias_dn: torch.Tensor | None = None, slot_tab: torch.Tensor | None = None,
                  max_batch: int = MAX_DECODE_TOKENS, gu_pairs_per_wave: int = 4, dn_pairs_per_wave: int = 2,
-                 k_split: int = 0, combine_in_down: bool = True, single_launch: bool = False):
+                 k_split: int = 0, combine_in_down: bool = True):
         """pool: uint8 [n, layout.slot_bytes] in the raw, PS4 or t950 (gfx950 tile) layout.  The t950 layout runs the
-        MFMA decode kernels (k_split waves per workgroup split K; 0 picks per batch: 8 for one token, else 4); with
-        combine_in_down, a single token takes two launches (the down kernel holds every expert of an output block and
-        sums the top-k itself) instead of three, and with single_launch one: gate_up and down + combine in one kernel
-        separated by a grid-wide barrier (the same arithmetic, bit for bit; measured slower than two launches on
-        MI355X, whose cross-XCD barrier costs as much as a kernel boundary).  The store layouts run the VALU kernels
-        (gu/dn_pairs_per_wave row pairs per wavefront)."""
+        block-scaled MFMA decode kernels (k_split waves per workgroup split K; 0 = automatic, 4); with
+        combine_in_down, a single token takes two launches (the down kernel holds every expert of an output block
+        and sums the top-k itself) instead of three.  The store layouts run the VALU kernels (gu/dn_pairs_per_wave
+        row pairs per wavefront)."""
         if layout.weight_repr not in ("mxfp4_g32", "mxfp4_g32_ps4", TILE_REPR):
             raise ValueError(f"ResidentExperts serves the raw, PS4 and t950 slot layouts, not {layout.weight_repr}")
-        if k_split not in (0, 1, 2, 4, 8):
-            raise ValueError("k_split must be 0 (automatic), 1, 2, 4 or 8")
+        if k_split not in (0, 4, 8):
+            raise ValueError("k_split must be 0 (automatic), 4 or 8")
         self.k_split = int(k_split)
         self.tiled = layout.weight_repr == TILE_REPR
         if pool.dtype is not torch.uint8 or pool.ndim != 2 or pool.shape[1] != layout.slot_bytes:
@@ -59,8 +57,6 @@ class ResidentExperts:
         self.gu_pairs, self.dn_pairs = int(gu_pairs_per_wave), int(dn_pairs_per_wave)
         dev = pool.device
         self.down_mode = 0 if combine_in_down else 1
-        self.single = bool(single_launch) and self.tiled
-        self.sync = torch.zeros(4, dtype=torch.int32, device=pool.device)
         self.h = torch.empty(max_batch * layout.top_k, layout.down_k, dtype=torch.bfloat16, device=dev)
         self.yw = torch.empty(max_batch * layout.top_k, layout.down_n, dtype=torch.bfloat16, device=dev)
 
@@ -90,12 +86,6 @@ class ResidentExperts:
             out = torch.empty(B, L.hidden, dtype=torch.bfloat16, device=hidden.device)
         elif out.dtype is not torch.bfloat16 or tuple(out.shape) != (B, L.hidden) or not out.is_contiguous():
             raise ValueError("out must be contiguous bf16 [B, hidden]")
-        if self.tiled and self.single and B == 1:
-            N.call("na_moe_layer_t950", hidden.data_ptr(), router_indices.data_ptr(), routing_weights.data_ptr(),
-                   self.pool.data_ptr(), L.slot_bytes, N.ptr(self.slot_tab), layer * L.n_experts,
-                   N.ptr(self.bias_gu), N.ptr(self.bias_dn), self.h.data_ptr(), self.sync.data_ptr(), out.data_ptr(),
-                   float(L.act_alpha), float(L.act_limit), N.events_array(events), N.stream(hidden.device))
-            return out
         if self.tiled:
             N.call("na_moe_decode_t950", hidden.data_ptr(), router_indices.data_ptr(), routing_weights.data_ptr(), B,
                    self.pool.data_ptr(), L.slot_bytes, N.ptr(self.slot_tab), layer * L.n_experts,
@@ -153,8 +143,6 @@ class ResidentExperts:
 
     def launches(self, batch: int, with_out: bool = True) -> tuple:
         """Names of the kernels one forward_decode call launches, in order (two timing events per launch)."""
-        if self.tiled and self.single and batch == 1:
-            return ("layer",)
         if self.tiled and self.down_mode == 0 and with_out and batch == 1:
             return ("gate_up", "down_combine")
         return ("gate_up", "down", "combine") if with_out else ("gate_up", "down")

@@ -142,8 +142,8 @@ def _t950_case(B, seed, bias, nslot=10):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("B,k_split,bias", [(1, 4, False), (1, 8, True), (1, 0, False), (1, 1, True), (2, 2, True),
-                                            (4, 4, True), (8, 4, False), (8, 2, True), (8, 8, True)])
+@pytest.mark.parametrize("B,k_split,bias", [(1, 4, False), (1, 8, True), (1, 0, False), (2, 8, True), (2, 4, False),
+                                            (4, 4, True), (8, 4, False), (8, 8, True)])
 def test_moe_decode_t950_matches_oracle_and_store_path(B, k_split, bias):
     import torch
     from neural_amd.moe.experts import ResidentExperts
@@ -234,10 +234,8 @@ def test_down_with_combine_matches_expert_major_path(B):
     tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
     tiles.repack_to_t950(raw, tp)
     tabd, bg, bd = torch.from_numpy(tab).to(dev), bgu.to(dev), bdn.to(dev)
-    two = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=True,
-                          single_launch=False)
-    three = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=False,
-                            single_launch=False)
+    two = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=True)
+    three = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=False)
     assert two.launches(B) == (("gate_up", "down_combine") if B == 1 else ("gate_up", "down", "combine"))
     assert len(three.launches(B)) == 3
     rng = np.random.default_rng(B)
@@ -276,90 +274,118 @@ def test_down_with_combine_matches_expert_major_path(B):
                 assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale, (name, call, b, d.max(), scale)
 
 
+def _e4m3_table():
+    """Values of the 256 OCP E4M3 codes (NaN at 0x7f / 0xff): sign, 4 exponent bits (bias 7), 3 mantissa bits."""
+    c = np.arange(256)
+    e, m = (c >> 3) & 15, c & 7
+    v = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1 + m / 8.0) * 2.0 ** (e - 7))
+    v = np.where(c & 0x80, -v, v)
+    return np.where((c & 0x7F) == 0x7F, np.nan, v)
+
+
+def _e4m3_rne(v):
+    """Round each value to the nearest finite E4M3 value, ties to the even code: a brute-force search of the table."""
+    tab = _e4m3_table()
+    codes = np.array([c for c in range(256) if np.isfinite(tab[c])])
+    vals = tab[codes]
+    d = np.abs(vals[None, :] - np.asarray(v, np.float64)[:, None])
+    best = d.min(axis=1, keepdims=True)
+    tie_ok = (d == best) & ((codes[None, :] & 1) == 0)
+    pick = np.where(tie_ok.any(axis=1), np.argmax(tie_ok, axis=1), np.argmin(d, axis=1))
+    return vals[pick]
+
+
 @pytest.mark.gpu
-@pytest.mark.parametrize("with_bias", [True, False])
-def test_single_launch_layer_matches_two_launch_path(with_bias):
-    """One token's layer in one launch (gate_up, a grid-wide barrier, down + combine) gives the two-launch path's
-    output bit for bit, over consecutive calls (the barrier words are left at zero), invalid ids (+0 contributions),
-    duplicate ids, and graph replays; and it matches the oracle."""
+def test_x8_quantiser_round_trip_and_rounding():
+    """The decode kernels' activation quantiser (two E4M3 rows hi, lo with one E8M0 scale per 32-element block and
+    row): the scales are 2^(e - 7) of the block's largest magnitude (frexp); hi is the round-to-nearest-even E4M3 of
+    x / s_hi and lo that of (x - hi s_hi) / s_lo (a brute-force search of the code table); and hi s_hi + lo s_lo
+    reproduces x exactly for every element within 2^13 of its block's largest magnitude and to within 2^-21 of that
+    magnitude below it.  Rows: N(0, 1) at three magnitudes, zeros, blocks with one large and many tiny elements,
+    bf16 subnormals."""
     import torch
-    from neural_amd.moe.experts import ResidentExperts
-    from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
+    from neural_amd import _native as N
     dev = _dev()
-    slots, x, ids, w, tab, bgu, bdn = _t950_case(1, 950 + int(with_bias), True, nslot=8)
-    print(f"case single-launch layer bias={with_bias}", flush=True)
-    raw = torch.from_numpy(np.stack(slots)).to(dev)
-    tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
-    tiles.repack_to_t950(raw, tp)
-    tabd = torch.from_numpy(tab).to(dev)
-    bg, bd = (bgu.to(dev), bdn.to(dev)) if with_bias else (None, None)
-    one = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, single_launch=True)
-    two = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4)    # the layer kernel's K split
-    assert one.launches(1) == ("layer",) and two.launches(1) == ("gate_up", "down_combine")
-    rng = np.random.default_rng(17)
-    cache = {}
-    for call in range(4):
-        idc = ids.copy()
-        if call == 1:
-            idc[0, 1] = -1
-            idc[0, 3] = 200
-        if call == 2:
-            idc[0, 2] = idc[0, 0]                            # the same expert twice
-        xn = synth.bf16_normal(rng, (1, 2880))
-        xd, idd = xn.to(dev), torch.from_numpy(idc).to(dev)
-        wd = torch.from_numpy(w).to(torch.bfloat16).to(dev)
-        layer = 2 + call
-        a = one.forward_decode(layer, xd, idd, wd)
-        c = two.forward_decode(layer, xd, idd, wd)
-        torch.cuda.synchronize()
-        diff = (a.float() - c.float()).abs()
-        assert torch.equal(a, c), (call, int((diff > 0).sum()), float(diff.max()), idc.tolist(),
-                                   torch.nonzero(diff[0] > 0)[:8].flatten().tolist())
-        assert int(one.sync[:3].abs().sum()) == 0, one.sync
-        ys = []
-        for k in range(4):
-            e = int(idc[0, k])
-            if not 0 <= e < 128:
-                ys.append(np.zeros(2880, np.float32))
-                continue
-            g = layer * 128 + e
-            sl = int(tab[g])
-            if sl not in cache:
-                cache[sl] = mo.expert_weights(slots[sl])
-            bgv = bgu[g].float().numpy() if with_bias else np.zeros(5760, np.float32)
-            bdv = bdn[g].float().numpy() if with_bias else np.zeros(2880, np.float32)
-            ys.append(mo.expert_forward_bf16(xn.float().numpy(), None, bgv, bdv, weights=cache[sl])[0])
-        want = mo.combine_bf16(np.stack(ys), w[0])
-        got = a.float().cpu().numpy()[0]
-        d = np.abs(got - want)
-        assert d.max() <= 2e-2 + 1e-2 * np.abs(want).max(), (call, d.max())
-    # graph replays with the routing changed on the device between them
-    xd = synth.bf16_normal(rng, (1, 2880)).to(dev)
-    idd = torch.from_numpy(ids.copy()).to(dev)
-    wd = torch.from_numpy(w).to(torch.bfloat16).to(dev)
-    out = torch.empty(1, 2880, dtype=torch.bfloat16, device=dev)
-    one.forward_decode(5, xd, idd, wd, out=out)
+    rng = np.random.default_rng(21)
+    rows = [synth.bf16_normal(rng, (2880,)).float().numpy() * 2.0 ** k for k in (-20, 0, 20)]
+    rows.append(np.zeros(2880, np.float32))
+    spread = synth.bf16_normal(rng, (2880,)).float().numpy() * 1e-6
+    spread[::32] = 300.0
+    spread[5::64] = -1e-30
+    rows.append(spread)
+    rows.append(synth.bf16_normal(rng, (2880,)).float().numpy() * 1e-39)      # bf16 subnormals (last row)
+    x = torch.from_numpy(np.stack(rows)).to(torch.bfloat16)
+    R = x.shape[0]
+    xf = x.float().numpy().astype(np.float64)
+    xd = x.to(dev)
+    hi = torch.zeros(R, 2880, dtype=torch.uint8, device=dev)
+    lo = torch.zeros_like(hi)
+    sc = torch.zeros(R, 2, 90, dtype=torch.uint8, device=dev)
+    N.call("na_selftest_x8", xd.data_ptr(), R, hi.data_ptr(), lo.data_ptr(), sc.data_ptr(), N.stream(dev))
     torch.cuda.synchronize()
-    gr = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(gr):
-        one.forward_decode(5, xd, idd, wd, out=out)
-    for rep in range(3):
-        idd.copy_(torch.from_numpy(np.roll(ids, rep, axis=1).copy()))
-        gr.replay()
-        torch.cuda.synchronize()
-        want = two.forward_decode(5, xd, idd, wd)
-        torch.cuda.synchronize()
-        assert torch.equal(out, want), rep
-    assert int(one.sync[:3].abs().sum()) == 0
+    tab = _e4m3_table()
+    hv, lv, s = tab[hi.cpu().numpy()], tab[lo.cpu().numpy()], sc.cpu().numpy().astype(np.int64)
+    assert np.isfinite(hv).all() and np.isfinite(lv).all()
+    blocks = xf.reshape(R, 90, 32)
+    amax = np.abs(blocks).max(axis=2)
+    want_sh = np.clip(np.frexp(amax)[1] + 119, 1, 254)
+    want_sh = np.where(amax == 0, 1, want_sh)
+    assert np.array_equal(s[:, 0], want_sh)
+    s_hi = np.repeat(2.0 ** (s[:, 0] - 127), 32, axis=1)
+    s_lo = np.repeat(2.0 ** (s[:, 1] - 127), 32, axis=1)
+    err = np.abs(hv * s_hi + lv * s_lo - xf)
+    n = R - 1                                      # the normal rows; the converter may flush bf16 subnormals
+    assert np.array_equal(hv[:n], _e4m3_rne((xf[:n] / s_hi[:n]).ravel()).reshape(n, 2880))
+    r = xf[:n] - hv[:n] * s_hi[:n]
+    assert np.array_equal(lv[:n], _e4m3_rne((r / s_lo[:n]).ravel()).reshape(n, 2880))
+    big = np.repeat(amax, 32, axis=1)[:n]
+    near = np.abs(xf[:n]) >= big * 2.0 ** -13
+    assert (err[:n][near] == 0).all()
+    assert (err[:n] <= big * 2.0 ** -21).all()
+    assert (err[n] <= 2.0 ** -126).all()
+
+
+@pytest.mark.gpu
+def test_block_scaled_mfma_operand_order():
+    """One v_mfma_scale_f32_16x16x128_f8f6f4 exactly as the decode kernels issue it: A = E4M3 codes with one E8M0
+    scale per row and 32-K block, B = a t950 k-tile (lane 16 q + n holds bytes 4q .. 4q + 3 of groups 0..3 of row n)
+    put into the MFMA's order by the lane swaps, with one E8M0 scale per row and group; against the fp64 product."""
+    import torch
+    from neural_amd import _native as N
+    dev = _dev()
+    rng = np.random.default_rng(31)
+    tab = _e4m3_table()
+    a = rng.integers(0, 256, (16, 128), dtype=np.uint8)
+    a[(a & 0x7F) == 0x7F] = 0x11
+    sa = rng.integers(118, 135, (16, 4), dtype=np.uint8)
+    sb = rng.integers(118, 135, (16, 4), dtype=np.uint8)
+    tile = rng.integers(0, 256, 1024, dtype=np.uint8)
+    # B[k][n]: group j = k // 32, element e = k % 32 = nibble e % 2 of code byte e // 2 of (row n, group j), which the
+    # t950 tile holds at lane 16 (byte // 4) + n, dword j, byte byte % 4
+    B = np.zeros((128, 16))
+    for n in range(16):
+        for k in range(128):
+            j, e = divmod(k, 32)
+            byte = e // 2
+            v = tile[16 * (16 * (byte // 4) + n) + 4 * j + byte % 4]
+            B[k, n] = mo.E2M1[(v >> 4) if e % 2 else (v & 15)] * 2.0 ** (int(sb[n, j]) - 127)
+    A = tab[a] * np.repeat(2.0 ** (sa.astype(np.int64) - 127), 32, axis=1)
+    want = A @ B
+    d = torch.zeros(16, 16, dtype=torch.float32, device=dev)
+    ta = [torch.from_numpy(v.copy()).to(dev) for v in (a, sa, tile, sb)]
+    N.call("na_selftest_mfma8", ta[0].data_ptr(), ta[1].data_ptr(), ta[2].data_ptr(), ta[3].data_ptr(), d.data_ptr(),
+           N.stream(dev))
+    torch.cuda.synchronize()
+    assert np.abs(d.cpu().numpy() - want).max() <= 1e-4 * np.abs(want).max()
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("B", [1, 2, 8])
 def test_duplicate_ids_in_a_token(B):
     """A token whose top-4 list names one expert more than once (and an invalid id twice): each pair is that expert's
-    output times its own weight, as the reference's per-pair GEMV computes it.  Every decode path (t950 single
-    launch, two launches, expert-major three launches; store layout) against the oracle, and the t950 paths against
-    each other bit for bit."""
+    output times its own weight, as the reference's per-pair GEMV computes it.  Every decode path (t950 two launches,
+    expert-major three launches; store layout) against the oracle, and the t950 paths against each other bit for
+    bit."""
     import torch
     from neural_amd.moe.experts import ResidentExperts
     from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_T950
@@ -376,8 +402,7 @@ def test_duplicate_ids_in_a_token(B):
     tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
     tiles.repack_to_t950(raw, tp)
     tabd, bg, bd = torch.from_numpy(tab).to(dev), bgu.to(dev), bdn.to(dev)
-    paths = {"single": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, single_launch=True),
-             "two": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4),   # the layer kernel's K split
+    paths = {"two": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4),   # down + combine's K split
              "three": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=False),
              "store": ResidentExperts(raw, GPTOSS_LAYOUT, bg, bd, tabd)}
     xd, idd = x.to(dev), torch.from_numpy(ids).to(dev)
@@ -385,10 +410,7 @@ def test_duplicate_ids_in_a_token(B):
     layer = 4
     got = {nm: rx.forward_decode(layer, xd, idd, wd).float().cpu().numpy() for nm, rx in paths.items()}
     torch.cuda.synchronize()
-    if B == 1:
-        assert np.array_equal(got["single"], got["two"]) and np.array_equal(got["two"], got["three"])
-    else:
-        assert np.array_equal(got["single"], got["three"])
+    assert np.array_equal(got["two"], got["three"])
     cache = {}
     for b in range(B):
         ys = []
