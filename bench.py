@@ -14,7 +14,8 @@ Also printed on the same JSON line:
   roofline      the dominant kernel (gate_up): algorithmic bytes per launch (distinct experts x 8,812,800 B of E2M1
                 codes + E8M0 scales) / its average launch duration, measured with events timestamped by the
                 dispatches themselves (hipExtLaunchKernel) on the launch stream, over an eager pass of the same
-                steps; peak = 8 TB/s.
+                steps queued behind a spin kernel (so the launches run back to back, as in the graph replays);
+                peak = 8 TB/s.
   cpu_baseline  the reference's own C expert kernel (kernels/gptoss_cpu_multi.c, AVX-512, or gptoss_cpu_portable.c,
                 built from source into oracle/_ref/) on this host's cores over a bounded sample of the same workload.
 """
@@ -73,6 +74,13 @@ def measured_traffic(kernel, layout, batch, k_split):
 def effective_k_split(k_split, batch):
     """The k_split the library runs for a requested one (0 = automatic, as na_moe_decode_t950 picks it)."""
     return k_split if k_split > 0 else 4
+
+
+def queue_behind_spin(torch, ms=4.0):
+    """Hold the stream with a spin kernel of about `ms` so that the eager launches the host issues next queue up behind
+    it and run back to back, as inside the timed graph replays (issued one by one from Python, each launch would
+    otherwise start on an idle GPU and include its wake-up latency)."""
+    torch.cuda._sleep(int(ms * 2.4e6))
 
 
 def log(msg):
@@ -213,6 +221,7 @@ def bench_prefill(A):
     per = {nm: 0.0 for nm in names}
     R = 5
     for _ in range(R):
+        queue_behind_spin(torch)
         rx.forward_prefill(0, x, ids, wts, out=out, events=ev)
         torch.cuda.synchronize()
         for i, nm in enumerate(names):
@@ -352,6 +361,7 @@ def bench_model(A):
     acc = {nm: 0.0 for nm in names}
     att_full = att_slide = 0.0
     for _ in range(R):
+        queue_behind_spin(torch, 8.0)
         model.step(events=ev)
         torch.cuda.synchronize()
         for li in range(N_LAYERS):
@@ -490,6 +500,8 @@ def main():
     ap.add_argument("--sets", type=int, default=16, help="routing sets (graphs) cycled over the steps")
     ap.add_argument("--roofline-steps", type=int, default=20)
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--no-batch-sweep", action="store_true",
+                    help="experts workload: skip the shorter runs of configuration 1's other batch sizes")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--gu-pairs", type=int, default=4, help="gate_up row pairs per wavefront (1, 2, 4)")
     ap.add_argument("--dn-pairs", type=int, default=2, help="down row pairs per wavefront (1, 2, 4)")
@@ -574,83 +586,92 @@ def main():
     bias_dn = torch.zeros(n_slots, L.down_n, dtype=torch.bfloat16, device=dev)
     rx = ResidentExperts(pool, L, bias_gu, bias_dn, gu_pairs_per_wave=A.gu_pairs, dn_pairs_per_wave=A.dn_pairs,
                          k_split=A.k_split, combine_in_down=A.down != "expert")
-    launches = rx.launches(A.batch)
-    per_layer = len(launches)
+
+    def measure(B, steps, warmup, n_sets, roofline_steps):
+        """Graph-replayed 36-layer steps of batch B (n_sets routing sets cycled), then the per-kernel pass."""
+        launches = rx.launches(B)
+        per_layer = len(launches)
+        rng = np.random.default_rng(2026 + B)
+        ids_np, w_np = routing_sets(rng, n_sets, B)
+        distinct = np.array([[len(set(ids_np[s, l].reshape(-1).tolist())) for l in range(N_LAYERS)]
+                             for s in range(n_sets)])
+        ids = torch.from_numpy(ids_np).to(dev)
+        wts = torch.from_numpy(w_np).to(torch.bfloat16).to(dev)
+        x = synth.bf16_normal(rng, (N_LAYERS, B, H)).to(dev)
+        out = torch.empty(N_LAYERS, B, H, dtype=torch.bfloat16, device=dev)
+
+        def step(s, events=None):
+            for l in range(N_LAYERS):
+                rx.forward_decode(l, x[l], ids[s, l], wts[s, l], out=out[l],
+                                  events=None if events is None else events[l])
+
+        # eager warm-up, then one graph per routing set
+        step(0)
+        torch.cuda.synchronize()
+        graphs = []
+        cs = torch.cuda.Stream()
+        cs.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cs):
+            step(0)
+        torch.cuda.current_stream().wait_stream(cs)
+        for s in range(n_sets):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                step(s)
+            graphs.append(gr)
+        torch.cuda.synchronize()
+        log(f"B={B}: captured {len(graphs)} graphs of {per_layer * N_LAYERS} kernels; warm-up {warmup} steps")
+        for i in range(warmup):
+            graphs[i % n_sets].replay()
+        torch.cuda.synchronize()
+
+        # ------------------------------------------------------------------ timed region
+        t0 = time.perf_counter()
+        for i in range(steps):
+            graphs[i % n_sets].replay()
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        ms_step = el / steps * 1e3
+        tok_s = B * steps / el
+        step_bytes = np.mean([distinct[i % n_sets].sum() for i in range(steps)]) * SLOT_ALGO_BYTES
+        log(f"B={B}: timed {steps} steps: {ms_step:.3f} ms/step, {tok_s:.1f} tok/s, "
+            f"{step_bytes / (ms_step * 1e-3) / 1e9:.0f} GB/s whole-step")
+
+        # ------------------------------------------------------------------ roofline pass (per-kernel events)
+        per_kernel_bytes = {"gate_up": GATE_UP_BYTES, "down": DOWN_BYTES, "down_combine": DOWN_BYTES, "combine": 0}
+        kernels = tuple((nm, per_kernel_bytes[nm]) for nm in launches)
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * len(kernels))] for _ in range(N_LAYERS)]
+        for row in ev:
+            for e in row:
+                e.record()
+        torch.cuda.synchronize()
+        tot = {nm: [0.0, 0.0, 0] for nm, _ in kernels}
+        for r in range(roofline_steps):
+            s = r % n_sets
+            queue_behind_spin(torch)
+            step(s, events=ev)
+            torch.cuda.synchronize()
+            for l in range(N_LAYERS):
+                d = int(distinct[s, l])
+                for k, (nm, per) in enumerate(kernels):
+                    ms = ev[l][2 * k].elapsed_time(ev[l][2 * k + 1])
+                    tot[nm][0] += ms
+                    tot[nm][1] += d * per
+                    tot[nm][2] += 1
+        kern = {nm: {"avg_us": v[0] / v[2] * 1e3, "gbps": (v[1] / (v[0] * 1e-3) / 1e9) if v[0] else 0.0}
+                for nm, v in tot.items()}
+        for nm, v in kern.items():
+            log(f"B={B}: kernel {nm}: avg {v['avg_us']:.2f} us/launch, {v['gbps']:.0f} GB/s algorithmic")
+        dom = kernels[0][0]
+        return {"tok_s": tok_s, "ms_step": ms_step, "step_bytes": step_bytes, "distinct": distinct, "kern": kern,
+                "dom": dom, "per_launch": tot[dom][1] / tot[dom][2], "ids_np": ids_np}
 
     B = A.batch
-    rng = np.random.default_rng(2026)
-    ids_np, w_np = routing_sets(rng, A.sets, B)
-    distinct = np.array([[len(set(ids_np[s, l].reshape(-1).tolist())) for l in range(N_LAYERS)]
-                         for s in range(A.sets)])
-    ids = torch.from_numpy(ids_np).to(dev)
-    wts = torch.from_numpy(w_np).to(torch.bfloat16).to(dev)
-    x = synth.bf16_normal(rng, (N_LAYERS, B, H)).to(dev)
-    out = torch.empty(N_LAYERS, B, H, dtype=torch.bfloat16, device=dev)
-
-    def step(s, events=None):
-        for l in range(N_LAYERS):
-            rx.forward_decode(l, x[l], ids[s, l], wts[s, l], out=out[l],
-                              events=None if events is None else events[l])
-
-    # eager warm-up, then one graph per routing set
-    step(0)
-    torch.cuda.synchronize()
-    graphs = []
-    cs = torch.cuda.Stream()
-    cs.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(cs):
-        step(0)
-    torch.cuda.current_stream().wait_stream(cs)
-    for s in range(A.sets):
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr):
-            step(s)
-        graphs.append(gr)
-    torch.cuda.synchronize()
-    log(f"captured {len(graphs)} graphs of {per_layer * N_LAYERS} kernels; warm-up {A.warmup} steps")
-    for i in range(A.warmup):
-        graphs[i % A.sets].replay()
-    torch.cuda.synchronize()
-
-    # ------------------------------------------------------------------ timed region
-    t0 = time.perf_counter()
-    for i in range(A.steps):
-        graphs[i % A.sets].replay()
-    torch.cuda.synchronize()
-    el = time.perf_counter() - t0
-    ms_step = el / A.steps * 1e3
-    tok_s = B * A.steps / el
-    step_bytes = np.mean([distinct[i % A.sets].sum() for i in range(A.steps)]) * SLOT_ALGO_BYTES
-    log(f"timed {A.steps} steps: {ms_step:.3f} ms/step, {tok_s:.1f} tok/s, "
-        f"{step_bytes / (ms_step * 1e-3) / 1e9:.0f} GB/s whole-step")
-
-    # ------------------------------------------------------------------ roofline pass (per-kernel events)
-    per_kernel_bytes = {"gate_up": GATE_UP_BYTES, "down": DOWN_BYTES, "down_combine": DOWN_BYTES, "combine": 0}
-    kernels = tuple((nm, per_kernel_bytes[nm]) for nm in launches)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * len(kernels))] for _ in range(N_LAYERS)]
-    for row in ev:
-        for e in row:
-            e.record()
-    torch.cuda.synchronize()
-    tot = {nm: [0.0, 0.0, 0] for nm, _ in kernels}
-    for r in range(A.roofline_steps):
-        s = r % A.sets
-        step(s, events=ev)
-        torch.cuda.synchronize()
-        for l in range(N_LAYERS):
-            d = int(distinct[s, l])
-            for k, (nm, per) in enumerate(kernels):
-                ms = ev[l][2 * k].elapsed_time(ev[l][2 * k + 1])
-                tot[nm][0] += ms
-                tot[nm][1] += d * per
-                tot[nm][2] += 1
-    kern = {nm: {"avg_us": v[0] / v[2] * 1e3, "gbps": (v[1] / (v[0] * 1e-3) / 1e9) if v[0] else 0.0}
-            for nm, v in tot.items()}
-    for nm, v in kern.items():
-        log(f"kernel {nm}: avg {v['avg_us']:.2f} us/launch, {v['gbps']:.0f} GB/s algorithmic")
-    dom = kernels[0][0]
+    m = measure(B, A.steps, A.warmup, A.sets, A.roofline_steps)
+    tok_s, ms_step, step_bytes, distinct, kern = m["tok_s"], m["ms_step"], m["step_bytes"], m["distinct"], m["kern"]
+    ids_np, dom = m["ids_np"], m["dom"]
     top = kern[dom]
-    per_launch = tot[dom][1] / tot[dom][2]
+    per_launch = m["per_launch"]
     kname = "k_moe_gate_up_t950" if A.layout == "t950" \
         else "k_moe_gate_up"
     traffic, why = measured_traffic(kname, A.layout, B, effective_k_split(A.k_split, B))
@@ -665,6 +686,20 @@ def main():
             roofline[f"{nm}_avg_launch_us"] = round(v["avg_us"], 3)
             if v["gbps"]:
                 roofline[f"{nm}_kernel_gbps"] = round(v["gbps"], 1)
+    # the configuration's other batch sizes (shorter runs on the same resident pool)
+    batch_sweep = {}
+    if not A.no_batch_sweep:
+        for Bs in (1, 2, 4, 8):
+            if Bs == B:
+                continue
+            ms_ = measure(Bs, max(A.steps // 4, 20), 5, 8, max(A.roofline_steps // 4, 2))
+            kd = ms_["kern"][ms_["dom"]]
+            batch_sweep[str(Bs)] = {"tok_s": round(ms_["tok_s"], 1), "ms_per_step": round(ms_["ms_step"], 4),
+                                    "distinct_experts_per_layer": round(float(ms_["distinct"].mean()), 3),
+                                    "step_hbm_gbps": round(ms_["step_bytes"] / (ms_["ms_step"] * 1e-3) / 1e9, 1),
+                                    "gate_up_avg_launch_us": round(kd["avg_us"], 3),
+                                    "gate_up_gbps": round(kd["gbps"], 1),
+                                    "gate_up_frac": round(kd["gbps"] / HBM_PEAK_GBS, 4)}
 
     cpu = None
     if not A.skip_cpu:
@@ -685,7 +720,8 @@ def main():
                       "pool_gb": round(n_slots * L.slot_bytes / 1e9, 2),
                       "distinct_experts_per_layer": round(float(distinct.mean()), 3),
                       "step_algorithmic_gb": round(step_bytes / 1e9, 4),
-                      "step_hbm_gbps": round(step_bytes / (ms_step * 1e-3) / 1e9, 1)},
+                      "step_hbm_gbps": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
+                      "batch_sweep": batch_sweep},
            "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(res), flush=True)
 
