@@ -1,14 +1,18 @@
-// MXFP4 GEMM on gfx950 for prompt processing: the reference's mxfp4_gemm / grouped GEMM arithmetic (per 32-element
+// MXFP4 GEMMs on gfx950 for prompt processing: the reference's mxfp4_gemm / grouped GEMM arithmetic (per 32-element
 // group, E2M1 x 2^(s-127) dequantised exactly to bf16, bf16 x bf16 products accumulated in fp32, one bf16 rounding of
-// each output; reference neural/q80/mxfp4_kernels.py:87-126, 242-295) on v_mfma_f32_16x16x32_bf16, and the fused
-// MoE prefill layer built on it (reference server.py:1837-1936, _expert_gemms :1977-2040).
+// each output; reference neural/q80/mxfp4_kernels.py:87-126, 242-295) and the fused MoE prefill layer (reference
+// server.py:1837-1936, _expert_gemms :1977-2040).
 //
-// Workgroup tile: 64 tokens x (4 waves x NB row blocks of 16 weight rows; NB = 3, or 4 in the SwiGLU gate_up
-// kernel), K walked in k-tiles of 4 groups (128 elements).  Per k-tile the workgroup stages the 64 x 128 activation
-// tile in LDS (double buffered, gathered through a row map: token-permuted rows for the MoE path), each wave loads
-// its blocks' codes and scales (next k-tile in flight while the current one computes), reads its 16 A fragments
-// once, dequantises each block's codes in registers with v_cvt_scalef32_pk_bf16_fp4 and runs 16 NB MFMAs.  The activations stay bf16: an FP4 or
-// FP8 MFMA would need quantised activations and would no longer give the reference's results.
+// The fused layer (k_prefill_gate_up / k_prefill_down) runs on the block-scaled v_mfma_scale_f32_16x16x128_f8f6f4:
+// E2M1 codes and E8M0 scales as stored, activations as two exact E4M3 rows (hi, lo) with one E8M0 scale per 32
+// elements each, so hi w + lo w are the reference's bf16 x E2M1 products; see the block-scaled section below.
+//
+// The plain and grouped GEMM entry points take bf16 activations without a workspace and run on
+// v_mfma_f32_16x16x32_bf16: workgroup tile 64 tokens x (4 waves x 3 row blocks of 16 weight rows), K walked in k-tiles
+// of 4 groups (128 elements); per k-tile the workgroup stages the 64 x 128 activation tile in LDS (double buffered,
+// gathered through a row map), each wave loads its blocks' codes and scales (next k-tile in flight while the current
+// one computes), reads its 16 A fragments once, dequantises each block's codes in registers with
+// v_cvt_scalef32_pk_bf16_fp4 and runs 16 NB MFMAs.
 //
 // Weight layouts (template W): the store's raw and PS4 slots (row r: 1,440 code bytes, then a raw 90-byte or PS4
 // 46-byte scale row; lane (q, n) reads the 16 bytes of group 4t + q of row n, so MFMA j covers elements 8j..8j+7 of
@@ -235,12 +239,45 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemm_grouped(const uint8_t* __res
 // pairs by expert (order[offs[e] + i] = the i-th pair of expert e in increasing p) and a tile table
 // tiles[i] = (expert, first sorted position, rows <= 64), ntiles.  Invalid ids are in no expert's list and
 // contribute +0 (the combine skips them).
+// Quantised row ("q row", kQRow bytes): hi codes [0, 2880), lo codes [2880, 5760), hi scales [5760, 5856) and lo
+// scales [5856, 5952), scale bytes 90..95 of each half zero (the last k-tile's groups 90, 91 are padding).
+constexpr int kQRow = 2 * kH + 2 * kX8ScPitch;        // 5,952
+constexpr int kQLo = kH;
+constexpr int kQSh = 2 * kH;
+constexpr int kQSl = 2 * kH + kX8ScPitch;
+
 struct PTile {
   int e, p0, cnt, pad;
 };
 
-__global__ __launch_bounds__(256) void k_prefill_count(const int64_t* __restrict__ ids, int P,
-                                                       int* __restrict__ counts) {
+// Blocks 0..127: counts[e] = pairs routed to expert e.  Blocks 128..: x quantised into q rows, one 8-element chunk
+// per thread (4 consecutive threads = one 32-element block; 360 chunks per row, so a block never straddles rows).
+__global__ __launch_bounds__(256) void k_prefill_count(const int64_t* __restrict__ ids, int P, int* __restrict__ counts,
+                                                       const uint16_t* __restrict__ x, int T, uint8_t* __restrict__ xq) {
+  if (blockIdx.x >= 128) {
+    const long long g = (long long)(blockIdx.x - 128) * 256 + threadIdx.x;
+    const bool ok = g < (long long)T * kChunks;
+    const long long row = ok ? g / kChunks : 0;
+    const int c = ok ? (int)(g - row * kChunks) : 0;
+    const uint4 v = ok ? *reinterpret_cast<const uint4*>(x + row * kH + 8 * c) : make_uint4(0, 0, 0, 0);
+    uint2 hi, lo;
+    uint32_t sh, sl;
+    x8_quant_chunk(v, hi, lo, sh, sl);
+    if (ok) {
+      uint8_t* dst = xq + row * kQRow;
+      *reinterpret_cast<uint2*>(dst + 8 * c) = hi;
+      *reinterpret_cast<uint2*>(dst + kQLo + 8 * c) = lo;
+      if ((c & 3) == 0) {
+        dst[kQSh + (c >> 2)] = (uint8_t)sh;
+        dst[kQSl + (c >> 2)] = (uint8_t)sl;
+      }
+      if (c < kX8ScPitch - kGK) {
+        dst[kQSh + kGK + c] = 0;
+        dst[kQSl + kGK + c] = 0;
+      }
+    }
+    return;
+  }
   const int e = blockIdx.x;
   __shared__ int part[4];
   int c = 0;
@@ -291,21 +328,225 @@ __global__ __launch_bounds__(256) void k_prefill_order(const int64_t* __restrict
   }
 }
 
-// gate_up + bias + clamped SwiGLU: tile i, column group a.  Wave w owns intermediate blocks jb, jb + 1
-// (jb = 8 a + 2 w; columns 16 jb .. 16 jb + 31) and reads their gate rows (blocks jb, jb + 1) and up rows (blocks
-// 180 + jb, 181 + jb), so the SwiGLU pairs registers of one lane.  h rows are in sorted pair order: h[p0 + m][j].
-// grid (max tiles, 23); in the last column group waves 2 and 3 have no blocks.
+// ---------------------------------------------------------------- block-scaled products of the fused layer
+// The layer's two GEMMs run on v_mfma_scale_f32_16x16x128_f8f6f4 with the E2M1 codes and E8M0 scales as stored (B)
+// and the activations as two exact E4M3 rows (A: hi and lo, one E8M0 scale per 32-element block each; the exactness
+// argument is the one of x8_quant_chunk in t950.h).  Each k-tile of 128 elements is one MFMA per (16 tokens, 16 weight
+// rows) and activation row (hi, lo): the hi + lo products are the reference's bf16 x E2M1 products, accumulated in
+// fp32.  Activations are quantised once per row, not per workgroup: x per token by the first launch, h per sorted pair
+// by the gate_up epilogue.
+//
+constexpr int kQPitch = 2 * kPKT + 16;                 // LDS bytes per staged row: hi 128 | lo 128 | pad 16
+constexpr int kQStage = kPBM * kQPitch + kPBM * 8;     // one k-tile: 64 rows, then 8 scale bytes per row
+constexpr int kGuSlots = 3;                            // gate_up: 23 column groups over 8 XCDs, 3 per XCD
+constexpr int kDnSlots = 2;                            // down: 15 column groups, 2 per XCD
+
+// Staging of one k-tile of 64 q rows: pieces of 16 B, thread tid owns piece (tid & 15) of rows (tid >> 4) + 16 i
+// (pieces 0..7 hi, 8..15 lo); threads 0..63 also own the 4 hi and 4 lo scale bytes of row tid, stored interleaved
+// (hi g, lo g) per group g of the k-tile.
+struct QStage {
+  uint4 v[4];
+  uint2 s;
+};
+
+NA_DEVICE void q_load(const uint8_t* const (&rp)[4], const uint8_t* srow, int t, int tid, QStage& a) {
+  const int c16 = tid & 15, e0 = t * kPKT + 16 * (c16 & 7), half = (c16 >> 3) * kQLo;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    a.v[i] = e0 < kH ? *reinterpret_cast<const uint4*>(rp[i] + half + e0) : make_uint4(0, 0, 0, 0);
+  if (tid < 64) {
+    a.s.x = *reinterpret_cast<const uint32_t*>(srow + kQSh + 4 * t);
+    a.s.y = *reinterpret_cast<const uint32_t*>(srow + kQSl + 4 * t);
+  }
+}
+
+NA_DEVICE void q_store(uint8_t* buf, int tid, const QStage& a) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    *reinterpret_cast<uint4*>(buf + ((tid >> 4) + 16 * i) * kQPitch + 16 * (tid & 15)) = a.v[i];
+  if (tid < 64)                                        // interleaved at the store, so the loads are not waited on early
+    *reinterpret_cast<uint2*>(buf + kPBM * kQPitch + 8 * tid) =
+        make_uint2(__byte_perm(a.s.x, a.s.y, 0x5140), __byte_perm(a.s.x, a.s.y, 0x7362));
+}
+
+// FP4 B operand of k-tile t in the MFMA order (lane 16 kb + n: the 16 code bytes of group 4t + kb of row n), groups
+// beyond K zeroed.  The raw and PS4 loads already are in that order; the t950 tiles are transposed across the lanes.
 template <int W>
-__global__ __launch_bounds__(256) void k_prefill_gate_up(
-    const uint16_t* __restrict__ x, const int* __restrict__ order, const PTile* __restrict__ tiles,
+NA_DEVICE mfma_i32x8_t w_operand8(uint4 c, int t, int lane) {
+  if constexpr (W == kWT950) {
+    if (t == kTFull) {                                 // half tile: the lane's 8 bytes are groups 88, 89
+      c.z = 0;
+      c.w = 0;
+    }
+    tile_to_mfma_b(c.x, c.y, c.z, c.w);
+  } else {
+    if (4 * t + (lane >> 4) >= kGK) c = make_uint4(0, 0, 0, 0);
+  }
+  return mfma_i32x8_t{(int)c.x, (int)c.y, (int)c.z, (int)c.w, 0, 0, 0, 0};
+}
+
+constexpr int kWScBytes = kTRows * kTScalePitch;      // 1,536 E8M0 bytes of one t950 row block
+
+// One wave's weight stream over its NB row blocks.  t950: the code bytes of a k-tile per load (the E8M0 rows of the
+// blocks are staged once in the wave's LDS area wsc and read per k-tile from there); raw / PS4: codes and the lane's
+// scale per load.
+template <int W, int NB>
+struct WStream {
+  WSrc src;
+  const int* blk;
+  const uint8_t* wsc;
+  int lane;
+
+  NA_DEVICE void load(int t, uint4 (&c)[NB], uint32_t (&sc)[NB]) const {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      if constexpr (W == kWT950) {
+        const uint8_t* bk = src.codes + (long long)blk[nb] * kTBlock;
+        c[nb] = load16(bk + (t < kTFull ? t * 1024 + 16 * lane : kTFull * 1024 + 8 * lane));
+        sc[nb] = 0;
+      } else {
+        w_load<W>(src, blk[nb], t, lane, c[nb], sc[nb]);
+      }
+    }
+  }
+  NA_DEVICE int scale(int t, int nb, uint32_t sc) const {
+    if constexpr (W == kWT950)
+      return wsc[nb * kWScBytes + (lane & 15) * kTScalePitch + 4 * t + (lane >> 4)];
+    else
+      return (int)(sc & 0xff);
+  }
+};
+
+// One k-tile of gemm8_tile.  A of k-tile t is staged in LDS at cur and the weights of k-tile t are in (c, sc).  It
+// issues the loads of A of k-tile t + 2 (into a_in) and of the weights of k-tile t + 2 (into (c2, sc2)), runs the
+// MFMAs, stores A of k-tile t + 1 (loaded one step earlier, a_out) at nxt and meets the barrier.
+template <int W, int NB>
+NA_DEVICE void gemm8_step(int t, const WStream<W, NB>& ws, bool live, const uint8_t* const (&rp)[4],
+                          const uint8_t* srow, const uint8_t* cur, uint8_t* nxt, const QStage& a_out, QStage& a_in,
+                          const uint4 (&c)[NB], const uint32_t (&sc)[NB], uint4 (&c2)[NB], uint32_t (&sc2)[NB],
+                          f32x4_t (&acc)[4][NB]) {
+  const int tid = threadIdx.x, lane = tid & 63, kb = lane >> 4, m = lane & 15;
+  if (t + 2 < kPTiles) {
+    q_load(rp, srow, t + 2, tid, a_in);
+    ws.load(t + 2, c2, sc2);
+  }
+  if (live) {
+    mfma_i32x8_t b[NB];
+    int sb[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      b[nb] = w_operand8<W>(c[nb], t, lane);
+      sb[nb] = ws.scale(t, nb, sc[nb]);
+    }
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const uint8_t* row = cur + (16 * tt + m) * kQPitch + 16 * kb;
+      const uint4 h0 = *reinterpret_cast<const uint4*>(row), h1 = *reinterpret_cast<const uint4*>(row + 64);
+      const uint4 l0 = *reinterpret_cast<const uint4*>(row + 128), l1 = *reinterpret_cast<const uint4*>(row + 192);
+      const uint32_t s2 = *reinterpret_cast<const uint16_t*>(cur + kPBM * kQPitch + (16 * tt + m) * 8 + 2 * kb);
+      const int sh = (int)(s2 & 0xff), sl = (int)(s2 >> 8);
+      const mfma_i32x8_t ah = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+      const mfma_i32x8_t al = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        acc[tt][nb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ah, b[nb], acc[tt][nb], 0, 4, 0, sh, 0, sb[nb]);
+        acc[tt][nb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(al, b[nb], acc[tt][nb], 0, 4, 0, sl, 0, sb[nb]);
+      }
+    }
+  }
+  // The MFMAs are issued before the LDS stores, which wait for their k-tile's loads: an empty asm that takes every
+  // accumulator (and orders memory) keeps the compiler from sinking the MFMAs below those stores.
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) asm volatile("" : "+v"(acc[tt][nb])::"memory");
+  if (t + 1 < kPTiles) q_store(nxt, tid, a_out);
+  __syncthreads();
+}
+
+// acc[tt][nb] = D of tokens 16 tt .. 16 tt + 15 x row block blk[nb] (lane (q, n): tokens 16 tt + 4 q + r, row n),
+// over the 23 k-tiles.  rp[i]: q row of staged row (tid >> 4) + 16 i; srow: q row of staged row tid & 63.  Both
+// operand streams run two k-tiles ahead of the MFMAs: the activations through three LDS buffers of a k-tile (64 rows'
+// 256 code bytes and 8 scale bytes each, loaded into registers two steps before and stored one step before their
+// use), each wave's weight codes through three register sets; the k-loop is unrolled by 3 so that every buffer and
+// register set is fixed at compile time.  Each wave reads one token tile's hi and lo fragments at a time and feeds
+// them to its NB row blocks.  lds: 3 x kQStage bytes; wsc: this wave's LDS area of NB x 1,536 bytes (t950 scale
+// rows).  A wave without work (live = false) stages and meets every barrier but runs no MFMA.  All 256 threads must
+// call it.
+template <int W, int NB>
+NA_DEVICE void gemm8_tile(const WSrc& src, const int (&blk)[NB], bool live, const uint8_t* const (&rp)[4],
+                          const uint8_t* srow, uint8_t* lds, uint8_t* wsc, f32x4_t (&acc)[4][NB]) {
+  const int tid = threadIdx.x, lane = tid & 63;
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[tt][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const WStream<W, NB> ws{src, blk, wsc, lane};
+  if constexpr (W == kWT950) {                         // the blocks' E8M0 rows: 96 pieces of 16 B each
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const uint8_t* sp = src.codes + (long long)blk[nb] * kTBlock + kTCodes;
+      const uint4 v0 = load16(sp + 16 * lane);
+      *reinterpret_cast<uint4*>(wsc + nb * kWScBytes + 16 * lane) = v0;
+      if (lane < kWScBytes / 16 - 64) {
+        const uint4 v1 = load16(sp + 1024 + 16 * lane);
+        *reinterpret_cast<uint4*>(wsc + nb * kWScBytes + 1024 + 16 * lane) = v1;
+      }
+    }
+  }
+  uint8_t* const b0 = lds;
+  uint8_t* const b1 = lds + kQStage;
+  uint8_t* const b2 = lds + 2 * kQStage;
+  uint4 c0[NB], c1[NB], c2[NB];
+  uint32_t s0[NB], s1[NB], s2[NB];
+  QStage a0, a1, a2;                                   // a_k: A of the k-tiles = k (mod 3) while in flight
+  q_load(rp, srow, 0, tid, a0);
+  ws.load(0, c0, s0);
+  q_load(rp, srow, 1, tid, a1);
+  ws.load(1, c1, s1);
+  q_store(b0, tid, a0);
+  __syncthreads();
+  int t = 0;
+  for (; t + 3 <= kPTiles; t += 3) {                   // k-tiles 0 .. 20
+    gemm8_step<W, NB>(t, ws, live, rp, srow, b0, b1, a1, a2, c0, s0, c2, s2, acc);
+    gemm8_step<W, NB>(t + 1, ws, live, rp, srow, b1, b2, a2, a0, c1, s1, c0, s0, acc);
+    gemm8_step<W, NB>(t + 2, ws, live, rp, srow, b2, b0, a0, a1, c2, s2, c1, s1, acc);
+  }
+  gemm8_step<W, NB>(t, ws, live, rp, srow, b0, b1, a1, a2, c0, s0, c2, s2, acc);       // 21
+  gemm8_step<W, NB>(t + 1, ws, live, rp, srow, b1, b2, a2, a0, c1, s1, c0, s0, acc);   // 22
+}
+
+// Workgroup b -> (tile, column group): the dispatcher deals workgroups to the 8 XCDs in turn (XCD b % 8), so XCD x
+// is given column groups slots * x .. slots * x + slots - 1 of every tile, tiles in order.  Each XCD's L2 then holds
+// the weight rows of its few column groups while the tiles of one expert pass through it, and every weight byte
+// crosses from HBM about once.
+template <int SLOTS>
+NA_DEVICE void xcd_tile(int b, int& tile, int& col) {
+  const int s = b >> 3;
+  tile = s / SLOTS;
+  col = SLOTS * (b & 7) + s % SLOTS;
+}
+
+// gate_up + bias + clamped SwiGLU on the block-scaled MFMA: tile i, column group y (128 intermediate columns).
+// Wave w owns intermediate blocks jb, jb + 1 (jb = 8 y + 2 w) and reads their gate rows (blocks jb, jb + 1) and up
+// rows (blocks 180 + jb, 181 + jb), so the SwiGLU pairs registers of one lane.  x rows come quantised (xq, one q row
+// per token) and are gathered through the pair order; h leaves as q rows in sorted pair order, each 32-column block
+// (one wave's columns of one row) with its own E8M0 scales.  Grid: max tiles x 24 (xcd_tile<3>); in column group 22
+// waves 2 and 3 have no blocks.
+template <int W>
+__global__ __launch_bounds__(256, 2) void k_prefill_gate_up(
+    const uint8_t* __restrict__ xq, const int* __restrict__ order, const PTile* __restrict__ tiles,
     const int* __restrict__ ntiles, const uint8_t* __restrict__ pool, long long slot_bytes,
     const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ bias_gu,
-    uint16_t* __restrict__ h, float alpha, float limit) {
-  __shared__ __align__(16) uint8_t lds_a[2 * kPBM * kPApitch];
-  if ((int)blockIdx.x >= *ntiles) return;
-  const PTile tl = tiles[blockIdx.x];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q = lane >> 4, n = lane & 15;
-  const int jb = 8 * blockIdx.y + 2 * wave;
+    uint8_t* __restrict__ hq, float alpha, float limit) {
+  __shared__ __align__(16) uint8_t lds[3 * kQStage + 4 * 4 * kWScBytes];
+  int ti, y;
+  xcd_tile<kGuSlots>(blockIdx.x, ti, y);
+  if (ti >= *ntiles || y >= 23) return;
+  const PTile tl = tiles[ti];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, q = lane >> 4,
+            n = lane & 15;
+  const int jb = 8 * y + 2 * wave;
   const bool live = jb < kTUpBlock0;
   const int jl = live ? jb : 0;
   const int blk[4] = {jl, jl + 1, kTUpBlock0 + jl, kTUpBlock0 + jl + 1};
@@ -313,58 +554,123 @@ __global__ __launch_bounds__(256) void k_prefill_gate_up(
   const long long slot = slot_tab ? slot_tab[gid] : gid;
   const uint8_t* sb = pool + slot * slot_bytes;
   const WSrc src = W == kWT950 ? WSrc{sb, nullptr} : WSrc{sb, sb + kOffGateScales};
-  f32x4_t acc[4][4];
-  gemm_tile<W, 4>(src, blk, live,
-                  [=](int row) { return x + (long long)(order[tl.p0 + min(row, tl.cnt - 1)] >> 2) * kH; }, lds_a,
-                  acc);
-  if (!live) return;
-  // gu = bf16(acc) + bias (bf16 rounding of each op, as the reference's torch ops), then the clamped SwiGLU
-  const uint16_t* bg = bias_gu ? bias_gu + gid * kGU : nullptr;
+  const uint8_t* rp[4];
 #pragma unroll
-  for (int hb = 0; hb < 2; ++hb) {
-    const int j = 16 * (jl + hb) + n;
-    const float bgv = bg ? bf16_to_f32(bg[j]) : 0.f, buv = bg ? bf16_to_f32(bg[kI + j]) : 0.f;
+  for (int i = 0; i < 4; ++i)
+    rp[i] = xq + (long long)(order[tl.p0 + min((tid >> 4) + 16 * i, tl.cnt - 1)] >> 2) * kQRow;
+  const uint8_t* srow = xq + (long long)(order[tl.p0 + min(tid & 63, tl.cnt - 1)] >> 2) * kQRow;
+  f32x4_t acc[4][4];
+  gemm8_tile<W, 4>(src, blk, live, rp, srow, lds, lds + 3 * kQStage + wave * 4 * kWScBytes, acc);
+  // h = bf16(SwiGLU(bf16(acc) + bias)) (the reference's bf16 rounding points), quantised per (row, 32-column block)
+  // into LDS: oh[row] = hi codes of the workgroup's 128 columns | lo codes, os[row] = 4 hi | 4 lo scale bytes.
+  uint8_t* oh = lds;
+  uint8_t* os = lds + kPBM * 2 * kPKT;
+  if (live) {
+    const uint16_t* bg = bias_gu ? bias_gu + gid * kGU : nullptr;
+    float bgv[2], buv[2];
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      const int j = 16 * (jl + hb) + n;
+      bgv[hb] = bg ? bf16_to_f32(bg[j]) : 0.f;
+      buv[hb] = bg ? bf16_to_f32(bg[kI + j]) : 0.f;
+    }
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = 16 * tt + 4 * q + r;
-        float g = rb(acc[tt][hb][r]), u = rb(acc[tt][2 + hb][r]);
-        if (bg) {
-          g = rb(g + bgv);
-          u = rb(u + buv);
+        float hv[2];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+          float g = rb(acc[tt][hb][r]), u = rb(acc[tt][2 + hb][r]);
+          if (bg) {
+            g = rb(g + bgv[hb]);
+            u = rb(u + buv[hb]);
+          }
+          hv[hb] = rb(swiglu_clamp_bf16(g, u, alpha, limit));
         }
-        const uint16_t hv = f32_to_bf16(swiglu_clamp_bf16(g, u, alpha, limit));
-        const uint32_t hi = (uint32_t)__shfl_xor((int)hv, 1) & 0xffff;
-        if (m < tl.cnt && !(n & 1))
-          *reinterpret_cast<uint32_t*>(h + (long long)(tl.p0 + m) * kI + j) = (uint32_t)hv | (hi << 16);
+        float mx = fmaxf(fabsf(hv[0]), fabsf(hv[1]));
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const uint32_t sh = x8_scale_byte(mx);
+        const float s_hi = e8m0_f32(sh);
+        fp8x2_t o2 = {0, 0};
+        o2 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o2, hv[0], hv[1], s_hi, false);
+        const uint32_t hc = __builtin_bit_cast(uint32_t, o2);
+        const auto d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hc, s_hi, false);
+        const float r0 = hv[0] - d[0], r1 = hv[1] - d[1];
+        float mr = fmaxf(fabsf(r0), fabsf(r1));
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) mr = fmaxf(mr, __shfl_xor(mr, o));
+        const uint32_t sl = x8_scale_byte(mr);
+        fp8x2_t l2 = {0, 0};
+        l2 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(l2, r0, r1, e8m0_f32(sl), false);
+        const uint32_t lc = __builtin_bit_cast(uint32_t, l2);
+        const int row = 16 * tt + 4 * q + r, c = 32 * wave + n;
+        oh[row * 2 * kPKT + c] = (uint8_t)hc;
+        oh[row * 2 * kPKT + c + 16] = (uint8_t)(hc >> 8);
+        oh[row * 2 * kPKT + kPKT + c] = (uint8_t)lc;
+        oh[row * 2 * kPKT + kPKT + c + 16] = (uint8_t)(lc >> 8);
+        if (n == 0) {
+          os[row * 8 + wave] = (uint8_t)sh;
+          os[row * 8 + 4 + wave] = (uint8_t)sl;
+        }
       }
+  }
+  __syncthreads();
+  // q rows out: 16-byte pieces of the valid columns (64 in column group 22), scale bytes 4 y .. 4 y + 3 (group 22:
+  // bytes 88, 89 and the zero padding 90..95).
+  const int ncol = y == 22 ? 64 : 128;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int pc = tid + 256 * i, row = pc >> 4, c16 = pc & 15, c8 = c16 & 7;
+    if (row < tl.cnt && 16 * c8 < ncol)
+      *reinterpret_cast<uint4*>(hq + (long long)(tl.p0 + row) * kQRow + (c16 >> 3) * kQLo + kPKT * y + 16 * c8) =
+          *reinterpret_cast<const uint4*>(oh + row * 2 * kPKT + 16 * c16);
+  }
+  if (tid < tl.cnt && tid < kPBM) {
+    uint8_t* dst = hq + (long long)(tl.p0 + tid) * kQRow;
+    const uint32_t sh4 = *reinterpret_cast<const uint32_t*>(os + tid * 8);
+    const uint32_t sl4 = *reinterpret_cast<const uint32_t*>(os + tid * 8 + 4);
+    if (y < 22) {
+      *reinterpret_cast<uint32_t*>(dst + kQSh + 4 * y) = sh4;
+      *reinterpret_cast<uint32_t*>(dst + kQSl + 4 * y) = sl4;
+    } else {
+      *reinterpret_cast<uint2*>(dst + kQSh + 88) = make_uint2(sh4 & 0xffff, 0);
+      *reinterpret_cast<uint2*>(dst + kQSl + 88) = make_uint2(sl4 & 0xffff, 0);
+    }
   }
 }
 
 // down + bias, x routing weight, scattered back to pair order: ys[p][n] = bf16(bf16(bf16(y) + b) * w[p]) with p the
-// pair of sorted position p0 + m.  grid (max tiles, 15); wave w: row blocks 12 y + 3 w + i.
+// pair of sorted position p0 + m.  A = the h q rows of the tile (consecutive sorted positions).  Grid: max tiles x 16
+// (xcd_tile<2>); wave w: row blocks 12 y + 3 w + i.
 template <int W>
-__global__ __launch_bounds__(256) void k_prefill_down(
-    const uint16_t* __restrict__ h, const int* __restrict__ order, const PTile* __restrict__ tiles,
+__global__ __launch_bounds__(256, 2) void k_prefill_down(
+    const uint8_t* __restrict__ hq, const int* __restrict__ order, const PTile* __restrict__ tiles,
     const int* __restrict__ ntiles, const uint16_t* __restrict__ wts, const uint8_t* __restrict__ pool,
     long long slot_bytes, const int64_t* __restrict__ slot_tab, long long expert_base,
     const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ ys) {
-  __shared__ __align__(16) uint8_t lds_a[2 * kPBM * kPApitch];
-  if ((int)blockIdx.x >= *ntiles) return;
-  const PTile tl = tiles[blockIdx.x];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q = lane >> 4, n = lane & 15;
+  __shared__ __align__(16) uint8_t lds[3 * kQStage + 4 * kPNB * kWScBytes];
+  int ti, y;
+  xcd_tile<kDnSlots>(blockIdx.x, ti, y);
+  if (ti >= *ntiles || y >= kH / kPRows) return;
+  const PTile tl = tiles[ti];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, q = lane >> 4,
+            n = lane & 15;
   int blk[kPNB];
 #pragma unroll
-  for (int i = 0; i < kPNB; ++i) blk[i] = blockIdx.y * (4 * kPNB) + kPNB * wave + i;
+  for (int i = 0; i < kPNB; ++i) blk[i] = y * (4 * kPNB) + kPNB * wave + i;
   const long long gid = expert_base + tl.e;
   const long long slot = slot_tab ? slot_tab[gid] : gid;
   const uint8_t* sb = pool + slot * slot_bytes;
   const WSrc src = W == kWT950 ? WSrc{sb + kTDownOff, nullptr}
                                : WSrc{sb + kOffDownCodes, sb + kOffGateScales + (long long)kGU * (W == kWRaw ? kGK : kPs4Row)};
+  const uint8_t* rp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) rp[i] = hq + (long long)(tl.p0 + min((tid >> 4) + 16 * i, tl.cnt - 1)) * kQRow;
+  const uint8_t* srow = hq + (long long)(tl.p0 + min(tid & 63, tl.cnt - 1)) * kQRow;
   f32x4_t acc[4][kPNB];
-  gemm_tile<W, kPNB>(src, blk, true, [=](int row) { return h + (long long)(tl.p0 + min(row, tl.cnt - 1)) * kI; },
-                     lds_a, acc);
+  gemm8_tile<W, kPNB>(src, blk, true, rp, srow, lds, lds + 3 * kQStage + wave * kPNB * kWScBytes, acc);
   int pr[4][4];                                       // pair of each of the lane's 16 tokens
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt)
@@ -380,9 +686,9 @@ __global__ __launch_bounds__(256) void k_prefill_down(
       for (int r = 0; r < 4; ++r) {
         const int m = 16 * tt + 4 * q + r;
         const int p = pr[tt][r];
-        float y = rb(acc[tt][nb][r]);
-        if (bias_dn) y = rb(y + bd);
-        const uint16_t v = f32_to_bf16(y * bf16_to_f32(wts[p]));
+        float yv = rb(acc[tt][nb][r]);
+        if (bias_dn) yv = rb(yv + bd);
+        const uint16_t v = f32_to_bf16(yv * bf16_to_f32(wts[p]));
         const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
         if (m < tl.cnt && !(n & 1))
           *reinterpret_cast<uint32_t*>(ys + (long long)p * kH + 16 * blk[nb] + n) = (uint32_t)v | (hi << 16);
@@ -410,7 +716,7 @@ __global__ __launch_bounds__(256) void k_prefill_combine(const uint32_t* __restr
 
 // Workspace of the fused prefill layer for T tokens (P = 4 T pairs): byte offsets, 256-aligned.
 struct PrefillWs {
-  long long counts, ntiles, order, tiles, h, ys, total;
+  long long counts, ntiles, order, tiles, xq, h, ys, total;
   int max_tiles;
 };
 
@@ -424,8 +730,9 @@ static PrefillWs prefill_ws(int T) {
   w.ntiles = 512;
   w.order = 1024;
   w.tiles = align256(w.order + P * 4);
-  w.h = align256(w.tiles + (long long)w.max_tiles * sizeof(PTile));
-  w.ys = align256(w.h + P * kI * 2);
+  w.xq = align256(w.tiles + (long long)w.max_tiles * sizeof(PTile));
+  w.h = align256(w.xq + (long long)T * kQRow);
+  w.ys = align256(w.h + P * kQRow);
   w.total = align256(w.ys + P * kH * 2);
   return w;
 }
@@ -467,21 +774,24 @@ int na_moe_prefill(const void* x, const int64_t* topk_ids, const void* topk_w, i
   int* ntiles = (int*)(ws + w.ntiles);
   int* order = (int*)(ws + w.order);
   PTile* tiles = (PTile*)(ws + w.tiles);
-  uint16_t* h = (uint16_t*)(ws + w.h);
+  uint8_t* xq = ws + w.xq;
+  uint8_t* hq = ws + w.h;
   uint16_t* ys = (uint16_t*)(ws + w.ys);
   hipEvent_t ev[10] = {};
   if (events)
     for (int i = 0; i < 10; ++i) ev[i] = (hipEvent_t)events[i];
   const int P = 4 * T;
-  launch_p(k_prefill_count, dim3(128), dim3(256), stream, ev[0], ev[1], topk_ids, P, counts);
+  const long long qblocks = ((long long)T * kChunks + 255) / 256;
+  launch_p(k_prefill_count, dim3((unsigned)(128 + qblocks)), dim3(256), stream, ev[0], ev[1], topk_ids, P, counts,
+           (const uint16_t*)x, T, xq);
   launch_p(k_prefill_order, dim3(128), dim3(256), stream, ev[2], ev[3], topk_ids, P, (const int*)counts, order, tiles,
            ntiles);
-  const dim3 gg(w.max_tiles, (kTUpBlock0 + 7) / 8), gd(w.max_tiles, kH / kPRows), blk(256);
+  const dim3 gg(w.max_tiles * 8 * kGuSlots), gd(w.max_tiles * 8 * kDnSlots), blk(256);
 #define NA_PREFILL_GEMMS(W)                                                                                          \
-  launch_p(k_prefill_gate_up<W>, gg, blk, stream, ev[4], ev[5], (const uint16_t*)x, (const int*)order,                \
+  launch_p(k_prefill_gate_up<W>, gg, blk, stream, ev[4], ev[5], (const uint8_t*)xq, (const int*)order,                \
            (const PTile*)tiles, (const int*)ntiles, (const uint8_t*)pool, slot_bytes, slot_tab, expert_base,          \
-           (const uint16_t*)bias_gu, h, alpha, limit);                                                                 \
-  launch_p(k_prefill_down<W>, gd, blk, stream, ev[6], ev[7], (const uint16_t*)h, (const int*)order,                   \
+           (const uint16_t*)bias_gu, hq, alpha, limit);                                                                \
+  launch_p(k_prefill_down<W>, gd, blk, stream, ev[6], ev[7], (const uint8_t*)hq, (const int*)order,                    \
            (const PTile*)tiles, (const int*)ntiles, (const uint16_t*)topk_w, (const uint8_t*)pool, slot_bytes,        \
            slot_tab, expert_base, (const uint16_t*)bias_dn, ys);
   if (layout == kWT950) {

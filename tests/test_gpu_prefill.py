@@ -156,10 +156,10 @@ def test_forward_prefill_matches_oracle(layout):
         _close(got[t], mo.combine_bf16(np.stack(ys), w[t]), f"{layout} token {t}")
 
 
-def test_prefill_raw_equals_ps4_bitwise():
+def test_prefill_raw_equals_ps4_equals_t950_bitwise():
     import torch
     from neural_amd.moe.experts import ResidentExperts
-    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4
+    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4, GPTOSS_LAYOUT_T950
     dev = _dev()
     rng = np.random.default_rng(77)
     slots = [synth.slot_raw(rng) for _ in range(5)]
@@ -172,4 +172,8 @@ def test_prefill_raw_equals_ps4_bitwise():
     for packed, L in ((False, GPTOSS_LAYOUT), (True, GPTOSS_LAYOUT_PS4)):
         rx = ResidentExperts(_pool(slots, packed, dev), L, None, None, tab)
         outs.append(rx.forward_prefill(11, x, idd, wd))
+    t950 = torch.empty((5, tiles.SLOT_T950), dtype=torch.uint8, device=dev)
+    tiles.repack_to_t950(_pool(slots, False, dev), t950)
+    outs.append(ResidentExperts(t950, GPTOSS_LAYOUT_T950, None, None, tab).forward_prefill(11, x, idd, wd))
     assert torch.equal(outs[0], outs[1])
+    assert torch.equal(outs[0], outs[2]), "the t950 tiles feed the MFMA the same operands as the raw rows"
