@@ -166,7 +166,8 @@ def swiglu_clamp_bf16(gu: np.ndarray, alpha=ACT_ALPHA, limit=ACT_LIMIT) -> np.nd
     gate = np.minimum(gu[..., :i], np.float32(limit))
     up = np.clip(gu[..., i:], np.float32(-limit), np.float32(limit))
     t = rb(gate * np.float32(alpha))
-    s = rb((1.0 / (1.0 + np.exp(-t.astype(np.float64)))).astype(np.float32))
+    with np.errstate(over="ignore"):                  # exp(-t) = inf for t < -709 gives sigmoid 0, as it should
+        s = rb((1.0 / (1.0 + np.exp(-t.astype(np.float64)))).astype(np.float32))
     glu = rb(gate * s)
     return rb(rb(up + np.float32(1.0)) * glu)
 

@@ -177,3 +177,56 @@ def test_prefill_raw_equals_ps4_equals_t950_bitwise():
     outs.append(ResidentExperts(t950, GPTOSS_LAYOUT_T950, None, None, tab).forward_prefill(11, x, idd, wd))
     assert torch.equal(outs[0], outs[1])
     assert torch.equal(outs[0], outs[2]), "the t950 tiles feed the MFMA the same operands as the raw rows"
+
+
+def test_forward_prefill_wide_range_rows_match_oracle():
+    """Activation rows scaled by 2^-30 .. 2^30 (the E8M0 scales of the quantised x and h rows follow each row's own
+    magnitude), a zero row, a row with one non-zero element, and elements spanning 2^-12 of their block's maximum:
+    every output within 2 bf16 ulps of the oracle's for 99 % of the elements, and none beyond 2^-6 of its row's
+    largest magnitude (the reference's bf16 x E2M1 products are reproduced exactly by the hi + lo rows; the remaining
+    differences are fp32 against fp64 accumulation and the bf16 roundings that follow)."""
+    import torch
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
+    dev = _dev()
+    rng = np.random.default_rng(4242)
+    nslot = 3
+    slots = [synth.slot_raw(rng) for _ in range(nslot)]
+    T = 41
+    x = rng.standard_normal((T, 2880)).astype(np.float32)
+    x *= np.exp2(np.arange(T) - 20.0 + (np.arange(T) % 3) * 5 - 5)[:, None]
+    x[:, 5::32] *= 2.0 ** -12                           # elements far below their block's maximum
+    x[7] = 0.0
+    x[11] = 0.0
+    x[11, 1234] = 3.5
+    x = rb(x)
+    xt = torch.from_numpy(x).to(torch.bfloat16)
+    ids, w = _routing(rng, T, nexp=128, invalid=False)
+    n = 36 * 128
+    tab = (np.arange(n) % nslot).astype(np.int64)
+    raw = _pool(slots, False, dev)
+    pool = torch.empty((nslot, tiles.SLOT_T950), dtype=torch.uint8, device=dev)
+    tiles.repack_to_t950(raw, pool)
+    rx = ResidentExperts(pool, GPTOSS_LAYOUT_T950, None, None, torch.from_numpy(tab).to(dev))
+    layer = 2
+    print(f"case forward_prefill wide range T={T}", flush=True)
+    got = rx.forward_prefill(layer, xt.to(dev), torch.from_numpy(ids).to(dev),
+                             torch.from_numpy(w).to(torch.bfloat16).to(dev)).float().cpu().numpy()
+    assert np.isfinite(got).all()
+    cache = {}
+    zb = np.zeros(5760, np.float32), np.zeros(2880, np.float32)
+    within, total = 0, 0
+    for t in list(range(0, T, 4)) + [7, 11, T - 1]:
+        ys = []
+        for k in range(4):
+            s = int(tab[layer * 128 + int(ids[t, k])])
+            if s not in cache:
+                cache[s] = mo.expert_weights(slots[s])
+            ys.append(mo.expert_forward_bf16(x[t:t + 1], None, zb[0], zb[1], weights=cache[s])[0])
+        want = mo.combine_bf16(np.stack(ys), w[t])
+        d = np.abs(got[t] - want)
+        ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 1e-38))) - 7)
+        within += int((d <= 2 * ulp).sum())
+        total += d.size
+        assert d.max() <= 2.0 ** -6 * np.abs(want).max() + 1e-30, (t, d.max(), np.abs(want).max())
+    assert within >= 0.99 * total, (within, total)
