@@ -7,17 +7,12 @@
 // E2M1 codes and E8M0 scales as stored, activations as two exact E4M3 rows (hi, lo) with one E8M0 scale per 32
 // elements each, so hi w + lo w are the reference's bf16 x E2M1 products; see the block-scaled section below.
 //
-// The plain and grouped GEMM entry points take bf16 activations without a workspace and run on
-// v_mfma_f32_16x16x32_bf16: workgroup tile 64 tokens x (4 waves x 3 row blocks of 16 weight rows), K walked in k-tiles
-// of 4 groups (128 elements); per k-tile the workgroup stages the 64 x 128 activation tile in LDS (double buffered,
-// gathered through a row map), each wave loads its blocks' codes and scales (next k-tile in flight while the current
-// one computes), reads its 16 A fragments once, dequantises each block's codes in registers with
-// v_cvt_scalef32_pk_bf16_fp4 and runs 16 NB MFMAs.
+// The plain and grouped GEMM entry points (bf16 activations, no workspace) run the same tiles, the activations
+// quantised into hi + lo rows while they are staged.
 //
 // Weight layouts (template W): the store's raw and PS4 slots (row r: 1,440 code bytes, then a raw 90-byte or PS4
-// 46-byte scale row; lane (q, n) reads the 16 bytes of group 4t + q of row n, so MFMA j covers elements 8j..8j+7 of
-// each lane's group) and the t950 tiles (lane (q, n) reads the 16 bytes of its tile: MFMA j covers group 4t + j,
-// elements 8q..8q+7).  The A operand follows the same K mapping, so every product pairs the right x and w.
+// 46-byte scale row; lane (q, n) reads the 16 bytes of group 4t + q of row n, already the MFMA's B order) and the t950
+// tiles (lane (q, n) reads the 16 bytes of its tile, transposed across the lane quarters into the B order).
 #include "common.h"
 #include "t950.h"
 
@@ -29,7 +24,6 @@ enum WLayout : int { kWRaw = 0, kWPs4 = 1, kWT950 = 2 };
 
 constexpr int kPBM = 64;                 // tokens per tile
 constexpr int kPKT = 128;                // K elements per k-tile
-constexpr int kPApitch = kPKT * 2 + 16;  // LDS bytes per staged activation row (padded)
 constexpr int kPTiles = kTTiles;         // 23 k-tiles: 22 full + groups 88, 89
 
 // One matrix (gate_up or down) of one expert, as the kernels address it.
@@ -59,103 +53,7 @@ NA_DEVICE void w_load(const WSrc& s, int rblk, int t, int lane, uint4& c, uint32
       const uint32_t nib = row[1 + (g >> 1)];
       e = row[0] + ((g & 1) ? (nib >> 4) : (nib & 15));
     }
-    sc = e * 0x01010101u;                             // the same scale for the lane's 4 MFMAs
-  }
-}
-
-// B operand of MFMA j from the lane's codes, with the groups beyond K zeroed.
-template <int W>
-NA_DEVICE bf16x8_t w_operand(const uint4& c, uint32_t sc, int t, int j, int lane) {
-  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-  const int q = lane >> 4;
-  const int g = W == kWT950 ? 4 * t + j : 4 * t + q;
-  const uint32_t code = g < kGK ? w[j] : 0u;
-  return dequant8(code, e8m0_f32((sc >> (8 * j)) & 0xff));
-}
-
-// LDS byte offset, within a staged activation row, of the 8 A elements of MFMA j for lane group q.
-template <int W>
-NA_DEVICE int a_offset(int j, int q) {
-  return W == kWT950 ? (32 * j + 8 * q) * 2 : (32 * q + 8 * j) * 2;
-}
-
-// Activation tile staging: piece p = tid + 256 i (i < 4) of the 64 x 16 pieces of 16 bytes; row = p / 16.
-struct AStage {
-  uint4 v[4];
-};
-
-template <typename RowPtr>
-NA_DEVICE void a_load(RowPtr row_ptr, int t, int tid, AStage& a) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int p = tid + 256 * i, row = p >> 4, c16 = p & 15;
-    const int e0 = t * kPKT + 8 * c16;               // first element of the piece
-    a.v[i] = e0 < kH ? *reinterpret_cast<const uint4*>(row_ptr(row) + e0) : make_uint4(0, 0, 0, 0);
-  }
-}
-
-NA_DEVICE void a_store(uint8_t* lds, int tid, const AStage& a) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int p = tid + 256 * i, row = p >> 4, c16 = p & 15;
-    *reinterpret_cast<uint4*>(lds + row * kPApitch + 16 * c16) = a.v[i];
-  }
-}
-
-// acc[tt][nb] = D of token tile tt (tokens 16 tt .. 16 tt + 15) x row block blk[nb] of this wave: lane (q, n)
-// holds tokens 16 tt + 4 q + r, r = 0..3, row n of the block.  Per k-tile the wave reads its 16 A fragments from LDS
-// once and feeds each to NB MFMAs per group (one per row block), so LDS traffic per MFMA falls as 1 / NB.  A wave
-// without work (live = false) still stages activations and meets every barrier; its loads use block blk[0] (valid
-// memory) and it runs no MFMA.  All 256 threads must call it (barriers inside).
-template <int W, int NB, typename RowPtr>
-NA_DEVICE void gemm_tile(const WSrc& src, const int (&blk)[NB], bool live, RowPtr row_ptr,
-                         uint8_t* lds_a /* 2 x 64 x kPApitch */, f32x4_t (&acc)[4][NB]) {
-  const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, n = lane & 15;
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[tt][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  AStage an;
-  uint4 cn[NB];
-  uint32_t sn[NB];
-  a_load(row_ptr, 0, tid, an);
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) w_load<W>(src, blk[nb], 0, lane, cn[nb], sn[nb]);
-  a_store(lds_a, tid, an);
-  __syncthreads();
-  for (int t = 0; t < kPTiles; ++t) {
-    uint4 c[NB];
-    uint32_t sc[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      c[nb] = cn[nb];
-      sc[nb] = sn[nb];
-    }
-    const uint8_t* cur = lds_a + (t & 1) * (kPBM * kPApitch);
-    if (t + 1 < kPTiles) {                           // next k-tile in flight during this one's MFMAs
-      a_load(row_ptr, t + 1, tid, an);
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) w_load<W>(src, blk[nb], t + 1, lane, cn[nb], sn[nb]);
-    }
-    bf16x8_t a[4][4];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        a[tt][j] = *reinterpret_cast<const bf16x8_t*>(cur + (16 * tt + n) * kPApitch + a_offset<W>(j, q));
-    if (live) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bf16x8_t b = w_operand<W>(c[nb], sc[nb], t, j, lane);
-#pragma unroll
-          for (int tt = 0; tt < 4; ++tt)
-            acc[tt][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tt][j], b, acc[tt][nb], 0, 0, 0);
-        }
-    }
-    if (t + 1 < kPTiles) a_store(lds_a + ((t + 1) & 1) * (kPBM * kPApitch), tid, an);
-    __syncthreads();
+    sc = e;
   }
 }
 
@@ -166,72 +64,6 @@ template <int W>
 NA_DEVICE WSrc w_src(const uint8_t* blocks, long long sb_slot, const uint8_t* scales, long long ss_slot,
                      long long slot) {
   return WSrc{blocks + slot * sb_slot, scales ? scales + slot * ss_slot : nullptr};
-}
-
-// ------------------------------------------------------------------------------- plain GEMM (mxfp4_gemm)
-// out[e][m][n] = bf16(sum_k x[m][k] w_e[n][k]); grid (E * ceil(M / 64), N / 192); wave w: row blocks
-// 12 y + 3 w + i.
-NA_DEVICE void store_tile(uint16_t* out_row0, long long pitch, const f32x4_t (&acc)[4][kPNB], const int (&blk)[kPNB],
-                          int m_limit) {
-  const int lane = threadIdx.x & 63, q = lane >> 4, n = lane & 15;
-#pragma unroll
-  for (int nb = 0; nb < kPNB; ++nb)
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = 16 * tt + 4 * q + r;
-        const uint16_t v = f32_to_bf16(acc[tt][nb][r]);
-        const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
-        if (m < m_limit && !(n & 1))
-          *reinterpret_cast<uint32_t*>(out_row0 + (long long)m * pitch + 16 * blk[nb] + n) = (uint32_t)v | (hi << 16);
-      }
-}
-
-template <int W>
-__global__ __launch_bounds__(256) void k_mxfp4_gemm(const uint16_t* __restrict__ x, int M,
-                                                    const uint8_t* __restrict__ blocks, long long sb_slot,
-                                                    const uint8_t* __restrict__ scales, long long ss_slot,
-                                                    const int64_t* __restrict__ slots, uint16_t* __restrict__ out,
-                                                    int N) {
-  __shared__ __align__(16) uint8_t lds_a[2 * kPBM * kPApitch];
-  const int mt = (M + kPBM - 1) / kPBM;
-  const int e = blockIdx.x / mt, m0 = (blockIdx.x - e * mt) * kPBM;
-  const int wave = threadIdx.x >> 6;
-  int blk[kPNB];
-#pragma unroll
-  for (int i = 0; i < kPNB; ++i) blk[i] = blockIdx.y * (4 * kPNB) + kPNB * wave + i;
-  const WSrc src = w_src<W>(blocks, sb_slot, scales, ss_slot, slots[e]);
-  f32x4_t acc[4][kPNB];
-  gemm_tile<W, kPNB>(src, blk, true, [=](int row) { return x + (long long)min(m0 + row, M - 1) * kH; }, lds_a, acc);
-  store_tile(out + ((long long)e * M + m0) * N, N, acc, blk, M - m0);
-}
-
-// --------------------------------------------------------------- grouped GEMM (GroupedGemmPlan descriptors)
-// tiles int64 [ntiles][5] = (x address, out address, slot, pair M, pm); rows [pm * block_m, min(M, pm * block_m +
-// block_m)) of the pair, walked in 64-row sub-tiles (block_m <= 64: one).  grid (ntiles, N / 192).
-template <int W>
-__global__ __launch_bounds__(256) void k_mxfp4_gemm_grouped(const uint8_t* __restrict__ blocks, long long sb_slot,
-                                                            const uint8_t* __restrict__ scales, long long ss_slot,
-                                                            const int64_t* __restrict__ tiles, int block_m, int N) {
-  __shared__ __align__(16) uint8_t lds_a[2 * kPBM * kPApitch];
-  const int64_t* d = tiles + (long long)blockIdx.x * 5;
-  const uint16_t* x = reinterpret_cast<const uint16_t*>(d[0]);
-  uint16_t* out = reinterpret_cast<uint16_t*>(d[1]);
-  const long long slot = d[2];
-  const int M = (int)d[3], pm = (int)d[4];
-  const int wave = threadIdx.x >> 6;
-  int blk[kPNB];
-#pragma unroll
-  for (int i = 0; i < kPNB; ++i) blk[i] = blockIdx.y * (4 * kPNB) + kPNB * wave + i;
-  const WSrc src = w_src<W>(blocks, sb_slot, scales, ss_slot, slot);
-  const int r0 = pm * block_m, r1 = min(M, r0 + block_m);
-  for (int m0 = r0; m0 < r1; m0 += kPBM) {
-    f32x4_t acc[4][kPNB];
-    gemm_tile<W, kPNB>(src, blk, true, [=](int row) { return x + (long long)min(m0 + row, r1 - 1) * kH; }, lds_a,
-                       acc);
-    store_tile(out + (long long)m0 * N, N, acc, blk, r1 - m0);
-  }
 }
 
 // ------------------------------------------------------------------------------------ fused MoE prefill layer
@@ -349,25 +181,65 @@ struct QStage {
   uint2 s;
 };
 
-NA_DEVICE void q_load(const uint8_t* const (&rp)[4], const uint8_t* srow, int t, int tid, QStage& a) {
-  const int c16 = tid & 15, e0 = t * kPKT + 16 * (c16 & 7), half = (c16 >> 3) * kQLo;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    a.v[i] = e0 < kH ? *reinterpret_cast<const uint4*>(rp[i] + half + e0) : make_uint4(0, 0, 0, 0);
-  if (tid < 64) {
-    a.s.x = *reinterpret_cast<const uint32_t*>(srow + kQSh + 4 * t);
-    a.s.y = *reinterpret_cast<const uint32_t*>(srow + kQSl + 4 * t);
-  }
-}
+// Activation rows that arrive quantised (q rows): rp[i] = q row of staged row (tid >> 4) + 16 i, srow = q row of
+// staged row tid & 63.
+struct QRows {
+  using Stage = QStage;
+  const uint8_t* rp[4];
+  const uint8_t* srow;
 
-NA_DEVICE void q_store(uint8_t* buf, int tid, const QStage& a) {
+  NA_DEVICE void load(int t, int tid, QStage& a) const {
+    const int c16 = tid & 15, e0 = t * kPKT + 16 * (c16 & 7), half = (c16 >> 3) * kQLo;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    *reinterpret_cast<uint4*>(buf + ((tid >> 4) + 16 * i) * kQPitch + 16 * (tid & 15)) = a.v[i];
-  if (tid < 64)                                        // interleaved at the store, so the loads are not waited on early
-    *reinterpret_cast<uint2*>(buf + kPBM * kQPitch + 8 * tid) =
-        make_uint2(__byte_perm(a.s.x, a.s.y, 0x5140), __byte_perm(a.s.x, a.s.y, 0x7362));
-}
+    for (int i = 0; i < 4; ++i)
+      a.v[i] = e0 < kH ? *reinterpret_cast<const uint4*>(rp[i] + half + e0) : make_uint4(0, 0, 0, 0);
+    if (tid < 64) {
+      a.s.x = *reinterpret_cast<const uint32_t*>(srow + kQSh + 4 * t);
+      a.s.y = *reinterpret_cast<const uint32_t*>(srow + kQSl + 4 * t);
+    }
+  }
+  NA_DEVICE void store(uint8_t* buf, int tid, const QStage& a) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<uint4*>(buf + ((tid >> 4) + 16 * i) * kQPitch + 16 * (tid & 15)) = a.v[i];
+    if (tid < 64)                                      // interleaved at the store, so the loads are not waited on early
+      *reinterpret_cast<uint2*>(buf + kPBM * kQPitch + 8 * tid) =
+          make_uint2(__byte_perm(a.s.x, a.s.y, 0x5140), __byte_perm(a.s.x, a.s.y, 0x7362));
+  }
+};
+
+// bf16 activation rows quantised while they are staged (the GEMM entry points, which have no workspace): thread tid
+// owns the 8-element piece tid & 15 of rows (tid >> 4) + 16 i, so the 4 pieces of a 32-element block sit in 4
+// consecutive lanes, as x8_quant_chunk needs.  rp[i] = bf16 row of staged row (tid >> 4) + 16 i.
+struct XStage {
+  uint4 v[4];
+};
+
+struct XRows {
+  using Stage = XStage;
+  const uint16_t* rp[4];
+
+  NA_DEVICE void load(int t, int tid, XStage& a) const {
+    const int e0 = t * kPKT + 8 * (tid & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      a.v[i] = e0 < kH ? *reinterpret_cast<const uint4*>(rp[i] + e0) : make_uint4(0, 0, 0, 0);
+  }
+  NA_DEVICE void store(uint8_t* buf, int tid, const XStage& a) const {
+    const int c16 = tid & 15;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint2 hi, lo;
+      uint32_t sh, sl;
+      x8_quant_chunk(a.v[i], hi, lo, sh, sl);
+      const int row = (tid >> 4) + 16 * i;
+      *reinterpret_cast<uint2*>(buf + row * kQPitch + 8 * c16) = hi;
+      *reinterpret_cast<uint2*>(buf + row * kQPitch + kPKT + 8 * c16) = lo;
+      if ((c16 & 3) == 0)
+        *reinterpret_cast<uint16_t*>(buf + kPBM * kQPitch + row * 8 + 2 * (c16 >> 2)) = (uint16_t)(sh | (sl << 8));
+    }
+  }
+};
 
 // FP4 B operand of k-tile t in the MFMA order (lane 16 kb + n: the 16 code bytes of group 4t + kb of row n), groups
 // beyond K zeroed.  The raw and PS4 loads already are in that order; the t950 tiles are transposed across the lanes.
@@ -420,14 +292,14 @@ struct WStream {
 // One k-tile of gemm8_tile.  A of k-tile t is staged in LDS at cur and the weights of k-tile t are in (c, sc).  It
 // issues the loads of A of k-tile t + 2 (into a_in) and of the weights of k-tile t + 2 (into (c2, sc2)), runs the
 // MFMAs, stores A of k-tile t + 1 (loaded one step earlier, a_out) at nxt and meets the barrier.
-template <int W, int NB>
-NA_DEVICE void gemm8_step(int t, const WStream<W, NB>& ws, bool live, const uint8_t* const (&rp)[4],
-                          const uint8_t* srow, const uint8_t* cur, uint8_t* nxt, const QStage& a_out, QStage& a_in,
+template <int W, int NB, typename S>
+NA_DEVICE void gemm8_step(int t, const WStream<W, NB>& ws, bool live, const S& st, const uint8_t* cur, uint8_t* nxt,
+                          const typename S::Stage& a_out, typename S::Stage& a_in,
                           const uint4 (&c)[NB], const uint32_t (&sc)[NB], uint4 (&c2)[NB], uint32_t (&sc2)[NB],
                           f32x4_t (&acc)[4][NB]) {
   const int tid = threadIdx.x, lane = tid & 63, kb = lane >> 4, m = lane & 15;
   if (t + 2 < kPTiles) {
-    q_load(rp, srow, t + 2, tid, a_in);
+    st.load(t + 2, tid, a_in);
     ws.load(t + 2, c2, sc2);
   }
   if (live) {
@@ -460,12 +332,12 @@ NA_DEVICE void gemm8_step(int t, const WStream<W, NB>& ws, bool live, const uint
   for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) asm volatile("" : "+v"(acc[tt][nb])::"memory");
-  if (t + 1 < kPTiles) q_store(nxt, tid, a_out);
+  if (t + 1 < kPTiles) st.store(nxt, tid, a_out);
   __syncthreads();
 }
 
 // acc[tt][nb] = D of tokens 16 tt .. 16 tt + 15 x row block blk[nb] (lane (q, n): tokens 16 tt + 4 q + r, row n),
-// over the 23 k-tiles.  rp[i]: q row of staged row (tid >> 4) + 16 i; srow: q row of staged row tid & 63.  Both
+// over the 23 k-tiles; st stages the activation rows (QRows or XRows).  Both
 // operand streams run two k-tiles ahead of the MFMAs: the activations through three LDS buffers of a k-tile (64 rows'
 // 256 code bytes and 8 scale bytes each, loaded into registers two steps before and stored one step before their
 // use), each wave's weight codes through three register sets; the k-loop is unrolled by 3 so that every buffer and
@@ -473,9 +345,9 @@ NA_DEVICE void gemm8_step(int t, const WStream<W, NB>& ws, bool live, const uint
 // them to its NB row blocks.  lds: 3 x kQStage bytes; wsc: this wave's LDS area of NB x 1,536 bytes (t950 scale
 // rows).  A wave without work (live = false) stages and meets every barrier but runs no MFMA.  All 256 threads must
 // call it.
-template <int W, int NB>
-NA_DEVICE void gemm8_tile(const WSrc& src, const int (&blk)[NB], bool live, const uint8_t* const (&rp)[4],
-                          const uint8_t* srow, uint8_t* lds, uint8_t* wsc, f32x4_t (&acc)[4][NB]) {
+template <int W, int NB, typename S>
+NA_DEVICE void gemm8_tile(const WSrc& src, const int (&blk)[NB], bool live, const S& st, uint8_t* lds, uint8_t* wsc,
+                          f32x4_t (&acc)[4][NB]) {
   const int tid = threadIdx.x, lane = tid & 63;
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt)
@@ -499,21 +371,21 @@ NA_DEVICE void gemm8_tile(const WSrc& src, const int (&blk)[NB], bool live, cons
   uint8_t* const b2 = lds + 2 * kQStage;
   uint4 c0[NB], c1[NB], c2[NB];
   uint32_t s0[NB], s1[NB], s2[NB];
-  QStage a0, a1, a2;                                   // a_k: A of the k-tiles = k (mod 3) while in flight
-  q_load(rp, srow, 0, tid, a0);
+  typename S::Stage a0, a1, a2;                        // a_k: A of the k-tiles = k (mod 3) while in flight
+  st.load(0, tid, a0);
   ws.load(0, c0, s0);
-  q_load(rp, srow, 1, tid, a1);
+  st.load(1, tid, a1);
   ws.load(1, c1, s1);
-  q_store(b0, tid, a0);
+  st.store(b0, tid, a0);
   __syncthreads();
   int t = 0;
   for (; t + 3 <= kPTiles; t += 3) {                   // k-tiles 0 .. 20
-    gemm8_step<W, NB>(t, ws, live, rp, srow, b0, b1, a1, a2, c0, s0, c2, s2, acc);
-    gemm8_step<W, NB>(t + 1, ws, live, rp, srow, b1, b2, a2, a0, c1, s1, c0, s0, acc);
-    gemm8_step<W, NB>(t + 2, ws, live, rp, srow, b2, b0, a0, a1, c2, s2, c1, s1, acc);
+    gemm8_step<W, NB, S>(t, ws, live, st, b0, b1, a1, a2, c0, s0, c2, s2, acc);
+    gemm8_step<W, NB, S>(t + 1, ws, live, st, b1, b2, a2, a0, c1, s1, c0, s0, acc);
+    gemm8_step<W, NB, S>(t + 2, ws, live, st, b2, b0, a0, a1, c2, s2, c1, s1, acc);
   }
-  gemm8_step<W, NB>(t, ws, live, rp, srow, b0, b1, a1, a2, c0, s0, c2, s2, acc);       // 21
-  gemm8_step<W, NB>(t + 1, ws, live, rp, srow, b1, b2, a2, a0, c1, s1, c0, s0, acc);   // 22
+  gemm8_step<W, NB, S>(t, ws, live, st, b0, b1, a1, a2, c0, s0, c2, s2, acc);       // 21
+  gemm8_step<W, NB, S>(t + 1, ws, live, st, b1, b2, a2, a0, c1, s1, c0, s0, acc);   // 22
 }
 
 // Workgroup b -> (tile, column group): the dispatcher deals workgroups to the 8 XCDs in turn (XCD b % 8), so XCD x
@@ -534,7 +406,7 @@ NA_DEVICE void xcd_tile(int b, int& tile, int& col) {
 // (one wave's columns of one row) with its own E8M0 scales.  Grid: max tiles x 24 (xcd_tile<3>); in column group 22
 // waves 2 and 3 have no blocks.
 template <int W>
-__global__ __launch_bounds__(256, 2) void k_prefill_gate_up(
+__global__ __launch_bounds__(256, W == kWT950 ? 2 : 1) void k_prefill_gate_up(
     const uint8_t* __restrict__ xq, const int* __restrict__ order, const PTile* __restrict__ tiles,
     const int* __restrict__ ntiles, const uint8_t* __restrict__ pool, long long slot_bytes,
     const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ bias_gu,
@@ -554,13 +426,13 @@ __global__ __launch_bounds__(256, 2) void k_prefill_gate_up(
   const long long slot = slot_tab ? slot_tab[gid] : gid;
   const uint8_t* sb = pool + slot * slot_bytes;
   const WSrc src = W == kWT950 ? WSrc{sb, nullptr} : WSrc{sb, sb + kOffGateScales};
-  const uint8_t* rp[4];
+  QRows st;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    rp[i] = xq + (long long)(order[tl.p0 + min((tid >> 4) + 16 * i, tl.cnt - 1)] >> 2) * kQRow;
-  const uint8_t* srow = xq + (long long)(order[tl.p0 + min(tid & 63, tl.cnt - 1)] >> 2) * kQRow;
+    st.rp[i] = xq + (long long)(order[tl.p0 + min((tid >> 4) + 16 * i, tl.cnt - 1)] >> 2) * kQRow;
+  st.srow = xq + (long long)(order[tl.p0 + min(tid & 63, tl.cnt - 1)] >> 2) * kQRow;
   f32x4_t acc[4][4];
-  gemm8_tile<W, 4>(src, blk, live, rp, srow, lds, lds + 3 * kQStage + wave * 4 * kWScBytes, acc);
+  gemm8_tile<W, 4>(src, blk, live, st, lds, lds + 3 * kQStage + wave * 4 * kWScBytes, acc);
   // h = bf16(SwiGLU(bf16(acc) + bias)) (the reference's bf16 rounding points), quantised per (row, 32-column block)
   // into LDS: oh[row] = hi codes of the workgroup's 128 columns | lo codes, os[row] = 4 hi | 4 lo scale bytes.
   uint8_t* oh = lds;
@@ -665,12 +537,12 @@ __global__ __launch_bounds__(256, 2) void k_prefill_down(
   const uint8_t* sb = pool + slot * slot_bytes;
   const WSrc src = W == kWT950 ? WSrc{sb + kTDownOff, nullptr}
                                : WSrc{sb + kOffDownCodes, sb + kOffGateScales + (long long)kGU * (W == kWRaw ? kGK : kPs4Row)};
-  const uint8_t* rp[4];
+  QRows st;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) rp[i] = hq + (long long)(tl.p0 + min((tid >> 4) + 16 * i, tl.cnt - 1)) * kQRow;
-  const uint8_t* srow = hq + (long long)(tl.p0 + min(tid & 63, tl.cnt - 1)) * kQRow;
+  for (int i = 0; i < 4; ++i) st.rp[i] = hq + (long long)(tl.p0 + min((tid >> 4) + 16 * i, tl.cnt - 1)) * kQRow;
+  st.srow = hq + (long long)(tl.p0 + min(tid & 63, tl.cnt - 1)) * kQRow;
   f32x4_t acc[4][kPNB];
-  gemm8_tile<W, kPNB>(src, blk, true, rp, srow, lds, lds + 3 * kQStage + wave * kPNB * kWScBytes, acc);
+  gemm8_tile<W, kPNB>(src, blk, true, st, lds, lds + 3 * kQStage + wave * kPNB * kWScBytes, acc);
   int pr[4][4];                                       // pair of each of the lane's 16 tokens
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt)
@@ -693,6 +565,78 @@ __global__ __launch_bounds__(256, 2) void k_prefill_down(
         if (m < tl.cnt && !(n & 1))
           *reinterpret_cast<uint32_t*>(ys + (long long)p * kH + 16 * blk[nb] + n) = (uint32_t)v | (hi << 16);
       }
+  }
+}
+
+// ------------------------------------------------------------------------------- plain GEMM (mxfp4_gemm)
+// out[e][m][n] = bf16(sum_k x[m][k] w_e[n][k]); grid (E * ceil(M / 64), N / 192); wave w: row blocks 12 y + 3 w + i.
+// The same block-scaled tiles as the fused layer, the activations quantised into hi + lo rows while staged.
+NA_DEVICE void store_tile(uint16_t* out_row0, long long pitch, const f32x4_t (&acc)[4][kPNB], const int (&blk)[kPNB],
+                          int m_limit) {
+  const int lane = threadIdx.x & 63, q = lane >> 4, n = lane & 15;
+#pragma unroll
+  for (int nb = 0; nb < kPNB; ++nb)
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * tt + 4 * q + r;
+        const uint16_t v = f32_to_bf16(acc[tt][nb][r]);
+        const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
+        if (m < m_limit && !(n & 1))
+          *reinterpret_cast<uint32_t*>(out_row0 + (long long)m * pitch + 16 * blk[nb] + n) = (uint32_t)v | (hi << 16);
+      }
+}
+
+template <int W>
+__global__ __launch_bounds__(256, 2) void k_mxfp4_gemm(const uint16_t* __restrict__ x, int M,
+                                                       const uint8_t* __restrict__ blocks, long long sb_slot,
+                                                       const uint8_t* __restrict__ scales, long long ss_slot,
+                                                       const int64_t* __restrict__ slots, uint16_t* __restrict__ out,
+                                                       int N) {
+  __shared__ __align__(16) uint8_t lds[3 * kQStage + 4 * kPNB * kWScBytes];
+  const int mt = (M + kPBM - 1) / kPBM;
+  const int e = blockIdx.x / mt, m0 = (blockIdx.x - e * mt) * kPBM;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int blk[kPNB];
+#pragma unroll
+  for (int i = 0; i < kPNB; ++i) blk[i] = blockIdx.y * (4 * kPNB) + kPNB * wave + i;
+  const WSrc src = w_src<W>(blocks, sb_slot, scales, ss_slot, slots[e]);
+  XRows st;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) st.rp[i] = x + (long long)min(m0 + (tid >> 4) + 16 * i, M - 1) * kH;
+  f32x4_t acc[4][kPNB];
+  gemm8_tile<W, kPNB>(src, blk, true, st, lds, lds + 3 * kQStage + wave * kPNB * kWScBytes, acc);
+  store_tile(out + ((long long)e * M + m0) * N, N, acc, blk, M - m0);
+}
+
+// --------------------------------------------------------------- grouped GEMM (GroupedGemmPlan descriptors)
+// tiles int64 [ntiles][5] = (x address, out address, slot, pair M, pm); rows [pm * block_m, min(M, pm * block_m +
+// block_m)) of the pair, walked in 64-row sub-tiles (block_m <= 64: one).  grid (ntiles, N / 192).
+template <int W>
+__global__ __launch_bounds__(256) void k_mxfp4_gemm_grouped(const uint8_t* __restrict__ blocks, long long sb_slot,
+                                                               const uint8_t* __restrict__ scales, long long ss_slot,
+                                                               const int64_t* __restrict__ tiles, int block_m, int N) {
+  __shared__ __align__(16) uint8_t lds[3 * kQStage + 4 * kPNB * kWScBytes];
+  const int64_t* d = tiles + (long long)blockIdx.x * 5;
+  const uint16_t* x = reinterpret_cast<const uint16_t*>(d[0]);
+  uint16_t* out = reinterpret_cast<uint16_t*>(d[1]);
+  const long long slot = d[2];
+  const int M = (int)d[3], pm = (int)d[4];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int blk[kPNB];
+#pragma unroll
+  for (int i = 0; i < kPNB; ++i) blk[i] = blockIdx.y * (4 * kPNB) + kPNB * wave + i;
+  const WSrc src = w_src<W>(blocks, sb_slot, scales, ss_slot, slot);
+  const int r0 = pm * block_m, r1 = min(M, r0 + block_m);
+  for (int m0 = r0; m0 < r1; m0 += kPBM) {
+    XRows st;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.rp[i] = x + (long long)min(m0 + (tid >> 4) + 16 * i, r1 - 1) * kH;
+    f32x4_t acc[4][kPNB];
+    gemm8_tile<W, kPNB>(src, blk, true, st, lds, lds + 3 * kQStage + wave * kPNB * kWScBytes, acc);
+    store_tile(out + (long long)m0 * N, N, acc, blk, r1 - m0);
+    __syncthreads();                                   // the next sub-tile restages the scale rows and buffers
   }
 }
 

@@ -26,18 +26,6 @@ constexpr int kTUpBlock0 = kI / kTRows;             // first row block of the up
 
 NA_DEVICE float e8m0_f32(uint32_t s) { return __uint_as_float(s << 23); }
 
-// 8 bf16 B values (one MFMA operand) from one code dword and its scale: v_cvt_scalef32_pk_bf16_fp4 per byte (low
-// nibble first), exact for the E8M0 range of the store (E2M1 x 2^(s-127) is a bf16).
-NA_DEVICE bf16x8_t dequant8(uint32_t w, float scale) {
-  typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4v;
-  u32x4v r;
-  r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0));
-  r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1));
-  r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2));
-  r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3));
-  return __builtin_bit_cast(bf16x8_t, r);
-}
-
 typedef int mfma_i32x8_t __attribute__((ext_vector_type(8)));
 typedef short fp8x2_t __attribute__((ext_vector_type(2)));
 
