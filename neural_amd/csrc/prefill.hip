@@ -121,40 +121,57 @@ __global__ __launch_bounds__(256) void k_prefill_count(const int64_t* __restrict
   if (threadIdx.x == 0) counts[e] = part[0] + part[1] + part[2] + part[3];
 }
 
+// Block e: the expert's tiles and its pairs in increasing p.  The prefix over the experts before e comes from one
+// wave's shuffles; the pairs are walked 8,192 at a time, wave w taking 2,048 consecutive ones in 32 coalesced steps of
+// 64: one ballot per step gives each lane its place among the wave's hits, and a 4-entry scan places the waves.
 __global__ __launch_bounds__(256) void k_prefill_order(const int64_t* __restrict__ ids, int P,
                                                        const int* __restrict__ counts, int* __restrict__ order,
                                                        PTile* __restrict__ tiles, int* __restrict__ ntiles) {
   const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   __shared__ int wcnt[4];
   __shared__ int base_s[2];
-  if (tid == 0) {
-    int off = 0, tb = 0, tt = 0;
-    for (int i = 0; i < 128; ++i) {
-      const int c = counts[i];
-      if (i < e) {
-        off += c;
-        tb += (c + kPBM - 1) / kPBM;
-      }
-      tt += (c + kPBM - 1) / kPBM;
+  if (wave == 0) {
+    const int c0 = counts[lane], c1 = counts[64 + lane];
+    const int t0 = (c0 + kPBM - 1) / kPBM, t1 = (c1 + kPBM - 1) / kPBM;
+    int off = (lane < e ? c0 : 0) + (64 + lane < e ? c1 : 0);
+    int tb = (lane < e ? t0 : 0) + (64 + lane < e ? t1 : 0);
+    int tt = t0 + t1;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      off += __shfl_xor(off, o);
+      tb += __shfl_xor(tb, o);
+      tt += __shfl_xor(tt, o);
     }
-    base_s[0] = off;
-    base_s[1] = tb;
-    if (e == 0) *ntiles = tt;
+    if (lane == 0) {
+      base_s[0] = off;
+      base_s[1] = tb;
+      if (e == 0) *ntiles = tt;
+    }
   }
   __syncthreads();
   const int off = base_s[0], tb = base_s[1], c = counts[e];
   for (int m = tid; m * kPBM < c; m += 256) tiles[tb + m] = PTile{e, off + m * kPBM, min(kPBM, c - m * kPBM), 0};
-  int run = 0;                                        // pairs of expert e before this chunk
-  for (int p0 = 0; p0 < P; p0 += 256) {
-    const int p = p0 + tid;
-    const bool hit = p < P && ids[p] == e;
-    const uint64_t bal = __ballot(hit);
-    const int before = __popcll(bal & ((1ull << lane) - 1));
-    if (lane == 0) wcnt[wave] = __popcll(bal);
+  const uint64_t lt = (1ull << lane) - 1;
+  int run = 0;                                        // pairs of expert e before this round
+  for (int p0 = 0; p0 < P; p0 += 8192) {
+    const int wp0 = p0 + 2048 * wave;
+    uint64_t bal[32];
+    int wn = 0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const int p = wp0 + 64 * j + lane;
+      bal[j] = __ballot(p < P && ids[p] == e);
+      wn += __popcll(bal[j]);
+    }
+    if (lane == 0) wcnt[wave] = wn;
     __syncthreads();
-    int wbase = run;
-    for (int w = 0; w < wave; ++w) wbase += wcnt[w];
-    if (hit) order[off + wbase + before] = p;
+    int pos = off + run;
+    for (int w = 0; w < wave; ++w) pos += wcnt[w];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      if ((bal[j] >> lane) & 1) order[pos + __popcll(bal[j] & lt)] = wp0 + 64 * j + lane;
+      pos += __popcll(bal[j]);
+    }
     run += wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
     __syncthreads();
   }
@@ -641,21 +658,37 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemm_grouped(const uint8_t* __res
 }
 
 // out[t][n] = bf16(sum_k ys[4 t + k][n]) over the valid ranks k, fp32 sum in top-k order (server.py:2340-2341).
-__global__ __launch_bounds__(256) void k_prefill_combine(const uint32_t* __restrict__ ys, const int64_t* __restrict__ ids,
-                                                         int T, uint32_t* __restrict__ out) {
+// One thread per 8 columns of a token: 16-byte loads of the four ranks' rows, one 16-byte store.
+__global__ __launch_bounds__(256) void k_prefill_combine(const uint16_t* __restrict__ ys, const int64_t* __restrict__ ids,
+                                                         int T, uint16_t* __restrict__ out) {
   const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (long long)T * (kH / 2)) return;
-  const int t = (int)(i / (kH / 2)), c = (int)(i - (long long)t * (kH / 2));
-  float a0 = 0.f, a1 = 0.f;
+  if (i >= (long long)T * (kH / 8)) return;
+  const int t = (int)(i / (kH / 8)), c8 = (int)(i - (long long)t * (kH / 8));
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  uint4 v[4];
+  bool ok[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {                       // all four loads in flight before the sums
+    const long long e = ids[4 * t + k];
+    ok[k] = e >= 0 && e < 128;
+    v[k] = ok[k] ? *reinterpret_cast<const uint4*>(ys + (long long)(4 * t + k) * kH + 8 * c8) : make_uint4(0, 0, 0, 0);
+  }
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const long long e = ids[4 * t + k];
-    if (e < 0 || e >= 128) continue;
-    const uint32_t v = ys[(long long)(4 * t + k) * (kH / 2) + c];
-    a0 += bf16_to_f32((uint16_t)(v & 0xffff));
-    a1 += bf16_to_f32((uint16_t)(v >> 16));
+    if (!ok[k]) continue;
+    const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      a[2 * j] += bf16_to_f32((uint16_t)(w[j] & 0xffff));
+      a[2 * j + 1] += bf16_to_f32((uint16_t)(w[j] >> 16));
+    }
   }
-  out[i] = (uint32_t)f32_to_bf16(a0) | ((uint32_t)f32_to_bf16(a1) << 16);
+  uint4 o;
+  o.x = (uint32_t)f32_to_bf16(a[0]) | ((uint32_t)f32_to_bf16(a[1]) << 16);
+  o.y = (uint32_t)f32_to_bf16(a[2]) | ((uint32_t)f32_to_bf16(a[3]) << 16);
+  o.z = (uint32_t)f32_to_bf16(a[4]) | ((uint32_t)f32_to_bf16(a[5]) << 16);
+  o.w = (uint32_t)f32_to_bf16(a[6]) | ((uint32_t)f32_to_bf16(a[7]) << 16);
+  *reinterpret_cast<uint4*>(out + (long long)t * kH + 8 * c8) = o;
 }
 
 // Workspace of the fused prefill layer for T tokens (P = 4 T pairs): byte offsets, 256-aligned.
@@ -746,9 +779,9 @@ int na_moe_prefill(const void* x, const int64_t* topk_ids, const void* topk_w, i
     NA_PREFILL_GEMMS(kWRaw)
   }
 #undef NA_PREFILL_GEMMS
-  const long long nc = (long long)T * (kH / 2);
+  const long long nc = (long long)T * (kH / 8);
   launch_p(k_prefill_combine, dim3((unsigned)((nc + 255) / 256)), dim3(256), stream, ev[8], ev[9],
-           (const uint32_t*)ys, topk_ids, T, (uint32_t*)out);
+           (const uint16_t*)ys, topk_ids, T, (uint16_t*)out);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
