@@ -270,11 +270,28 @@ __global__ __launch_bounds__(256) void k_decode_attn(
     L.fin[row][1] = 1.f / S;
   }
   __syncthreads();
-  for (int i = tid; i < kRep * kHD; i += 256) {
-    const int row = i / kHD;
-    float o = 0.f;
-    for (int cc = 0; cc < ns; ++cc) o += pbase[cc * kPartFloats + 2 * kRep + i] * L.cw[cc][row];
-    orow[i] = f32_to_bf16(o * L.fin[row][1]);
+  // Thread tid: outputs 2 tid, 2 tid + 1 (row tid / 32); the partials are read 32 chunks at a time with every load
+  // issued before the first use, so the combine costs one round trip per 32 chunks, not one per few chunks.
+  {
+    const int i = 2 * tid, row = i / kHD;
+    float o0 = 0.f, o1 = 0.f;
+    for (int cb = 0; cb < ns; cb += 32) {              // uniform; ns <= 64
+      float2 v[32];
+#pragma unroll
+      for (int j = 0; j < 32; ++j)
+        v[j] = cb + j < ns ? *reinterpret_cast<const float2*>(pbase + (cb + j) * kPartFloats + 2 * kRep + i)
+                           : make_float2(0.f, 0.f);
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        if (cb + j < ns) {
+          const float w = L.cw[cb + j][row];
+          o0 += v[j].x * w;
+          o1 += v[j].y * w;
+        }
+      }
+    }
+    const float inv = L.fin[row][1];
+    *reinterpret_cast<uint32_t*>(orow + i) = (uint32_t)f32_to_bf16(o0 * inv) | ((uint32_t)f32_to_bf16(o1 * inv) << 16);
   }
 }
 
