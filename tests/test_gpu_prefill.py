@@ -230,3 +230,42 @@ def test_forward_prefill_wide_range_rows_match_oracle():
         total += d.size
         assert d.max() <= 2.0 ** -6 * np.abs(want).max() + 1e-30, (t, d.max(), np.abs(want).max())
     assert within >= 0.99 * total, (within, total)
+
+
+@pytest.mark.parametrize("T", [1, 64, 65])
+def test_forward_prefill_tile_edges(T):
+    """One token; and every token's rank-0 expert the same, so that expert holds exactly 64 or 65 pairs (one full
+    64-row tile, or a full tile plus a one-row tile): the tiles' edge rows against the oracle."""
+    import torch
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
+    dev = _dev()
+    rng = np.random.default_rng(100 + T)
+    nslot = 4
+    slots = [synth.slot_raw(rng) for _ in range(nslot)]
+    x = synth.bf16_normal(rng, (T, 2880))
+    ids = np.stack([np.concatenate([[7], rng.choice(np.delete(np.arange(128), 7), 3, replace=False)])
+                    for _ in range(T)]).astype(np.int64)
+    w = mo.rb(rng.dirichlet(np.ones(4), size=T).astype(np.float32))
+    n = 36 * 128
+    tab = (np.arange(n) % nslot).astype(np.int64)
+    bgu = synth.bf16_normal(rng, (n, 5760), 0.02)
+    bdn = synth.bf16_normal(rng, (n, 2880), 0.02)
+    pool = torch.empty((nslot, tiles.SLOT_T950), dtype=torch.uint8, device=dev)
+    tiles.repack_to_t950(_pool(slots, False, dev), pool)
+    rx = ResidentExperts(pool, GPTOSS_LAYOUT_T950, bgu.to(dev), bdn.to(dev), torch.from_numpy(tab).to(dev))
+    layer = 9
+    print(f"case forward_prefill tile edges T={T}", flush=True)
+    got = rx.forward_prefill(layer, x.to(dev), torch.from_numpy(ids).to(dev),
+                             torch.from_numpy(w).to(torch.bfloat16).to(dev)).float().cpu().numpy()
+    cache = {}
+    for t in sorted({0, T // 2, T - 1, min(63, T - 1), min(64, T - 1)}):
+        ys = []
+        for k in range(4):
+            g = layer * 128 + int(ids[t, k])
+            s = int(tab[g])
+            if s not in cache:
+                cache[s] = mo.expert_weights(slots[s])
+            ys.append(mo.expert_forward_bf16(x[t:t + 1].float().numpy(), None, bgu[g].float().numpy(),
+                                             bdn[g].float().numpy(), weights=cache[s])[0])
+        _close(got[t], mo.combine_bf16(np.stack(ys), w[t]), f"T={T} token {t}")
