@@ -177,12 +177,14 @@ int na_mxfp4_gemm(const void* x, int M, int K, const void* blocks, long long sb_
 int na_mxfp4_gemm_grouped(const void* blocks, long long sb_slot, const void* scales, long long ss_slot, int layout,
                           const int64_t* tiles, int ntiles, int block_m, int N, int K, hipStream_t stream);
 
-/* Bytes of workspace na_moe_prefill needs for T tokens (-1 if out of range). */
+/* Bytes of workspace na_moe_prefill needs for T tokens (-1 if out of range): about 53 KB per token (the quantised
+ * x rows, the quantised h and the bf16 outputs of the 4 T pairs, the order and the tile table). */
 long long na_moe_prefill_workspace_bytes(int T);
 
 /* One MoE layer over T prompt tokens, all experts resident.  Replaces server.py:1837-1936 (moe_prefill) with the
- * expert products of _expert_gemms :1977-2040 for resident experts; five launches: pair counts, stable expert
- * order + 64-token tiles, gate_up + bias + clamped SwiGLU, down + bias + routing weight, top-k sum.
+ * expert products of _expert_gemms :1977-2040 for resident experts; five launches: pair counts (with x quantised
+ * into exact E4M3 hi + lo rows), stable expert order + 64-token tiles, gate_up + bias + clamped SwiGLU on the
+ * block-scaled FP8 x FP4 MFMA (h out as E4M3 hi + lo rows), down + bias + routing weight, top-k sum.
  *   x [T, 2880] bf16; topk_ids int64 [T, 4] (ids outside [0, 128) contribute +0); topk_w bf16 [T, 4]
  *   pool / slot_bytes / slot_tab / expert_base / biases as na_moe_decode; layout 0 raw, 1 PS4, 2 t950
  *   workspace: na_moe_prefill_workspace_bytes(T) bytes, 16-byte aligned

@@ -109,7 +109,7 @@ class ResidentExperts:
         reference's GEMM arithmetic.  Five launches on the current stream, no host synchronisation: pair counts per
         expert, a stable expert-major order of the pairs with its 64-token tiles, gate_up + bias + clamped SwiGLU
         (activation rows gathered through the order), down + bias + routing weight (scattered back to pair order),
-        and the top-k sum.  The workspace (~ T x 92 KB) is allocated through torch's caching allocator.
+        and the top-k sum.  The workspace (~ T x 53 KB) is allocated through torch's caching allocator.
         events: None or ten recorded timing events (start/stop of each launch; measurement only)."""
         L = self.layout
         T = hidden.shape[0]
