@@ -269,3 +269,30 @@ def test_forward_prefill_tile_edges(T):
             ys.append(mo.expert_forward_bf16(x[t:t + 1].float().numpy(), None, bgu[g].float().numpy(),
                                              bdn[g].float().numpy(), weights=cache[s])[0])
         _close(got[t], mo.combine_bf16(np.stack(ys), w[t]), f"T={T} token {t}")
+
+
+def test_mxfp4_gemm_wide_range_rows():
+    """The GEMM entry point quantises bf16 rows into E4M3 hi + lo while staging them: rows scaled by 2^-30 .. 2^30,
+    a zero row and elements 2^-12 below their block's maximum, each output within 2^-7 of its row's largest magnitude
+    of the fp64 product of the exactly dequantised weights (bf16 output rounding is 2^-8)."""
+    import torch
+    from neural_amd.moe.layout import GPTOSS_LAYOUT, mxfp4_pool_views
+    from neural_amd.q80 import mxfp4_kernels as mk
+    dev = _dev()
+    rng = np.random.default_rng(99)
+    slots = [synth.slot_raw(rng)]
+    gb, db, gs, ds = mxfp4_pool_views(_pool(slots, False, dev), GPTOSS_LAYOUT)
+    M = 41
+    x = rng.standard_normal((M, 2880)).astype(np.float32)
+    x *= np.exp2(np.arange(M) - 20.0 + (np.arange(M) % 3) * 5 - 5)[:, None]
+    x[:, 9::32] *= 2.0 ** -12
+    x[13] = 0.0
+    x = rb(x)
+    print(f"case mxfp4_gemm wide range M={M}", flush=True)
+    got = mk.mxfp4_gemm(torch.from_numpy(x).to(torch.bfloat16).to(dev), gb, gs,
+                        torch.tensor([0], dtype=torch.int64, device=dev))[0].float().cpu().numpy()
+    want = mo.gemv_f64(x, mo.expert_weights(slots[0])[0])
+    d = np.abs(got - want)
+    assert np.isfinite(got).all() and not d[13].any()
+    tol = 2.0 ** -7 * np.abs(want).max(axis=1, keepdims=True)
+    assert (d <= tol).all(), float((d / np.maximum(tol, 1e-38)).max())
