@@ -327,6 +327,7 @@ NA_DEVICE void gemm8_step(int t, const WStream<W, NB>& ws, bool live, const S& s
       b[nb] = w_operand8<W>(c[nb], t, lane);
       sb[nb] = ws.scale(t, nb, sc[nb]);
     }
+    __builtin_amdgcn_s_setprio(1);                     // the MFMA burst issues ahead of the other wave's staging
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       const uint8_t* row = cur + (16 * tt + m) * kQPitch + 16 * kb;
@@ -349,6 +350,7 @@ NA_DEVICE void gemm8_step(int t, const WStream<W, NB>& ws, bool live, const S& s
   for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) asm volatile("" : "+v"(acc[tt][nb])::"memory");
+  __builtin_amdgcn_s_setprio(0);
   if (t + 1 < kPTiles) st.store(nxt, tid, a_out);
   __syncthreads();
 }
