@@ -150,18 +150,6 @@ def cpu_baseline(pool_dev, ids, B, seconds=12.0):
             "gbps": round(4 * SLOT_ALGO_BYTES / t_call / 1e9, 2)}
 
 
-def zipf_routing(rng, T, n_exp=128, s=1.1):
-    """Per token 4 distinct experts drawn without replacement with probability ~ Zipf(s) over a fixed random rank
-    permutation of the experts; softmax weights of random logits (configuration 2)."""
-    ranks = rng.permutation(n_exp)
-    p = 1.0 / np.arange(1, n_exp + 1) ** s
-    p /= p.sum()
-    ids = np.stack([ranks[rng.choice(n_exp, TOPK, replace=False, p=p)] for _ in range(T)]).astype(np.int64)
-    lg = rng.standard_normal((T, TOPK)).astype(np.float32)
-    e = np.exp(lg - lg.max(-1, keepdims=True))
-    return ids, (e / e.sum(-1, keepdims=True)).astype(np.float32)
-
-
 def bench_prefill(A):
     """Configuration 2: one MoE layer over T = 2048 prompt tokens (hidden 2880, 128 experts, top-4, Zipf(1.1) expert
     popularity), weights MXFP4 as configuration 0 in the t950 pool, x bf16 N(0,1), zero biases.  One step = the fused
@@ -188,7 +176,7 @@ def bench_prefill(A):
     tab = torch.arange(N_LAYERS * N_EXPERTS, dtype=torch.int64, device=dev) % N_EXPERTS
     rx = ResidentExperts(pool, L, None, None, tab)
     rng = np.random.default_rng(2048)
-    ids_np, w_np = zipf_routing(rng, T)
+    ids_np, w_np = synth.zipf_routing(rng, T)
     counts = np.bincount(ids_np.reshape(-1), minlength=N_EXPERTS)
     ids = torch.from_numpy(ids_np).to(dev)
     wts = torch.from_numpy(w_np).to(torch.bfloat16).to(dev)
@@ -259,29 +247,6 @@ def bench_prefill(A):
     print(json.dumps(res), flush=True)
 
 
-def build_t950_pool(dev, seed):
-    """All 36 x 128 experts resident in the t950 layout: raw store slots (uniform E2M1 code bytes, E8M0 exponents
-    uniform in [119, 125]) generated on the device 128 at a time and repacked, the way a store is loaded."""
-    import torch
-
-    from neural_amd import synth, tiles
-    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_T950
-
-    n_slots = N_LAYERS * N_EXPERTS
-    pool = torch.empty((n_slots, GPTOSS_LAYOUT_T950.slot_bytes), dtype=torch.uint8, device=dev)
-    g = torch.Generator(device=dev)
-    g.manual_seed(seed)
-    chunk = torch.empty((N_EXPERTS, GPTOSS_LAYOUT.slot_bytes), dtype=torch.uint8, device=dev)
-    cb = synth.CODE_BYTES
-    for c0 in range(0, n_slots, N_EXPERTS):
-        chunk[:, :cb].random_(0, 256, generator=g)
-        chunk[:, cb:].random_(synth.SCALE_LO, synth.SCALE_HI + 1, generator=g)
-        tiles.repack_to_t950(chunk, pool[c0:c0 + N_EXPERTS])
-    torch.cuda.synchronize()
-    del chunk
-    return pool
-
-
 def bench_model(A):
     """Configuration 4: full 36-layer GPT-OSS-120B-shaped greedy decode on one GPU.  Random-init weights (attention,
     router, embedding and lm_head bf16 N(0, 0.02), norms 1 + N(0, 0.02), sinks N(0, 1), vocab 201088), all 36 x 128
@@ -302,7 +267,9 @@ def bench_model(A):
     dev = torch.device("cuda", 0)
     ctx, n_new = A.context, A.steps
     log(f"model: building the expert pool ({N_LAYERS * N_EXPERTS} slots, t950)")
-    pool = build_t950_pool(dev, 4242)
+    from neural_amd import synth
+
+    pool = synth.t950_pool_device(N_LAYERS * N_EXPERTS, dev, 4242)
     L = GPTOSS_LAYOUT_T950
     rx = ResidentExperts(pool, L, None, None, max_batch=1, k_split=A.k_split, combine_in_down=A.down != "expert")
     log("model: random-init dense weights")

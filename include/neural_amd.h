@@ -181,6 +181,15 @@ int na_mxfp4_gemm_grouped(const void* blocks, long long sb_slot, const void* sca
  * x rows, the quantised h and the bf16 outputs of the 4 T pairs, the order and the tile table). */
 long long na_moe_prefill_workspace_bytes(int T);
 
+/* Where na_moe_prefill keeps its routing tables inside the workspace of T tokens (no counterpart in the reference,
+ * whose routing tables are torch tensors: server.py:2246-2254 stable argsort, bincount; mxfp4_kernels.py:298-315
+ * tile rows).  offsets (9 values) <- byte offsets of counts (int32 [128]: pairs per expert), ntiles (int32 [1]),
+ * order (int32 [4 T]: pair indices p = 4 t + k sorted by expert, stable in p; the first sum(counts) entries are
+ * valid), tiles (int32 [max_tiles][4] = (expert, first sorted position, rows <= 64, 0), ntiles valid), the quantised
+ * x rows, the quantised h rows, the bf16 pair outputs, then the total bytes and max_tiles.  For tests and tools that
+ * inspect the routing of a call; returns 0, or -1 for T outside [1, 2^20]. */
+int na_moe_prefill_workspace_layout(int T, long long* offsets);
+
 /* One MoE layer over T prompt tokens, all experts resident.  Replaces server.py:1837-1936 (moe_prefill) with the
  * expert products of _expert_gemms :1977-2040 for resident experts; five launches: pair counts (with x quantised
  * into exact E4M3 hi + lo rows), stable expert order + 64-token tiles, gate_up + bias + clamped SwiGLU on the

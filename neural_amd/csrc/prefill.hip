@@ -736,6 +736,14 @@ long long na_moe_prefill_workspace_bytes(int T) {
   return prefill_ws(T).total;
 }
 
+int na_moe_prefill_workspace_layout(int T, long long* offsets) {
+  if (T <= 0 || T > (1 << 20) || !offsets) return kErrArgs;
+  const PrefillWs w = prefill_ws(T);
+  const long long v[9] = {w.counts, w.ntiles, w.order, w.tiles, w.xq, w.h, w.ys, w.total, w.max_tiles};
+  for (int i = 0; i < 9; ++i) offsets[i] = v[i];
+  return kOk;
+}
+
 int na_moe_prefill(const void* x, const int64_t* topk_ids, const void* topk_w, int T, const void* pool,
                    long long slot_bytes, int layout, const int64_t* slot_tab, long long expert_base,
                    const void* bias_gu, const void* bias_dn, void* workspace, long long ws_bytes, void* out,

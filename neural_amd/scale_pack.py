@@ -1,88 +1,94 @@
-"""PS4 scale codec of the GPT-OSS expert store (weight_repr "mxfp4_g32_ps4"), host side.
+"""Host codec of the PS4 scale rows (weight_repr "mxfp4_g32_ps4"), the packed form of an expert slot's E8M0 region.
 
-Same names and contract as the reference's tools/scale_pack.py:36-97 (``SpanError``, ``row_spans``,
-``pack_scale_rows``, ``unpack_scale_rows``, ``pack_slot``, ``unpack_slot``):
+Byte format (reference tools/scale_pack.py:6-12, read by kernels/gptoss_cpu_cap2.c:358-361 and the GPU kernels):
+a slot keeps its 12,441,600 E2M1 code bytes unchanged and stores each of its 8,640 scale rows (5,760 gate_up rows,
+then 2,880 down rows) of 90 E8M0 exponents in 46 bytes: the row's smallest exponent, then the 90 offsets from it as
+4-bit fields, two per byte, the even group in the low nibble.  An exponent range above 15 within a row has no
+encoding, so packing reports such rows (SpanError) instead of clipping them.
 
-    raw slot  (13,219,200 B) = 12,441,600 code bytes | 8,640 scale rows x 90 B (gate rows, then down rows)
-    PS4 slot  (12,839,040 B) = the same code bytes   | 8,640 scale rows x 46 B
-    PS4 row: byte 0 = base = min of the row's 90 scale bytes; byte 1 + k = d[2k] | d[2k+1] << 4 with d = s - base.
-
-Lossless iff every row's span (max - min) <= 15; packing refuses wider rows (SpanError) and never clips.
+Public names follow the reference's codec (pack_scale_rows, unpack_scale_rows, pack_slot, unpack_slot, SpanError) so
+its callers keep working; the geometry comes from neural_amd.moe.layout.
 """
 from __future__ import annotations
 
 import numpy as np
 
-H, GU, GK, RB = 2880, 5760, 90, 1440
-OFF_DC = GU * RB
-OFF_GS = OFF_DC + H * RB
-OFF_DS = OFF_GS + GU * GK
-SLOT_RAW = OFF_DS + H * GK
-NROWS = GU + H
-SR_P4 = 1 + GK // 2
-SLOT_PACKED = OFF_GS + NROWS * SR_P4
-assert SLOT_RAW == 13_219_200 and SLOT_PACKED == 12_839_040
+from .moe.layout import GPTOSS_LAYOUT as _RAW, GPTOSS_LAYOUT_PS4 as _PS4
+
+HIDDEN = _RAW.down_n                                   # 2880
+GATE_UP_ROWS = _RAW.gate_up_n                          # 5760
+GROUPS = _RAW.gate_groups                              # 90 exponents per weight row
+DOWN_CODES_AT = _RAW.gate_pack_bytes                   # 8,294,400: first byte of the down codes
+SCALES_AT = _RAW.off_gate_scales                       # 12,441,600: the scale region (both layouts)
+SCALE_ROWS = GATE_UP_ROWS + HIDDEN                     # 8,640
+PS4_ROW_BYTES = 1 + GROUPS // 2                        # 46
+RAW_SLOT_BYTES = _RAW.slot_bytes                       # 13,219,200
+PS4_SLOT_BYTES = _PS4.slot_bytes                       # 12,839,040
+if SCALES_AT + SCALE_ROWS * PS4_ROW_BYTES != PS4_SLOT_BYTES or SCALES_AT + SCALE_ROWS * GROUPS != RAW_SLOT_BYTES:
+    raise ImportError("expert layout and PS4 geometry disagree")
+
+_NIBBLE_WEIGHTS = np.array([1, 16], np.uint8)        # (even, odd) offset -> one byte
 
 
 class SpanError(ValueError):
-    """Scale rows spanning more than 15 exponent steps cannot be stored as 4-bit deltas."""
+    """Raised by the packers for scale rows whose exponents differ by more than 15; ``rows`` holds their indices
+    (within the rows given) and ``spans`` their max - min."""
 
     def __init__(self, rows, spans):
-        self.rows, self.spans = np.asarray(rows), np.asarray(spans)
-        super().__init__(f"{len(self.rows)} scale row(s) with span > 15 (rows {self.rows[:8].tolist()}..., "
-                         f"spans {self.spans[:8].tolist()}...)")
+        self.rows = np.asarray(rows, np.int64)
+        self.spans = np.asarray(spans, np.int64)
+        shown = ", ".join(f"row {r}: range {s}" for r, s in zip(self.rows[:6].tolist(), self.spans[:6].tolist()))
+        more = "" if self.rows.size <= 6 else f" (+{self.rows.size - 6} more)"
+        super().__init__(f"PS4 stores 4-bit exponent offsets; {self.rows.size} scale row(s) exceed a range of 15: "
+                         f"{shown}{more}")
 
 
-def row_spans(raw) -> np.ndarray:
-    """max - min of each scale row of a raw slot (or of a [..., 8640 * 90] scale region)."""
-    sc = np.asarray(raw, np.uint8)[..., OFF_GS:].reshape(-1, NROWS, GK)
-    return sc.max(axis=-1).astype(np.int16) - sc.min(axis=-1).astype(np.int16)
+def _as_matrix(a, width: int, what: str) -> np.ndarray:
+    m = np.asarray(a)
+    if m.dtype != np.uint8 or m.ndim != 2 or m.shape[1] != width:
+        raise ValueError(f"{what}: expected a uint8 array of shape [rows, {width}], got {m.dtype} {m.shape}")
+    return m
 
 
 def pack_scale_rows(sc, want_span: bool = False):
-    """raw u8 [n, 90] -> PS4 u8 [n, 46].  SpanError for any row with span > 15."""
-    sc = np.asarray(sc, np.uint8)
-    if sc.ndim != 2 or sc.shape[1] != GK:
-        raise ValueError(f"scale rows must be [n, {GK}], got {sc.shape}")
-    base = sc.min(axis=1)
-    delta = sc - base[:, None]
-    span = delta.max(axis=1) if sc.shape[0] else np.zeros(0, np.uint8)
-    bad = np.flatnonzero(span > 15)
-    if bad.size:
-        raise SpanError(bad, span[bad].astype(np.int16))
-    rows = np.empty((sc.shape[0], SR_P4), np.uint8)
-    rows[:, 0] = base
-    rows[:, 1:] = delta[:, 0::2] | (delta[:, 1::2] << 4)
-    return (rows, span) if want_span else rows
+    """E8M0 rows u8 [n, 90] -> PS4 rows u8 [n, 46].  want_span: also return each row's max - min (u8 [n])."""
+    rows = _as_matrix(sc, GROUPS, "pack_scale_rows")
+    lowest = rows.min(axis=1, initial=255)
+    offsets = rows - lowest[:, None]                          # no wrap: every entry >= its row minimum
+    widest = offsets.max(axis=1, initial=0)
+    over = widest > 15
+    if over.any():
+        idx = np.nonzero(over)[0]
+        raise SpanError(idx, widest[idx])
+    pairs = offsets.reshape(rows.shape[0], GROUPS // 2, 2)
+    body = (pairs * _NIBBLE_WEIGHTS).sum(axis=2, dtype=np.uint8)
+    packed = np.concatenate([lowest[:, None], body], axis=1)
+    return (packed, widest) if want_span else packed
 
 
 def unpack_scale_rows(rows) -> np.ndarray:
-    """PS4 u8 [n, 46] -> raw u8 [n, 90] (exact inverse of pack_scale_rows)."""
-    rows = np.asarray(rows, np.uint8)
-    if rows.ndim != 2 or rows.shape[1] != SR_P4:
-        raise ValueError(f"packed rows must be [n, {SR_P4}], got {rows.shape}")
-    base = rows[:, 0:1]
-    sc = np.empty((rows.shape[0], GK), np.uint8)
-    sc[:, 0::2] = base + (rows[:, 1:] & 15)
-    sc[:, 1::2] = base + (rows[:, 1:] >> 4)
-    return sc
+    """PS4 rows u8 [n, 46] -> E8M0 rows u8 [n, 90]: the exact inverse of pack_scale_rows (u8 arithmetic wraps, as the
+    kernels' byte reads do, for rows no packer produced)."""
+    packed = _as_matrix(rows, PS4_ROW_BYTES, "unpack_scale_rows")
+    body = packed[:, 1:]
+    offsets = np.stack([body & 0x0F, body >> 4], axis=2).reshape(packed.shape[0], GROUPS)
+    return (offsets + packed[:, :1]).astype(np.uint8)
+
+
+def _split(slot, size: int, what: str):
+    s = np.asarray(slot)
+    if s.dtype != np.uint8 or s.shape != (size,):
+        raise ValueError(f"{what}: expected uint8 [{size}], got {s.dtype} {s.shape}")
+    return s[:SCALES_AT], s[SCALES_AT:]
 
 
 def pack_slot(raw) -> np.ndarray:
-    raw = np.asarray(raw, np.uint8)
-    if raw.shape != (SLOT_RAW,):
-        raise ValueError(f"raw slot must be [{SLOT_RAW}] bytes, got {raw.shape}")
-    out = np.empty(SLOT_PACKED, np.uint8)
-    out[:OFF_GS] = raw[:OFF_GS]
-    out[OFF_GS:] = pack_scale_rows(raw[OFF_GS:].reshape(NROWS, GK)).ravel()
-    return out
+    """Raw slot u8 [13,219,200] -> PS4 slot u8 [12,839,040] (codes copied, scale rows packed)."""
+    codes, scales = _split(raw, RAW_SLOT_BYTES, "pack_slot")
+    return np.concatenate([codes, pack_scale_rows(scales.reshape(SCALE_ROWS, GROUPS)).reshape(-1)])
 
 
 def unpack_slot(packed) -> np.ndarray:
-    packed = np.asarray(packed, np.uint8)
-    if packed.shape != (SLOT_PACKED,):
-        raise ValueError(f"packed slot must be [{SLOT_PACKED}] bytes, got {packed.shape}")
-    out = np.empty(SLOT_RAW, np.uint8)
-    out[:OFF_GS] = packed[:OFF_GS]
-    out[OFF_GS:] = unpack_scale_rows(packed[OFF_GS:].reshape(NROWS, SR_P4)).ravel()
-    return out
+    """PS4 slot u8 [12,839,040] -> raw slot u8 [13,219,200] (exact inverse of pack_slot)."""
+    codes, rows = _split(packed, PS4_SLOT_BYTES, "unpack_slot")
+    return np.concatenate([codes, unpack_scale_rows(rows.reshape(SCALE_ROWS, PS4_ROW_BYTES)).reshape(-1)])

@@ -22,8 +22,8 @@ FULL_TILES = 22
 CODE_BYTES = FULL_TILES * 1024 + 512          # 23,040 per row block
 SCALE_PITCH = 96
 BLOCK_BYTES = CODE_BYTES + ROWS * SCALE_PITCH  # 24,576
-GATE_BLOCKS = sp.GU // ROWS                   # 360
-DOWN_BLOCKS = sp.H // ROWS                    # 180
+GATE_BLOCKS = sp.GATE_UP_ROWS // ROWS                   # 360
+DOWN_BLOCKS = sp.HIDDEN // ROWS                    # 180
 SLOT_T950 = (GATE_BLOCKS + DOWN_BLOCKS) * BLOCK_BYTES
 assert SLOT_T950 == 13_271_040
 
@@ -32,7 +32,7 @@ assert SLOT_T950 == 13_271_040
 def _codes_to_blocks(codes: np.ndarray) -> np.ndarray:
     """codes u8 [N, 90, 16] -> [N / 16, 23040] tile bytes."""
     nrb = codes.shape[0] // ROWS
-    c = codes.reshape(nrb, ROWS, sp.GK, 16)
+    c = codes.reshape(nrb, ROWS, sp.GROUPS, 16)
     full = c[:, :, :88, :].reshape(nrb, ROWS, FULL_TILES, 4, 4, 4)        # rb, n, t, j, q, b
     full = full.transpose(0, 2, 4, 1, 3, 5).reshape(nrb, FULL_TILES * 1024)  # rb, t, q, n, j, b
     tail = c[:, :, 88:, :].reshape(nrb, ROWS, 2, 4, 4)                   # rb, n, j, q, b
@@ -44,17 +44,17 @@ def _blocks_to_codes(blk: np.ndarray) -> np.ndarray:
     nrb = blk.shape[0]
     full = blk[:, :FULL_TILES * 1024].reshape(nrb, FULL_TILES, 4, ROWS, 4, 4).transpose(0, 3, 1, 4, 2, 5)
     tail = blk[:, FULL_TILES * 1024:CODE_BYTES].reshape(nrb, 4, ROWS, 2, 4).transpose(0, 2, 3, 1, 4)
-    c = np.empty((nrb, ROWS, sp.GK, 16), np.uint8)
+    c = np.empty((nrb, ROWS, sp.GROUPS, 16), np.uint8)
     c[:, :, :88, :] = full.reshape(nrb, ROWS, 88, 16)
     c[:, :, 88:, :] = tail.reshape(nrb, ROWS, 2, 16)
-    return c.reshape(nrb * ROWS, sp.GK, 16)
+    return c.reshape(nrb * ROWS, sp.GROUPS, 16)
 
 
 def _scales_to_blocks(sc: np.ndarray) -> np.ndarray:
     """raw scale rows u8 [N, 90] -> [N / 16, 1536]."""
     nrb = sc.shape[0] // ROWS
     out = np.zeros((nrb, ROWS, SCALE_PITCH), np.uint8)
-    out[:, :, :sp.GK] = sc.reshape(nrb, ROWS, sp.GK)
+    out[:, :, :sp.GROUPS] = sc.reshape(nrb, ROWS, sp.GROUPS)
     return out.reshape(nrb, ROWS * SCALE_PITCH)
 
 
@@ -62,16 +62,16 @@ def slot_to_t950(slot: np.ndarray, packed: bool = False) -> np.ndarray:
     """A raw (or PS4) store slot -> t950 slot bytes."""
     slot = np.asarray(slot, np.uint8)
     raw = sp.unpack_slot(slot) if packed else slot
-    if raw.shape != (sp.SLOT_RAW,):
-        raise ValueError(f"slot must be {sp.SLOT_RAW} (raw) or {sp.SLOT_PACKED} (PS4) bytes")
-    gc = raw[:sp.OFF_DC].reshape(sp.GU, sp.GK, 16)
-    dc = raw[sp.OFF_DC:sp.OFF_GS].reshape(sp.H, sp.GK, 16)
-    sc = raw[sp.OFF_GS:].reshape(sp.NROWS, sp.GK)
+    if raw.shape != (sp.RAW_SLOT_BYTES,):
+        raise ValueError(f"slot must be {sp.RAW_SLOT_BYTES} (raw) or {sp.PS4_SLOT_BYTES} (PS4) bytes")
+    gc = raw[:sp.DOWN_CODES_AT].reshape(sp.GATE_UP_ROWS, sp.GROUPS, 16)
+    dc = raw[sp.DOWN_CODES_AT:sp.SCALES_AT].reshape(sp.HIDDEN, sp.GROUPS, 16)
+    sc = raw[sp.SCALES_AT:].reshape(sp.SCALE_ROWS, sp.GROUPS)
     out = np.empty((GATE_BLOCKS + DOWN_BLOCKS, BLOCK_BYTES), np.uint8)
     out[:GATE_BLOCKS, :CODE_BYTES] = _codes_to_blocks(gc)
     out[GATE_BLOCKS:, :CODE_BYTES] = _codes_to_blocks(dc)
-    out[:GATE_BLOCKS, CODE_BYTES:] = _scales_to_blocks(sc[:sp.GU])
-    out[GATE_BLOCKS:, CODE_BYTES:] = _scales_to_blocks(sc[sp.GU:])
+    out[:GATE_BLOCKS, CODE_BYTES:] = _scales_to_blocks(sc[:sp.GATE_UP_ROWS])
+    out[GATE_BLOCKS:, CODE_BYTES:] = _scales_to_blocks(sc[sp.GATE_UP_ROWS:])
     return out.reshape(-1)
 
 
@@ -81,11 +81,11 @@ def t950_to_slot(t: np.ndarray, packed: bool = False) -> np.ndarray:
     if t.shape != (SLOT_T950,):
         raise ValueError(f"t950 slot must be {SLOT_T950} bytes")
     blk = t.reshape(GATE_BLOCKS + DOWN_BLOCKS, BLOCK_BYTES)
-    raw = np.empty(sp.SLOT_RAW, np.uint8)
-    raw[:sp.OFF_DC] = _blocks_to_codes(blk[:GATE_BLOCKS, :CODE_BYTES]).reshape(-1)
-    raw[sp.OFF_DC:sp.OFF_GS] = _blocks_to_codes(blk[GATE_BLOCKS:, :CODE_BYTES]).reshape(-1)
-    sc = blk[:, CODE_BYTES:].reshape(-1, ROWS, SCALE_PITCH)[:, :, :sp.GK].reshape(sp.NROWS, sp.GK)
-    raw[sp.OFF_GS:] = sc.reshape(-1)
+    raw = np.empty(sp.RAW_SLOT_BYTES, np.uint8)
+    raw[:sp.DOWN_CODES_AT] = _blocks_to_codes(blk[:GATE_BLOCKS, :CODE_BYTES]).reshape(-1)
+    raw[sp.DOWN_CODES_AT:sp.SCALES_AT] = _blocks_to_codes(blk[GATE_BLOCKS:, :CODE_BYTES]).reshape(-1)
+    sc = blk[:, CODE_BYTES:].reshape(-1, ROWS, SCALE_PITCH)[:, :, :sp.GROUPS].reshape(sp.SCALE_ROWS, sp.GROUPS)
+    raw[sp.SCALES_AT:] = sc.reshape(-1)
     return sp.pack_slot(raw) if packed else raw
 
 
@@ -102,7 +102,7 @@ def repack_to_t950(src, dst, packed: bool = False) -> None:
         raise ValueError("src and dst need the same slot count on one CUDA device")
     if src.stride(1) != 1 or dst.stride(1) != 1:
         raise ValueError("slot rows must be contiguous")
-    want = sp.SLOT_PACKED if packed else sp.SLOT_RAW
+    want = sp.PS4_SLOT_BYTES if packed else sp.RAW_SLOT_BYTES
     if src.shape[1] != want or dst.shape[1] < SLOT_T950:
         raise ValueError(f"src rows must be {want} bytes, dst rows >= {SLOT_T950}")
     if src.shape[0]:
@@ -122,7 +122,7 @@ def repack_from_t950(src, dst, packed: bool = False) -> None:
         raise ValueError("src and dst need the same slot count on one CUDA device")
     if src.stride(1) != 1 or dst.stride(1) != 1:
         raise ValueError("slot rows must be contiguous")
-    want = sp.SLOT_PACKED if packed else sp.SLOT_RAW
+    want = sp.PS4_SLOT_BYTES if packed else sp.RAW_SLOT_BYTES
     if dst.shape[1] != want or src.shape[1] < SLOT_T950:
         raise ValueError(f"dst rows must be {want} bytes, src rows >= {SLOT_T950}")
     if src.shape[0]:

@@ -153,12 +153,15 @@ class DecodeOracle:
 
     def moe_rows(self, li, hn, ids, wts):
         """Expert layer over prompt rows (server.py:1837-1936 moe_prefill): every (token, rank) pair through its
-        expert, then per token bf16(sum_k fp32(bf16(y_k * w_k))) in top-k order (server.py:2340-2341)."""
+        expert, then per token bf16(sum_k fp32(bf16(y_k * w_k))) in top-k order (server.py:2340-2341).  An id outside
+        [0, 128) (no expert; the masked contract of the GPU path) contributes +0."""
         hn = np.asarray(hn, np.float32)
         ids = np.asarray(ids, np.int64)
         T, K = ids.shape
         y = np.zeros((T, K, H), np.float32)
         for e in np.unique(ids):
+            if not 0 <= e < NE:
+                continue
             tt, kk = np.nonzero(ids == e)
             (wg, wd), bgu, bdn = self._expert(li, int(e))
             y[tt, kk] = expert_forward_bf16(hn[tt], None, bgu, bdn, weights=(wg, wd))

@@ -23,8 +23,8 @@ RAW_STORE_DESCRIPTOR = {"slot_bytes": 13219200, "n_layers": 36, "n_experts": 128
 
 
 def test_layout_arithmetic():
-    assert GPTOSS_LAYOUT.slot_bytes == 13_219_200 == sp.SLOT_RAW
-    assert GPTOSS_LAYOUT_PS4.slot_bytes == 12_839_040 == sp.SLOT_PACKED
+    assert GPTOSS_LAYOUT.slot_bytes == 13_219_200 == sp.RAW_SLOT_BYTES
+    assert GPTOSS_LAYOUT_PS4.slot_bytes == 12_839_040 == sp.PS4_SLOT_BYTES
     assert GPTOSS_LAYOUT_PS4.gate_saz_bytes == 5760 * 46 and GPTOSS_LAYOUT_PS4.down_saz_bytes == 2880 * 46
     assert GPTOSS_LAYOUT.gate_pack_bytes == GPTOSS_LAYOUT_PS4.gate_pack_bytes == 5760 * 1440
     assert (GPTOSS_LAYOUT.scale_layout_mode, GPTOSS_LAYOUT_PS4.scale_layout_mode) == (0, 1)
@@ -87,82 +87,109 @@ def test_launchers_infer_the_layout_from_the_view():
         _scale_layout(torch.zeros(2, 8, 180, dtype=torch.uint8)[:, :, ::2], GK, None)
 
 
-# ---------------------------------------------------------------- ragged tile plans (reference test_grouped_gemm_plan)
-def test_pair_local_tiles_at_every_bm_boundary():
-    descs = [(100, 200, i, m) for i, m in enumerate((0, 1, 15, 16, 17, 63, 64, 65, 128, 129))]
-    for bm in (16, 32, 64, 128):
-        rows = _grouped_tile_rows(descs, bm)
-        for desc in descs:
-            actual = [r for r in rows if r[2] == desc[2]]
-            assert [r[4] for r in actual] == list(range((desc[3] + bm - 1) // bm))
-            assert all(r[:4] == desc for r in actual)
-            positions = [p for r in actual for p in range(r[4] * bm, min((r[4] + 1) * bm, r[3]))]
-            assert positions == list(range(desc[3]))
+# ------------------------------------------------------------------- ragged tile plans (contract: mxfp4_kernels.py:298-382)
+# The tile table of a grouped launch lists, pair by pair in the order given, one row (x address, out address, slot,
+# M, pm) per block of block_m rows of the pair; tiles never span two pairs and empty pairs get none.
+
+def test_tile_rows_known_answer():
+    descs = [(0x1000, 0x9000, 5, 40), (0x2000, 0xA000, 7, 0), (0x3000, 0xB000, 1, 33), (0x1000, 0xC000, 5, 32)]
+    assert _grouped_tile_rows(descs, 32) == [
+        (0x1000, 0x9000, 5, 40, 0), (0x1000, 0x9000, 5, 40, 1),
+        (0x3000, 0xB000, 1, 33, 0), (0x3000, 0xB000, 1, 33, 1),
+        (0x1000, 0xC000, 5, 32, 0)]
+    assert [r[4] for r in _grouped_tile_rows(descs, 16)] == [0, 1, 2, 0, 1, 2, 0, 1]
+    assert len(_grouped_tile_rows(descs, 256)) == 3
+    assert _grouped_tile_rows([], 16) == []
 
 
-def test_plan_keeps_pointer_offsets_and_original_pair_boundaries():
-    xs = torch.empty(140 * 64 + 9, dtype=torch.bfloat16)
-    ys = torch.empty(140 * 33 + 13, dtype=torch.bfloat16)
-    pairs = [(xs[1:1 + 65 * 64].view(65, 64), 2, ys[3:3 + 65 * 33].view(65, 33)),
-             (xs[1 + 65 * 64:1 + 130 * 64].view(65, 64), 2, ys[3 + 65 * 33:3 + 130 * 33].view(65, 33))]
-    plan = GroupedGemmPlan(pairs, block_m=64)
-    assert plan.metadata.device.type == "cpu"
-    assert (plan.K, plan.N, plan.ntiles, plan.slots) == (64, 33, 4, (2, 2))
-    assert plan.metadata.tolist() == [
-        [pairs[0][0].data_ptr(), pairs[0][2].data_ptr(), 2, 65, 0],
-        [pairs[0][0].data_ptr(), pairs[0][2].data_ptr(), 2, 65, 1],
-        [pairs[1][0].data_ptr(), pairs[1][2].data_ptr(), 2, 65, 0],
-        [pairs[1][0].data_ptr(), pairs[1][2].data_ptr(), 2, 65, 1]]
-    assert plan.pairs[0][0] is pairs[0][0]
+@pytest.mark.parametrize("bm", [16, 64, 512])
+def test_tile_rows_cover_each_pair_exactly_once(bm):
+    rng = np.random.default_rng(bm)
+    ms = [0, 2, 31, 96, 97, 255, 256, 257, 1000] + rng.integers(0, 700, 6).tolist()
+    descs = [(0x4000 + 64 * i, 0x800000 + 64 * i, int(rng.integers(0, 4608)), m) for i, m in enumerate(ms)]
+    rows = _grouped_tile_rows(descs, bm)
+    covered = {}
+    for x, y, slot, m, pm in rows:
+        assert 0 <= pm * bm < m
+        covered.setdefault((x, y, slot, m), []).extend(range(pm * bm, min(m, (pm + 1) * bm)))
+    for d in descs:
+        assert covered.get(d, []) == list(range(d[3]))
+    assert len(rows) == sum(-(-m // bm) for m in ms)
 
 
-@pytest.mark.parametrize("bm", [0, 1, 15, 24, 63])
-def test_invalid_tile_height(bm):
+def test_plan_tables_follow_the_tensors_addresses():
+    K, N = 128, 48
+    xbuf = torch.empty(90 * K + 24, dtype=torch.bfloat16)
+    ybuf = torch.empty(90 * N + 40, dtype=torch.bfloat16)
+    xa = xbuf[8:8 + 70 * K].view(70, K)
+    xb = xbuf[8 + 70 * K:8 + 80 * K].view(10, K)
+    ya = ybuf[40:40 + 70 * N].view(70, N)
+    yb = ybuf[40 + 70 * N:40 + 80 * N].view(10, N)
+    plan = GroupedGemmPlan([(xa, 9, ya), (xb, 4, yb), (xa[:0], 3, ybuf[40 + 80 * N:40 + 90 * N].view(10, N)[:0])],
+                           block_m=32)
+    assert (plan.K, plan.N, plan.block_m, plan.slots, plan.ntiles) == (K, N, 32, (9, 4, 3), 4)
+    x0, y0 = xbuf.data_ptr() + 2 * 8, ybuf.data_ptr() + 2 * 40
+    assert plan.metadata.tolist() == [[x0, y0, 9, 70, 0], [x0, y0, 9, 70, 1], [x0, y0, 9, 70, 2],
+                                      [x0 + 2 * 70 * K, y0 + 2 * 70 * N, 4, 10, 0]]
+    assert plan.metadata.device.type == "cpu" and plan.metadata_host.shape == (4, 5)
+    assert plan.pairs[1][0] is xb
+
+
+@pytest.mark.parametrize("bm", [-16, 0, 8, 48, 100, 2 ** 20 + 1])
+def test_tile_height_must_be_a_power_of_two_of_16_or_more(bm):
     with pytest.raises(ValueError, match="power of two"):
-        _grouped_tile_rows((), bm)
+        _grouped_tile_rows([(0, 0, 0, 5)], bm)
 
 
-@pytest.mark.parametrize("desc", [(1, 2, -1, 3), (1, 2, 0, -3), (1, 2, 0, 2 ** 31), (-1, 2, 0, 3), (1, 2, 0)])
-def test_invalid_descriptor(desc):
+@pytest.mark.parametrize("desc", [(0x10, 0x20, -4, 8), (0x10, 0x20, 1, -1), (0x10, 0x20, 1, 2 ** 31),
+                                  (0x10, -0x20, 1, 8), (0x10, 0x20, 1), (0x10, 0x20, 1, 8, 0)])
+def test_malformed_descriptors_are_refused(desc):
     with pytest.raises(ValueError):
-        _grouped_tile_rows([desc], 64)
+        _grouped_tile_rows([desc], 16)
 
 
-def test_empty_pairs_are_safe():
-    assert GroupedGemmPlan([]).metadata.shape == (0, 5)
-    plan = GroupedGemmPlan([(torch.empty(0, 64, dtype=torch.bfloat16), 0, torch.empty(0, 16, dtype=torch.bfloat16))])
-    assert plan.ntiles == 0
+def test_plans_without_rows():
+    plan = GroupedGemmPlan([])
+    assert plan.ntiles == 0 and tuple(plan.metadata.shape) == (0, 5) and plan.slots == ()
+    z = torch.empty(0, 96, dtype=torch.bfloat16)
+    plan = GroupedGemmPlan([(z, 3, torch.empty(0, 8, dtype=torch.bfloat16)), (z, 5, torch.empty(0, 8,
+                                                                                             dtype=torch.bfloat16))])
+    assert plan.ntiles == 0 and plan.slots == (3, 5) and plan.aligned
 
 
-def test_alignment_hint_requires_both_pointers_and_row_pitches():
-    x = torch.empty(4, 64, dtype=torch.bfloat16)
-    y = torch.empty(4, 32, dtype=torch.bfloat16)
+def test_alignment_flag():
+    buf = torch.empty(4096, dtype=torch.bfloat16)
+    x, y = buf[:6 * 96].view(6, 96), buf[1024:1024 + 6 * 16].view(6, 16)
     assert GroupedGemmPlan([(x, 0, y)]).aligned
-    xp = torch.empty(4 * 64 + 1, dtype=torch.bfloat16)
-    yp = torch.empty(4 * 32 + 1, dtype=torch.bfloat16)
-    assert not GroupedGemmPlan([(xp[1:].view(4, 64), 0, y)]).aligned
-    assert not GroupedGemmPlan([(x, 0, yp[1:].view(4, 32))]).aligned
-    odd_pitch = torch.empty(4, 33, dtype=torch.bfloat16)
-    assert not GroupedGemmPlan([(x, 0, odd_pitch)]).aligned
-    assert GroupedGemmPlan([(x, 0, y), (x[:0], 1, y[:0])]).aligned
+    assert not GroupedGemmPlan([(buf[4:4 + 6 * 96].view(6, 96), 0, y)]).aligned            # 8-byte offset
+    assert not GroupedGemmPlan([(x, 0, buf[1025:1025 + 6 * 16].view(6, 16))]).aligned     # 2-byte offset
+    assert not GroupedGemmPlan([(x, 0, buf[1024:1024 + 6 * 12].view(6, 12))]).aligned     # 24-byte rows
+    assert GroupedGemmPlan([(x, 0, y), (buf[4:4].view(0, 96), 1, buf[2049:2049].view(0, 16))]).aligned  # empty: ignored
 
 
-def test_reject_overlapping_outputs_and_input_output_alias():
-    x = torch.empty(32, 64, dtype=torch.bfloat16)
-    y = torch.empty(32, 64, dtype=torch.bfloat16)
+def test_outputs_must_be_disjoint_from_each_other_and_the_inputs():
+    buf = torch.empty(64 * 64, dtype=torch.bfloat16)
+    a, b = buf[:8 * 64].view(8, 64), buf[8 * 64:16 * 64].view(8, 64)
+    GroupedGemmPlan([(a, 0, b), (a, 1, buf[16 * 64:24 * 64].view(8, 64))])              # repeated input: fine
     with pytest.raises(ValueError, match="output slices overlap"):
-        GroupedGemmPlan([(x[:16], 0, y[:16]), (x[16:], 1, y[8:24])])
+        GroupedGemmPlan([(a, 0, buf[16 * 64:24 * 64].view(8, 64)), (a, 1, buf[20 * 64:28 * 64].view(8, 64))])
     with pytest.raises(ValueError, match="overlap an input"):
-        GroupedGemmPlan([(x[:16], 0, x[16:]), (x[16:], 1, y[:16])])
+        GroupedGemmPlan([(a, 0, buf[4 * 64:12 * 64].view(8, 64))])
     with pytest.raises(ValueError, match="overlap an input"):
-        GroupedGemmPlan([(x, 0, x)])
+        GroupedGemmPlan([(a, 0, buf[30 * 64:38 * 64].view(8, 64)), (b, 1, a)])
 
 
-def test_reject_bad_shapes_dtypes_and_strides():
-    x = torch.empty(3, 64, dtype=torch.bfloat16)
-    y = torch.empty(3, 16, dtype=torch.bfloat16)
-    for pairs in ([(x, 0, y[:2])], [(x.float(), 0, y)], [(x[:, ::2], 0, y)],
-                  [(x, 0, y), (torch.empty(3, 32, dtype=torch.bfloat16), 1, y.clone())]):
+def test_pair_shapes_dtypes_strides_and_widths_are_checked():
+    x = torch.empty(5, 96, dtype=torch.bfloat16)
+    y = torch.empty(5, 24, dtype=torch.bfloat16)
+    bad = ([(x, 0, y[:4])],                                                 # row counts differ
+           [(x.half(), 0, y)],                                              # not bf16
+           [(x, 0, y.t().contiguous().t())],                                # not contiguous
+           [(x[:, :80], 0, y)],                                             # strided view
+           [(torch.empty(5, 48, dtype=torch.bfloat16), 0, y)],              # K not a multiple of 32
+           [(x, 0, y), (x, 1, torch.empty(5, 16, dtype=torch.bfloat16))],   # N differs between pairs
+           [(x.view(5, 96, 1), 0, y)])                                      # not 2-D
+    for pairs in bad:
         with pytest.raises(ValueError):
             GroupedGemmPlan(pairs)
 

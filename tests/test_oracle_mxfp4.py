@@ -54,7 +54,7 @@ def test_bf16_rounding_matches_torch():
 def _edge_slot(rng):
     """The known-answer edge rows of reference tools/scale_pack.py:122-125 on a synthetic slot."""
     raw = synth.slot_raw(rng, 105, 120)
-    sc = raw[sp.OFF_GS:].reshape(sp.NROWS, sp.GK)
+    sc = raw[sp.SCALES_AT:].reshape(sp.SCALE_ROWS, sp.GROUPS)
     sc[0, :] = 0
     sc[1, :] = 255
     sc[2, :] = 240
@@ -71,10 +71,10 @@ def test_ps4_known_answer_rows_round_trip():
     raw = _edge_slot(rng)
     for packer in (sp.pack_slot, mo.ps4_pack_slot):
         p = packer(raw)
-        assert p.shape == (sp.SLOT_PACKED,)
-        assert np.array_equal(p[:sp.OFF_GS], raw[:sp.OFF_GS])
+        assert p.shape == (sp.PS4_SLOT_BYTES,)
+        assert np.array_equal(p[:sp.SCALES_AT], raw[:sp.SCALES_AT])
         assert np.array_equal(sp.unpack_slot(p), raw) and np.array_equal(mo.ps4_unpack_slot(p), raw)
-    rows = sp.pack_slot(raw)[sp.OFF_GS:].reshape(sp.NROWS, sp.SR_P4)
+    rows = sp.pack_slot(raw)[sp.SCALES_AT:].reshape(sp.SCALE_ROWS, sp.PS4_ROW_BYTES)
     assert rows[0, 0] == 0 and not rows[0, 1:].any()                     # constant row: base, zero deltas
     assert rows[1, 0] == 255 and not rows[1, 1:].any()
     assert rows[2, 0] == 240 and rows[2, 1 + 17 // 2] >> 4 == 15         # group 17 (odd) in the high nibble
@@ -85,7 +85,7 @@ def test_ps4_known_answer_rows_round_trip():
 def test_ps4_span16_refused_never_clipped():
     rng = np.random.default_rng(2)
     raw = _edge_slot(rng)
-    sc = raw[sp.OFF_GS:].reshape(sp.NROWS, sp.GK)
+    sc = raw[sp.SCALES_AT:].reshape(sp.SCALE_ROWS, sp.GROUPS)
     sc[5, :] = 100
     sc[5, 44] = 116
     with pytest.raises(sp.SpanError) as ei:
@@ -97,7 +97,7 @@ def test_ps4_span16_refused_never_clipped():
 
 def test_ps4_product_codec_equals_oracle_codec():
     rng = np.random.default_rng(7)
-    sc = rng.integers(110, 126, size=(500, sp.GK)).astype(np.uint8)
+    sc = rng.integers(110, 126, size=(500, sp.GROUPS)).astype(np.uint8)
     assert np.array_equal(sp.pack_scale_rows(sc), mo.ps4_pack_rows(sc))
     assert np.array_equal(sp.unpack_scale_rows(sp.pack_scale_rows(sc)), sc)
 
@@ -130,7 +130,7 @@ def test_reference_c_kernel_reads_our_ps4_slots_bit_identically(experts4):
     assert np.array_equal(raw, packed)
     # negative control: one flipped delta nibble must change the output
     bad = sp.pack_slot(slots[0])
-    bad[sp.OFF_GS + 46 * 3000 + 20] ^= 0x01
+    bad[sp.SCALES_AT + 46 * 3000 + 20] ^= 0x01
     moved = ref.experts([bad] + [sp.pack_slot(s) for s in slots[1:]], x, bgu, bdn, w, threads=4, packed=True)
     assert not np.array_equal(moved, raw)
 

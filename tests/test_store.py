@@ -80,8 +80,8 @@ def test_store_files_and_metadata(stores):
     meta = json.load(open(os.path.join(stores["dst"], "metadata.json")))
     assert meta["magic"] == "Q80-PREPACKED-SLOTS" and meta["version"] == 1 and meta["model_id"] == MID
     assert meta["layout"]["weight_repr"] == "mxfp4_g32_ps4" and meta["layout"]["slot_bytes"] == 12_839_040
-    a = np.fromfile(os.path.join(stores["src"], "layer_0.slots"), np.uint8).reshape(2, sp.SLOT_RAW)
-    b = np.fromfile(os.path.join(stores["dst"], "layer_0.slots"), np.uint8).reshape(2, sp.SLOT_PACKED)
+    a = np.fromfile(os.path.join(stores["src"], "layer_0.slots"), np.uint8).reshape(2, sp.RAW_SLOT_BYTES)
+    b = np.fromfile(os.path.join(stores["dst"], "layer_0.slots"), np.uint8).reshape(2, sp.PS4_SLOT_BYTES)
     for e in range(2):
         assert np.array_equal(a[e], stores["slots"][e])
         assert np.array_equal(sp.unpack_slot(b[e]), a[e])

@@ -25,9 +25,9 @@ def test_codec_matches_byte_map(slot):
 
 def test_byte_map_is_a_bijection_onto_non_padding_bytes():
     m = to.source_to_dest_map()
-    assert np.unique(m).size == m.size == sp.SLOT_RAW
+    assert np.unique(m).size == m.size == sp.RAW_SLOT_BYTES
     pad = np.setdiff1d(np.arange(to.SLOT_T950), m)
-    assert pad.size == to.SLOT_T950 - sp.SLOT_RAW
+    assert pad.size == to.SLOT_T950 - sp.RAW_SLOT_BYTES
     off = pad % to.BLOCK
     assert (off >= to.CODE).all() and ((off - to.CODE) % to.PITCH >= 90).all()     # only scale-row padding
     # spot-check the closed form at the tile boundaries
@@ -103,7 +103,7 @@ def test_repack_kernels_equal_host_codec_and_round_trip():
     dev = _dev()
     rng = np.random.default_rng(8)
     raws = [synth.slot_raw(rng) for _ in range(3)]
-    raws[1][sp.OFF_GS:] = synth.slot_raw(rng, 100, 115)[sp.OFF_GS:]      # other exponents, span 15
+    raws[1][sp.SCALES_AT:] = synth.slot_raw(rng, 100, 115)[sp.SCALES_AT:]      # other exponents, span 15
     want = np.stack([tiles.slot_to_t950(r) for r in raws])
     src = torch.from_numpy(np.stack(raws)).to(dev)
     dst = torch.full((3, tiles.SLOT_T950), 0xAB, dtype=torch.uint8, device=dev)
