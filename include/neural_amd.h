@@ -117,6 +117,18 @@ int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
                        const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha, float limit,
                        int k_split, int down_mode, void* const* events, hipStream_t stream);
 
+/* na_moe_decode_t950 that allocates nothing and takes no scratch: h and the weighted expert outputs live in a
+ * file-scope device array of the library (368,640 bytes per device, for B <= 8; its address is looked up once per
+ * device on the first call there, with that device current).  No counterpart in the reference: it is for callers
+ * that cannot allocate or pass a workspace (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  out must not be NULL; B > 8 returns -3.  Every call on a device shares the array and leaves its last
+ * contents there: calls that overlap on one device (two streams, two threads) race.  Results equal
+ * na_moe_decode_t950's bit for bit. */
+int na_moe_decode_t950_noalloc(const void* x, const int64_t* topk_ids, const void* topk_w, int B, const void* pool,
+                               long long slot_bytes, const int64_t* slot_tab, long long expert_base,
+                               const void* bias_gu, const void* bias_dn, void* out, float alpha, float limit,
+                               int k_split, int down_mode, hipStream_t stream);
+
 /* ---- decode attention (GQA 64 query / 8 KV heads, head_dim 64, learned sinks, sliding window, rolling cache) */
 
 /* Floats of workspace na_decode_attention needs for B sequences and n_split chunks (-1 if out of range). */

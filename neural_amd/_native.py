@@ -32,6 +32,7 @@ SIGNATURES = {
     "na_repack_to_t950": [VP, I64, I32, VP, I64, I32, VP],
     "na_repack_from_t950": [VP, I64, VP, I64, I32, I32, VP],
     "na_moe_decode_t950": [VP, VP, VP, I32, VP, I64, VP, I64, VP, VP, VP, VP, VP, F32, F32, I32, I32, VP, VP],
+    "na_moe_decode_t950_noalloc": [VP, VP, VP, I32, VP, I64, VP, I64, VP, VP, VP, F32, F32, I32, I32, VP],
     "na_attn_workspace_floats": [I32, I32],
     "na_moe_prefill_workspace_bytes": [I32],
     "na_moe_prefill_workspace_layout": [I32, VP],

@@ -18,6 +18,7 @@
 #include <hip/hip_ext.h>
 
 #include <cmath>
+#include <mutex>
 
 namespace na {
 
@@ -806,6 +807,73 @@ static DownT pick_down_t950(int ks, int xt) {
   return ks == 4 ? down_t950_xt<4>(xt) : down_t950_xt<8>(xt);
 }
 
+// The t950 decode expert body of na_moe_decode_t950 with its scratch given: h (E4M3 hi + lo rows of the 4 B pairs,
+// 5,760 B each) and yw (bf16 weighted expert outputs of the pairs, 5,760 B each).
+static int decode_t950(const void* x, const int64_t* topk_ids, const void* topk_w, int B, const void* pool,
+                       long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
+                       const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha, float limit,
+                       int k_split, int down_mode, void* const* events, hipStream_t stream) {
+  if (!x || !topk_ids || !topk_w || !pool || !h_scratch || !yw_scratch || B <= 0) return kErrArgs;
+  if (down_mode != 0 && down_mode != 1) return kErrArgs;
+  if (B > 8) return kErrTooLarge;
+  if (slot_bytes < kTSlot || (slot_bytes & 15) || (reinterpret_cast<uintptr_t>(pool) & 15)) return kErrArgs;
+  if (k_split <= 0) k_split = 4;                    // automatic: the fastest measured on MI355X at every batch size
+  if (k_split != 4 && k_split != 8) return kErrArgs;
+  // down_mode 0, B = 1, with an output: gate_up, then down + combine (two launches); else gate_up, down, combine
+  // (at B = 2 the row-block kernel's 16-wave workgroups with two waves per expert measured slower than three launches)
+  const bool two = down_mode == 0 && out != nullptr && B == 1;
+  hipEvent_t ev[6] = {};
+  if (events)
+    for (int i = 0; i < (two ? 4 : 6); ++i) ev[i] = (hipEvent_t)events[i];
+  const uint32_t h8_sc = h8_scale_bytes(alpha, limit);
+  if (!h8_sc) return kErrArgs;
+  const int items = 4 * B;
+  const dim3 g1(items, kTDownBlocks);
+  const dim3 blk(64 * k_split);
+  const int xt = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
+  launch_t(pick_gate_up_t950(k_split, xt), g1, blk, stream, ev[0], ev[1], topk_ids, B, (const uint8_t*)pool,
+           slot_bytes, slot_tab, expert_base, (const uint16_t*)x, (const uint16_t*)bias_gu, (uint8_t*)h_scratch,
+           alpha, limit, h8_sc);
+  if (two) {
+    launch_t(k_moe_down_comb_t950, dim3(kTDownBlocks), dim3(64 * kDcWaves), stream, ev[2], ev[3], topk_ids, B,
+             (const uint8_t*)pool, slot_bytes, slot_tab, expert_base, (const uint8_t*)h_scratch,
+             (const uint16_t*)topk_w, (const uint16_t*)bias_dn, (uint16_t*)out, h8_sc);
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+  }
+  launch_t(pick_down_t950(k_split, xt), g1, blk, stream, ev[2], ev[3], topk_ids, B, (const uint8_t*)pool, slot_bytes,
+           slot_tab, expert_base, (const uint8_t*)h_scratch, (const uint16_t*)topk_w, (const uint16_t*)bias_dn,
+           (uint16_t*)yw_scratch, h8_sc);
+  if (out)
+    launch_t(k_combine_t950, dim3((B * kH / 2 + 255) / 256), dim3(256), stream, ev[4], ev[5],
+             (const uint32_t*)yw_scratch, B, (uint32_t*)out);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+// Scratch of na_moe_decode_t950_noalloc: h then yw of up to 8 tokens (32 pairs x 5,760 B each), 368,640 B per
+// device, held from the library's load until the process ends.  Every call on a device uses the same bytes: calls
+// that overlap on one device race.  Both parts are written before they are read in every call, so nothing needs
+// to start at zero.
+constexpr int kNoAllocMaxB = 8;
+constexpr long long kNoAllocPart = 4LL * kNoAllocMaxB * 2 * kH;
+static __device__ __align__(256) uint8_t scratch[2 * kNoAllocPart];
+
+// Device address of `scratch` on the current device, looked up once per device with hipGetSymbolAddress (the array's
+// host-side name is only a stand-in); nullptr if the lookup fails.
+static void* scratch_address() {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    addr[dev] = p;
+  }
+  return addr[dev];
+}
+
 }  // namespace na
 
 using namespace na;
@@ -844,40 +912,20 @@ int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
                        long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
                        const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha, float limit,
                        int k_split, int down_mode, void* const* events, hipStream_t stream) {
-  if (!x || !topk_ids || !topk_w || !pool || !h_scratch || !yw_scratch || B <= 0) return kErrArgs;
-  if (down_mode != 0 && down_mode != 1) return kErrArgs;
-  if (B > 8) return kErrTooLarge;
-  if (slot_bytes < kTSlot || (slot_bytes & 15) || (reinterpret_cast<uintptr_t>(pool) & 15)) return kErrArgs;
-  if (k_split <= 0) k_split = 4;                    // automatic: the fastest measured on MI355X at every batch size
-  if (k_split != 4 && k_split != 8) return kErrArgs;
-  // down_mode 0, B = 1, with an output: gate_up, then down + combine (two launches); else gate_up, down, combine
-  // (at B = 2 the row-block kernel's 16-wave workgroups with two waves per expert measured slower than three launches)
-  const bool two = down_mode == 0 && out != nullptr && B == 1;
-  hipEvent_t ev[6] = {};
-  if (events)
-    for (int i = 0; i < (two ? 4 : 6); ++i) ev[i] = (hipEvent_t)events[i];
-  const uint32_t h8_sc = h8_scale_bytes(alpha, limit);
-  if (!h8_sc) return kErrArgs;
-  const int items = 4 * B;
-  const dim3 g1(items, kTDownBlocks);
-  const dim3 blk(64 * k_split);
-  const int xt = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
-  launch_t(pick_gate_up_t950(k_split, xt), g1, blk, stream, ev[0], ev[1], topk_ids, B, (const uint8_t*)pool,
-           slot_bytes, slot_tab, expert_base, (const uint16_t*)x, (const uint16_t*)bias_gu, (uint8_t*)h_scratch,
-           alpha, limit, h8_sc);
-  if (two) {
-    launch_t(k_moe_down_comb_t950, dim3(kTDownBlocks), dim3(64 * kDcWaves), stream, ev[2], ev[3], topk_ids, B,
-             (const uint8_t*)pool, slot_bytes, slot_tab, expert_base, (const uint8_t*)h_scratch,
-             (const uint16_t*)topk_w, (const uint16_t*)bias_dn, (uint16_t*)out, h8_sc);
-    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
-  }
-  launch_t(pick_down_t950(k_split, xt), g1, blk, stream, ev[2], ev[3], topk_ids, B, (const uint8_t*)pool, slot_bytes,
-           slot_tab, expert_base, (const uint8_t*)h_scratch, (const uint16_t*)topk_w, (const uint16_t*)bias_dn,
-           (uint16_t*)yw_scratch, h8_sc);
-  if (out)
-    launch_t(k_combine_t950, dim3((B * kH / 2 + 255) / 256), dim3(256), stream, ev[4], ev[5],
-             (const uint32_t*)yw_scratch, B, (uint32_t*)out);
-  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+  return decode_t950(x, topk_ids, topk_w, B, pool, slot_bytes, slot_tab, expert_base, bias_gu, bias_dn, h_scratch,
+                     yw_scratch, out, alpha, limit, k_split, down_mode, events, stream);
+}
+
+int na_moe_decode_t950_noalloc(const void* x, const int64_t* topk_ids, const void* topk_w, int B, const void* pool,
+                               long long slot_bytes, const int64_t* slot_tab, long long expert_base,
+                               const void* bias_gu, const void* bias_dn, void* out, float alpha, float limit,
+                               int k_split, int down_mode, hipStream_t stream) {
+  if (!out) return kErrArgs;                         // the result must leave the shared scratch
+  if (B > kNoAllocMaxB) return kErrTooLarge;
+  uint8_t* base = static_cast<uint8_t*>(scratch_address());
+  if (!base) return kErrLaunch;
+  return decode_t950(x, topk_ids, topk_w, B, pool, slot_bytes, slot_tab, expert_base, bias_gu, bias_dn, base,
+                     base + kNoAllocPart, out, alpha, limit, k_split, down_mode, nullptr, stream);
 }
 
 }  // extern "C"
