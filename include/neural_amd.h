@@ -249,6 +249,17 @@ int na_core_oproj(const void* att, const void* Wo, const void* bo, const void* x
 int na_core_router(const void* mid, const void* post_w, float eps, const void* Wr, const void* br, void* hn,
                    float* logits, unsigned int* counter, int64_t* ids, void* wts, hipStream_t stream);
 
+/* The serving bookkeeping of a layer's routing, after na_core_router (one launch).  Replaces the stores of
+ * fused_core.py:417-441 (k_router: bx, pack[:H]) and :443-502 (k_topk's _emit and near misses) that feed the expert
+ * body and the host.  hn bf16 [2880], ids int64 [4], wts bf16 [4]: na_core_router's outputs; logits fp32 [128]: its
+ * logits (needed for near_miss).  slot_tab int64 (NULL: every expert resident at slot base + id), base = layer * 128.
+ * Outputs: bx bf16 [2880] <- hn (or NULL); pack fp32 [2880 + 12] (+4 with near_miss, or NULL) <- hn | weights | ids
+ * | resident flags (| ids of ranks 5-8); bslots int64 [4] (slot, 0 if not resident), bgids int64 [4] (base + id),
+ * bw bf16 [4] (weight, +0 if not resident). */
+int na_core_route_pack(const void* hn, const float* logits, const int64_t* ids, const void* wts,
+                       const int64_t* slot_tab, long long base, void* bx, float* pack, int near_miss, int64_t* bslots,
+                       int64_t* bgids, void* bw, hipStream_t stream);
+
 /* Workgroup partials na_core_lm_tail needs for a vocabulary (-1 if vocab <= 0). */
 long long na_core_lm_partials(int vocab);
 

@@ -45,6 +45,7 @@ SIGNATURES = {
     "na_core_oproj": [VP, VP, VP, VP, VP, VP],
     "na_core_router": [VP, VP, F32, VP, VP, VP, VP, VP, VP, VP, VP],
     "na_core_lm_partials": [I32],
+    "na_core_route_pack": [VP, VP, VP, VP, VP, I64, VP, VP, I32, VP, VP, VP, VP],
     "na_core_lm_tail": [VP, VP, VP, VP, F32, VP, I32, VP, VP, VP, VP, VP, I32, VP, VP, VP, I64, VP],
     "na_prefill_attention": [VP, VP, VP, I64, VP, VP, I64, I64, I64, I64, VP, VP, I64, I32, F32, I32, I32, VP, VP],
     "na_ring_write": [VP, VP, I32, VP, VP, I64, I64, I64, I64, I64, I32, VP],

@@ -572,6 +572,68 @@ __global__ __launch_bounds__(256) void k_rows_topk(const uint16_t* __restrict__ 
   top4_softmax(bf16_to_f32(lr[lane]), bf16_to_f32(lr[lane + 64]), lane, ids + 4 * t, wts + 4 * t);
 }
 
+
+// The serving bookkeeping around a routing na_core_router computed (reference fused_core.py:417-502, the k_router /
+// k_topk stores beyond the logits): bx <- hn; pack[0, H) <- hn widened to fp32; for rank j with expert i_j, weight
+// w_j, global id g = base + i_j and slot s = slot_tab ? slot_tab[g] : g (resident iff s >= 0): bslots[j] = s or 0,
+// bgids[j] = g, bw[j] = w_j or +0, pack[H + j] = w_j, pack[H + 4 + j] = i_j, pack[H + 8 + j] = 1 or 0; with
+// near_miss, pack[H + 12 + r] = the expert of rank 5 + r (repeated argmax of the logits without the top 4, lowest
+// index on ties).  One workgroup.
+__global__ __launch_bounds__(256) void k_route_pack(const uint16_t* __restrict__ hn, const float* __restrict__ logits,
+                                                    const int64_t* __restrict__ ids, const uint16_t* __restrict__ wts,
+                                                    const int64_t* __restrict__ slot_tab, long long base,
+                                                    uint16_t* __restrict__ bx, float* __restrict__ pack,
+                                                    int64_t* __restrict__ bslots, int64_t* __restrict__ bgids,
+                                                    uint16_t* __restrict__ bw, int near_miss) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kH; i += 256) {
+    const uint16_t h = hn[i];
+    if (bx) bx[i] = h;
+    if (pack) pack[i] = bf16_to_f32(h);
+  }
+  if (tid < 4) {
+    const int64_t e = ids[tid];
+    const long long g = base + e;
+    const int64_t s = slot_tab ? slot_tab[g] : g;
+    const bool hit = s >= 0;
+    bslots[tid] = hit ? s : 0;
+    bgids[tid] = g;
+    bw[tid] = hit ? wts[tid] : (uint16_t)0;
+    if (pack) {
+      pack[kH + tid] = bf16_to_f32(wts[tid]);
+      pack[kH + 4 + tid] = (float)e;
+      pack[kH + 8 + tid] = hit ? 1.f : 0.f;
+    }
+  }
+  if (!near_miss || tid >= 64) return;
+  float v0 = logits[tid], v1 = logits[tid + 64];
+  for (int j = 0; j < 4; ++j) {
+    const int64_t e = ids[j];
+    if (e == tid) v0 = -INFINITY;
+    if (e == tid + 64) v1 = -INFINITY;
+  }
+  for (int r = 0; r < 4; ++r) {
+    float v = v0;
+    int i = tid;
+    if (v1 > v) {                                   // ties keep the lower index
+      v = v1;
+      i = tid + 64;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(v, o);
+      const int oi = __shfl_xor(i, o);
+      if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+      }
+    }
+    if (tid == 0) pack[kH + 12 + r] = (float)i;
+    if (i == tid) v0 = -INFINITY;
+    if (i == tid + 64) v1 = -INFINITY;
+  }
+}
+
 }  // namespace na
 
 using namespace na;
@@ -612,6 +674,18 @@ int na_core_router(const void* mid, const void* post_w, float eps, const void* W
   hipLaunchKernelGGL(k_router_norm<kRouterTpr>, dim3(kNE / (256 / kRouterTpr)), dim3(256), 0, stream, (const uint16_t*)mid,
                      (const uint16_t*)post_w, eps, (const uint16_t*)Wr, (const uint16_t*)br, (uint16_t*)hn, logits,
                      (uint32_t*)counter, ids, (uint16_t*)wts);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int na_core_route_pack(const void* hn, const float* logits, const int64_t* ids, const void* wts,
+                       const int64_t* slot_tab, long long base, void* bx, float* pack, int near_miss, int64_t* bslots,
+                       int64_t* bgids, void* bw, hipStream_t stream) {
+  if (!ids || !wts || !bslots || !bgids || !bw || base < 0) return kErrArgs;
+  if ((bx || pack) && !hn) return kErrArgs;
+  if (near_miss && (!pack || !logits)) return kErrArgs;
+  hipLaunchKernelGGL(k_route_pack, dim3(1), dim3(256), 0, stream, (const uint16_t*)hn, logits, ids,
+                     (const uint16_t*)wts, slot_tab, base, (uint16_t*)bx, pack, bslots, bgids, (uint16_t*)bw,
+                     near_miss ? 1 : 0);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
