@@ -1,23 +1,30 @@
 """Benchmark of the GPT-OSS-120B MoE decode hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B] [--packed] [--skip-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--workload decode|experts|model|prefill|attention]
 
-Workload (configuration 1 of the benchmark plan): all 36 layers x 128 experts resident in one HBM pool (60.9 GB raw
-MXFP4 slots: uniform E2M1 codes, E8M0 exponents uniform in [119, 125]); B decode tokens; per token and layer, top-4
-of 128 experts from random router logits, softmax weights.  One STEP = the expert body of all 36 layers in sequence
-(per layer: gate_up GEMV + bias + clamped SwiGLU; down GEMV + bias + routing weight; top-k combine), captured as
-one hipGraph per routing set; 16 routing sets are cycled so the 256 MB Infinity Cache never serves a repeated
-expert.  With the t950 layout and B <= 2 the body of a layer is two launches (gate_up; down with the top-k combine),
-else three.  value = decode tokens per second of that step (B tokens per step), whole job.
-
-Also printed on the same JSON line:
-  roofline      the dominant kernel (gate_up): algorithmic bytes per launch (distinct experts x 8,812,800 B of E2M1
-                codes + E8M0 scales) / its average launch duration, measured with events timestamped by the
-                dispatches themselves (hipExtLaunchKernel) on the launch stream, over an eager pass of the same
-                steps queued behind a spin kernel (so the launches run back to back, as in the graph replays);
-                peak = 8 TB/s.
+Default workload ("decode"): one resident pool of all 36 layers x 128 MXFP4 experts (gfx950 tile layout, 61.2 GB,
+uniform E2M1 codes, E8M0 exponents uniform in [119, 125]) serves two measurements, printed as ONE JSON line:
+  value         configuration 4: full 36-layer GPT-OSS-120B-shaped greedy decode, random-init weights (vocab 201,088),
+                a 4096-token random context prefilled, then exactly K greedy tokens timed, one hipGraph replay per
+                token (embed, 36 x [QKV + RoPE + cache write, attention, o_proj, router + top-4, experts], lm_head +
+                argmax; the next step reads its token on the device).  value = tokens/s.
+  config1       configuration 1: the expert body alone (gate_up GEMV + bias + clamped SwiGLU, down GEMV + bias +
+                routing weight, top-k combine) of all 36 layers per step, random top-4 routing from 16 routing sets
+                cycled so the 256 MB Infinity Cache never serves a repeated expert; batch 1 plus the batch 2 / 4 / 8
+                sweep; whole-step HBM GB/s.
+  roofline      the dominant expert kernel (gate_up) of configuration 1 at batch 1: algorithmic bytes per launch
+                (4 experts x 8,812,800 B of E2M1 codes + E8M0 scales) / its average launch duration, from events
+                timestamped by the dispatches themselves on the launch stream (eager steps queued behind a spin
+                kernel, so the launches run back to back as in the graph replays); peak 8 TB/s; traffic = HBM bytes
+                per launch from the committed rocprofv3 --pmc table (null when the kernel sources changed since).
   cpu_baseline  the reference's own C expert kernel (kernels/gptoss_cpu_multi.c, AVX-512, or gptoss_cpu_portable.c,
-                built from source into oracle/_ref/) on this host's cores over a bounded sample of the same workload.
+                built from source into oracle/_ref/) on this host's cores: configuration 1's expert body, one
+                gptoss_experts(E=4) call per layer per token, at all physical cores of one socket (capped at the CPUs
+                this process may use) and at the reference's default of 8 threads.
+
+Other workloads print one line each: experts (configuration 1 alone, any layout), model (configuration 4 alone),
+prefill (configuration 2, with the reference CPU kernel's multi-token call as its baseline), attention
+(configuration 3).
 """
 from __future__ import annotations
 
@@ -98,33 +105,73 @@ def routing_sets(rng, n_sets, B):
     return ids.astype(np.int64), w
 
 
-def cpu_baseline(pool_dev, ids, B, seconds=12.0):
-    """The reference C kernel on host cores: gptoss_experts(4, ...) per token per layer (the reference has no batched
-    CPU decode), over a 160-expert (2.1 GB) host copy of the pool rotated per call so no CPU cache level can hold it.
-    ids: [36, B, 4] routing of one step; its distinct (layer, expert) slots, topped up with following slots, are
-    copied."""
+def cpu_info():
+    """CPU model, sockets, physical cores of the first socket, and the CPUs this process may use (affinity, capped
+    by a cgroup CPU quota when one is set)."""
+    model, sockets, cores0, phys = None, set(), set(), None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                    sockets.add(v)
+                elif k == "core id" and phys == min(sockets):
+                    cores0.add(v)
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as fh:
+            q, per = fh.read().split()[:2]
+            if q != "max":
+                quota = max(1, int(int(q) // int(per)))
+    except (OSError, ValueError):
+        pass
+    return {"model": model, "sockets": len(sockets) or None, "socket0_physical_cores": len(cores0) or None,
+            "affinity_cpus": usable, "cgroup_cpus": quota, "usable_cpus": min(usable, quota or usable)}
+
+
+def host_expert_slots(pool_dev, ids, n=160):
+    """Store-layout host copies of ``n`` experts of the pool: the distinct (layer, expert) slots of one routing
+    ids [36, B, 4], topped up with following slots (160 experts = 2.1 GB, so no CPU cache level holds them)."""
     import torch
 
-    from oracle.refkernels import RefExperts, cpu_has
+    from neural_amd import tiles
+    from neural_amd.moe.layout import GPTOSS_LAYOUT
 
-    name = "multi" if cpu_has("avx512f") else "portable"
-    ref = RefExperts(name)
-    threads = min(16, os.cpu_count() or 1)
     uniq = []
     for l in range(ids.shape[0]):
         for e in ids[l].reshape(-1).tolist():
             g = l * N_EXPERTS + int(e)
-            if g not in uniq and len(uniq) < 160:
+            if g not in uniq and len(uniq) < n:
                 uniq.append(g)
     g = 0
-    while len(uniq) < 160:
+    while len(uniq) < n:
         if g not in uniq:
             uniq.append(g)
         g += 1
-    host = [pool_dev[g].cpu().numpy() for g in uniq]
-    if host[0].size != SLOT_ALGO_BYTES:                    # t950 pool: the reference kernel reads the store layout
-        from neural_amd import tiles
-        host = [tiles.t950_to_slot(h) for h in host]
+    if pool_dev.shape[1] == SLOT_ALGO_BYTES:
+        return [pool_dev[g].cpu().numpy() for g in uniq]
+    buf = torch.empty(1, GPTOSS_LAYOUT.slot_bytes, dtype=torch.uint8, device=pool_dev.device)
+    out = []
+    for g in uniq:                                       # t950 pool: the reference kernel reads the store layout
+        tiles.repack_from_t950(pool_dev[g:g + 1], buf)
+        out.append(buf.cpu().numpy()[0].copy())
+    return out
+
+
+def cpu_baseline(host, threads, seconds=10.0):
+    """The reference C kernel on ``threads`` host cores: gptoss_experts(4, ...) per token per layer (the reference has
+    no batched CPU decode), rotating over the host expert copies so that every call reads cold slots."""
+    from oracle.refkernels import RefExperts, cpu_has
+
+    name = "multi" if cpu_has("avx512f") else "portable"
+    ref = RefExperts(name)
     rng = np.random.default_rng(5)
     x = rng.standard_normal(H).astype(np.float32)
     bgu = [np.zeros(5760, np.float32)] * 4
@@ -141,13 +188,79 @@ def cpu_baseline(pool_dev, ids, B, seconds=12.0):
         if el >= seconds and n >= N_LAYERS:
             break
     t_call = el / n
-    tok_s = 1.0 / (N_LAYERS * t_call)
-    return {"value": round(tok_s, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
-            "sample": f"{n} calls of gptoss_experts(E=4) (libgptoss_{name}.so, {threads} OpenMP threads) over a "
-                      f"{len(host)}-expert host copy rotated per call; one call = one layer of one token; "
-                      f"{t_call * 1e3:.3f} ms/call -> {4 * SLOT_ALGO_BYTES / t_call / 1e9:.1f} GB/s; "
-                      f"tok/s = 1 / (36 x ms/call)",
-            "gbps": round(4 * SLOT_ALGO_BYTES / t_call / 1e9, 2)}
+    return {"value": round(1.0 / (N_LAYERS * t_call), 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "library": f"libgptoss_{name}.so",
+            "sample": f"{n} calls of gptoss_experts(E=4) ({threads} OpenMP threads) over a {len(host)}-expert host "
+                      f"copy rotated per call; one call = the expert body of one layer for one token; "
+                      f"{t_call * 1e3:.3f} ms/call; tok/s = 1 / (36 x ms/call) (experts only: the reference has no "
+                      f"CPU dense core)",
+            "ms_per_call": round(t_call * 1e3, 4), "gbps": round(4 * SLOT_ALGO_BYTES / t_call / 1e9, 2)}
+
+
+def cpu_baselines(pool_dev, ids, seconds):
+    """cpu_baseline at all physical cores of the first socket (capped at the usable CPUs) and at 8 threads (the
+    reference server's default, server.py:107), with the host CPU described."""
+    info = cpu_info()
+    host = host_expert_slots(pool_dev, ids)
+    t_sock = min(info["socket0_physical_cores"] or info["usable_cpus"], info["usable_cpus"])
+    os.environ.setdefault("OMP_PROC_BIND", "close")
+    main = cpu_baseline(host, t_sock, seconds)
+    res = dict(main)
+    res["cpu"] = info
+    res["threads_rule"] = (f"min(physical cores of socket 0 = {info['socket0_physical_cores']}, CPUs this process "
+                           f"may use = {info['usable_cpus']})")
+    res["build"] = ("oracle/Makefile from the reference's kernels/*.c, gcc -O3 -fopenmp; libgptoss_multi.so adds "
+                    "-Dsb_inited=1, a declaration kernels/gptoss_cpu_cap2.c:113 makes only on Win32")
+    if t_sock != 8:
+        t8 = cpu_baseline(host, 8, seconds)
+        res["threads_8"] = {k: t8[k] for k in ("value", "cores", "ms_per_call", "gbps")}
+    return res
+
+
+def cpu_prefill_baseline(pool_dev, ids, w, x, threads, seconds):
+    """The reference CPU kernels' prompt path over one MoE layer (cpu_prefill.py:15-19, 118-315): the pairs grouped
+    by expert (stable in the token index), gptoss_experts_multi with unit pair weights, then gptoss_combine_pairs in
+    top-k order.  Timed: the two C calls, repeated until ``seconds`` have passed (at least once)."""
+    import torch
+
+    from neural_amd import tiles
+    from neural_amd.moe.layout import GPTOSS_LAYOUT
+    from oracle.refkernels import RefExperts
+
+    ref = RefExperts("multi")
+    T = ids.shape[0]
+    flat = ids.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    experts, counts = np.unique(flat, return_counts=True)
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    buf = torch.empty(1, GPTOSS_LAYOUT.slot_bytes, dtype=torch.uint8, device=pool_dev.device)
+    host = []
+    for e in experts:
+        tiles.repack_from_t950(pool_dev[int(e):int(e) + 1], buf)
+        host.append(buf.cpu().numpy()[0].copy())
+    X = np.ascontiguousarray(x[order // TOPK], np.float32)
+    ones = np.ones(len(order), np.float32)
+    idx = np.empty(T * TOPK, np.int32)
+    idx[order] = np.arange(len(order), dtype=np.int32)
+    idx = idx.reshape(T, TOPK)
+    bgu = [np.zeros(5760, np.float32)] * len(experts)
+    bdn = [np.zeros(2880, np.float32)] * len(experts)
+    ref.experts_multi(host[:1], [0, 1], X[:1], ones[:1], bgu[:1], bdn[:1], threads=threads)    # thread pool start
+    n, t0 = 0, time.perf_counter()
+    while True:
+        Y = ref.experts_multi(host, off, X, ones, bgu, bdn, threads=threads)
+        ref.combine_pairs(idx, w, Y, threads=threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    t_layer = el / n
+    return {"value": round(T / t_layer, 2), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "library": "libgptoss_multi.so",
+            "sample": f"the whole configuration-2 layer ({T} tokens, {len(order)} pairs over {len(experts)} experts), "
+                      f"{n} run(s) of gptoss_experts_multi (unit pair weights) + gptoss_combine_pairs on {threads} "
+                      f"OpenMP threads: {t_layer * 1e3:.1f} ms per layer",
+            "ms_per_layer": round(t_layer * 1e3, 2), "cpu": cpu_info()}
 
 
 def bench_prefill(A):
@@ -224,6 +337,18 @@ def bench_prefill(A):
     log(f"prefill T={T}: {el * 1e6:.1f} us/layer ({T / el:.0f} tok/s), {flop / el / 1e12:.1f} TFLOP/s; launches "
         + ", ".join(f"{nm} {v:.1f} us" for nm, v in per.items()))
     gu_flop = 2.0 * P * 5760 * 2880
+    cpu = None
+    if not A.skip_cpu:
+        try:
+            info = cpu_info()
+            threads = min(info["socket0_physical_cores"] or info["usable_cpus"], info["usable_cpus"])
+            log(f"cpu baseline (reference multi-token kernel, {threads} threads) ...")
+            cpu = cpu_prefill_baseline(pool, ids_np, wts.float().cpu().numpy(), x.float().cpu().numpy(), threads,
+                                       A.cpu_seconds)
+            log(f"cpu baseline: {cpu['value']} tok/s ({cpu['ms_per_layer']} ms per layer)")
+        except Exception as e:      # the baseline is reported, not required
+            log(f"cpu baseline unavailable: {e!r}")
+            cpu = {"value": None, "unit": "tok/s", "cores": 0, "kind": "reference", "sample": f"unavailable: {e}"}
     res = {"metric": "prefill MoE layer tokens/s (config 2)", "value": round(T / el, 1), "unit": "tok/s", "n_gpus": 1,
            "steps": steps, "ms_per_step": round(el * 1e3, 4), "higher_is_better": True, "dtype": "bf16",
            "data": "synthetic",
@@ -243,35 +368,29 @@ def bench_prefill(A):
                         "kernel": "k_prefill_gate_up + k_prefill_down",
                         "mfma_frac_exact": round(flop / el / 2.5e15, 4),
                         "mfma_frac_fp4_peak": round(flop / el / 10.1e15, 4)},
-           "cpu_baseline": None}
+           "cpu_baseline": cpu}
     print(json.dumps(res), flush=True)
 
 
-def bench_model(A):
-    """Configuration 4: full 36-layer GPT-OSS-120B-shaped greedy decode on one GPU.  Random-init weights (attention,
-    router, embedding and lm_head bf16 N(0, 0.02), norms 1 + N(0, 0.02), sinks N(0, 1), vocab 201088), all 36 x 128
-    MXFP4 experts resident (t950 layout, 61.2 GB), a context of 4096 random token ids prefilled (DecodeModel.prefill:
-    the prompt through every layer at once, its K/V written into the caches and its greedy successor appended; or,
-    with --context-mode decode, read token by token through the decode step), then greedy decode with one hipGraph
-    per step (embed, 36 x [QKV + RoPE +
+def run_model(A, pool, dev):
+    """Configuration 4 on a resident t950 pool: full 36-layer GPT-OSS-120B-shaped greedy decode on one GPU.
+    Random-init weights (attention, router, embedding and lm_head bf16 N(0, 0.02), norms 1 + N(0, 0.02), sinks N(0, 1),
+    vocab 201088), a context of 4096 random token ids prefilled (DecodeModel.prefill: the prompt through every layer
+    at once, its K/V written into the caches and its greedy successor appended; or, with --context-mode decode, read
+    token by token through the decode step), then greedy decode with one hipGraph per step (embed, 36 x [QKV + RoPE +
     cache write, attention, o_proj, router + top-4, experts], final norm + lm_head + argmax; the next step reads its
     token on the device).  Timed: exactly --steps greedy steps from the end of the context; the warm-up steps run
-    from the same context snapshot and are rolled back.  value = tokens / s.  The roofline is the expert gate_up
-    kernel's (the step's largest share), from dispatch-timestamped events over one eager step."""
+    from the same context snapshot and are rolled back; a second run from the snapshot must give the same tokens.
+    Per-launch times come from dispatch-timestamped events over eager steps.  Returns a dict of the results."""
     import torch
 
     from neural_amd.model import DecodeModel, random_weights
     from neural_amd.moe.experts import ResidentExperts
     from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
 
-    dev = torch.device("cuda", 0)
     ctx, n_new = A.context, A.steps
-    log(f"model: building the expert pool ({N_LAYERS * N_EXPERTS} slots, t950)")
-    from neural_amd import synth
-
-    pool = synth.t950_pool_device(N_LAYERS * N_EXPERTS, dev, 4242)
-    L = GPTOSS_LAYOUT_T950
-    rx = ResidentExperts(pool, L, None, None, max_batch=1, k_split=A.k_split, combine_in_down=A.down != "expert")
+    rx = ResidentExperts(pool, GPTOSS_LAYOUT_T950, None, None, max_batch=1, k_split=A.k_split,
+                         combine_in_down=A.down != "expert")
     log("model: random-init dense weights")
     w = random_weights(device=dev, seed=77)
     smax = ctx + max(n_new, A.warmup) + 2
@@ -316,7 +435,7 @@ def bench_model(A):
     model.run(n_new)
     torch.cuda.synchronize()
     same = bool(np.array_equal(model.seq[t_lo + 1:t_lo + 1 + n_new].cpu().numpy(), toks))
-    # ------------------------------------------------------------------ per-kernel events (one eager step)
+    # ------------------------------------------------------------------ per-kernel events (eager steps)
     model.restore(snap)
     names = rx.launches(1)
     ev = []
@@ -342,39 +461,62 @@ def bench_model(A):
                 att_slide += a
             else:
                 att_full += a
+    model.restore(snap)
     n_l = R * N_LAYERS
     avg = {nm: acc[nm] / n_l for nm in names}
-    dom = names[0]
-    gu_bytes = TOPK * GATE_UP_BYTES
-    gu_gbps = gu_bytes / (avg[dom] * 1e-6) / 1e9
-    kname = "k_moe_gate_up_t950"
     log("model: per launch " + ", ".join(f"{nm} {v:.2f} us" for nm, v in avg.items())
         + f", attention full {att_full / (n_l / 2):.2f} us, sliding {att_slide / (n_l / 2):.2f} us")
-    traffic, why = measured_traffic(kname, "t950", 1, effective_k_split(A.k_split, 1))
     dense = N_LAYERS * 2 * (5120 * 2880 + 2880 * 4096 + 128 * 2880) + 2 * 201088 * 2880
     experts = N_LAYERS * TOPK * SLOT_ALGO_BYTES
     kv = 2 * 2 * 8 * 64 * (18 * (ctx + n_new / 2) + 18 * 128)
     step_bytes = dense + experts + kv
-    res = {"metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": n_new,
-           "warmup": A.warmup, "ms_per_step": round(el / n_new * 1e3, 4), "higher_is_better": True,
-           "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-           "config": {"workload": f"config4: full 36-layer GPT-OSS-120B-shaped greedy decode, random-init weights, "
-                                  f"{ctx}-token context, {n_new} tokens, one hipGraph per step, experts t950 resident",
-                      "context": ctx, "tokens": n_new, "vocab": int(w.vocab), "attn_split_full": A.attn_split,
-                      "attn_split_sliding": A.sliding_split, "deterministic_tokens": same,
-                      "first_tokens": [int(t) for t in toks[:8]],
-                      "step_algorithmic_gb": round(step_bytes / 1e9, 3),
-                      "step_hbm_gbps": round(step_bytes / (el / n_new) / 1e9, 1),
-                      "launch_us": {**{nm: round(v, 2) for nm, v in avg.items()},
-                                    "attention_full": round(att_full / (n_l / 2), 2),
-                                    "attention_sliding": round(att_slide / (n_l / 2), 2)},
-                      "context_mode": A.context_mode,
-                      **({"context_prefill_ms": round(t_ctx * 1e3, 1), "prefill_tok_s": round(ctx / t_ctx, 1),
-                          "prefill_chunk": A.prefill_chunk} if A.context_mode == "prefill" else
-                         {"context_steps_per_s": round((ctx - 1) / t_ctx, 1)})},
-           "roofline": {"bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(gu_gbps / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kname,
-                        "avg_launch_us": round(avg[dom], 3), "algorithmic_bytes_per_launch": gu_bytes},
+    cfg = {"workload": f"config4: full 36-layer GPT-OSS-120B-shaped greedy decode, random-init weights, "
+                       f"{ctx}-token context, {n_new} tokens, one hipGraph per step, experts t950 resident",
+           "context": ctx, "tokens": n_new, "vocab": int(w.vocab), "attn_split_full": A.attn_split,
+           "attn_split_sliding": A.sliding_split, "deterministic_tokens": same,
+           "first_tokens": [int(t) for t in toks[:8]],
+           "step_algorithmic_gb": round(step_bytes / 1e9, 3),
+           "step_hbm_gbps": round(step_bytes / (el / n_new) / 1e9, 1),
+           "launch_us": {**{nm: round(v, 2) for nm, v in avg.items()},
+                         "attention_full": round(att_full / (n_l / 2), 2),
+                         "attention_sliding": round(att_slide / (n_l / 2), 2)},
+           "context_mode": A.context_mode,
+           **({"context_prefill_ms": round(t_ctx * 1e3, 1), "prefill_tok_s": round(ctx / t_ctx, 1),
+               "prefill_chunk": A.prefill_chunk} if A.context_mode == "prefill" else
+              {"context_steps_per_s": round((ctx - 1) / t_ctx, 1)})}
+    out = {"tok_s": tok_s, "ms_per_step": el / n_new * 1e3, "config": cfg, "gate_up_us": avg[names[0]]}
+    del model, w, rx
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
+def gate_up_roofline(avg_us, k_split):
+    """The roofline object of the gate_up kernel at batch 1 (4 distinct experts per launch)."""
+    gu_bytes = TOPK * GATE_UP_BYTES
+    gbps = gu_bytes / (avg_us * 1e-6) / 1e9
+    kname = "k_moe_gate_up_t950"
+    traffic, why = measured_traffic(kname, "t950", 1, effective_k_split(k_split, 1))
+    log(f"traffic: {traffic} ({why})")
+    return {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kname,
+            "avg_launch_us": round(avg_us, 3), "algorithmic_bytes_per_launch": gu_bytes}
+
+
+def bench_model(A):
+    """Configuration 4 alone (see run_model); roofline: gate_up inside the decode step."""
+    import torch
+
+    from neural_amd import synth
+
+    dev = torch.device("cuda", 0)
+    log(f"model: building the expert pool ({N_LAYERS * N_EXPERTS} slots, t950)")
+    pool = synth.t950_pool_device(N_LAYERS * N_EXPERTS, dev, 4242)
+    m = run_model(A, pool, dev)
+    res = {"metric": METRIC, "value": round(m["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": A.steps,
+           "warmup": A.warmup, "ms_per_step": round(m["ms_per_step"], 4), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic", "config": m["config"],
+           "roofline": {**gate_up_roofline(m["gate_up_us"], A.k_split), "workload": "config4 decode step"},
            "cpu_baseline": None}
     print(json.dumps(res), flush=True)
 
@@ -454,62 +596,177 @@ def bench_attention(A):
     print(json.dumps(res), flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 200; model: 256 tokens)")
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--batch", type=int, default=1)
-    ap.add_argument("--layout", choices=("t950", "raw", "ps4"), default="t950",
-                    help="resident slot layout: gfx950 tiles (MFMA kernels) or the store layouts (VALU kernels)")
-    ap.add_argument("--k-split", type=int, default=0,
-                    help="t950 gate_up: waves per workgroup splitting K (4, 8; 0 = automatic: 4)")
-    ap.add_argument("--down", choices=("combine", "expert"), default="combine",
-                    help="t950, batch 1: gate_up then down + combine (two launches, default), or expert-major down "
-                         "+ a combine kernel (expert)")
-    ap.add_argument("--sets", type=int, default=16, help="routing sets (graphs) cycled over the steps")
-    ap.add_argument("--roofline-steps", type=int, default=20)
-    ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--no-batch-sweep", action="store_true",
-                    help="experts workload: skip the shorter runs of configuration 1's other batch sizes")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--gu-pairs", type=int, default=4, help="gate_up row pairs per wavefront (1, 2, 4)")
-    ap.add_argument("--dn-pairs", type=int, default=2, help="down row pairs per wavefront (1, 2, 4)")
-    ap.add_argument("--workload", choices=("experts", "attention", "prefill", "model"), default="experts",
-                    help="experts: configuration 1 (the headline); prefill: configuration 2 (grouped GEMM layer); "
-                         "attention: configuration 3 (decode attention); model: configuration 4 (full decode)")
-    ap.add_argument("--tokens", type=int, default=2048, help="prefill: prompt tokens")
-    ap.add_argument("--context", type=int, default=4096, help="model: context tokens before the timed decode")
-    ap.add_argument("--context-mode", choices=("prefill", "decode"), default="prefill",
-                    help="model: build the context by prompt processing (default) or token by token through the "
-                         "decode step")
-    ap.add_argument("--prefill-chunk", type=int, default=4096, help="model: prompt block size of the prefill")
-    ap.add_argument("--attn-split", type=int, default=32, help="model: key chunks of full-attention layers")
-    ap.add_argument("--sliding-split", type=int, default=1, help="model: key chunks of sliding-window layers")
-    ap.add_argument("--calib-copy-mb", type=int, default=0,
-                    help="run one device-to-device copy of this many MB first (a known-size kernel that scales the "
-                         "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
-    A = ap.parse_args()
-    if A.steps is None:
-        A.steps = 256 if A.workload == "model" else 200
-    if A.gpus != 1:
-        print(f"bench.py: this build runs on one GPU per process and measures one GPU; --gpus {A.gpus} is not "
-              f"supported (sharding across GPUs is designed, not built)", file=sys.stderr)
-        sys.exit(2)
-    if A.workload == "attention":
-        return bench_attention(A)
-    if A.workload == "prefill":
-        return bench_prefill(A)
-    if A.workload == "model":
-        return bench_model(A)
-    if not 1 <= A.batch <= 8:
-        sys.exit("--batch must be in [1, 8]")
-
+def measure_experts(rx, dev, B, steps, warmup, n_sets, roofline_steps):
+    """Configuration 1 on ResidentExperts ``rx``: graph-replayed 36-layer expert-body steps of batch B (n_sets
+    routing sets cycled), then the per-kernel pass (eager steps with dispatch-timestamped events)."""
     import torch
 
+    from neural_amd import synth
+
+    launches = rx.launches(B)
+    per_layer = len(launches)
+    rng = np.random.default_rng(2026 + B)
+    ids_np, w_np = routing_sets(rng, n_sets, B)
+    distinct = np.array([[len(set(ids_np[s, l].reshape(-1).tolist())) for l in range(N_LAYERS)]
+                         for s in range(n_sets)])
+    ids = torch.from_numpy(ids_np).to(dev)
+    wts = torch.from_numpy(w_np).to(torch.bfloat16).to(dev)
+    x = synth.bf16_normal(rng, (N_LAYERS, B, H)).to(dev)
+    out = torch.empty(N_LAYERS, B, H, dtype=torch.bfloat16, device=dev)
+
+    def step(s, events=None):
+        for l in range(N_LAYERS):
+            rx.forward_decode(l, x[l], ids[s, l], wts[s, l], out=out[l], events=None if events is None else events[l])
+
+    step(0)                                               # eager warm-up, then one graph per routing set
+    torch.cuda.synchronize()
+    graphs = []
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        step(0)
+    torch.cuda.current_stream().wait_stream(cs)
+    for s in range(n_sets):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            step(s)
+        graphs.append(gr)
+    torch.cuda.synchronize()
+    log(f"config1 B={B}: captured {len(graphs)} graphs of {per_layer * N_LAYERS} kernels; warm-up {warmup} steps")
+    for i in range(warmup):
+        graphs[i % n_sets].replay()
+    torch.cuda.synchronize()
+    # ------------------------------------------------------------------ timed region
+    t0 = time.perf_counter()
+    for i in range(steps):
+        graphs[i % n_sets].replay()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    ms_step = el / steps * 1e3
+    tok_s = B * steps / el
+    step_bytes = np.mean([distinct[i % n_sets].sum() for i in range(steps)]) * SLOT_ALGO_BYTES
+    log(f"config1 B={B}: timed {steps} steps: {ms_step:.3f} ms/step, {tok_s:.1f} tok/s, "
+        f"{step_bytes / (ms_step * 1e-3) / 1e9:.0f} GB/s whole-step")
+    # ------------------------------------------------------------------ roofline pass (per-kernel events)
+    per_kernel_bytes = {"gate_up": GATE_UP_BYTES, "down": DOWN_BYTES, "down_combine": DOWN_BYTES, "combine": 0}
+    kernels = tuple((nm, per_kernel_bytes[nm]) for nm in launches)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * len(kernels))] for _ in range(N_LAYERS)]
+    for row in ev:
+        for e in row:
+            e.record()
+    torch.cuda.synchronize()
+    tot = {nm: [0.0, 0.0, 0] for nm, _ in kernels}
+    for r in range(roofline_steps):
+        s = r % n_sets
+        queue_behind_spin(torch)
+        step(s, events=ev)
+        torch.cuda.synchronize()
+        for l in range(N_LAYERS):
+            d = int(distinct[s, l])
+            for k, (nm, per) in enumerate(kernels):
+                ms = ev[l][2 * k].elapsed_time(ev[l][2 * k + 1])
+                tot[nm][0] += ms
+                tot[nm][1] += d * per
+                tot[nm][2] += 1
+    kern = {nm: {"avg_us": v[0] / v[2] * 1e3, "gbps": (v[1] / (v[0] * 1e-3) / 1e9) if v[0] else 0.0}
+            for nm, v in tot.items()}
+    for nm, v in kern.items():
+        log(f"config1 B={B}: kernel {nm}: avg {v['avg_us']:.2f} us/launch, {v['gbps']:.0f} GB/s algorithmic")
+    dom = kernels[0][0]
+    del graphs
+    return {"tok_s": tok_s, "ms_step": ms_step, "step_bytes": step_bytes, "distinct": distinct, "kern": kern,
+            "dom": dom, "per_launch": tot[dom][1] / tot[dom][2], "ids_np": ids_np}
+
+
+def batch_sweep(rx, dev, A, skip):
+    """Configuration 1's other batch sizes, shorter runs on the same resident pool."""
+    sweep = {}
+    for Bs in (1, 2, 4, 8):
+        if Bs == skip:
+            continue
+        m = measure_experts(rx, dev, Bs, max(A.steps // 4, 20), 5, 8, max(A.roofline_steps // 4, 2))
+        kd = m["kern"][m["dom"]]
+        sweep[str(Bs)] = {"tok_s": round(m["tok_s"], 1), "ms_per_step": round(m["ms_step"], 4),
+                          "distinct_experts_per_layer": round(float(m["distinct"].mean()), 3),
+                          "step_hbm_gbps": round(m["step_bytes"] / (m["ms_step"] * 1e-3) / 1e9, 1),
+                          "gate_up_avg_launch_us": round(kd["avg_us"], 3), "gate_up_gbps": round(kd["gbps"], 1),
+                          "gate_up_frac": round(kd["gbps"] / HBM_PEAK_GBS, 4)}
+    return sweep
+
+
+def config1_summary(m, L, B):
+    kern = m["kern"]
+    out = {"workload": f"config1: decode expert body (gate_up+SwiGLU-clamp+down+combine), 36 layers x 128 experts "
+                       f"resident ({L.weight_repr}), batch {B}, random top-4 routing",
+           "batch": B, "tok_s": round(m["tok_s"], 2), "ms_per_step": round(m["ms_step"], 4),
+           "distinct_experts_per_layer": round(float(m["distinct"].mean()), 3),
+           "step_algorithmic_gb": round(m["step_bytes"] / 1e9, 4),
+           "step_hbm_gbps": round(m["step_bytes"] / (m["ms_step"] * 1e-3) / 1e9, 1),
+           "step_hbm_frac": round(m["step_bytes"] / (m["ms_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    for nm, v in kern.items():
+        out[f"{nm}_avg_launch_us"] = round(v["avg_us"], 3)
+        if v["gbps"]:
+            out[f"{nm}_kernel_gbps"] = round(v["gbps"], 1)
+    return out
+
+
+NUMERICS = ("weights MXFP4 (E2M1 codes x E8M0 scales, consumed as stored by the block-scaled MFMA, exact); activations "
+            "bf16, fed to the MFMA as two exact E4M3 rows (hi + lo) per bf16 row: exact for every element within 2^13 "
+            "of its 32-element block's largest magnitude (x), and for every |h| >= 2^-9 between the expert products "
+            "(fixed scales); fp32 accumulation, bf16 outputs at the reference's rounding points")
+
+
+def bench_decode(A):
+    """The default workload: configuration 4 (value) and configuration 1 (config1, roofline) on one resident pool,
+    CPU baselines of the reference's expert kernel."""
+    import torch
+
+    from neural_amd import synth
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
+
+    dev = torch.device("cuda", 0)
+    L = GPTOSS_LAYOUT_T950
+    log(f"building the expert pool ({N_LAYERS * N_EXPERTS} slots, t950, "
+        f"{N_LAYERS * N_EXPERTS * L.slot_bytes / 1e9:.1f} GB)")
+    pool = synth.t950_pool_device(N_LAYERS * N_EXPERTS, dev, 4242)
+    m4 = run_model(A, pool, dev)
+    rx = ResidentExperts(pool, L, None, None, k_split=A.k_split, combine_in_down=A.down != "expert")
+    m1 = measure_experts(rx, dev, 1, max(A.steps, 100), max(A.warmup, 5), A.sets, A.roofline_steps)
+    c1 = config1_summary(m1, L, 1)
+    if not A.no_batch_sweep:
+        c1["batch_sweep"] = batch_sweep(rx, dev, A, 1)
+    roof = gate_up_roofline(m1["kern"][m1["dom"]]["avg_us"], A.k_split)
+    roof.update(workload="config1 batch 1 (the expert GEMV stream the metric's GB/s half names)",
+                config4_gate_up_avg_launch_us=round(m4["gate_up_us"], 3))
+    cpu = None
+    if not A.skip_cpu:
+        try:
+            log("cpu baseline (reference C kernel) ...")
+            cpu = cpu_baselines(pool, m1["ids_np"][0], A.cpu_seconds)
+            log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads ({cpu['gbps']} GB/s), "
+                f"8 threads: {cpu.get('threads_8', {}).get('value')}")
+        except Exception as e:      # the baseline is reported, not required
+            log(f"cpu baseline unavailable: {e!r}")
+            cpu = {"value": None, "unit": "tok/s", "cores": 0, "kind": "reference", "sample": f"unavailable: {e}"}
+    cfg = dict(m4["config"])
+    cfg["workload"] = (cfg["workload"] + "; config1 (expert GEMV stream, batch 1, 2, 4, 8) on the same pool under "
+                       "config1")
+    cfg["config1"] = c1
+    res = {"metric": METRIC, "value": round(m4["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": A.steps,
+           "warmup": A.warmup, "ms_per_step": round(m4["ms_per_step"], 4), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "numerics": NUMERICS, "data": "synthetic",
+           "config": cfg, "roofline": roof, "cpu_baseline": cpu}
+    print(json.dumps(res), flush=True)
+
+
+def bench_experts(A):
+    """Configuration 1 alone, on a pool of any layout (t950: MFMA kernels; raw / ps4: the VALU kernels)."""
+    import torch
+
+    from neural_amd import synth, tiles
     from neural_amd.moe.experts import ResidentExperts
     from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4, GPTOSS_LAYOUT_T950
-    from neural_amd import synth, tiles
 
     dev = torch.device("cuda", 0)
     if A.calib_copy_mb:
@@ -523,177 +780,103 @@ def main():
     L = {"t950": GPTOSS_LAYOUT_T950, "raw": GPTOSS_LAYOUT, "ps4": GPTOSS_LAYOUT_PS4}[A.layout]
     n_slots = N_LAYERS * N_EXPERTS
     log(f"allocating pool {n_slots} x {L.slot_bytes} B = {n_slots * L.slot_bytes / 1e9:.1f} GB ({L.weight_repr})")
-    pool = torch.empty((n_slots, L.slot_bytes), dtype=torch.uint8, device=dev)
-    g = torch.Generator(device=dev)
-    g.manual_seed(1234)
-
-    def fill_store(dst, ps4):
-        """uniform code bytes; E8M0 exponents uniform in [119, 125] (PS4: base 119, deltas 0..6)"""
+    if A.layout == "t950":
+        pool = synth.t950_pool_device(n_slots, dev, 4242)
+    else:
+        pool = torch.empty((n_slots, L.slot_bytes), dtype=torch.uint8, device=dev)
+        g = torch.Generator(device=dev)
+        g.manual_seed(1234)
         cb = GPTOSS_LAYOUT.gate_pack_bytes + GPTOSS_LAYOUT.down_pack_bytes
-        dst[:, :cb].random_(0, 256, generator=g)
-        if ps4:
-            sc = dst[:, cb:].view(dst.shape[0], -1, 46)
+        pool[:, :cb].random_(0, 256, generator=g)
+        if A.layout == "ps4":                       # E8M0 exponents uniform in [119, 125]: base 119, deltas 0..6
+            sc = pool[:, cb:].view(n_slots, -1, 46)
             sc[:, :, 0].fill_(synth.SCALE_LO)
             lo = torch.randint(0, 7, sc[:, :, 1:].shape, dtype=torch.uint8, device=dev, generator=g)
             hi = torch.randint(0, 7, sc[:, :, 1:].shape, dtype=torch.uint8, device=dev, generator=g)
             sc[:, :, 1:] = lo | (hi << 4)
+            del lo, hi
         else:
-            dst[:, cb:].random_(synth.SCALE_LO, synth.SCALE_HI + 1, generator=g)
-
-    if A.layout == "t950":
-        # the resident layout is produced the way a store is loaded: raw slots repacked on the device, 128 at a time
-        chunk = torch.empty((N_EXPERTS, GPTOSS_LAYOUT.slot_bytes), dtype=torch.uint8, device=dev)
-        for c0 in range(0, n_slots, N_EXPERTS):
-            fill_store(chunk, False)
-            tiles.repack_to_t950(chunk, pool[c0:c0 + N_EXPERTS])
-        torch.cuda.synchronize()
-        del chunk
-    else:
-        fill_store(pool, A.layout == "ps4")
+            pool[:, cb:].random_(synth.SCALE_LO, synth.SCALE_HI + 1, generator=g)
     torch.cuda.synchronize()
     log("pool filled")
     bias_gu = torch.zeros(n_slots, L.gate_up_n, dtype=torch.bfloat16, device=dev)
     bias_dn = torch.zeros(n_slots, L.down_n, dtype=torch.bfloat16, device=dev)
     rx = ResidentExperts(pool, L, bias_gu, bias_dn, gu_pairs_per_wave=A.gu_pairs, dn_pairs_per_wave=A.dn_pairs,
                          k_split=A.k_split, combine_in_down=A.down != "expert")
-
-    def measure(B, steps, warmup, n_sets, roofline_steps):
-        """Graph-replayed 36-layer steps of batch B (n_sets routing sets cycled), then the per-kernel pass."""
-        launches = rx.launches(B)
-        per_layer = len(launches)
-        rng = np.random.default_rng(2026 + B)
-        ids_np, w_np = routing_sets(rng, n_sets, B)
-        distinct = np.array([[len(set(ids_np[s, l].reshape(-1).tolist())) for l in range(N_LAYERS)]
-                             for s in range(n_sets)])
-        ids = torch.from_numpy(ids_np).to(dev)
-        wts = torch.from_numpy(w_np).to(torch.bfloat16).to(dev)
-        x = synth.bf16_normal(rng, (N_LAYERS, B, H)).to(dev)
-        out = torch.empty(N_LAYERS, B, H, dtype=torch.bfloat16, device=dev)
-
-        def step(s, events=None):
-            for l in range(N_LAYERS):
-                rx.forward_decode(l, x[l], ids[s, l], wts[s, l], out=out[l],
-                                  events=None if events is None else events[l])
-
-        # eager warm-up, then one graph per routing set
-        step(0)
-        torch.cuda.synchronize()
-        graphs = []
-        cs = torch.cuda.Stream()
-        cs.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(cs):
-            step(0)
-        torch.cuda.current_stream().wait_stream(cs)
-        for s in range(n_sets):
-            gr = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(gr):
-                step(s)
-            graphs.append(gr)
-        torch.cuda.synchronize()
-        log(f"B={B}: captured {len(graphs)} graphs of {per_layer * N_LAYERS} kernels; warm-up {warmup} steps")
-        for i in range(warmup):
-            graphs[i % n_sets].replay()
-        torch.cuda.synchronize()
-
-        # ------------------------------------------------------------------ timed region
-        t0 = time.perf_counter()
-        for i in range(steps):
-            graphs[i % n_sets].replay()
-        torch.cuda.synchronize()
-        el = time.perf_counter() - t0
-        ms_step = el / steps * 1e3
-        tok_s = B * steps / el
-        step_bytes = np.mean([distinct[i % n_sets].sum() for i in range(steps)]) * SLOT_ALGO_BYTES
-        log(f"B={B}: timed {steps} steps: {ms_step:.3f} ms/step, {tok_s:.1f} tok/s, "
-            f"{step_bytes / (ms_step * 1e-3) / 1e9:.0f} GB/s whole-step")
-
-        # ------------------------------------------------------------------ roofline pass (per-kernel events)
-        per_kernel_bytes = {"gate_up": GATE_UP_BYTES, "down": DOWN_BYTES, "down_combine": DOWN_BYTES, "combine": 0}
-        kernels = tuple((nm, per_kernel_bytes[nm]) for nm in launches)
-        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * len(kernels))] for _ in range(N_LAYERS)]
-        for row in ev:
-            for e in row:
-                e.record()
-        torch.cuda.synchronize()
-        tot = {nm: [0.0, 0.0, 0] for nm, _ in kernels}
-        for r in range(roofline_steps):
-            s = r % n_sets
-            queue_behind_spin(torch)
-            step(s, events=ev)
-            torch.cuda.synchronize()
-            for l in range(N_LAYERS):
-                d = int(distinct[s, l])
-                for k, (nm, per) in enumerate(kernels):
-                    ms = ev[l][2 * k].elapsed_time(ev[l][2 * k + 1])
-                    tot[nm][0] += ms
-                    tot[nm][1] += d * per
-                    tot[nm][2] += 1
-        kern = {nm: {"avg_us": v[0] / v[2] * 1e3, "gbps": (v[1] / (v[0] * 1e-3) / 1e9) if v[0] else 0.0}
-                for nm, v in tot.items()}
-        for nm, v in kern.items():
-            log(f"B={B}: kernel {nm}: avg {v['avg_us']:.2f} us/launch, {v['gbps']:.0f} GB/s algorithmic")
-        dom = kernels[0][0]
-        return {"tok_s": tok_s, "ms_step": ms_step, "step_bytes": step_bytes, "distinct": distinct, "kern": kern,
-                "dom": dom, "per_launch": tot[dom][1] / tot[dom][2], "ids_np": ids_np}
-
     B = A.batch
-    m = measure(B, A.steps, A.warmup, A.sets, A.roofline_steps)
-    tok_s, ms_step, step_bytes, distinct, kern = m["tok_s"], m["ms_step"], m["step_bytes"], m["distinct"], m["kern"]
-    ids_np, dom = m["ids_np"], m["dom"]
-    top = kern[dom]
-    per_launch = m["per_launch"]
-    kname = "k_moe_gate_up_t950" if A.layout == "t950" \
-        else "k_moe_gate_up"
+    m = measure_experts(rx, dev, B, A.steps, A.warmup, A.sets, A.roofline_steps)
+    c1 = config1_summary(m, L, B)
+    if not A.no_batch_sweep:
+        c1["batch_sweep"] = batch_sweep(rx, dev, A, B)
+    kname = "k_moe_gate_up_t950" if A.layout == "t950" else "k_moe_gate_up"
     traffic, why = measured_traffic(kname, A.layout, B, effective_k_split(A.k_split, B))
     log(f"traffic: {traffic} ({why})")
+    top = m["kern"][m["dom"]]
     roofline = {"bound": "hbm", "achieved": round(top["gbps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(top["gbps"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": kname,
-                "avg_launch_us": round(top["avg_us"], 3),
-                "algorithmic_bytes_per_launch": int(per_launch)}
-    for nm, v in kern.items():
-        if nm != dom:
-            roofline[f"{nm}_avg_launch_us"] = round(v["avg_us"], 3)
-            if v["gbps"]:
-                roofline[f"{nm}_kernel_gbps"] = round(v["gbps"], 1)
-    # the configuration's other batch sizes (shorter runs on the same resident pool)
-    batch_sweep = {}
-    if not A.no_batch_sweep:
-        for Bs in (1, 2, 4, 8):
-            if Bs == B:
-                continue
-            ms_ = measure(Bs, max(A.steps // 4, 20), 5, 8, max(A.roofline_steps // 4, 2))
-            kd = ms_["kern"][ms_["dom"]]
-            batch_sweep[str(Bs)] = {"tok_s": round(ms_["tok_s"], 1), "ms_per_step": round(ms_["ms_step"], 4),
-                                    "distinct_experts_per_layer": round(float(ms_["distinct"].mean()), 3),
-                                    "step_hbm_gbps": round(ms_["step_bytes"] / (ms_["ms_step"] * 1e-3) / 1e9, 1),
-                                    "gate_up_avg_launch_us": round(kd["avg_us"], 3),
-                                    "gate_up_gbps": round(kd["gbps"], 1),
-                                    "gate_up_frac": round(kd["gbps"] / HBM_PEAK_GBS, 4)}
-
+                "frac": round(top["gbps"] / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kname,
+                "avg_launch_us": round(top["avg_us"], 3), "algorithmic_bytes_per_launch": int(m["per_launch"])}
     cpu = None
     if not A.skip_cpu:
         try:
-            log("cpu baseline (reference C kernel) ...")
-            cpu = cpu_baseline(pool, ids_np[0], B, A.cpu_seconds)
-            log(f"cpu baseline: {cpu['value']} tok/s on {cpu['cores']} threads ({cpu['gbps']} GB/s)")
-        except Exception as e:      # the baseline is reported, not required
-            log(f"cpu baseline unavailable: {e!r}")
+            cpu = cpu_baselines(pool, m["ids_np"][0], A.cpu_seconds)
+        except Exception as e:
             cpu = {"value": None, "unit": "tok/s", "cores": 0, "kind": "reference", "sample": f"unavailable: {e}"}
-
-    res = {"metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": A.steps,
-           "warmup": A.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
-           "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-           "config": {"workload": f"config1: decode expert body (gate_up+SwiGLU-clamp+down+combine), 36 layers x "
-                                  f"128 experts resident ({L.weight_repr}), batch {B}, random top-4 routing",
-                      "batch": B, "layers": N_LAYERS, "experts_resident": n_slots,
-                      "pool_gb": round(n_slots * L.slot_bytes / 1e9, 2),
-                      "distinct_experts_per_layer": round(float(distinct.mean()), 3),
-                      "step_algorithmic_gb": round(step_bytes / 1e9, 4),
-                      "step_hbm_gbps": round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
-                      "batch_sweep": batch_sweep},
+    res = {"metric": METRIC, "value": round(m["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": A.steps,
+           "warmup": A.warmup, "ms_per_step": round(m["ms_step"], 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "bf16", "numerics": NUMERICS, "data": "synthetic", "config": c1,
            "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(res), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (decode / model: greedy tokens, default 256; experts: 200)")
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=1, help="experts workload: decode batch (1..8)")
+    ap.add_argument("--layout", choices=("t950", "raw", "ps4"), default="t950",
+                    help="experts workload: resident slot layout, gfx950 tiles (MFMA kernels) or the store layouts "
+                         "(VALU kernels)")
+    ap.add_argument("--k-split", type=int, default=0,
+                    help="t950 gate_up: waves per workgroup splitting K (4, 8; 0 = automatic: 4)")
+    ap.add_argument("--down", choices=("combine", "expert"), default="combine",
+                    help="t950, batch 1: gate_up then down + combine (two launches, default), or expert-major down "
+                         "+ a combine kernel (expert)")
+    ap.add_argument("--sets", type=int, default=16, help="routing sets (graphs) cycled over the steps")
+    ap.add_argument("--roofline-steps", type=int, default=20)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--no-batch-sweep", action="store_true",
+                    help="skip the shorter runs of configuration 1's other batch sizes")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--gu-pairs", type=int, default=4, help="VALU gate_up row pairs per wavefront (1, 2, 4)")
+    ap.add_argument("--dn-pairs", type=int, default=2, help="VALU down row pairs per wavefront (1, 2, 4)")
+    ap.add_argument("--workload", choices=("decode", "experts", "attention", "prefill", "model"), default="decode",
+                    help="decode: configuration 4 (value) + configuration 1 on one pool (the default); experts: "
+                         "configuration 1 alone; prefill: configuration 2; attention: configuration 3; model: "
+                         "configuration 4 alone")
+    ap.add_argument("--tokens", type=int, default=2048, help="prefill: prompt tokens")
+    ap.add_argument("--context", type=int, default=4096, help="decode / model: context tokens before the timed decode")
+    ap.add_argument("--context-mode", choices=("prefill", "decode"), default="prefill",
+                    help="model: build the context by prompt processing (default) or token by token through the "
+                         "decode step")
+    ap.add_argument("--prefill-chunk", type=int, default=4096, help="model: prompt block size of the prefill")
+    ap.add_argument("--attn-split", type=int, default=32, help="model: key chunks of full-attention layers")
+    ap.add_argument("--sliding-split", type=int, default=1, help="model: key chunks of sliding-window layers")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="experts: run one device-to-device copy of this many MB first (a known-size kernel that "
+                         "scales the FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")
+    A = ap.parse_args()
+    if A.steps is None:
+        A.steps = 256 if A.workload in ("decode", "model") else 200
+    if A.gpus != 1:
+        print(f"bench.py: this build runs on one GPU per process and measures one GPU; --gpus {A.gpus} is not "
+              f"supported (sharding across GPUs is designed, not built)", file=sys.stderr)
+        sys.exit(2)
+    if not 1 <= A.batch <= 8:
+        sys.exit("--batch must be in [1, 8]")
+    return {"attention": bench_attention, "prefill": bench_prefill, "model": bench_model, "experts": bench_experts,
+            "decode": bench_decode}[A.workload](A)
 
 
 if __name__ == "__main__":
