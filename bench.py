@@ -394,7 +394,8 @@ def run_model(A, pool, dev):
     log("model: random-init dense weights")
     w = random_weights(device=dev, seed=77)
     smax = ctx + max(n_new, A.warmup) + 2
-    model = DecodeModel(w, rx, smax=smax, n_split=A.attn_split, sliding_split=A.sliding_split)
+    model = DecodeModel(w, rx, smax=smax, n_split=A.attn_split, sliding_split=A.sliding_split,
+                        fused_attn=not A.unfused_attn)
     torch.cuda.synchronize()
     rng = np.random.default_rng(4096)
     prompt = rng.integers(0, w.vocab, ctx)
@@ -474,6 +475,8 @@ def run_model(A, pool, dev):
                        f"{ctx}-token context, {n_new} tokens, one hipGraph per step, experts t950 resident",
            "context": ctx, "tokens": n_new, "vocab": int(w.vocab), "attn_split_full": A.attn_split,
            "attn_split_sliding": A.sliding_split, "deterministic_tokens": same,
+           "attention_block": "four launches" if A.unfused_attn else "one launch per layer (na_core_attn_block)",
+           "sync_error": model.sync_error(),
            "first_tokens": [int(t) for t in toks[:8]],
            "step_algorithmic_gb": round(step_bytes / 1e9, 3),
            "step_hbm_gbps": round(step_bytes / (el / n_new) / 1e9, 1),
@@ -863,6 +866,8 @@ def main():
     ap.add_argument("--prefill-chunk", type=int, default=4096, help="model: prompt block size of the prefill")
     ap.add_argument("--attn-split", type=int, default=32, help="model: key chunks of full-attention layers")
     ap.add_argument("--sliding-split", type=int, default=1, help="model: key chunks of sliding-window layers")
+    ap.add_argument("--unfused-attn", action="store_true",
+                    help="model: QKV, attention, o_proj and router as four launches per layer instead of one")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="experts: run one device-to-device copy of this many MB first (a known-size kernel that "
                          "scales the FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run)")

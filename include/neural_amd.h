@@ -260,6 +260,26 @@ int na_core_route_pack(const void* hn, const float* logits, const int64_t* ids, 
                        const int64_t* slot_tab, long long base, void* bx, float* pack, int near_miss, int64_t* bslots,
                        int64_t* bgids, void* bw, hipStream_t stream);
 
+/* The attention block of one decode layer in ONE launch: na_core_qkv, na_decode_attention (B = 1), na_core_oproj and
+ * na_core_router, with their arguments and results (fused_core.py:581-629: k_qkv, k_attn / SplitAttn, k_oproj,
+ * k_router + k_topk), as four phases of one grid.  Each phase issues its loads (weights; the cache rows of earlier
+ * positions) before it waits for the phase it needs (device-coherent counters, bounded waits), so weight streams and
+ * cache reads overlap the phases before them.  Differences from the four calls: c and g feed o_proj's residual too
+ * (it is recomputed per row, not read from xbuf); mid is updated in place; results are bit-identical.
+ *   sync   uint32 [na_core_attn_block_sync_words()] (23,552 bytes: counters and release flags, each on its own 256-byte
+ *          line), zero before the first call; every completed call leaves it zero except word 0, an error flag that
+ *          a wait which gave up after its poll limit raises (and nothing clears): that call's outputs are not
+ *          valid.
+ *   n_split chunks of the attention (1..64); attn_work: na_attn_workspace_floats(1, n_split) floats (n_split > 1)
+ *   events NULL or 2 hipEvent_t (start / stop of the launch) */
+long long na_core_attn_block_sync_words(void);
+int na_core_attn_block(void* mid, const void* g, const float* c, void* xbuf, const void* in_w, const void* Wqkv,
+                       const void* bqkv, const int64_t* pos, const float* inv_freq, void* kc, void* vc,
+                       long long cache_rows, int ring, void* q, float eps, float att_scale, const void* sinks,
+                       float scaling, int window, int n_split, float* attn_work, void* att, const void* Wo,
+                       const void* bo, const void* post_w, const void* Wr, const void* br, void* hn, float* logits,
+                       int64_t* ids, void* wts, unsigned int* sync, void* const* events, hipStream_t stream);
+
 /* Workgroup partials na_core_lm_tail needs for a vocabulary (-1 if vocab <= 0). */
 long long na_core_lm_partials(int vocab);
 

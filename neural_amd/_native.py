@@ -45,6 +45,9 @@ SIGNATURES = {
     "na_core_oproj": [VP, VP, VP, VP, VP, VP],
     "na_core_router": [VP, VP, F32, VP, VP, VP, VP, VP, VP, VP, VP],
     "na_core_lm_partials": [I32],
+    "na_core_attn_block": [VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, I64, I32, VP, F32, F32, VP, F32, I32, I32, VP,
+                           VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP],
+    "na_core_attn_block_sync_words": [],
     "na_core_route_pack": [VP, VP, VP, VP, VP, I64, VP, VP, I32, VP, VP, VP, VP],
     "na_core_lm_tail": [VP, VP, VP, VP, F32, VP, I32, VP, VP, VP, VP, VP, I32, VP, VP, VP, I64, VP],
     "na_prefill_attention": [VP, VP, VP, I64, VP, VP, I64, I64, I64, I64, VP, VP, I64, I32, F32, I32, I32, VP, VP],
@@ -57,7 +60,7 @@ SIGNATURES = {
     "na_rows_topk": [VP, I32, VP, VP, VP],
 }
 RESTYPES = {"na_t950_slot_bytes": I64, "na_attn_workspace_floats": I64, "na_moe_prefill_workspace_bytes": I64,
-            "na_core_lm_partials": I64}
+            "na_core_lm_partials": I64, "na_core_attn_block_sync_words": I64}
 
 ERRORS = {-1: "invalid arguments", -2: "kernel launch failed", -3: "size beyond the kernel's limits"}
 

@@ -1,0 +1,333 @@
+// Device code of the GQA decode attention (64 query heads, 8 KV heads, head_dim 64, learned sinks), shared by the
+// standalone kernel (attention.hip) and the fused attention block of a decode layer (core.hip).  The algorithm and
+// its rounding points are described in attention.hip.
+#pragma once
+#include "common.h"
+#include "handoff.h"
+
+namespace na {
+
+constexpr int kNQ = 64, kNKV = 8, kHD = 64, kRep = 8;
+constexpr int kSub = 256;                          // keys per sub-chunk (4 waves x 64)
+constexpr int kAttnMaxSplit = 64;
+constexpr int kPartFloats = kRep + kRep + kRep * kHD;   // m[8], S[8], acc[8][64] per chunk
+constexpr int kVtPitch = kSub * 2 + 16;            // LDS bytes per V^T row (d), padded against bank conflicts
+constexpr int kPPitch = kSub * 2 + 16;             // LDS bytes per P row
+constexpr float kNegInf = -__builtin_huge_valf();
+
+struct AttnLds {
+  union {
+    __align__(16) uint8_t vt[kHD * kVtPitch];      // V^T of the sub-chunk, bf16 [d][key]
+    struct {                                       // after the last sub-chunk, the combine's chunk maxima and sums
+      float cm[kAttnMaxSplit][kRep];
+      float cs[kAttnMaxSplit][kRep];
+    };
+  };
+  __align__(16) uint8_t p[kRep * kPPitch];         // P of the sub-chunk, bf16 [row][key]: the MFMA's A rows 8..15
+                                                   // re-read rows 0..7 (their outputs are not used)
+  float mx[4][kRep];                               // per-wave row maxima
+  float sm[4][kRep];                               // per-wave row sums
+  uint32_t last;                                   // split-K: this workgroup combines
+};
+
+// Wave-wide max / sum over the 16 lanes of a row group (lanes 16 q .. 16 q + 15).
+NA_DEVICE float group16_max(float v) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+NA_DEVICE float group16_sum(float v) {
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+NA_DEVICE bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// Key range [c0, c1) of chunk c (empty when c0 >= c1): the reference's split rule over 64-key blocks of [lo, hi].
+NA_DEVICE void chunk_range(int lo, int hi, int c, int ns, int& c0, int& c1) {
+  const int n = hi - lo + 1;
+  const int nb = (n + 63) / 64;
+  const int bps = (nb + ns - 1) / ns;
+  c0 = lo + c * bps * 64;
+  c1 = min(c0 + bps * 64, hi + 1);
+}
+
+// The attention of workgroup `blk` (grid B x 8 x ns).  FUSED: q, and the K / V row of the step's own position, are
+// written earlier in the same launch (see handoff.h): the first sub-chunk's K / V loads are issued, then the
+// workgroup waits for its release flag `go`, then reads q, and that row with coherent loads; the output is written
+// with coherent stores and counted in *done (one count per sequence and KV head, done_n in all), whose completion
+// raises the flags `next`.
+struct AttnHandoff {
+  const uint32_t* go;
+  uint32_t* done;
+  uint32_t done_n;
+  uint32_t* next;
+  uint32_t* err;
+};
+
+template <bool FUSED>
+NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+                                const uint16_t* __restrict__ vc, long long cache_rows, const uint16_t* __restrict__ sinks,
+                                const int64_t* __restrict__ pos_p, uint16_t* __restrict__ out, float scaling,
+                                int window, int ring, int ns, float* __restrict__ work,
+                                uint32_t* __restrict__ counters, const AttnHandoff& hs) {
+  constexpr int kCounterStride = FUSED ? kLine : 1;   // fused: each head's split counter on its own line
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, n = lane & 15;          // row group (D rows 4g..4g+3) and column of this lane
+  const int c = blk % ns;
+  const int bh = blk / ns;                         // b * 8 + h
+  const int b = bh / kNKV, h = bh - b * kNKV;
+  const long long pos = pos_p[b];
+  const int hi = (int)pos;
+  const int lo = window > 0 ? max(hi - window + 1, 0) : 0;
+  int c0, c1;
+  chunk_range(lo, hi, c, ns, c0, c1);
+  const uint16_t* kbase = kc + ((long long)b * kNKV + h) * cache_rows * kHD;
+  const uint16_t* vbase = vc + ((long long)b * kNKV + h) * cache_rows * kHD;
+
+  // A operand: query rows (row n of the head for lanes n < 8, zero rows otherwise), d = 8g.. and 32 + 8g..
+  const uint16_t* qrow = q + ((long long)b * kNQ + h * kRep + min(n, kRep - 1)) * kHD;
+  uint4 qa0 = make_uint4(0, 0, 0, 0), qa1 = make_uint4(0, 0, 0, 0);
+  if constexpr (!FUSED) {
+    qa0 = *reinterpret_cast<const uint4*>(qrow + 8 * g);
+    qa1 = *reinterpret_cast<const uint4*>(qrow + 32 + 8 * g);
+    if (n >= kRep) qa0 = qa1 = make_uint4(0, 0, 0, 0);
+  }
+  bool waited = !FUSED;
+
+  float m_run[4], s_run[4];                        // rows 4g + r (meaningful for g < 2)
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};              // P V: D[rows 4g + r][d = 16 wave + n]
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    m_run[r] = kNegInf;
+    s_run[r] = 0.f;
+  }
+
+  for (int k0 = c0; k0 < c1; k0 += kSub) {
+    // ---- loads: K and V rows of this wave's 64 keys (4 blocks of 16), all issued before any use
+    const int kw = k0 + 64 * wave;
+    uint4 kr[4][2], vr[4][2];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int key = min(kw + 16 * kb + n, hi);   // clamped: masked below, always a valid row
+      long long row = ring > 0 ? key % ring : key;
+      row = min(row, cache_rows - 1);
+      const uint16_t* kp = kbase + row * kHD + 8 * g;
+      const uint16_t* vp = vbase + row * kHD + 8 * g;
+      kr[kb][0] = *reinterpret_cast<const uint4*>(kp);
+      kr[kb][1] = *reinterpret_cast<const uint4*>(kp + 32);
+      vr[kb][0] = *reinterpret_cast<const uint4*>(vp);
+      vr[kb][1] = *reinterpret_cast<const uint4*>(vp + 32);
+    }
+    if (FUSED && !waited) {
+      // every load above reads keys older than the step (or is replaced below); now the step's own q, K and V
+      wait_go(hs.go, hs.err);
+      waited = true;
+      if (n < kRep) {                              // q: read by nothing in the launch before (ordinary loads)
+        qa0 = *reinterpret_cast<const uint4*>(qrow + 8 * g);
+        qa1 = *reinterpret_cast<const uint4*>(qrow + 32 + 8 * g);
+      }
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        if (kw + 16 * kb + n == hi) {
+          long long row = ring > 0 ? (long long)hi % ring : hi;
+          row = min(row, cache_rows - 1);
+          const uint16_t* kp = kbase + row * kHD + 8 * g;
+          const uint16_t* vp = vbase + row * kHD + 8 * g;
+          kr[kb][0] = load16_coherent(kp);
+          kr[kb][1] = load16_coherent(kp + 32);
+          vr[kb][0] = load16_coherent(vp);
+          vr[kb][1] = load16_coherent(vp + 32);
+        }
+      }
+    }
+    // ---- scores s = bf16(bf16(q . k) * scaling), -inf outside [k0, c1)
+    float s[4][4];                                 // [block][r]
+    float wmax[4] = {kNegInf, kNegInf, kNegInf, kNegInf};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa0), as_bf16x8(kr[kb][0]), d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa1), as_bf16x8(kr[kb][1]), d, 0, 0, 0);
+      const int key = kw + 16 * kb + n;
+      const bool ok = key < c1;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s[kb][r] = ok ? rb(rb(d[r]) * scaling) : kNegInf;
+        wmax[r] = fmaxf(wmax[r], s[kb][r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wmax[r] = group16_max(wmax[r]);
+    if (n == 0 && g < 2) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) L.mx[wave][4 * g + r] = wmax[r];
+    }
+    // ---- V^T to LDS: lane (g, n) holds d = 8g..8g+7 and 32+8g.. of key 16 kb + n of this wave's 64
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int kcol = 64 * wave + 16 * kb + n;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const uint32_t w4[4] = {vr[kb][hf].x, vr[kb][hf].y, vr[kb][hf].z, vr[kb][hf].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int dd = 32 * hf + 8 * g + i;
+          *reinterpret_cast<uint16_t*>(L.vt + dd * kVtPitch + 2 * kcol) =
+              (uint16_t)((i & 1) ? (w4[i >> 1] >> 16) : (w4[i >> 1] & 0xffff));
+        }
+      }
+    }
+    __syncthreads();
+    // ---- sub-chunk max (exact, any order), new running max, P = bf16(exp(s - m_new)), row sums
+    float m_new[4], alpha[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 4 * min(g, 1) + r;
+      float mx = fmaxf(fmaxf(L.mx[0][row], L.mx[1][row]), fmaxf(L.mx[2][row], L.mx[3][row]));
+      m_new[r] = fmaxf(m_run[r], mx);
+      alpha[r] = m_new[r] == kNegInf ? 1.f : expf(m_run[r] - m_new[r]);
+    }
+    float psum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int kcol = 64 * wave + 16 * kb + n;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = s[kb][r] == kNegInf ? 0.f : expf(s[kb][r] - m_new[r]);
+        const uint16_t pb = f32_to_bf16(e);
+        psum[r] += bf16_to_f32(pb);
+        if (g < 2) *reinterpret_cast<uint16_t*>(L.p + (4 * g + r) * kPPitch + 2 * kcol) = pb;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) psum[r] = group16_sum(psum[r]);
+    if (n == 0 && g < 2) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) L.sm[wave][4 * g + r] = psum[r];
+    }
+    __syncthreads();
+    // ---- running state: S = S alpha + sum of the 4 waves (fixed order); acc = acc alpha + P V
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 4 * min(g, 1) + r;
+      const float sub = ((L.sm[0][row] + L.sm[1][row]) + L.sm[2][row]) + L.sm[3][row];
+      s_run[r] = s_run[r] * alpha[r] + sub;
+      m_run[r] = m_new[r];
+      acc[r] *= alpha[r];
+    }
+    const int nks = (min(kSub, c1 - k0) + 31) / 32;     // 32-key steps holding live keys (P is 0 past c1)
+#pragma unroll
+    for (int ks = 0; ks < kSub / 32; ++ks) {
+      if (ks < nks) {                                  // uniform
+        const uint4 pa = *reinterpret_cast<const uint4*>(L.p + (n & (kRep - 1)) * kPPitch + 2 * (32 * ks + 8 * g));
+        const uint4 vb = *reinterpret_cast<const uint4*>(L.vt + (16 * wave + n) * kVtPitch + 2 * (32 * ks + 8 * g));
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pa), as_bf16x8(vb), acc, 0, 0, 0);
+      }
+    }
+    __syncthreads();                               // LDS is rewritten by the next sub-chunk
+  }
+
+  // ---- finish: a single chunk writes the output; otherwise publish the partial, the last arriver combines
+  const uint16_t* sk = sinks + h * kRep;
+  uint16_t* orow = out + ((long long)b * kNQ + h * kRep) * kHD;
+  if (ns == 1) {
+    if (g < 2) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float sink = bf16_to_f32(sk[4 * g + r]);
+        const float m = fmaxf(sink, m_run[r]);
+        const float a = m_run[r] == kNegInf ? 0.f : expf(m_run[r] - m);
+        const float S = expf(sink - m) + s_run[r] * a;   // the combine's formula, so one chunk == split at pos < 64
+        const uint16_t o = f32_to_bf16((0.f + acc[r] * a) * (1.f / S));
+        if constexpr (FUSED) store_coherent(orow + (4 * g + r) * kHD + 16 * wave + n, o);
+        else orow[(4 * g + r) * kHD + 16 * wave + n] = o;
+      }
+    }
+    if constexpr (FUSED) publish_done(hs.done, bh, hs.done_n, hs.next);
+    return;
+  }
+  float* part = work + ((long long)bh * ns + c) * kPartFloats;
+  if (g < 2) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 4 * g + r;
+      __hip_atomic_store(part + 2 * kRep + row * kHD + 16 * wave + n, acc[r], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      if (wave == 0 && n == 0) {
+        __hip_atomic_store(part + row, m_run[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(part + kRep + row, s_run[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  // Publication: every wave waits until its own device-coherent stores are acknowledged, the workgroup barrier
+  // orders the four waves, then one count per workgroup.  The counter's last incrementer reads the partials with
+  // device-coherent loads (an acknowledged agent-scope store is visible to every agent-scope load).
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  uint32_t& last = L.last;
+  if (tid == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(counters + bh * kCounterStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == (uint32_t)ns - 1;
+    if (last) __hip_atomic_store(counters + bh * kCounterStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last) return;
+  // Combine.  One acquire fence (the partials were published with device-coherent stores before the count), then
+  // one round of plain loads, all in flight together: thread tid's two outputs i = 2 tid, 2 tid + 1 (row i / 64) of
+  // the first 32 chunks into registers, every chunk's maxima and sums into LDS.  Then each thread forms its row's
+  // maximum m, weights w_c = exp(m_c - m) and S itself (in chunk order) and out[row][d] = sum_c acc_c[row][d] w_c / S.
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const float* pbase = work + (long long)bh * ns * kPartFloats;
+  const int i = 2 * tid, row = i / kHD;
+  float2 v[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j)
+    v[j] = j < ns ? *reinterpret_cast<const float2*>(pbase + j * kPartFloats + 2 * kRep + i) : make_float2(0.f, 0.f);
+  for (int k = tid; k < ns * kRep; k += 256) {
+    const int cc = k / kRep, r = k - cc * kRep;
+    L.cm[cc][r] = pbase[cc * kPartFloats + r];
+    L.cs[cc][r] = pbase[cc * kPartFloats + kRep + r];
+  }
+  __syncthreads();
+  const float sink = bf16_to_f32(sk[row]);
+  float m = sink;
+  for (int cc = 0; cc < ns; ++cc) m = fmaxf(m, L.cm[cc][row]);
+  float S = expf(sink - m), o0 = 0.f, o1 = 0.f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    if (j < ns) {
+      const float mc = L.cm[j][row];
+      const float w = mc == kNegInf ? 0.f : expf(mc - m);
+      S += L.cs[j][row] * w;
+      o0 += v[j].x * w;
+      o1 += v[j].y * w;
+    }
+  }
+  for (int cb = 32; cb < ns; cb += 32) {               // uniform; ns <= 64
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+      v[j] = cb + j < ns ? *reinterpret_cast<const float2*>(pbase + (cb + j) * kPartFloats + 2 * kRep + i)
+                         : make_float2(0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      if (cb + j < ns) {
+        const float mc = L.cm[cb + j][row];
+        const float w = mc == kNegInf ? 0.f : expf(mc - m);
+        S += L.cs[cb + j][row] * w;
+        o0 += v[j].x * w;
+        o1 += v[j].y * w;
+      }
+    }
+  }
+  {
+    const float inv = 1.f / S;
+    const uint32_t o = (uint32_t)f32_to_bf16(o0 * inv) | ((uint32_t)f32_to_bf16(o1 * inv) << 16);
+    if constexpr (FUSED) store_coherent(reinterpret_cast<uint32_t*>(orow + i), o);
+    else *reinterpret_cast<uint32_t*>(orow + i) = o;
+  }
+  if constexpr (FUSED) publish_done(hs.done, bh, hs.done_n, hs.next);
+}
+
+}  // namespace na

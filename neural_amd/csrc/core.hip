@@ -13,7 +13,9 @@
 // GEMV layout: a workgroup of 256 threads computes 16 weight rows; thread (r = tid / 16, j = tid % 16) streams row
 // r's 16-byte chunks j, j + 16, ... (all issued before the first use) against the normed activation staged in LDS,
 // and the 16 lanes of a row group sum with xor shuffles.
+#include "attention_dev.h"
 #include "common.h"
+#include "handoff.h"
 
 #include <hip/hip_ext.h>
 
@@ -183,22 +185,43 @@ __global__ __launch_bounds__(256) void k_embed(const uint16_t* __restrict__ emb,
     *reinterpret_cast<uint4*>(mid + 8 * ch) = *reinterpret_cast<const uint4*>(emb + t * kH + 8 * ch);
 }
 
+// Lines (kLine words) of the fused attention block's sync buffer (handoff.h): each counter and flag on its own line.
+constexpr int kSyncErr = 0, kSyncRouter = 1;
+constexpr int kSyncSplit = 2;                                   // 8 lines: the attention's split counters
+constexpr int kSyncQkvCnt = 10, kSyncQkvGo = 18;               // 8 lines each: QKV counts and release per KV group
+constexpr int kSyncCnt = 26;                                    // 2 phases (attention, o_proj) x (top + kGo groups)
+constexpr int kSyncGo = kSyncCnt + 2 * (1 + kGo);               // 2 phases x kGo release flags (o_proj, router)
+constexpr int kSyncLines = kSyncGo + 2 * kGo;                   // 92 lines, 23,552 bytes
+constexpr int kSyncWords = kSyncLines * kLine;
+NA_DEVICE constexpr int sync_qkv_cnt(int grp) { return (kSyncQkvCnt + grp) * kLine; }
+NA_DEVICE constexpr int sync_qkv_go(int grp) { return (kSyncQkvGo + grp) * kLine; }
+NA_DEVICE constexpr int sync_cnt(int phase) { return (kSyncCnt + phase * (1 + kGo)) * kLine; }
+NA_DEVICE constexpr int sync_go(int phase, int i) { return (kSyncGo + phase * kGo + i) * kLine; }
+
+// The router's last workgroup returns every release flag to zero (lanes of one wave): every waiter has passed its
+// wait by then (the router's counter is complete only after every router workgroup waited, the router's flags were
+// raised only after every o_proj workgroup finished, which each waited for the attention's, and so on).
+NA_DEVICE void sync_reset(uint32_t* sync, int lane) {
+  for (int i = lane; i < 8 + 2 * kGo; i += 64)
+    store_coherent(sync + (i < 8 ? sync_qkv_go(i) : sync_go((i - 8) / kGo, (i - 8) % kGo)), 0u);
+}
+
 // QKV: ROWS = 256 / TPR rows per workgroup, grid 5120 / ROWS; workgroup (head, c) computes the rows of dims
 // d = c * ROWS/2 + (0 .. ROWS/2 - 1) (row groups 0 .. ROWS/2 - 1) and of their RoPE partners d + 32 (the other row
-// groups) of head `head` (0..63 q, 64..71 k, 72..79 v).
-template <int TPR>
-__global__ __launch_bounds__(256) void k_qkv(const uint16_t* __restrict__ mid, const uint16_t* __restrict__ g,
-                                             const float* __restrict__ cext, uint16_t* __restrict__ xbuf,
-                                             const uint16_t* __restrict__ in_w, const uint16_t* __restrict__ W,
-                                             const uint16_t* __restrict__ bias, const int64_t* __restrict__ pos_p,
-                                             const float* __restrict__ inv_freq, uint16_t* __restrict__ kc,
-                                             uint16_t* __restrict__ vc, long long rows, int ring,
-                                             uint16_t* __restrict__ qout, float eps, float att_scale) {
+// groups) of head `head` (0..63 q, 64..71 k, 72..79 v).  FUSED (the first phase of k_attn_block): q and the K / V
+// row at pos are written with coherent stores and the workgroup is counted in *done.  hc: kH bf16 of LDS, ys: ROWS
+// floats of LDS.
+template <int TPR, bool FUSED>
+NA_DEVICE void qkv_body(int blk, uint16_t* hc, float* ys, const uint16_t* __restrict__ mid,
+                        const uint16_t* __restrict__ g, const float* __restrict__ cext, uint16_t* __restrict__ xbuf,
+                        const uint16_t* __restrict__ in_w, const uint16_t* __restrict__ W,
+                        const uint16_t* __restrict__ bias, const int64_t* __restrict__ pos_p,
+                        const float* __restrict__ inv_freq, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                        long long rows, int ring, uint16_t* __restrict__ qout, float eps, float att_scale,
+                        uint32_t* sync) {
   constexpr int ROWS = 256 / TPR, HALF = ROWS / 2, PER_HEAD = 64 / ROWS;
-  __shared__ __align__(16) uint16_t hc[kH];
-  __shared__ float ys[ROWS];
   const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
-  const int head = blockIdx.x / PER_HEAD, c = blockIdx.x % PER_HEAD;
+  const int head = blk / PER_HEAD, c = blk % PER_HEAD;
   const int d = HALF * c + (r % HALF);
   const int row = head * 64 + 32 * (r / HALF) + d;
   NormIn ni;
@@ -214,47 +237,109 @@ __global__ __launch_bounds__(256) void k_qkv(const uint16_t* __restrict__ mid, c
   const float s = rw.dot(hc, j);
   if (j == 0) ys[r] = rb(s + bf16_to_f32(bv));
   __syncthreads();
-  if (tid >= HALF) return;                           // thread t < HALF writes dims 32c' + t and its partner
-  const int dd = HALF * c + tid;
-  const float ya = ys[tid], yb = ys[tid + HALF];
-  float o1 = ya, o2 = yb;
-  if (head < 64 + 8) {                               // q and k heads: RoPE
-    const float fr = freq * (float)pos;
-    const float cs = rb(cosf(fr) * att_scale), sn = rb(sinf(fr) * att_scale);
-    o1 = rb(rb(ya * cs) - rb(yb * sn));
-    o2 = rb(rb(yb * cs) + rb(ya * sn));
+  if (tid < HALF) {                                  // thread t < HALF writes dims 32c' + t and its partner
+    const int dd = HALF * c + tid;
+    const float ya = ys[tid], yb = ys[tid + HALF];
+    float o1 = ya, o2 = yb;
+    if (head < 64 + 8) {                             // q and k heads: RoPE
+      const float fr = freq * (float)pos;
+      const float cs = rb(cosf(fr) * att_scale), sn = rb(sinf(fr) * att_scale);
+      o1 = rb(rb(ya * cs) - rb(yb * sn));
+      o2 = rb(rb(yb * cs) + rb(ya * sn));
+    }
+    uint16_t* dst = nullptr;
+    if (head < 64) {
+      dst = qout + head * 64;
+    } else {
+      const long long slot = ring > 0 ? pos % ring : pos;
+      if (slot >= 0 && slot < rows)                  // a position outside the cache is stored nowhere
+        dst = (head < 72 ? kc + (long long)(head - 64) * rows * 64 : vc + (long long)(head - 72) * rows * 64) +
+              slot * 64;
+    }
+    if (dst) {
+      if constexpr (FUSED) {
+        store_coherent(dst + dd, f32_to_bf16(o1));
+        store_coherent(dst + 32 + dd, f32_to_bf16(o2));
+      } else {
+        dst[dd] = f32_to_bf16(o1);
+        dst[32 + dd] = f32_to_bf16(o2);
+      }
+    }
   }
-  if (head < 64) {
-    qout[head * 64 + dd] = f32_to_bf16(o1);
-    qout[head * 64 + 32 + dd] = f32_to_bf16(o2);
-  } else {
-    const long long slot = ring > 0 ? pos % ring : pos;
-    if (slot < 0 || slot >= rows) return;           // a position outside the cache is stored nowhere
-    uint16_t* cache = head < 72 ? kc + (long long)(head - 64) * rows * 64 : vc + (long long)(head - 72) * rows * 64;
-    cache[slot * 64 + dd] = f32_to_bf16(o1);
-    cache[slot * 64 + 32 + dd] = f32_to_bf16(o2);
+  if constexpr (FUSED) {                             // KV group of this head: its 8 q heads, its k and v heads
+    const int grp = head < 64 ? head / 8 : head < 72 ? head - 64 : head - 72;
+    publish_group(sync + sync_qkv_cnt(grp), 10 * PER_HEAD, sync + sync_qkv_go(grp));
   }
 }
 
-// o_proj + residual: 256 / TPR rows per workgroup: mid[n] = bf16(xbuf[n] + bf16(att . Wo[n] + bo[n])).
 template <int TPR>
-__global__ __launch_bounds__(256) void k_oproj(const uint16_t* __restrict__ att, const uint16_t* __restrict__ Wo,
-                                               const uint16_t* __restrict__ bo, const uint16_t* __restrict__ xbuf,
-                                               uint16_t* __restrict__ mid) {
+__global__ __launch_bounds__(256) void k_qkv(const uint16_t* __restrict__ mid, const uint16_t* __restrict__ g,
+                                             const float* __restrict__ cext, uint16_t* __restrict__ xbuf,
+                                             const uint16_t* __restrict__ in_w, const uint16_t* __restrict__ W,
+                                             const uint16_t* __restrict__ bias, const int64_t* __restrict__ pos_p,
+                                             const float* __restrict__ inv_freq, uint16_t* __restrict__ kc,
+                                             uint16_t* __restrict__ vc, long long rows, int ring,
+                                             uint16_t* __restrict__ qout, float eps, float att_scale) {
+  __shared__ __align__(16) uint16_t hc[kH];
+  __shared__ float ys[256 / TPR];
+  qkv_body<TPR, false>(blockIdx.x, hc, ys, mid, g, cext, xbuf, in_w, W, bias, pos_p, inv_freq, kc, vc, rows, ring,
+                       qout, eps, att_scale, nullptr);
+}
+
+// o_proj + residual: 256 / TPR rows per workgroup: mid[n] = bf16(x[n] + bf16(att . Wo[n] + bo[n])), x = xbuf.
+// FUSED (the third phase of k_attn_block): the weight rows are loaded first, the workgroup then waits until
+// *ready >= ready_target (the attention output is complete), reads att with coherent loads, recomputes its rows of x
+// from mid, g and c (the residual the QKV phase normalised), and writes mid with coherent stores, counted in *done.
+template <int TPR, bool FUSED>
+NA_DEVICE void oproj_body(int blk, uint16_t* hc, const uint16_t* __restrict__ att, const uint16_t* __restrict__ Wo,
+                          const uint16_t* __restrict__ bo, const uint16_t* __restrict__ xbuf,
+                          const uint16_t* __restrict__ g, const float* __restrict__ cext, uint16_t* __restrict__ mid,
+                          const uint32_t* go, uint32_t* done, uint32_t done_n, uint32_t* next, uint32_t* err) {
   constexpr int ROWS = 256 / TPR;
-  __shared__ __align__(16) uint16_t hc[kHq];
   const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
-  const int row = ROWS * blockIdx.x + r;
+  const int row = ROWS * blk + r;
   VecIn<kHq> a;
-  a.load(att);
-  const uint16_t bv = bo[row], xv = xbuf[row];
+  if constexpr (!FUSED) a.load(att);
+  const uint16_t bv = bo[row];
+  uint16_t xv;
+  float gx = 0.f, cx = 0.f;
+  if constexpr (FUSED) {
+    xv = mid[row];
+    if (g) gx = bf16_to_f32(g[row]);
+    if (cext) cx = cext[row];
+  } else {
+    xv = xbuf[row];
+  }
   __builtin_amdgcn_sched_barrier(0);
   RowChunks<kHq, TPR> rw;
   rw.load(Wo + (long long)row * kHq, j);
   __builtin_amdgcn_sched_barrier(0);
+  float x = bf16_to_f32(xv);
+  if constexpr (FUSED) {
+    if (g) x = rb(x + rb(gx + (cext ? rb(cx) : 0.f)));
+    wait_go(go, err);
+    // ordinary loads: nothing in this launch reads att before its producers finish, and a kernel boundary leaves
+    // no stale copy in any L2, so the first read of a line on an XCD fetches the final bytes and later ones hit
+    a.load(att);
+  }
   a.store(hc);
   const float s = rw.dot(hc, j);
-  if (j == 0) mid[row] = f32_to_bf16(bf16_to_f32(xv) + rb(s + bf16_to_f32(bv)));
+  const uint16_t o = f32_to_bf16(x + rb(s + bf16_to_f32(bv)));
+  if constexpr (FUSED) {
+    if (j == 0) store_coherent(mid + row, o);
+    publish_done(done, blk, done_n, next);
+  } else {
+    if (j == 0) mid[row] = o;
+  }
+}
+
+template <int TPR>
+__global__ __launch_bounds__(256) void k_oproj(const uint16_t* __restrict__ att, const uint16_t* __restrict__ Wo,
+                                               const uint16_t* __restrict__ bo, const uint16_t* __restrict__ xbuf,
+                                               uint16_t* __restrict__ mid) {
+  __shared__ __align__(16) uint16_t hc[kHq];
+  oproj_body<TPR, false>(blockIdx.x, hc, att, Wo, bo, xbuf, nullptr, nullptr, mid, nullptr, nullptr, 0, nullptr,
+                         nullptr);
 }
 
 // post-attention RMSNorm + router + top-4: 256 / TPR experts per workgroup, grid 128 / (256 / TPR).  Workgroup 0 writes hn (the experts' input);
@@ -293,6 +378,55 @@ NA_DEVICE void top4_softmax(float v0, float v1, int lane, int64_t* __restrict__ 
   }
 }
 
+// Router phase: NR = 128 / (256 / TPR) workgroups; workgroup `blk` computes 256 / TPR logits.  FUSED (the last phase
+// of k_attn_block): the weights and the norm weight are loaded first, then the workgroup waits until
+// *ready >= ready_target (o_proj has written mid) and reads mid with coherent loads; the workgroup that selects the
+// top 4 also returns the launch's phase counters (reset, 3 words) to zero: every waiter has passed by then.
+template <int TPR, bool FUSED>
+NA_DEVICE void router_body(int blk, int nr, uint16_t* hc, uint32_t& last, const uint16_t* __restrict__ mid,
+                           const uint16_t* __restrict__ post_w, float eps, const uint16_t* __restrict__ Wr,
+                           const uint16_t* __restrict__ br, uint16_t* __restrict__ hn, float* __restrict__ logits,
+                           uint32_t* __restrict__ counter, int64_t* __restrict__ ids, uint16_t* __restrict__ wts,
+                           const uint32_t* go, uint32_t* sync, uint32_t* err) {
+  constexpr int ROWS = 256 / TPR;
+  const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
+  const int e = ROWS * blk + r;
+  NormIn ni;
+  if constexpr (FUSED) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) ni.w[i] = *reinterpret_cast<const uint4*>(post_w + 8 * min(tid + 256 * i, kH / 8 - 1));
+  } else {
+    ni.load(mid, nullptr, nullptr, post_w);
+  }
+  const uint16_t bv = br[e];
+  __builtin_amdgcn_sched_barrier(0);
+  RowChunks<kH, TPR> rw;
+  rw.load(Wr + (long long)e * kH, j);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (FUSED) {
+    wait_go(go, err);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) ni.m[i] = load16_coherent(mid + 8 * min(tid + 256 * i, kH / 8 - 1));
+  }
+  norm_finish(ni, false, false, eps, hc, nullptr);
+  if (blk == 0)
+    for (int i = tid; i < kH / 8; i += 256)
+      *reinterpret_cast<uint4*>(hn + 8 * i) = *reinterpret_cast<const uint4*>(hc + 8 * i);
+  const float s = rw.dot(hc, j);
+  if (j == 0) __hip_atomic_store(logits + e, rb(s + bf16_to_f32(bv)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)nr - 1;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last || tid >= 64) return;
+  if constexpr (FUSED) sync_reset(sync, tid);
+  top4_softmax(__hip_atomic_load(logits + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+               __hip_atomic_load(logits + tid + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), tid, ids, wts);
+}
+
 template <int TPR>
 __global__ __launch_bounds__(256) void k_router_norm(const uint16_t* __restrict__ mid, const uint16_t* __restrict__ post_w,
                                                      float eps, const uint16_t* __restrict__ Wr,
@@ -301,32 +435,8 @@ __global__ __launch_bounds__(256) void k_router_norm(const uint16_t* __restrict_
                                                      int64_t* __restrict__ ids, uint16_t* __restrict__ wts) {
   __shared__ __align__(16) uint16_t hc[kH];
   __shared__ uint32_t last;
-  constexpr int ROWS = 256 / TPR;
-  const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
-  const int e = ROWS * blockIdx.x + r;
-  NormIn ni;
-  ni.load(mid, nullptr, nullptr, post_w);
-  const uint16_t bv = br[e];
-  __builtin_amdgcn_sched_barrier(0);
-  RowChunks<kH, TPR> rw;
-  rw.load(Wr + (long long)e * kH, j);
-  __builtin_amdgcn_sched_barrier(0);
-  norm_finish(ni, false, false, eps, hc, nullptr);
-  if (blockIdx.x == 0)
-    for (int i = tid; i < kH / 8; i += 256)
-      *reinterpret_cast<uint4*>(hn + 8 * i) = *reinterpret_cast<const uint4*>(hc + 8 * i);
-  const float s = rw.dot(hc, j);
-  if (j == 0) __hip_atomic_store(logits + e, rb(s + bf16_to_f32(bv)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) {
-    last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
-    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!last || tid >= 64) return;
-  top4_softmax(__hip_atomic_load(logits + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-               __hip_atomic_load(logits + tid + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), tid, ids, wts);
+  router_body<TPR, false>(blockIdx.x, gridDim.x, hc, last, mid, post_w, eps, Wr, br, hn, logits, counter, ids, wts,
+                          nullptr, nullptr, nullptr);
 }
 
 // Tail 1: x = bf16(mid + bf16(g + bf16(c))); hn = bf16(w * (x * r)) (one workgroup).
@@ -634,6 +744,92 @@ __global__ __launch_bounds__(256) void k_route_pack(const uint16_t* __restrict__
   }
 }
 
+
+// ---------------------------------------------------------------- the attention block of a decode layer, one launch
+// Phases by workgroup id (see handoff.h): [QKV: 640][attention: 8 ns][o_proj: 720][router: 32].  Each phase issues
+// its own loads first (weights, the older keys of the cache) and then waits for what it needs: the attention of KV
+// head h for the 80 QKV workgroups of its group (query heads 8h .. 8h + 7, K and V head h: q and the step's K / V
+// row), o_proj for the 8 attention heads, the router for every o_proj row.  sync: kSyncWords uint32 (the layout above), zero before the first launch and left zero except the error
+// flag (line kSyncErr), which a wait that gave up raises and nothing clears.
+constexpr int kBlkQkv = kQkvRows / (256 / kQkvTpr);
+constexpr int kBlkOproj = kH / (256 / kOprojTpr);
+constexpr int kBlkRouter = kNE / (256 / kRouterTpr);
+
+union AttnBlockLds {
+  AttnLds attn;
+  struct {
+    __align__(16) uint16_t hc[kHq];
+    float ys[256];
+    uint32_t last;
+  } core;
+};
+
+struct AttnBlockArgs {
+  uint16_t* mid;
+  const uint16_t* g;
+  const float* c;
+  uint16_t* xbuf;
+  const uint16_t* in_w;
+  const uint16_t* Wqkv;
+  const uint16_t* bqkv;
+  const int64_t* pos;
+  const float* inv_freq;
+  uint16_t* kc;
+  uint16_t* vc;
+  long long cache_rows;
+  int ring;
+  int window;
+  int ns;
+  float eps;
+  float att_scale;
+  float scaling;
+  uint16_t* q;
+  const uint16_t* sinks;
+  float* work;
+  uint16_t* att;
+  const uint16_t* Wo;
+  const uint16_t* bo;
+  const uint16_t* post_w;
+  const uint16_t* Wr;
+  const uint16_t* br;
+  uint16_t* hn;
+  float* logits;
+  int64_t* ids;
+  uint16_t* wts;
+  uint32_t* sync;
+};
+
+__global__ __launch_bounds__(256, 4) void k_attn_block(AttnBlockArgs a) {
+  __shared__ AttnBlockLds L;
+  uint32_t* sync = a.sync;
+  uint32_t* err = sync + kSyncErr * kLine;
+  int blk = blockIdx.x;
+  if (blk < kBlkQkv) {                                  // QKV -> the release of its KV group
+    qkv_body<kQkvTpr, true>(blk, L.core.hc, L.core.ys, a.mid, a.g, a.c, a.xbuf, a.in_w, a.Wqkv, a.bqkv, a.pos,
+                            a.inv_freq, a.kc, a.vc, a.cache_rows, a.ring, a.q, a.eps, a.att_scale, sync);
+    return;
+  }
+  blk -= kBlkQkv;
+  const int natt = kNKV * a.ns;
+  if (blk < natt) {                                     // attention (one count per head) -> o_proj's flags
+    decode_attn_body<true>(L.attn, blk, a.q, a.kc, a.vc, a.cache_rows, a.sinks, a.pos, a.att, a.scaling, a.window,
+                           a.ring, a.ns, a.work, sync + kSyncSplit * kLine,
+                           AttnHandoff{sync + sync_qkv_go((blk / a.ns) % kNKV), sync + sync_cnt(0), (uint32_t)kNKV,
+                                       sync + sync_go(0, 0), err});
+    return;
+  }
+  blk -= natt;
+  if (blk < kBlkOproj) {                                // o_proj -> the router's flags
+    oproj_body<kOprojTpr, true>(blk, L.core.hc, a.att, a.Wo, a.bo, nullptr, a.g, a.c, a.mid,
+                                sync + sync_go(0, blk % kGo), sync + sync_cnt(1), (uint32_t)kBlkOproj,
+                                sync + sync_go(1, 0), err);
+    return;
+  }
+  blk -= kBlkOproj;
+  router_body<kRouterTpr, true>(blk, kBlkRouter, L.core.hc, L.core.last, a.mid, a.post_w, a.eps, a.Wr, a.br, a.hn,
+                                a.logits, sync + kSyncRouter * kLine, a.ids, a.wts, sync + sync_go(1, blk % kGo), sync,
+                                err);
+}
 }  // namespace na
 
 using namespace na;
@@ -688,6 +884,38 @@ int na_core_route_pack(const void* hn, const float* logits, const int64_t* ids, 
                      near_miss ? 1 : 0);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
+
+int na_core_attn_block(void* mid, const void* g, const float* c, void* xbuf, const void* in_w, const void* Wqkv,
+                       const void* bqkv, const int64_t* pos, const float* inv_freq, void* kc, void* vc,
+                       long long cache_rows, int ring, void* q, float eps, float att_scale, const void* sinks,
+                       float scaling, int window, int n_split, float* attn_work, void* att, const void* Wo,
+                       const void* bo, const void* post_w, const void* Wr, const void* br, void* hn, float* logits,
+                       int64_t* ids, void* wts, unsigned int* sync, void* const* events, hipStream_t stream) {
+  if (!mid || !xbuf || !in_w || !Wqkv || !bqkv || !pos || !inv_freq || !kc || !vc || !q || !sinks || !att || !Wo ||
+      !bo || !post_w || !Wr || !br || !hn || !logits || !ids || !wts || !sync || cache_rows <= 0 || ring < 0)
+    return kErrArgs;
+  if (c && !g) return kErrArgs;
+  if (ring > 0 && (window <= 0 || ring < window || cache_rows != ring)) return kErrArgs;
+  if (n_split <= 0 || n_split > kAttnMaxSplit || window < 0 || (n_split > 1 && !attn_work)) return kErrArgs;
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc) |
+       reinterpret_cast<uintptr_t>(att)) & 15)
+    return kErrArgs;
+  AttnBlockArgs a{(uint16_t*)mid, (const uint16_t*)g, c, (uint16_t*)xbuf, (const uint16_t*)in_w,
+                  (const uint16_t*)Wqkv, (const uint16_t*)bqkv, pos, inv_freq, (uint16_t*)kc, (uint16_t*)vc,
+                  cache_rows, ring, window, n_split, eps, att_scale, scaling, (uint16_t*)q, (const uint16_t*)sinks,
+                  attn_work, (uint16_t*)att, (const uint16_t*)Wo, (const uint16_t*)bo, (const uint16_t*)post_w,
+                  (const uint16_t*)Wr, (const uint16_t*)br, (uint16_t*)hn, logits, ids, (uint16_t*)wts,
+                  (uint32_t*)sync};
+  const dim3 grid((unsigned)(kBlkQkv + kNKV * n_split + kBlkOproj + kBlkRouter)), block(256);
+  hipEvent_t e0 = events ? (hipEvent_t)events[0] : nullptr, e1 = events ? (hipEvent_t)events[1] : nullptr;
+  if (e0 || e1)
+    hipExtLaunchKernelGGL(k_attn_block, grid, block, 0, stream, e0, e1, 0, a);
+  else
+    hipLaunchKernelGGL(k_attn_block, grid, block, 0, stream, a);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+long long na_core_attn_block_sync_words(void) { return kSyncWords; }
 
 long long na_core_lm_partials(int vocab) { return vocab > 0 ? (vocab + 256 / kLmTpr - 1) / (256 / kLmTpr) : -1; }
 

@@ -128,12 +128,14 @@ class DecodeModel:
     smax:       positions the full-attention K/V caches hold (the sequence buffer holds smax tokens)
     n_split:    key chunks of full-attention layers (1..64); sliding layers use ``sliding_split``
     ring:       rows of a sliding layer's rolling K/V cache (>= its window; 0: linear caches of smax rows)
+    fused_attn: run each layer's QKV, attention, o_proj and router as one launch (na_core_attn_block) instead of four
 
     The step reads its input token from ``seq[pos]`` and writes the argmax to ``pred[pos + 1]`` and, unless
     ``pos + 1 < n_forced``, to ``seq[pos + 1]``; it then advances ``pos``.  All of that state lives on the device."""
 
     def __init__(self, weights: DecodeWeights, experts: ResidentExperts, smax: int, n_split: int = 32,
-                 sliding_split: int = 1, ring: int | None = None, keep_logits: bool = False, sample: bool = False):
+                 sliding_split: int = 1, ring: int | None = None, keep_logits: bool = False, sample: bool = False,
+                 fused_attn: bool = True):
         dev = weights.embed.device
         if dev.type != "cuda":
             raise ValueError("weights must be on a CUDA device")
@@ -183,6 +185,8 @@ class DecodeModel:
             raise ValueError("n_split and sliding_split must be in [1, 64]")
         self.attn_work = z(max(N.lib().na_attn_workspace_floats(1, ns_max), 1), dt=torch.float32)
         self.attn_counters = z(NKV, dt=torch.int32)
+        self.fused_attn = bool(fused_attn)
+        self.sync = z(N.lib().na_core_attn_block_sync_words(), dt=torch.int32)   # fused block's counters and flags
         self.graph = None
 
     def _check_weights(self):
@@ -220,18 +224,31 @@ class DecodeModel:
     # ------------------------------------------------------------------------------------------------ launches
     def layer(self, li: int, events: dict | None = None) -> None:
         """One layer's launches on the current stream (no host synchronisation, capturable).  events: None, or a dict
-        with "attn" (2 timing events) and/or "experts" (the expert launches' events, ResidentExperts.launches(1)) for
-        dispatch-timestamped timing of an eager call (measurement only)."""
+        with "attn" (2 timing events: the attention launch, or with fused_attn the whole attention block) and/or
+        "experts" (the expert launches' events, ResidentExperts.launches(1)) for dispatch-timestamped timing of an
+        eager call (measurement only)."""
         ly = self.w.layers[li]
         s = N.stream(self.dev)
         kc, vc = self.kc[li], self.vc[li]
         ring = self.ring if ly.sliding else 0
         rows = kc.shape[2]
+        ns = self.sliding_split if ly.sliding else self.n_split
+        if self.fused_attn:
+            N.call("na_core_attn_block", self.mid.data_ptr(), self.g.data_ptr() if li else None, None,
+                   self.xbuf.data_ptr(), ly.in_w.data_ptr(), ly.Wqkv.data_ptr(), ly.bqkv.data_ptr(),
+                   self.pos.data_ptr(), self.inv_freq.data_ptr(), kc.data_ptr(), vc.data_ptr(), rows, ring,
+                   self.q.data_ptr(), EPS, float(self.att_scale), ly.sinks.data_ptr(), float(self.scaling),
+                   int(ly.sliding), ns, self.attn_work.data_ptr(), self.att.data_ptr(), ly.Wo.data_ptr(),
+                   ly.bo.data_ptr(), ly.post_w.data_ptr(), ly.Wr.data_ptr(), ly.br.data_ptr(), self.hn.data_ptr(),
+                   self.r_logits.data_ptr(), self.ids.data_ptr(), self.wts.data_ptr(), self.sync.data_ptr(),
+                   N.events_array(events.get("attn")) if events else None, s)
+            self.rx.forward_decode(li, self.hn, self.ids, self.wts, out=self.g,
+                                   events=events.get("experts") if events else None)
+            return
         N.call("na_core_qkv", self.mid.data_ptr(), self.g.data_ptr() if li else None, None, self.xbuf.data_ptr(),
                ly.in_w.data_ptr(), ly.Wqkv.data_ptr(), ly.bqkv.data_ptr(), self.pos.data_ptr(),
                self.inv_freq.data_ptr(), kc.data_ptr(), vc.data_ptr(), rows, ring, self.q.data_ptr(), EPS,
                float(self.att_scale), s)
-        ns = self.sliding_split if ly.sliding else self.n_split
         N.call("na_decode_attention", self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), rows, ly.sinks.data_ptr(),
                self.pos.data_ptr(), self.att.data_ptr(), 1, float(self.scaling), int(ly.sliding), ring, ns,
                self.attn_work.data_ptr(), self.attn_counters.data_ptr(),
@@ -377,6 +394,10 @@ class DecodeModel:
         return x, m
 
     # ------------------------------------------------------------------------------------------------ graphs
+    def sync_error(self) -> bool:
+        """Whether a fused attention block ever gave up a wait (its outputs were then invalid).  Reads the device."""
+        return bool(int(self.sync[0].item()))
+
     def capture(self) -> torch.cuda.CUDAGraph:
         """Capture one step as a hipGraph (replay = one greedy step at the device-side position).  The capture itself
         runs nothing; state is untouched."""

@@ -1,0 +1,80 @@
+"""The fused attention block of a decode layer (na_core_attn_block: QKV, attention, o_proj and router as four phases
+of one launch, reference fused_core.py:581-629) against the four separate launches it replaces, on the GPU.
+
+Bar: bit-identical outputs (q, the K / V rows, xbuf, att, mid, hn, router logits' selection and weights) and caches
+over consecutive decode steps of a 2-layer model with a sliding layer on a 16-row ring and a full layer, for the full
+layer's attention in 1, 4 and 32 chunks (chunks past the position are empty), across the ring wrap; the launch leaves
+its counters at zero and its error flag clear; graph replays equal eager steps.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+H, NE, VOCAB, WIN, N_SLOTS, SMAX = 2880, 128, 4096, 16, 8, 64
+
+
+@pytest.fixture(scope="module")
+def parts():
+    import torch
+    from neural_amd import synth
+    from neural_amd.model import random_weights
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT_T950 as LT
+
+    dev = torch.device("cuda", 0)
+    print("case attention block fixture: 2 layers, vocab 4096, window 16", flush=True)
+    w = random_weights(n_layers=2, vocab=VOCAB, device="cpu", seed=17, window=WIN, norm_std=0.1).to(dev)
+    pool = synth.t950_pool_device(2 * N_SLOTS, dev, seed=61)
+    n = LT.n_layers * LT.n_experts
+    tab = np.zeros(n, np.int64)
+    for li in range(2):
+        tab[li * NE:(li + 1) * NE] = li * N_SLOTS + np.arange(NE) % N_SLOTS
+    rx = ResidentExperts(pool, LT, None, None, torch.from_numpy(tab).to(dev), max_batch=1)
+    return dict(dev=dev, w=w, rx=rx)
+
+
+def _pair(parts, ns):
+    from neural_amd.model import DecodeModel
+    a = DecodeModel(parts["w"], parts["rx"], smax=SMAX, n_split=ns, fused_attn=True)
+    b = DecodeModel(parts["w"], parts["rx"], smax=SMAX, n_split=ns, fused_attn=False)
+    return a, b
+
+
+@pytest.mark.parametrize("ns", [1, 4, 32])
+def test_fused_block_equals_four_launches(parts, ns):
+    import torch
+    print(f"case attention block fused vs 4 launches, n_split={ns}", flush=True)
+    fa, fb = _pair(parts, ns)
+    prompt = np.random.default_rng(300 + ns).integers(0, VOCAB, 12)
+    fa.reset(prompt)
+    fb.reset(prompt)
+    for p in range(40):                                  # past the 16-row ring's wrap, prompt then greedy
+        for m in (fa, fb):
+            m.embed()
+        for li in range(2):
+            fa.layer(li)
+            fb.layer(li)
+            torch.cuda.synchronize()
+            for nm in ("q", "att", "xbuf", "mid", "hn", "ids", "wts", "g"):
+                assert torch.equal(getattr(fa, nm), getattr(fb, nm)), (p, li, nm)
+            assert torch.equal(fa.kc[li], fb.kc[li]) and torch.equal(fa.vc[li], fb.vc[li]), (p, li)
+        for m in (fa, fb):
+            m.tail()
+        torch.cuda.synchronize()
+        assert int(fa.tok.item()) == int(fb.tok.item()), p
+    assert torch.equal(fa.seq, fb.seq)
+    assert not fa.sync_error()
+    assert int(fa.sync.abs().sum()) == 0, fa.sync.cpu().tolist()
+
+
+def test_fused_block_graph_replay_equals_eager(parts):
+    import torch
+    print("case attention block graph replay vs eager", flush=True)
+    fa, _ = _pair(parts, 8)
+    prompt = np.random.default_rng(5).integers(0, VOCAB, 9)
+    eager = fa.generate(prompt, 30, graph=False)
+    first = fa.generate(prompt, 30, graph=True)
+    again = fa.generate(prompt, 30, graph=True)
+    assert torch.equal(eager, first) and torch.equal(first, again)
+    assert not fa.sync_error() and int(fa.sync.abs().sum()) == 0
