@@ -22,9 +22,11 @@ uniform E2M1 codes, E8M0 exponents uniform in [119, 125]) serves two measurement
                 gptoss_experts(E=4) call per layer per token, at all physical cores of one socket (capped at the CPUs
                 this process may use) and at the reference's default of 8 threads.
 
-Other workloads print one line each: experts (configuration 1 alone, any layout), model (configuration 4 alone),
-prefill (configuration 2, with the reference CPU kernel's multi-token call as its baseline), attention
-(configuration 3).
+Other workloads print one line each: experts (configuration 1 alone, any layout: t950 runs the MFMA kernels, raw and
+ps4 the VALU na_moe_decode kernels), model (configuration 4 alone), prefill (configuration 2, with the reference CPU
+kernel's multi-token call as its baseline and a per-expert GEMM sweep over M = 64 .. 2048 tokens per expert),
+attention (configuration 3), gemv (the reference-named mxfp4_gemv at configuration 1's shapes on a raw or PS4 pool)
+and mfma (the matrix cores' issue rate for the scaled FP8 x FP4 and the bf16 instructions).
 """
 from __future__ import annotations
 
@@ -337,6 +339,7 @@ def bench_prefill(A):
     log(f"prefill T={T}: {el * 1e6:.1f} us/layer ({T / el:.0f} tok/s), {flop / el / 1e12:.1f} TFLOP/s; launches "
         + ", ".join(f"{nm} {v:.1f} us" for nm, v in per.items()))
     gu_flop = 2.0 * P * 5760 * 2880
+    sweep = expert_gemm_sweep(rx, dev) if not A.no_batch_sweep else None
     cpu = None
     if not A.skip_cpu:
         try:
@@ -361,7 +364,8 @@ def bench_prefill(A):
                       "layer_tflops": round(flop / el / 1e12, 2),
                       "gate_up_tflops": round(gu_flop / (per["gate_up"] * 1e-6) / 1e12, 2),
                       "roofline_time_us": round(t_roof * 1e6, 1),
-                      "roofline_fraction": round(t_roof / el, 4)},
+                      "roofline_fraction": round(t_roof / el, 4),
+                      "expert_gemm_sweep": sweep},
            "roofline": {"bound": "hbm" if (wbytes + abytes) / (HBM_PEAK_GBS * 1e9) >= flop / 2.5e15 else "mfma",
                         "achieved": round((wbytes + abytes) / el / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round((wbytes + abytes) / el / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
@@ -763,6 +767,212 @@ def bench_decode(A):
     print(json.dumps(res), flush=True)
 
 
+def store_pool(dev, n_slots, layout, seed):
+    """A device pool of n_slots expert slots in a store layout ("raw" E8M0 rows or "ps4" packed 4-bit scale rows):
+    uniform E2M1 code bytes, E8M0 exponents uniform in [119, 125] (PS4: base 119, nibble deltas 0..6)."""
+    import torch
+
+    from neural_amd import synth
+    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4
+
+    L = GPTOSS_LAYOUT_PS4 if layout == "ps4" else GPTOSS_LAYOUT
+    pool = torch.empty((n_slots, L.slot_bytes), dtype=torch.uint8, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    cb = GPTOSS_LAYOUT.gate_pack_bytes + GPTOSS_LAYOUT.down_pack_bytes
+    pool[:, :cb].random_(0, 256, generator=g)
+    if layout == "ps4":
+        sc = pool[:, cb:].view(n_slots, -1, 46)
+        sc[:, :, 0].fill_(synth.SCALE_LO)
+        lo = torch.randint(0, 7, sc[:, :, 1:].shape, dtype=torch.uint8, device=dev, generator=g)
+        hi = torch.randint(0, 7, sc[:, :, 1:].shape, dtype=torch.uint8, device=dev, generator=g)
+        sc[:, :, 1:] = lo | (hi << 4)
+        del lo, hi
+    else:
+        pool[:, cb:].random_(synth.SCALE_LO, synth.SCALE_HI + 1, generator=g)
+    return pool
+
+
+def bench_gemv(A):
+    """The reference-named decode GEMV (q80.mxfp4_kernels.mxfp4_gemv, the VALU kernel k_mxfp4_gemv) at configuration
+    1's shapes on a resident store-layout pool (raw E8M0 rows, or PS4 with --layout ps4): per layer, the 4 routed
+    slots' gate_up rows [4 x 5760 x 2880] against one shared x row, then their down rows [4 x 2880 x 2880] against
+    per-expert rows (per_expert_x=True), the reference's unfused decode call pattern (mxfp4_kernels.py:474-489).
+    Timed: graph replays of 36 layers; per launch: dispatch-ordered events on the launch stream."""
+    import torch
+
+    from neural_amd import synth
+    from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4, mxfp4_pool_views
+    from neural_amd.q80.mxfp4_kernels import mxfp4_gemv
+
+    dev = torch.device("cuda", 0)
+    layout = "ps4" if A.layout == "ps4" else "raw"
+    L = GPTOSS_LAYOUT_PS4 if layout == "ps4" else GPTOSS_LAYOUT
+    n_slots = N_LAYERS * N_EXPERTS
+    log(f"gemv: allocating {layout} pool {n_slots} x {L.slot_bytes} B = {n_slots * L.slot_bytes / 1e9:.1f} GB")
+    pool = store_pool(dev, n_slots, layout, 77)
+    gb, db, gs, ds = mxfp4_pool_views(pool, L)
+    rng = np.random.default_rng(4747)
+    n_sets = A.sets
+    ids_np, _ = routing_sets(rng, n_sets, 1)
+    slots = torch.from_numpy(ids_np[:, :, 0, :] + np.arange(N_LAYERS)[None, :, None] * N_EXPERTS).to(dev)
+    x = synth.bf16_normal(rng, (N_LAYERS, 1, H)).to(dev)
+    hh = synth.bf16_normal(rng, (N_LAYERS, TOPK, H)).to(dev)
+
+    def step(s, ev=None):
+        for l in range(N_LAYERS):
+            if ev is not None:
+                ev[l][0].record()
+            mxfp4_gemv(x[l], gb, gs, slots[s, l])
+            if ev is not None:
+                ev[l][1].record()
+            mxfp4_gemv(hh[l], db, ds, slots[s, l], per_expert_x=True)
+            if ev is not None:
+                ev[l][2].record()
+
+    step(0)
+    torch.cuda.synchronize()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        step(0)
+    torch.cuda.current_stream().wait_stream(cs)
+    graphs = []
+    for s in range(n_sets):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            step(s)
+        graphs.append(gr)
+    for i in range(A.warmup):
+        graphs[i % n_sets].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(A.steps):
+        graphs[i % n_sets].replay()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    ms_step = el / A.steps * 1e3
+    step_bytes = N_LAYERS * TOPK * SLOT_ALGO_BYTES
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(N_LAYERS)]
+    for row in ev:
+        for e in row:
+            e.record()
+    torch.cuda.synchronize()
+    gu_ms = dn_ms = 0.0
+    R = max(A.roofline_steps, 1)
+    for r in range(R):
+        queue_behind_spin(torch)
+        step(r % n_sets, ev)
+        torch.cuda.synchronize()
+        for l in range(N_LAYERS):
+            gu_ms += ev[l][0].elapsed_time(ev[l][1])
+            dn_ms += ev[l][1].elapsed_time(ev[l][2])
+    n = R * N_LAYERS
+    gu_us, dn_us = gu_ms / n * 1e3, dn_ms / n * 1e3
+    gu_gbps = TOPK * GATE_UP_BYTES / (gu_us * 1e-6) / 1e9
+    dn_gbps = TOPK * DOWN_BYTES / (dn_us * 1e-6) / 1e9
+    log(f"gemv {layout}: {ms_step:.3f} ms/step ({step_bytes / (ms_step * 1e-3) / 1e9:.0f} GB/s whole step); "
+        f"gate_up {gu_us:.2f} us ({gu_gbps:.0f} GB/s), down {dn_us:.2f} us ({dn_gbps:.0f} GB/s)")
+    res = {"metric": "MXFP4 expert GEMV HBM GB/s (reference-named mxfp4_gemv, VALU kernel, decode shapes)",
+           "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 1), "unit": "GB/s", "n_gpus": 1, "steps": A.steps,
+           "warmup": A.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+           "config": {"workload": f"config1 shapes through mxfp4_gemv: 36 layers x (gate_up [4 x 5760 x 2880] + down "
+                                  f"[4 x 2880 x 2880]) per step, {layout} store-layout pool (61 GB), random top-4 "
+                                  f"routing from {n_sets} sets", "layout": layout,
+                      "gate_up_avg_launch_us": round(gu_us, 3), "down_avg_launch_us": round(dn_us, 3),
+                      "down_gbps": round(dn_gbps, 1), "down_frac": round(dn_gbps / HBM_PEAK_GBS, 4)},
+           "roofline": {"bound": "hbm", "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gu_gbps / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_mxfp4_gemv (gate_up)",
+                        "algorithmic_bytes_per_launch": TOPK * GATE_UP_BYTES},
+           "cpu_baseline": None}
+    print(json.dumps(res), flush=True)
+
+
+def bench_mfma(A):
+    """Matrix-core issue rate on this GPU: a grid of 256-thread workgroups each running chains of four independent
+    MFMAs on register operands (na_bench_mfma_rate): kind 0 the scaled 16x16x128 FP8 x FP4 instruction the prefill
+    and decode tile kernels use, kind 1 the bf16 16x16x32 one.  Timed with events the dispatch itself stamps."""
+    import torch
+
+    from neural_amd import _native as N
+
+    dev = torch.device("cuda", 0)
+    blocks = 256 * 8
+    out = torch.empty(blocks * 4, dtype=torch.float32, device=dev)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    for e in ev:
+        e.record()
+    torch.cuda.synchronize()
+    res = {}
+    for kind, name, flop, peaks in ((0, "scaled_f8f6f4_16x16x128 (E4M3 x E2M1)", 2 * 16 * 16 * 128,
+                                     {"fp8": 5.0e15, "fp4": 10.1e15}),
+                                    (1, "bf16_16x16x32", 2 * 16 * 16 * 32, {"bf16": 2.5e15})):
+        iters = 4096
+        N.call("na_bench_mfma_rate", kind, blocks, iters, out.data_ptr(), None, N.stream(dev))
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(5):
+            N.call("na_bench_mfma_rate", kind, blocks, 20000, out.data_ptr(), N.events_array(ev), N.stream(dev))
+            torch.cuda.synchronize()
+            ms = ev[0].elapsed_time(ev[1])
+            best = ms if best is None else min(best, ms)
+        total = blocks * 4 * 20000 * 4 * flop
+        rate = total / (best * 1e-3)
+        res[name] = {"ms": round(best, 4), "tflops": round(rate / 1e12, 1),
+                     **{f"frac_{k}_peak": round(rate / v, 4) for k, v in peaks.items()}}
+        log(f"mfma {name}: {rate / 1e12:.0f} TFLOP/s ({best:.3f} ms)")
+    k0 = res["scaled_f8f6f4_16x16x128 (E4M3 x E2M1)"]["tflops"]
+    print(json.dumps({"metric": "MFMA issue rate", "value": k0, "unit": "TFLOP/s", "n_gpus": 1, "steps": 5,
+                      "higher_is_better": True, "dtype": "f8f6f4", "data": "synthetic",
+                      "config": {"workload": f"{blocks} workgroups x 4 waves x 20000 rounds of 4 independent MFMAs",
+                                 "kinds": res,
+                                 "exact_product_rate_tflops": round(k0 / 2, 1),
+                                 "note": "the prefill kernels issue two scaled MFMAs (E4M3 hi and lo) per exact "
+                                         "bf16 x E2M1 product, so half kind 0's rate is their ceiling"}}),
+          flush=True)
+
+
+def expert_gemm_sweep(rx, dev, sizes=(64, 128, 330, 1024, 2048), reps=5):
+    """Per-expert GEMM rates of the prefill kernels: every token routed to the same four experts (M pairs each), so
+    each expert's gate_up and down products are M x 5760 x 2880 and M x 2880 x 2880; launch durations from
+    dispatch-stamped events."""
+    import torch
+
+    from neural_amd import synth
+
+    out = {}
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(10)]
+    for e in ev:
+        e.record()
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(330)
+    for M in sizes:
+        ids = torch.tensor([[5, 17, 64, 101]] * M, dtype=torch.int64, device=dev)
+        wts = torch.full((M, TOPK), 0.25, dtype=torch.bfloat16, device=dev)
+        x = synth.bf16_normal(rng, (M, H)).to(dev)
+        y = torch.empty(M, H, dtype=torch.bfloat16, device=dev)
+        rx.forward_prefill(0, x, ids, wts, out=y)
+        torch.cuda.synchronize()
+        gu = dn = 0.0
+        for _ in range(reps):
+            queue_behind_spin(torch, 2.0)
+            rx.forward_prefill(0, x, ids, wts, out=y, events=ev)
+            torch.cuda.synchronize()
+            gu += ev[4].elapsed_time(ev[5]) / reps
+            dn += ev[6].elapsed_time(ev[7]) / reps
+        gf = 2.0 * TOPK * M * 5760 * 2880
+        df = 2.0 * TOPK * M * 2880 * 2880
+        out[str(M)] = {"gate_up_us": round(gu * 1e3, 2), "down_us": round(dn * 1e3, 2),
+                       "gate_up_tflops": round(gf / (gu * 1e-3) / 1e12, 1),
+                       "down_tflops": round(df / (dn * 1e-3) / 1e12, 1),
+                       "gate_up_frac_exact": round(gf / (gu * 1e-3) / 2.5e15, 4),
+                       "down_frac_exact": round(df / (dn * 1e-3) / 2.5e15, 4)}
+        log(f"expert GEMM M={M}: gate_up {gu * 1e3:.1f} us ({out[str(M)]['gate_up_tflops']} TFLOP/s), "
+            f"down {dn * 1e3:.1f} us ({out[str(M)]['down_tflops']} TFLOP/s)")
+    return out
+
+
 def bench_experts(A):
     """Configuration 1 alone, on a pool of any layout (t950: MFMA kernels; raw / ps4: the VALU kernels)."""
     import torch
@@ -786,20 +996,7 @@ def bench_experts(A):
     if A.layout == "t950":
         pool = synth.t950_pool_device(n_slots, dev, 4242)
     else:
-        pool = torch.empty((n_slots, L.slot_bytes), dtype=torch.uint8, device=dev)
-        g = torch.Generator(device=dev)
-        g.manual_seed(1234)
-        cb = GPTOSS_LAYOUT.gate_pack_bytes + GPTOSS_LAYOUT.down_pack_bytes
-        pool[:, :cb].random_(0, 256, generator=g)
-        if A.layout == "ps4":                       # E8M0 exponents uniform in [119, 125]: base 119, deltas 0..6
-            sc = pool[:, cb:].view(n_slots, -1, 46)
-            sc[:, :, 0].fill_(synth.SCALE_LO)
-            lo = torch.randint(0, 7, sc[:, :, 1:].shape, dtype=torch.uint8, device=dev, generator=g)
-            hi = torch.randint(0, 7, sc[:, :, 1:].shape, dtype=torch.uint8, device=dev, generator=g)
-            sc[:, :, 1:] = lo | (hi << 4)
-            del lo, hi
-        else:
-            pool[:, cb:].random_(synth.SCALE_LO, synth.SCALE_HI + 1, generator=g)
+        pool = store_pool(dev, n_slots, A.layout, 1234)
     torch.cuda.synchronize()
     log("pool filled")
     bias_gu = torch.zeros(n_slots, L.gate_up_n, dtype=torch.bfloat16, device=dev)
@@ -854,10 +1051,12 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--gu-pairs", type=int, default=4, help="VALU gate_up row pairs per wavefront (1, 2, 4)")
     ap.add_argument("--dn-pairs", type=int, default=2, help="VALU down row pairs per wavefront (1, 2, 4)")
-    ap.add_argument("--workload", choices=("decode", "experts", "attention", "prefill", "model"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "experts", "attention", "prefill", "model", "gemv", "mfma"),
+                    default="decode",
                     help="decode: configuration 4 (value) + configuration 1 on one pool (the default); experts: "
                          "configuration 1 alone; prefill: configuration 2; attention: configuration 3; model: "
-                         "configuration 4 alone")
+                         "configuration 4 alone; gemv: the reference-named mxfp4_gemv at configuration 1's shapes; "
+                         "mfma: matrix-core issue rate")
     ap.add_argument("--tokens", type=int, default=2048, help="prefill: prompt tokens")
     ap.add_argument("--context", type=int, default=4096, help="decode / model: context tokens before the timed decode")
     ap.add_argument("--context-mode", choices=("prefill", "decode"), default="prefill",
@@ -881,7 +1080,7 @@ def main():
     if not 1 <= A.batch <= 8:
         sys.exit("--batch must be in [1, 8]")
     return {"attention": bench_attention, "prefill": bench_prefill, "model": bench_model, "experts": bench_experts,
-            "decode": bench_decode}[A.workload](A)
+            "decode": bench_decode, "gemv": bench_gemv, "mfma": bench_mfma}[A.workload](A)
 
 
 if __name__ == "__main__":

@@ -86,6 +86,12 @@ int na_selftest_mfma(const void* a, const void* b, float* d, hipStream_t stream)
 int na_selftest_x8(const void* in, int rows, void* hi, void* lo, void* sc, hipStream_t stream);
 int na_selftest_mfma8(const void* a, const void* sa, const void* tile, const void* sb, float* d, hipStream_t stream);
 
+/* Matrix-core rate probe (measurement only; no reference counterpart): `blocks` workgroups of 4 waves, each wave
+ * running `iters` x 4 independent MFMAs on register operands: kind 0 the block-scaled v_mfma_scale_f32_16x16x128_f8f6f4
+ * (E4M3 x E2M1, 65,536 flops each), kind 1 v_mfma_f32_16x16x32_bf16 (16,384 flops each).  out: float [4 blocks].
+ * events: NULL or 2 hipEvent_t timestamped by the dispatch. */
+int na_bench_mfma_rate(int kind, int blocks, int iters, float* out, void* const* events, hipStream_t stream);
+
 /* ---- gfx950 tile layout ("t950", weight_repr "mxfp4_g32_t950").  No counterpart in the reference's store; it is
  * this build's resident layout, a lossless permutation of the reference's slot (neural/moe/layout.py:143-186,
  * tools/scale_pack.py:6-12): 540 blocks of 16 rows, each 22.5 KiB of codes in v_mfma_f32_16x16x32_bf16 B-operand

@@ -28,6 +28,7 @@ SIGNATURES = {
     "na_selftest_bf16": [VP, VP, VP, VP, I64, VP],
     "na_selftest_x8": [VP, I32, VP, VP, VP, VP],
     "na_selftest_mfma8": [VP, VP, VP, VP, VP, VP],
+    "na_bench_mfma_rate": [I32, I32, I32, VP, VP, VP],
     "na_t950_slot_bytes": [],
     "na_repack_to_t950": [VP, I64, I32, VP, I64, I32, VP],
     "na_repack_from_t950": [VP, I64, VP, I64, I32, I32, VP],

@@ -2,6 +2,8 @@
 #include "common.h"
 #include "t950.h"
 
+#include <hip/hip_ext.h>
+
 namespace na {
 
 // out[2 * b + i] = bf16 bits of element i (0 = low nibble) of byte b, through the same helper the GEMV kernels use.
@@ -90,6 +92,41 @@ __global__ void k_selftest_mfma8(const uint8_t* __restrict__ a, const uint8_t* _
   for (int r = 0; r < 4; ++r) d[(4 * kb + r) * 16 + m] = acc[r];
 }
 
+
+// Matrix-core rate probe: every wave runs `iters` rounds of 4 independent MFMAs on register operands, kind 0 the
+// block-scaled v_mfma_scale_f32_16x16x128_f8f6f4 with E4M3 A and E2M1 B (the instruction of the decode and prefill
+// expert kernels), kind 1 v_mfma_f32_16x16x32_bf16 (the prompt attention's).  Operands are constant ones (E4M3 0x38,
+// E2M1 0x2, bf16 1.0, E8M0 127), so the accumulators stay finite; out[wave] = their sum keeps every MFMA live.
+// Flops per MFMA: 2 x 16 x 16 x 128 (kind 0), 2 x 16 x 16 x 32 (kind 1).
+template <int KIND>
+__global__ __launch_bounds__(256) void k_mfma_rate(int iters, float* __restrict__ out) {
+  f32x4_t acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if constexpr (KIND == 0) {
+    const int one8 = 0x38383838, one4 = 0x22222222;
+    const mfma_i32x8_t a = {one8, one8, one8, one8, one8, one8, one8, one8};
+    const mfma_i32x8_t b = {one4, one4, one4, one4, 0, 0, 0, 0};
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc[j], 0, 4, 0, 127, 0, 127);
+    }
+  } else {
+    bf16x8_t a;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = (__bf16)1.0f;
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, a, acc[j], 0, 0, 0);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+  if ((threadIdx.x & 63) == 0) out[blockIdx.x * 4 + (threadIdx.x >> 6)] = s;
+}
+
 }  // namespace na
 
 extern "C" {
@@ -134,6 +171,17 @@ int na_selftest_mfma8(const void* a, const void* sa, const void* tile, const voi
   if (!a || !sa || !tile || !sb || !d) return na::kErrArgs;
   hipLaunchKernelGGL(na::k_selftest_mfma8, dim3(1), dim3(64), 0, stream, (const uint8_t*)a, (const uint8_t*)sa,
                      (const uint8_t*)tile, (const uint8_t*)sb, d);
+  return hipGetLastError() == hipSuccess ? na::kOk : na::kErrLaunch;
+}
+
+int na_bench_mfma_rate(int kind, int blocks, int iters, float* out, void* const* events, hipStream_t stream) {
+  if ((kind != 0 && kind != 1) || blocks <= 0 || iters <= 0 || !out) return na::kErrArgs;
+  hipEvent_t e0 = events ? (hipEvent_t)events[0] : nullptr, e1 = events ? (hipEvent_t)events[1] : nullptr;
+  auto kern = kind == 0 ? na::k_mfma_rate<0> : na::k_mfma_rate<1>;
+  if (e0 || e1)
+    hipExtLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, stream, e0, e1, 0, iters, out);
+  else
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), 0, stream, iters, out);
   return hipGetLastError() == hipSuccess ? na::kOk : na::kErrLaunch;
 }
 

@@ -138,6 +138,15 @@ NA_DEVICE float dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+// Largest value over the 16 lanes of each row of the wavefront (lanes 16 r .. 16 r + 15), returned to all 16: DPP
+// quad_perm [1,0,3,2], [2,3,0,1], then row_ror 4 and 8.  Must run with all lanes active.
+NA_DEVICE float row16_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x124>(v));
+  return fmaxf(v, dpp<0x128>(v));
+}
+
 // Sum over the 64 lanes of a wavefront, returned (wave-uniform) to every lane.  Must run with all lanes active.
 // Fixed order: lane pairs, quads (DPP quad_perm), rows of 16 (DPP row_ror 4, 8), then the four row sums.
 NA_DEVICE float wave_total(float v) {

@@ -4,8 +4,12 @@
 // server.py:1837-1936, _expert_gemms :1977-2040).
 //
 // The fused layer (k_prefill_gate_up / k_prefill_down) runs on the block-scaled v_mfma_scale_f32_16x16x128_f8f6f4:
-// E2M1 codes and E8M0 scales as stored, activations as two exact E4M3 rows (hi, lo) with one E8M0 scale per 32
-// elements each, so hi w + lo w are the reference's bf16 x E2M1 products; see the block-scaled section below.
+// E2M1 codes and E8M0 scales as stored, activations as two E4M3 rows (hi, lo) with one E8M0 scale per 32 elements
+// each (x per 32-element block of a row; h per 32 columns of a row, quantised in the gate_up epilogue).  hi w + lo w
+// is the reference's bf16 x E2M1 product exactly for every element within 2^13 of its block's largest magnitude m;
+// an element further below m is reproduced to within 2^-21 m (the remainder's 4 significant bits on the lo grid),
+// so an output deviates from the reference's by at most 2^-21 sum_k |w_k| m_k before its bf16 rounding (t950.h
+// states the quantiser).
 //
 // The plain and grouped GEMM entry points (bf16 activations, no workspace) run the same tiles, the activations
 // quantised into hi + lo rows while they are staged.
@@ -189,6 +193,9 @@ constexpr int kQPitch = 2 * kPKT + 16;                 // LDS bytes per staged r
 constexpr int kQStage = kPBM * kQPitch + kPBM * 8;     // one k-tile: 64 rows, then 8 scale bytes per row
 constexpr int kGuSlots = 3;                            // gate_up: 23 column groups over 8 XCDs, 3 per XCD
 constexpr int kDnSlots = 2;                            // down: 15 column groups, 2 per XCD
+constexpr int kYPitch = 2 * kPRows + 16;              // LDS bytes per row of a staged down output tile
+constexpr int kOhPitch = 2 * kPKT + 8;                 // LDS bytes per row of gate_up's staged h codes (rows 4 apart
+                                                       // start 8 banks apart)
 
 // Staging of one k-tile of 64 q rows: pieces of 16 B, thread tid owns piece (tid & 15) of rows (tid >> 4) + 16 i
 // (pieces 0..7 hi, 8..15 lo); threads 0..63 also own the 4 hi and 4 lo scale bytes of row tid, stored interleaved
@@ -309,7 +316,7 @@ struct WStream {
 // One k-tile of gemm8_tile.  A of k-tile t is staged in LDS at cur and the weights of k-tile t are in (c, sc).  It
 // issues the loads of A of k-tile t + 2 (into a_in) and of the weights of k-tile t + 2 (into (c2, sc2)), runs the
 // MFMAs, stores A of k-tile t + 1 (loaded one step earlier, a_out) at nxt and meets the barrier.
-template <int W, int NB, typename S>
+template <int W, int NB, int NT, typename S>
 NA_DEVICE void gemm8_step(int t, const WStream<W, NB>& ws, bool live, const S& st, const uint8_t* cur, uint8_t* nxt,
                           const typename S::Stage& a_out, typename S::Stage& a_in,
                           const uint4 (&c)[NB], const uint32_t (&sc)[NB], uint4 (&c2)[NB], uint32_t (&sc2)[NB],
@@ -329,7 +336,7 @@ NA_DEVICE void gemm8_step(int t, const WStream<W, NB>& ws, bool live, const S& s
     }
     __builtin_amdgcn_s_setprio(1);                     // the MFMA burst issues ahead of the other wave's staging
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
+    for (int tt = 0; tt < NT; ++tt) {
       const uint8_t* row = cur + (16 * tt + m) * kQPitch + 16 * kb;
       const uint4 h0 = *reinterpret_cast<const uint4*>(row), h1 = *reinterpret_cast<const uint4*>(row + 64);
       const uint4 l0 = *reinterpret_cast<const uint4*>(row + 128), l1 = *reinterpret_cast<const uint4*>(row + 192);
@@ -356,7 +363,8 @@ NA_DEVICE void gemm8_step(int t, const WStream<W, NB>& ws, bool live, const S& s
 }
 
 // acc[tt][nb] = D of tokens 16 tt .. 16 tt + 15 x row block blk[nb] (lane (q, n): tokens 16 tt + 4 q + r, row n),
-// over the 23 k-tiles; st stages the activation rows (QRows or XRows).  Both
+// over the 23 k-tiles for tt < NT (the 16-token blocks that hold rows; the others stay zero); st stages the
+// activation rows (QRows or XRows).  Both
 // operand streams run two k-tiles ahead of the MFMAs: the activations through three LDS buffers of a k-tile (64 rows'
 // 256 code bytes and 8 scale bytes each, loaded into registers two steps before and stored one step before their
 // use), each wave's weight codes through three register sets; the k-loop is unrolled by 3 so that every buffer and
@@ -364,9 +372,9 @@ NA_DEVICE void gemm8_step(int t, const WStream<W, NB>& ws, bool live, const S& s
 // them to its NB row blocks.  lds: 3 x kQStage bytes; wsc: this wave's LDS area of NB x 1,536 bytes (t950 scale
 // rows).  A wave without work (live = false) stages and meets every barrier but runs no MFMA.  All 256 threads must
 // call it.
-template <int W, int NB, typename S>
-NA_DEVICE void gemm8_tile(const WSrc& src, const int (&blk)[NB], bool live, const S& st, uint8_t* lds, uint8_t* wsc,
-                          f32x4_t (&acc)[4][NB]) {
+template <int W, int NB, int NT, typename S>
+NA_DEVICE void gemm8_tile_n(const WSrc& src, const int (&blk)[NB], bool live, const S& st, uint8_t* lds, uint8_t* wsc,
+                            f32x4_t (&acc)[4][NB]) {
   const int tid = threadIdx.x, lane = tid & 63;
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt)
@@ -399,12 +407,25 @@ NA_DEVICE void gemm8_tile(const WSrc& src, const int (&blk)[NB], bool live, cons
   __syncthreads();
   int t = 0;
   for (; t + 3 <= kPTiles; t += 3) {                   // k-tiles 0 .. 20
-    gemm8_step<W, NB, S>(t, ws, live, st, b0, b1, a1, a2, c0, s0, c2, s2, acc);
-    gemm8_step<W, NB, S>(t + 1, ws, live, st, b1, b2, a2, a0, c1, s1, c0, s0, acc);
-    gemm8_step<W, NB, S>(t + 2, ws, live, st, b2, b0, a0, a1, c2, s2, c1, s1, acc);
+    gemm8_step<W, NB, NT, S>(t, ws, live, st, b0, b1, a1, a2, c0, s0, c2, s2, acc);
+    gemm8_step<W, NB, NT, S>(t + 1, ws, live, st, b1, b2, a2, a0, c1, s1, c0, s0, acc);
+    gemm8_step<W, NB, NT, S>(t + 2, ws, live, st, b2, b0, a0, a1, c2, s2, c1, s1, acc);
   }
-  gemm8_step<W, NB, S>(t, ws, live, st, b0, b1, a1, a2, c0, s0, c2, s2, acc);       // 21
-  gemm8_step<W, NB, S>(t + 1, ws, live, st, b1, b2, a2, a0, c1, s1, c0, s0, acc);   // 22
+  gemm8_step<W, NB, NT, S>(t, ws, live, st, b0, b1, a1, a2, c0, s0, c2, s2, acc);       // 21
+  gemm8_step<W, NB, NT, S>(t + 1, ws, live, st, b1, b2, a2, a0, c1, s1, c0, s0, acc);   // 22
+}
+
+// gemm8_tile_n for a tile whose rows fill ntt (1..4) 16-token blocks: the MFMAs of empty blocks are not issued
+// (variants for 1, 2 and 4 blocks; 3 runs as 4).  ntt is workgroup-uniform.
+template <int W, int NB, typename S>
+NA_DEVICE void gemm8_tile(const WSrc& src, const int (&blk)[NB], bool live, int ntt, const S& st, uint8_t* lds,
+                          uint8_t* wsc, f32x4_t (&acc)[4][NB]) {
+  if (ntt > 2)
+    gemm8_tile_n<W, NB, 4, S>(src, blk, live, st, lds, wsc, acc);
+  else if (ntt == 2)
+    gemm8_tile_n<W, NB, 2, S>(src, blk, live, st, lds, wsc, acc);
+  else
+    gemm8_tile_n<W, NB, 1, S>(src, blk, live, st, lds, wsc, acc);
 }
 
 // Workgroup b -> (tile, column group): the dispatcher deals workgroups to the 8 XCDs in turn (XCD b % 8), so XCD x
@@ -451,11 +472,12 @@ __global__ __launch_bounds__(256, W == kWT950 ? 2 : 1) void k_prefill_gate_up(
     st.rp[i] = xq + (long long)(order[tl.p0 + min((tid >> 4) + 16 * i, tl.cnt - 1)] >> 2) * kQRow;
   st.srow = xq + (long long)(order[tl.p0 + min(tid & 63, tl.cnt - 1)] >> 2) * kQRow;
   f32x4_t acc[4][4];
-  gemm8_tile<W, 4>(src, blk, live, st, lds, lds + 3 * kQStage + wave * 4 * kWScBytes, acc);
+  const int ntt = (tl.cnt + 15) >> 4;
+  gemm8_tile<W, 4>(src, blk, live, ntt, st, lds, lds + 3 * kQStage + wave * 4 * kWScBytes, acc);
   // h = bf16(SwiGLU(bf16(acc) + bias)) (the reference's bf16 rounding points), quantised per (row, 32-column block)
   // into LDS: oh[row] = hi codes of the workgroup's 128 columns | lo codes, os[row] = 4 hi | 4 lo scale bytes.
   uint8_t* oh = lds;
-  uint8_t* os = lds + kPBM * 2 * kPKT;
+  uint8_t* os = lds + kPBM * kOhPitch;
   if (live) {
     const uint16_t* bg = bias_gu ? bias_gu + gid * kGU : nullptr;
     float bgv[2], buv[2];
@@ -466,7 +488,8 @@ __global__ __launch_bounds__(256, W == kWT950 ? 2 : 1) void k_prefill_gate_up(
       buv[hb] = bg ? bf16_to_f32(bg[kI + j]) : 0.f;
     }
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
+    for (int tt = 0; tt < 4; ++tt) {
+      if (tt >= ntt) break;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         float hv[2];
@@ -479,9 +502,7 @@ __global__ __launch_bounds__(256, W == kWT950 ? 2 : 1) void k_prefill_gate_up(
           }
           hv[hb] = rb(swiglu_clamp_bf16(g, u, alpha, limit));
         }
-        float mx = fmaxf(fabsf(hv[0]), fabsf(hv[1]));
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        const float mx = row16_max(fmaxf(fabsf(hv[0]), fabsf(hv[1])));
         const uint32_t sh = x8_scale_byte(mx);
         const float s_hi = e8m0_f32(sh);
         fp8x2_t o2 = {0, 0};
@@ -489,23 +510,22 @@ __global__ __launch_bounds__(256, W == kWT950 ? 2 : 1) void k_prefill_gate_up(
         const uint32_t hc = __builtin_bit_cast(uint32_t, o2);
         const auto d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hc, s_hi, false);
         const float r0 = hv[0] - d[0], r1 = hv[1] - d[1];
-        float mr = fmaxf(fabsf(r0), fabsf(r1));
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) mr = fmaxf(mr, __shfl_xor(mr, o));
+        const float mr = row16_max(fmaxf(fabsf(r0), fabsf(r1)));
         const uint32_t sl = x8_scale_byte(mr);
         fp8x2_t l2 = {0, 0};
         l2 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(l2, r0, r1, e8m0_f32(sl), false);
         const uint32_t lc = __builtin_bit_cast(uint32_t, l2);
         const int row = 16 * tt + 4 * q + r, c = 32 * wave + n;
-        oh[row * 2 * kPKT + c] = (uint8_t)hc;
-        oh[row * 2 * kPKT + c + 16] = (uint8_t)(hc >> 8);
-        oh[row * 2 * kPKT + kPKT + c] = (uint8_t)lc;
-        oh[row * 2 * kPKT + kPKT + c + 16] = (uint8_t)(lc >> 8);
+        oh[row * kOhPitch + c] = (uint8_t)hc;
+        oh[row * kOhPitch + c + 16] = (uint8_t)(hc >> 8);
+        oh[row * kOhPitch + kPKT + c] = (uint8_t)lc;
+        oh[row * kOhPitch + kPKT + c + 16] = (uint8_t)(lc >> 8);
         if (n == 0) {
           os[row * 8 + wave] = (uint8_t)sh;
           os[row * 8 + 4 + wave] = (uint8_t)sl;
         }
       }
+    }
   }
   __syncthreads();
   // q rows out: 16-byte pieces of the valid columns (64 in column group 22), scale bytes 4 y .. 4 y + 3 (group 22:
@@ -514,9 +534,12 @@ __global__ __launch_bounds__(256, W == kWT950 ? 2 : 1) void k_prefill_gate_up(
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int pc = tid + 256 * i, row = pc >> 4, c16 = pc & 15, c8 = c16 & 7;
-    if (row < tl.cnt && 16 * c8 < ncol)
+    if (row < tl.cnt && 16 * c8 < ncol) {
+      const uint2 a0 = *reinterpret_cast<const uint2*>(oh + row * kOhPitch + 16 * c16);
+      const uint2 a1 = *reinterpret_cast<const uint2*>(oh + row * kOhPitch + 16 * c16 + 8);
       *reinterpret_cast<uint4*>(hq + (long long)(tl.p0 + row) * kQRow + (c16 >> 3) * kQLo + kPKT * y + 16 * c8) =
-          *reinterpret_cast<const uint4*>(oh + row * 2 * kPKT + 16 * c16);
+          make_uint4(a0.x, a0.y, a1.x, a1.y);
+    }
   }
   if (tid < tl.cnt && tid < kPBM) {
     uint8_t* dst = hq + (long long)(tl.p0 + tid) * kQRow;
@@ -561,29 +584,42 @@ __global__ __launch_bounds__(256, 2) void k_prefill_down(
   for (int i = 0; i < 4; ++i) st.rp[i] = hq + (long long)(tl.p0 + min((tid >> 4) + 16 * i, tl.cnt - 1)) * kQRow;
   st.srow = hq + (long long)(tl.p0 + min(tid & 63, tl.cnt - 1)) * kQRow;
   f32x4_t acc[4][kPNB];
-  gemm8_tile<W, kPNB>(src, blk, true, st, lds, lds + 3 * kQStage + wave * kPNB * kWScBytes, acc);
-  int pr[4][4];                                       // pair of each of the lane's 16 tokens
+  const int ntt = (tl.cnt + 15) >> 4;
+  gemm8_tile<W, kPNB>(src, blk, true, ntt, st, lds, lds + 3 * kQStage + wave * kPNB * kWScBytes, acc);
+  // y = bf16(bf16(bf16(acc) + b) * w[p]) per element, staged as the tile's 64 rows x 192 columns in LDS (the A stages
+  // are free after the last k-tile's barrier), then written back with 16-byte stores: one 384-byte piece per pair.
+  uint8_t* yt = lds;
+  float wv[4][4];                                     // routing weight of each of the lane's 16 tokens
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) pr[tt][r] = order[tl.p0 + min(16 * tt + 4 * q + r, tl.cnt - 1)];
+    for (int r = 0; r < 4; ++r) wv[tt][r] = bf16_to_f32(wts[order[tl.p0 + min(16 * tt + 4 * q + r, tl.cnt - 1)]]);
 #pragma unroll
   for (int nb = 0; nb < kPNB; ++nb) {
-    const int col = 16 * blk[nb] + n;
-    const float bd = bias_dn ? bf16_to_f32(bias_dn[gid * kH + col]) : 0.f;
+    const int cl = 16 * (kPNB * wave + nb) + n;        // column within the workgroup's 192
+    const float bd = bias_dn ? bf16_to_f32(bias_dn[gid * kH + 16 * blk[nb] + n]) : 0.f;
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
+    for (int tt = 0; tt < 4; ++tt) {
+      if (tt >= ntt) break;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = 16 * tt + 4 * q + r;
-        const int p = pr[tt][r];
         float yv = rb(acc[tt][nb][r]);
         if (bias_dn) yv = rb(yv + bd);
-        const uint16_t v = f32_to_bf16(yv * bf16_to_f32(wts[p]));
-        const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
-        if (m < tl.cnt && !(n & 1))
-          *reinterpret_cast<uint32_t*>(ys + (long long)p * kH + 16 * blk[nb] + n) = (uint32_t)v | (hi << 16);
+        const uint32_t v = f32_to_bf16(yv * wv[tt][r]);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false) & 0xffff;
+        if (!(n & 1))
+          *reinterpret_cast<uint32_t*>(yt + (16 * tt + 4 * q + r) * kYPitch + 2 * cl) = v | (hi << 16);
       }
+    }
+  }
+  __syncthreads();
+  constexpr int kPieces = kPRows * 2 / 16;            // 24 pieces of 16 bytes per row
+#pragma unroll
+  for (int i = 0; i < kPBM * kPieces / 256; ++i) {
+    const int pc = tid + 256 * i, row = pc / kPieces, piece = pc - row * kPieces;
+    if (row < tl.cnt)
+      *reinterpret_cast<uint4*>(ys + (long long)order[tl.p0 + row] * kH + kPRows * y + 8 * piece) =
+          *reinterpret_cast<const uint4*>(yt + row * kYPitch + 16 * piece);
   }
 }
 
@@ -600,8 +636,8 @@ NA_DEVICE void store_tile(uint16_t* out_row0, long long pitch, const f32x4_t (&a
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = 16 * tt + 4 * q + r;
-        const uint16_t v = f32_to_bf16(acc[tt][nb][r]);
-        const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
+        const uint32_t v = f32_to_bf16(acc[tt][nb][r]);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false) & 0xffff;
         if (m < m_limit && !(n & 1))
           *reinterpret_cast<uint32_t*>(out_row0 + (long long)m * pitch + 16 * blk[nb] + n) = (uint32_t)v | (hi << 16);
       }
@@ -625,7 +661,7 @@ __global__ __launch_bounds__(256, 2) void k_mxfp4_gemm(const uint16_t* __restric
 #pragma unroll
   for (int i = 0; i < 4; ++i) st.rp[i] = x + (long long)min(m0 + (tid >> 4) + 16 * i, M - 1) * kH;
   f32x4_t acc[4][kPNB];
-  gemm8_tile<W, kPNB>(src, blk, true, st, lds, lds + 3 * kQStage + wave * kPNB * kWScBytes, acc);
+  gemm8_tile_n<W, kPNB, 4>(src, blk, true, st, lds, lds + 3 * kQStage + wave * kPNB * kWScBytes, acc);
   store_tile(out + ((long long)e * M + m0) * N, N, acc, blk, M - m0);
 }
 
@@ -653,7 +689,7 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemm_grouped(const uint8_t* __res
 #pragma unroll
     for (int i = 0; i < 4; ++i) st.rp[i] = x + (long long)min(m0 + (tid >> 4) + 16 * i, r1 - 1) * kH;
     f32x4_t acc[4][kPNB];
-    gemm8_tile<W, kPNB>(src, blk, true, st, lds, lds + 3 * kQStage + wave * kPNB * kWScBytes, acc);
+    gemm8_tile_n<W, kPNB, 4>(src, blk, true, st, lds, lds + 3 * kQStage + wave * kPNB * kWScBytes, acc);
     store_tile(out + (long long)m0 * N, N, acc, blk, r1 - m0);
     __syncthreads();                                   // the next sub-tile restages the scale rows and buffers
   }
