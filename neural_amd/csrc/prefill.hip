@@ -559,7 +559,7 @@ __global__ __launch_bounds__(256, W == kWT950 ? 2 : 1) void k_prefill_gate_up(
 // pair of sorted position p0 + m.  A = the h q rows of the tile (consecutive sorted positions).  Grid: max tiles x 16
 // (xcd_tile<2>); wave w: row blocks 12 y + 3 w + i.
 template <int W>
-__global__ __launch_bounds__(256, 2) void k_prefill_down(
+__global__ __launch_bounds__(256, W == kWT950 ? 2 : 1) void k_prefill_down(
     const uint8_t* __restrict__ hq, const int* __restrict__ order, const PTile* __restrict__ tiles,
     const int* __restrict__ ntiles, const uint16_t* __restrict__ wts, const uint8_t* __restrict__ pool,
     long long slot_bytes, const int64_t* __restrict__ slot_tab, long long expert_base,
