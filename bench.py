@@ -798,9 +798,11 @@ def bench_gemv(A):
     1's shapes on a resident store-layout pool (raw E8M0 rows, or PS4 with --layout ps4): per layer, the 4 routed
     slots' gate_up rows [4 x 5760 x 2880] against one shared x row, then their down rows [4 x 2880 x 2880] against
     per-expert rows (per_expert_x=True), the reference's unfused decode call pattern (mxfp4_kernels.py:474-489).
-    Timed: graph replays of 36 layers; per launch: dispatch-ordered events on the launch stream."""
+    Timed: graph replays of 36 layers; per launch: events that the dispatches stamp themselves (eager steps queued
+    behind a spin kernel)."""
     import torch
 
+    from neural_amd import _native as N
     from neural_amd import synth
     from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4, mxfp4_pool_views
     from neural_amd.q80.mxfp4_kernels import mxfp4_gemv
@@ -820,16 +822,20 @@ def bench_gemv(A):
     hh = synth.bf16_normal(rng, (N_LAYERS, TOPK, H)).to(dev)
 
     def step(s, ev=None):
+        """One configuration-1 step through mxfp4_gemv; with ev, the same launches through the C ABI with dispatch-
+        stamped events (ev[l] = 4 recorded events: gate_up start/end, down start/end)."""
         for l in range(N_LAYERS):
-            if ev is not None:
-                ev[l][0].record()
-            mxfp4_gemv(x[l], gb, gs, slots[s, l])
-            if ev is not None:
-                ev[l][1].record()
-            mxfp4_gemv(hh[l], db, ds, slots[s, l], per_expert_x=True)
-            if ev is not None:
-                ev[l][2].record()
+            if ev is None:
+                mxfp4_gemv(x[l], gb, gs, slots[s, l])
+                mxfp4_gemv(hh[l], db, ds, slots[s, l], per_expert_x=True)
+                continue
+            for k, (xx, bl, sc, n) in enumerate(((x[l], gb, gs, 5760), (hh[l], db, ds, 2880))):
+                N.call("na_mxfp4_gemv", xx.data_ptr(), k, bl.data_ptr(), bl.stride(0), sc.data_ptr(), sc.stride(0),
+                       int(layout == "ps4"), slots[s, l].data_ptr(), TOPK, None, 0, outs[k].data_ptr(), n, H, 2,
+                       N.events_array(ev[l][2 * k:2 * k + 2]), N.stream(dev))
 
+    outs = (torch.empty(TOPK, 5760, dtype=torch.bfloat16, device=dev),
+            torch.empty(TOPK, 2880, dtype=torch.bfloat16, device=dev))
     step(0)
     torch.cuda.synchronize()
     cs = torch.cuda.Stream()
@@ -853,7 +859,7 @@ def bench_gemv(A):
     el = time.perf_counter() - t0
     ms_step = el / A.steps * 1e3
     step_bytes = N_LAYERS * TOPK * SLOT_ALGO_BYTES
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(N_LAYERS)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(N_LAYERS)]
     for row in ev:
         for e in row:
             e.record()
@@ -866,7 +872,7 @@ def bench_gemv(A):
         torch.cuda.synchronize()
         for l in range(N_LAYERS):
             gu_ms += ev[l][0].elapsed_time(ev[l][1])
-            dn_ms += ev[l][1].elapsed_time(ev[l][2])
+            dn_ms += ev[l][2].elapsed_time(ev[l][3])
     n = R * N_LAYERS
     gu_us, dn_us = gu_ms / n * 1e3, dn_ms / n * 1e3
     gu_gbps = TOPK * GATE_UP_BYTES / (gu_us * 1e-6) / 1e9

@@ -36,10 +36,11 @@ int na_selftest_fp4(void* out, hipStream_t stream);
  *   active   optional per-slot weight (active_dtype 1 = bf16, 2 = fp32, 0 = none): a zero writes +0 rows and reads
  *            no weights; NaN or nonzero computes
  *   out      bf16 [E, N], N even
- *   pairs_per_wave  row pairs streamed per wavefront: 1, 2 or 4 (<= 0: default 2) */
+ *   pairs_per_wave  row pairs streamed per wavefront: 1, 2 or 4 (<= 0: default 2)
+ *   events   NULL, or two hipEvent_t that the dispatch stamps at its start and end (measurement only) */
 int na_mxfp4_gemv(const void* x, int per_expert_x, const void* blocks, long long sb_slot, const void* scales,
                   long long ss_slot, int packed, const int64_t* slots, int E, const void* active, int active_dtype,
-                  void* out, int N, int K, int pairs_per_wave, hipStream_t stream);
+                  void* out, int N, int K, int pairs_per_wave, void* const* events, hipStream_t stream);
 
 /* Fused decode expert body for B <= 8 tokens: gate_up GEMV (+ bias, clamped SwiGLU), down GEMV (+ bias, x routing
  * weight) and, when `out` is not NULL, the top-k combine; three launches.  Replaces the reference's b_body

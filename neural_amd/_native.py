@@ -21,7 +21,7 @@ VP, I32, I64, F32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_f
 SIGNATURES = {
     "na_version": [],
     "na_selftest_fp4": [VP, VP],
-    "na_mxfp4_gemv": [VP, I32, VP, I64, VP, I64, I32, VP, I32, VP, I32, VP, I32, I32, I32, VP],
+    "na_mxfp4_gemv": [VP, I32, VP, I64, VP, I64, I32, VP, I32, VP, I32, VP, I32, I32, I32, VP, VP],
     "na_moe_decode": [VP, VP, VP, I32, VP, I64, I32, VP, I64, VP, VP, VP, VP, VP, F32, F32, I32, I32, VP, VP],
     "na_router_topk": [VP, I32, VP, VP, I32, VP, VP, VP, VP, VP],
     "na_selftest_mfma": [VP, VP, VP, VP],

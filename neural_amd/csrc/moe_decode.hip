@@ -548,7 +548,7 @@ extern "C" {
 
 int na_mxfp4_gemv(const void* x, int per_expert_x, const void* blocks, long long sb_slot, const void* scales,
                   long long ss_slot, int packed, const int64_t* slots, int E, const void* active, int active_dtype,
-                  void* out, int N, int K, int pairs_per_wave, hipStream_t stream) {
+                  void* out, int N, int K, int pairs_per_wave, void* const* events, hipStream_t stream) {
   if (!x || !blocks || !scales || !slots || !out || E <= 0 || N <= 0 || (N & 1) || K != kH) return kErrArgs;
   if (active_dtype < 0 || active_dtype > 2 || (active_dtype && !active)) return kErrArgs;
   if (pairs_per_wave <= 0) pairs_per_wave = 2;
@@ -556,8 +556,9 @@ int na_mxfp4_gemv(const void* x, int per_expert_x, const void* blocks, long long
   const int per_wg = kWaves * pairs_per_wave;
   dim3 grid(E, (N / 2 + per_wg - 1) / per_wg);
   const long long xs = per_expert_x ? K : 0;
+  hipEvent_t e0 = events ? (hipEvent_t)events[0] : nullptr, e1 = events ? (hipEvent_t)events[1] : nullptr;
   launch(packed ? gemv_kernel<1>(pairs_per_wave) : gemv_kernel<0>(pairs_per_wave), grid, dim3(kThreads), stream,
-         nullptr, nullptr, (const uint16_t*)x, xs, (const uint8_t*)blocks, sb_slot, (const uint8_t*)scales, ss_slot,
+         e0, e1, (const uint16_t*)x, xs, (const uint8_t*)blocks, sb_slot, (const uint8_t*)scales, ss_slot,
          slots, active, active_dtype, (uint16_t*)out, N);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }

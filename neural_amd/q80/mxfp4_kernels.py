@@ -92,7 +92,7 @@ def _gemv(x, blocks, scales, slots, active, per_expert_x, block_n, packed):
     pairs = 2 if int(block_n) >= 32 else 1     # row pairs per wavefront (the Triton block_n has no direct analogue)
     N.call("na_mxfp4_gemv", x.data_ptr(), int(per_expert_x), blocks.data_ptr(), blocks.stride(0),
            scales.data_ptr(), scales.stride(0), int(pk), slots.data_ptr(), E, N.ptr(active), adt, out.data_ptr(),
-           n, gk * 32, pairs, N.stream(x.device))
+           n, gk * 32, pairs, None, N.stream(x.device))
     return out
 
 

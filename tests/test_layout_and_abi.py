@@ -217,7 +217,7 @@ def test_library_rejects_bad_arguments_without_launching():
     """Argument validation happens before any HIP call, so it is checkable without a GPU."""
     from neural_amd import _native as N
     lib = N.lib()
-    assert lib.na_mxfp4_gemv(None, 0, None, 0, None, 0, 0, None, 4, None, 0, None, 5760, 2880, 0, None) == -1
+    assert lib.na_mxfp4_gemv(None, 0, None, 0, None, 0, 0, None, 4, None, 0, None, 5760, 2880, 0, None, None) == -1
     assert lib.na_moe_decode(None, None, None, 1, None, 0, 0, None, 0, None, None, None, None, None,
                              ctypes.c_float(1.702), ctypes.c_float(7.0), 0, 0, None, None) == -1
 
