@@ -16,6 +16,7 @@ from oracle.bf16 import rb
 from neural_amd import scale_pack as sp
 from neural_amd import synth
 from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4, mxfp4_pool_views
+from tolerance import ulp_profile
 
 pytestmark = pytest.mark.gpu
 
@@ -98,6 +99,8 @@ def test_mxfp4_gemv_matches_oracle(dev, pools, host_slots, weights_cache, packed
         want = rb(mo.gemv_f64(xs[i:i + 1] if per else xs, w).astype(np.float32))[0]
         ok, *info = within_tol(got[i], want)
         assert ok, (i, info)
+        prof = ulp_profile(got[i], want)        # exact products, fp32 sums, one rounding: within one bf16 ulp
+        assert prof[0] >= 0.999 and prof[1] == 1.0, (i, prof)
 
 
 def test_gemv_raw_equals_ps4_bitwise(dev, pools):
@@ -173,6 +176,8 @@ def test_moe_decode_matches_oracle(dev, pools, host_slots, weights_cache, B, bia
         want = mo.combine_bf16(np.stack(ys), w[b])
         ok, *info = within_tol(got[b], want)
         assert ok, (b, info)
+        prof = ulp_profile(got[b], want)        # per element: rounding flips at the body's bf16 points only
+        assert prof[1] >= 0.99 and prof[2] >= 0.995, (b, prof)
 
 
 def test_moe_decode_raw_equals_ps4_and_graph_replay(dev, pools):

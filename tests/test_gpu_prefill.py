@@ -13,6 +13,7 @@ import pytest
 
 from oracle import mxfp4_oracle as mo
 from oracle.bf16 import rb
+from tolerance import ulp_profile
 from neural_amd import synth, tiles
 
 pytestmark = pytest.mark.gpu
@@ -27,6 +28,8 @@ def _close(got, want, tag):
     d = np.abs(got - want)
     scale = np.abs(want).max()
     assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale + 1e-6, (tag, d.max(), d.mean(), scale)
+    prof = ulp_profile(got, want)       # per element: at least 98 % within 2 bf16 ulps, 99 % within 4 (worst measured
+    assert prof[1] >= 0.98 and prof[2] >= 0.99, (tag, prof)     # on the GPU: 99.0 % / 99.4 %)
 
 
 def _pool(slots, packed, dev):

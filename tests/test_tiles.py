@@ -11,6 +11,12 @@ from oracle import tiles_oracle as to
 from neural_amd import scale_pack as sp
 from neural_amd import synth
 from neural_amd import tiles
+from tolerance import ulp_profile
+
+# per element against the oracle: the body's bf16 rounding points, and h between the two products as E4M3 hi + lo
+# under fixed scales (exact for |h| >= 2^-9), leave rounding flips that the next product carries: at least 97.5 %
+# of outputs within 2 bf16 ulps and 99 % within 4 (measured on the GPU: 98.4 % / 99.3 % at worst)
+T950_FRAC2, T950_FRAC4 = 0.975, 0.99
 
 
 @pytest.fixture(scope="module")
@@ -181,6 +187,8 @@ def test_moe_decode_t950_matches_oracle_and_store_path(B, k_split, bias):
         for name, arr in (("t950", got[b]), ("store", ref_store[b])):
             d = np.abs(arr - want)
             assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale, (name, b, d.max(), d.mean(), scale)
+            prof = ulp_profile(arr, want)
+            assert prof[1] >= T950_FRAC2 and prof[2] >= T950_FRAC4, (name, b, prof)
 
 
 @pytest.mark.gpu
@@ -272,6 +280,8 @@ def test_down_with_combine_matches_expert_major_path(B):
             for name, arr in (("two", a[b]), ("three", c[b])):
                 d = np.abs(arr - want)
                 assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale, (name, call, b, d.max(), scale)
+                prof = ulp_profile(arr, want)
+                assert prof[1] >= T950_FRAC2 and prof[2] >= T950_FRAC4, (name, call, b, prof)
 
 
 def _e4m3_table():
@@ -430,3 +440,5 @@ def test_duplicate_ids_in_a_token(B):
         for nm, arr in got.items():
             d = np.abs(arr[b] - want)
             assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale, (nm, b, d.max(), scale)
+            prof = ulp_profile(arr[b], want)
+            assert prof[1] >= T950_FRAC2 and prof[2] >= T950_FRAC4, (nm, b, prof)
