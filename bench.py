@@ -655,7 +655,8 @@ def measure_experts(rx, dev, B, steps, warmup, n_sets, roofline_steps):
     log(f"config1 B={B}: timed {steps} steps: {ms_step:.3f} ms/step, {tok_s:.1f} tok/s, "
         f"{step_bytes / (ms_step * 1e-3) / 1e9:.0f} GB/s whole-step")
     # ------------------------------------------------------------------ roofline pass (per-kernel events)
-    per_kernel_bytes = {"gate_up": GATE_UP_BYTES, "down": DOWN_BYTES, "down_combine": DOWN_BYTES, "combine": 0}
+    per_kernel_bytes = {"gate_up": GATE_UP_BYTES, "down": DOWN_BYTES, "down_combine": DOWN_BYTES, "combine": 0,
+                        "experts": GATE_UP_BYTES + DOWN_BYTES}
     kernels = tuple((nm, per_kernel_bytes[nm]) for nm in launches)
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * len(kernels))] for _ in range(N_LAYERS)]
     for row in ev:

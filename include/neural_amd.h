@@ -3,7 +3,8 @@
  * Every entry point takes raw device pointers, plain sizes and the hipStream_t to launch on; it allocates nothing,
  * never synchronises and never reads device data on the host, so it can be recorded into a hipGraph.  Return value:
  * 0 = launched, -1 = invalid arguments (nothing launched), -2 = launch error (hipGetLastError), -3 = a size beyond
- * the kernel's fixed limits (nothing launched).
+ * the kernel's fixed limits (nothing launched), -4 = the device cannot hold every workgroup of a launch that needs
+ * them resident together (nothing launched).
  *
  * Data conventions: bf16 tensors are arrays of uint16 bit patterns; expert slots follow the store layout of the
  * reference (neural/moe/layout.py:143-186): gate_codes [5760][90][16] | down_codes [2880][90][16] | scales, with raw
@@ -123,6 +124,22 @@ int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
                        long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
                        const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha, float limit,
                        int k_split, int down_mode, void* const* events, hipStream_t stream);
+
+/* Words (uint32) of the sync buffer na_moe_decode_t950_one needs (32,000 bytes). */
+long long na_moe_one_sync_words(void);
+
+/* The expert body of one token (B = 1) over a t950 pool in a single launch: the same contract and the same bits as
+ * na_moe_decode_t950 (server.py:508-518, b_body; seam neural/moe/gptoss_adapter.py:267-284), out required.  720
+ * workgroups each run one (expert, 16-row block) of gate_up, publish their h (device-coherent stores, counted), load
+ * the matching down row block, wait for every workgroup's h, run the down block, and the last of each output block's
+ * four workgroups sums the top-k.  h_scratch and yw_scratch hold 4 x 5,760 bytes each.  sync: na_moe_one_sync_words
+ * uint32, zero before the first call, owned by one stream (calls that overlap on one sync buffer race); word 0 (a
+ * wait that gave up) stays set once raised.  Returns -4 where the device cannot hold the 720 workgroups at once.
+ * events: NULL or 2 recorded events (the launch's start and stop). */
+int na_moe_decode_t950_one(const void* x, const int64_t* topk_ids, const void* topk_w, const void* pool,
+                           long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
+                           const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha,
+                           float limit, unsigned int* sync, void* const* events, hipStream_t stream);
 
 /* na_moe_decode_t950 that allocates nothing and takes no scratch: h and the weighted expert outputs live in a
  * file-scope device array of the library (368,640 bytes per device, for B <= 8; its address is looked up once per

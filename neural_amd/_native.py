@@ -34,6 +34,8 @@ SIGNATURES = {
     "na_repack_from_t950": [VP, I64, VP, I64, I32, I32, VP],
     "na_moe_decode_t950": [VP, VP, VP, I32, VP, I64, VP, I64, VP, VP, VP, VP, VP, F32, F32, I32, I32, VP, VP],
     "na_moe_decode_t950_noalloc": [VP, VP, VP, I32, VP, I64, VP, I64, VP, VP, VP, F32, F32, I32, I32, VP],
+    "na_moe_decode_t950_one": [VP, VP, VP, VP, I64, VP, I64, VP, VP, VP, VP, VP, F32, F32, VP, VP, VP],
+    "na_moe_one_sync_words": [],
     "na_attn_workspace_floats": [I32, I32],
     "na_moe_prefill_workspace_bytes": [I32],
     "na_moe_prefill_workspace_layout": [I32, VP],
@@ -61,9 +63,10 @@ SIGNATURES = {
     "na_rows_topk": [VP, I32, VP, VP, VP],
 }
 RESTYPES = {"na_t950_slot_bytes": I64, "na_attn_workspace_floats": I64, "na_moe_prefill_workspace_bytes": I64,
-            "na_core_lm_partials": I64, "na_core_attn_block_sync_words": I64}
+            "na_core_lm_partials": I64, "na_core_attn_block_sync_words": I64, "na_moe_one_sync_words": I64}
 
-ERRORS = {-1: "invalid arguments", -2: "kernel launch failed", -3: "size beyond the kernel's limits"}
+ERRORS = {-1: "invalid arguments", -2: "kernel launch failed", -3: "size beyond the kernel's limits",
+          -4: "the device cannot hold every workgroup of the launch at once"}
 
 
 class NativeLibraryMissing(RuntimeError):

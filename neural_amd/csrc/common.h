@@ -20,6 +20,7 @@ enum Status : int {
   kErrArgs = -1,        // null pointer, bad size or unsupported geometry
   kErrLaunch = -2,      // hipGetLastError after the launch
   kErrTooLarge = -3,    // a size beyond what the kernel's fixed buffers hold
+  kErrResident = -4,    // the device cannot hold every workgroup of a launch at once (a launch that needs it)
 };
 
 // ---- GPT-OSS-120B expert geometry (reference neural/moe/layout.py:143-157)

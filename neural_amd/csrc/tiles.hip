@@ -13,6 +13,7 @@
 // E2M1 nibbles unchanged and the scales the store's E8M0 bytes unchanged (PS4 rows are expanded), so the repack is a
 // byte permutation plus padding and round-trips exactly (na_repack_from_t950).
 #include "common.h"
+#include "handoff.h"
 #include "t950.h"
 
 #include <hip/hip_ext.h>
@@ -256,26 +257,45 @@ NA_DEVICE void h8_codes(uint16_t hv, uint32_t sh, uint32_t sl, uint8_t& hi, uint
   lo = (uint8_t)(__builtin_bit_cast(uint32_t, o2) & 0xff);
 }
 
-// h of D column n = lane % 16 (output row 16b + n) of `pair` -> its hi and lo bytes (a byte store each).
+// h of D column n = lane % 16 (output row 16b + n) of `pair` -> its hi and lo bytes (a byte store each).  COH: the
+// stores are device-coherent (written through to the coherent point), for a reader in the same launch on another XCD.
+template <bool COH = false>
 NA_DEVICE void store_h8(uint8_t* h8, int pair, int b, uint16_t hv, uint32_t sh, uint32_t sl, bool ok) {
   uint8_t hi, lo;
   h8_codes(hv, sh, sl, hi, lo);
   uint8_t* row = h8 + (long long)pair * kH8Row + 16 * b + (threadIdx.x & 15);
   if (ok) {
-    row[0] = hi;
-    row[kI] = lo;
+    if constexpr (COH) {
+      __hip_atomic_store(row, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(row + kI, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      row[0] = hi;
+      row[kI] = lo;
+    }
   }
 }
 
 // The pairs' h8 rows of up to XT staged tokens through registers: piece p = tid + NTH k < nt x 360; piece q = p % 360
 // of token t = p / 360 is bytes 16 (q % 180) .. of its hi (q < 180) or lo row.
-template <int XT, int NTH, typename PairOf>
+// 16 bytes at base + off with one device-coherent (sc1) load: what the same launch wrote on another XCD.  base is
+// uniform across the wave (a buffer resource is scalar), off per lane and 16-byte aligned.
+NA_DEVICE uint4 load16_sc1(const void* base, uint32_t off) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 16);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <int XT, int NTH, typename PairOf, bool COH = false>
 NA_DEVICE void h8_load(int tid, const uint8_t* h8, PairOf pair_of, int nt, XRegs<XT, NTH>& xr) {
 #pragma unroll
   for (int k = 0; k < XRegs<XT, NTH>::XP; ++k) {
     const int p = tid + NTH * k;
     const int t = p / kH8Pieces, q = p - t * kH8Pieces;
-    if (p < nt * kH8Pieces) xr.v[k] = load16(h8 + (long long)pair_of(t) * kH8Row + 16 * q);
+    if (p < nt * kH8Pieces) {
+      const uint32_t off = (uint32_t)pair_of(t) * kH8Row + 16 * q;
+      xr.v[k] = COH ? load16_sc1(h8, off) : load16(h8 + off);
+    }
   }
 }
 
@@ -357,10 +377,15 @@ NA_DEVICE void token_sums(const f32x4_t& acc, float& y0, float& y1) {
 
 // Store the bf16 values v held as D columns n = lane % 16 (16 lanes per D row) as 32-bit pairs: even lanes write
 // (v[n], v[n + 1]) to row_ptr + n.  All lanes must call it (it exchanges values between neighbouring lanes).
+template <bool COH = false>
 NA_DEVICE void store_row_pairs(uint16_t* row_ptr, uint16_t v, bool ok) {
   const int lane = threadIdx.x & 63;
   const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
-  if (ok && !(lane & 1)) *reinterpret_cast<uint32_t*>(row_ptr + (lane & 15)) = (uint32_t)v | (hi << 16);
+  if (ok && !(lane & 1)) {
+    uint32_t* d = reinterpret_cast<uint32_t*>(row_ptr + (lane & 15));
+    if constexpr (COH) store_coherent(d, (uint32_t)v | (hi << 16));
+    else *d = (uint32_t)v | (hi << 16);
+  }
 }
 
 // The id of this lane's pair (lanes past the pairs re-read the last one): the first read of a decode kernel, issued
@@ -426,6 +451,7 @@ NA_DEVICE int pair_at(uint64_t users, int u) {
 // The duplicate pairs' h: for token u = 2 (lane / 16) + e < nt (user pair p), the same value v[e] also goes to every
 // other pair of p's token that `all` routes to the expert (columns 16b .. 16b + 15).  Kept out of line of the common
 // path, which stores only the users' rows.
+template <bool COH>
 __device__ __noinline__ void dup_rows_store_h8(uint8_t* h8, uint64_t users, uint64_t all, int nt, int b, uint16_t v0,
                                                uint16_t v1, uint32_t sh, uint32_t sl) {
   const int lane = threadIdx.x & 63;
@@ -435,11 +461,12 @@ __device__ __noinline__ void dup_rows_store_h8(uint8_t* h8, uint64_t users, uint
     const int u = 2 * (lane >> 4) + e;
     const int p = pair_at(users, min(u, nt - 1));
     const uint32_t dm = token_dups(all, p) & ~(1u << (p & 3));
-    for (int k = 0; k < 4; ++k) store_h8(h8, (p & ~3) + k, b, v[e], sh, sl, u < nt && ((dm >> k) & 1));
+    for (int k = 0; k < 4; ++k) store_h8<COH>(h8, (p & ~3) + k, b, v[e], sh, sl, u < nt && ((dm >> k) & 1));
   }
 }
 
 // As dup_rows_store for the down outputs: pair q gets bf16(y[e] x w[q]) with its own routing weight.
+template <bool COH>
 __device__ __noinline__ void dup_rows_store_w(uint16_t* yw, uint64_t users, uint64_t all, int nt, int b, float y0,
                                               float y1, const uint16_t* wts) {
   const int lane = threadIdx.x & 63;
@@ -451,8 +478,8 @@ __device__ __noinline__ void dup_rows_store_w(uint16_t* yw, uint64_t users, uint
     const uint32_t dm = token_dups(all, p) & ~(1u << (p & 3));
     for (int k = 0; k < 4; ++k) {
       const int q = (p & ~3) + k;
-      store_row_pairs(yw + (long long)q * kH + 16 * b, f32_to_bf16(y[e] * bf16_to_f32(wts[q])),
-                      u < nt && ((dm >> k) & 1));
+      store_row_pairs<COH>(yw + (long long)q * kH + 16 * b, f32_to_bf16(y[e] * bf16_to_f32(wts[q])),
+                           u < nt && ((dm >> k) & 1));
     }
   }
 }
@@ -487,22 +514,21 @@ struct DecodeLds {
 // Order: route and slot -> every global load (codes, scales, x, bias) -> x quantised to E4M3 and the scales to LDS,
 // barrier -> one MFMA per tile (each waits only for its own codes) -> fixed-order sum of the KS partial sums through
 // LDS -> epilogue in wave 0, which reads nothing from global memory.
-template <int KS, int XT>
-__global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
-    const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
-    const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ x,
-    const uint16_t* __restrict__ bias_gu, uint8_t* __restrict__ h8, float alpha, float limit, uint32_t h8_sc) {
+// The body of workgroup (item, b); every wave returns from it (waves past the first right after the K reduction).
+// COH: h is stored device-coherently (the single-launch expert body reads it in the same launch).
+template <int KS, int XT, bool COH>
+NA_DEVICE void gate_up_body(DecodeLds<KS, XT>& L, int item, int b, long long rid, int B,
+                            const uint8_t* __restrict__ pool, long long slot_bytes,
+                            const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ x,
+                            const uint16_t* __restrict__ bias_gu, uint8_t* __restrict__ h8, float alpha, float limit,
+                            uint32_t h8_sc) {
   constexpr int MT = (kTTiles + KS - 1) / KS;
   constexpr int NTH = 64 * KS;
-  __shared__ DecodeLds<KS, XT> L;
-  const long long rid = route_ids_load(ids, 4 * B);
-  args_at_entry(x, bias_gu, h8, alpha, limit, (int)h8_sc);   // past the preloaded arguments: fetched while ids fly
   int nt, distinct, valid;
   uint64_t users, all;
-  const int e = route_t950<4 * XT>(rid, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
+  const int e = route_t950<4 * XT>(rid, 4 * B, item, nt, users, all, distinct, valid);
   if (e < 0 || e == 128) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int b = blockIdx.y;
   const long long gid = expert_base + e;
   const long long slot = slot_tab ? slot_tab[gid] : gid;
   const uint8_t* gblk = pool + slot * slot_bytes + (long long)b * kTBlock;
@@ -574,35 +600,51 @@ __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
       ub = rb(ub + bf16_to_f32(buj));
     }
     hv[q] = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
-    store_h8(h8, pair_at(users, min(u, nt - 1)), b, hv[q], h8_sc & 0xff, h8_sc >> 8, u < nt);
+    store_h8<COH>(h8, pair_at(users, min(u, nt - 1)), b, hv[q], h8_sc & 0xff, h8_sc >> 8, u < nt);
   }
-  if (all != users) dup_rows_store_h8(h8, users, all, nt, b, hv[0], hv[1], h8_sc & 0xff, h8_sc >> 8);   // rare
+  if (all != users) dup_rows_store_h8<COH>(h8, users, all, nt, b, hv[0], hv[1], h8_sc & 0xff, h8_sc >> 8);   // rare
+}
+
+template <int KS, int XT>
+__global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
+    const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
+    const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ x,
+    const uint16_t* __restrict__ bias_gu, uint8_t* __restrict__ h8, float alpha, float limit, uint32_t h8_sc) {
+  __shared__ DecodeLds<KS, XT> L;
+  const long long rid = route_ids_load(ids, 4 * B);
+  args_at_entry(x, bias_gu, h8, alpha, limit, (int)h8_sc);   // past the preloaded arguments: fetched while ids fly
+  gate_up_body<KS, XT, false>(L, blockIdx.x, blockIdx.y, rid, B, pool, slot_bytes, slot_tab, expert_base, x, bias_gu,
+                              h8, alpha, limit, h8_sc);
 }
 
 // down, expert-major: output block b (rows n = 16b .. 16b + 15) of the item-th distinct expert from each routed
 // token's own h row (E4M3 from the gate_up kernel), + bias, x routing weight -> yw[pair, n].  An invalid id (128)
 // writes +0 for its pairs and reads no weights.  The top-k sum is left to k_combine_t950.  Load order as in the
-// gate_up kernel.
-template <int KS, int XT>
-__global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
-    const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
-    const int64_t* __restrict__ slot_tab, long long expert_base, const uint8_t* __restrict__ h8,
-    const uint16_t* __restrict__ wts, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw, uint32_t h8_sc) {
+// gate_up kernel.  Every wave returns from the body (waves past the first right after the K reduction).
+// COH (the single-launch expert body): h was written earlier in the same launch, so the weight rows are loaded first,
+// then wait() (the release of h), then h with device-coherent loads; yw is stored device-coherently, and only by
+// wave 0 (whose acknowledged stores the caller counts).
+template <int KS, int XT, bool COH, typename Wait>
+NA_DEVICE void down_body(DecodeLds<KS, XT>& L, int item, int b, long long rid, int B, const uint8_t* __restrict__ pool,
+                         long long slot_bytes, const int64_t* __restrict__ slot_tab, long long expert_base,
+                         const uint8_t* __restrict__ h8, const uint16_t* __restrict__ wts,
+                         const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw, uint32_t h8_sc, Wait wait) {
   constexpr int MT = (kTTiles + KS - 1) / KS;
   constexpr int NTH = 64 * KS;
-  __shared__ DecodeLds<KS, XT> L;
-  const long long rid = route_ids_load(ids, 4 * B);
-  args_at_entry(h8, wts, bias_dn, yw, (int)h8_sc);    // past the preloaded arguments: fetched while the ids fly
   int nt, distinct, valid;
   uint64_t users, all;
-  const int e = route_t950<4 * XT>(rid, 4 * B, blockIdx.x, nt, users, all, distinct, valid);
+  const int e = route_t950<4 * XT>(rid, 4 * B, item, nt, users, all, distinct, valid);
   if (e < 0) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int b = blockIdx.y;
   if (e == 128) {                                      // invalid ids: each of their pairs contributes +0
-    for (int i = tid; i < 4 * B * (kTRows / 2); i += NTH) {
+    if (COH && wave != 0) return;
+    for (int i = COH ? lane : tid; i < 4 * B * (kTRows / 2); i += COH ? 64 : NTH) {
       const int q = i / (kTRows / 2), c = i - q * (kTRows / 2);
-      if ((all >> q) & 1) *reinterpret_cast<uint32_t*>(yw + (long long)q * kH + 16 * b + 2 * c) = 0u;
+      uint32_t* d = reinterpret_cast<uint32_t*>(yw + (long long)q * kH + 16 * b + 2 * c);
+      if ((all >> q) & 1) {
+        if constexpr (COH) store_coherent(d, 0u);
+        else *d = 0u;
+      }
     }
     return;
   }
@@ -614,7 +656,8 @@ __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
   ScaleRegs<1, NTH> sr;
   scale_load<1, NTH>(tid, blk, blk, sr);
   XRegs<XT, NTH> xr;
-  h8_load<XT, NTH>(tid, h8, [users](int t) { return pair_at(users, t); }, nt, xr);
+  const auto pair_of = [users](int t) { return pair_at(users, t); };
+  if constexpr (!COH) h8_load<XT, NTH>(tid, h8, pair_of, nt, xr);
   const int n = 16 * b + (lane & 15);
   // epilogue operands are loaded now and converted at their use, so no wait is placed before the barrier
   const uint16_t bdn = (bias_dn ? bias_dn + gid * kH : wts)[bias_dn ? n : 0];   // unconditional load
@@ -623,6 +666,10 @@ __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
   for (int q = 0; q < 2; ++q) wr[q] = wts[pair_at(users, min(2 * (lane >> 4) + q, nt - 1))];
   CodeRegs<MT> rd;
   code_load<MT>(blk, lane, t0, t1, rd);
+  if constexpr (COH) {
+    wait();
+    h8_load<XT, NTH, decltype(pair_of), true>(tid, h8, pair_of, nt, xr);
+  }
   __builtin_amdgcn_sched_barrier(0);
   h8_store<XT, NTH>(tid, L.x, nt, xr, h8_sc & 0xff, h8_sc >> 8);
   scale_store<1, NTH>(tid, L.sc, sr);
@@ -657,10 +704,26 @@ __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
     float y = rb(y2[q]);
     if (bias_dn) y = rb(y + bf16_to_f32(bdn));
     yb[q] = y;
-    store_row_pairs(yw + (long long)pair_at(users, min(u, nt - 1)) * kH + 16 * b,
-                    f32_to_bf16(y * bf16_to_f32(wr[q])), u < nt);
+    store_row_pairs<COH>(yw + (long long)pair_at(users, min(u, nt - 1)) * kH + 16 * b,
+                         f32_to_bf16(y * bf16_to_f32(wr[q])), u < nt);
   }
-  if (all != users) dup_rows_store_w(yw, users, all, nt, b, yb[0], yb[1], wts);   // uniform, rare
+  if (all != users) dup_rows_store_w<COH>(yw, users, all, nt, b, yb[0], yb[1], wts);   // uniform, rare
+}
+
+struct NoWait {
+  NA_DEVICE void operator()() const {}
+};
+
+template <int KS, int XT>
+__global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
+    const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
+    const int64_t* __restrict__ slot_tab, long long expert_base, const uint8_t* __restrict__ h8,
+    const uint16_t* __restrict__ wts, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw, uint32_t h8_sc) {
+  __shared__ DecodeLds<KS, XT> L;
+  const long long rid = route_ids_load(ids, 4 * B);
+  args_at_entry(h8, wts, bias_dn, yw, (int)h8_sc);    // past the preloaded arguments: fetched while the ids fly
+  down_body<KS, XT, false>(L, blockIdx.x, blockIdx.y, rid, B, pool, slot_bytes, slot_tab, expert_base, h8, wts,
+                           bias_dn, yw, h8_sc, NoWait{});
 }
 
 __global__ __launch_bounds__(256) void k_combine_t950(const uint32_t* __restrict__ yw, int B,
@@ -762,6 +825,112 @@ __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
     for (int k = 0; k < 4; ++k) a += L.yw[k][tid];
     out[16 * b + tid] = f32_to_bf16(a);
   }
+}
+
+// ---- the expert body of one token in a single launch (na_moe_decode_t950_one): 720 workgroups, workgroup blk = 4b +
+// item runs k_moe_gate_up_t950<4, 1>'s (item, gate_up row block b) with h stored device-coherently, then
+// k_moe_down_t950<4, 1>'s (item, down row block b) and, for the last of block b's four workgroups, k_combine_t950's sum
+// of block b.  The arithmetic is those kernels', so the output equals the two- and three-launch paths bit for bit.
+// Handoffs (handoff.h): wave 0 of each workgroup (the only wave that stores h) counts the workgroup once its h stores
+// are acknowledged, two-level; the count's completion raises kGo release flags to this launch's generation number.
+// Each workgroup issues its down row block's loads (weights, scales, bias) before it waits for the release, then
+// reads h device-coherently.  The generation (line kOneGen, read by thread 0 at entry) advances by one per launch,
+// so the flags never need clearing.  Block b's workgroups count on block b's counter after their yw stores are
+// acknowledged; the fourth reads the four slices device-coherently and writes out.
+// Every workgroup waits for every other's gate_up part, so all 720 must be resident at once: the host launches this
+// kernel only where the occupancy query allows it (3 workgroups per CU x 256 CUs = 768 on MI355X).  The waits are
+// bounded (handoff.h): a broken assumption shows as the error word, never as a hang.
+// sync: kOneSyncLines lines of kLine uint32, zero before the first launch; line 0 = the error word (raised by a wait
+// that gave up, never cleared here).
+constexpr int kOneWgs = 4 * kTDownBlocks;       // 720
+constexpr int kOneErr = 0, kOneGen = 1, kOneCnt = 2, kOneGo = kOneCnt + 1 + kGo, kOneBlk = kOneGo + kGo;
+constexpr int kOneSyncLines = kOneBlk + kTDownBlocks / 2;   // 125 lines, 32,000 bytes (two block counters a line)
+
+NA_DEVICE uint32_t* one_block_counter(uint32_t* sync, int b) {
+  return sync + (kOneBlk + b / 2) * kLine + (b & 1) * (kLine / 2);
+}
+
+// Wave 0 of workgroup blk after its last h store (the other waves stored nothing): its stores acknowledged, lane 0
+// counts the workgroup two-level (handoff.h publish_done's counters); the wave that completes the count raises the
+// kGo flags and the generation word to gen.  Only thread 0 read the generation word, before this count, so every
+// workgroup has read it before it advances.
+NA_DEVICE void one_publish(uint32_t* sync, int blk, uint32_t gen) {
+  __builtin_amdgcn_s_waitcnt(0);
+  const int lane = threadIdx.x & 63;
+  uint32_t* cnt = sync + kOneCnt * kLine;
+  int top = 0;
+  if (lane == 0) {
+    const uint32_t gi = (uint32_t)blk % kGo;
+    const uint32_t quota = ((uint32_t)kOneWgs - gi + kGo - 1) / kGo;
+    uint32_t* gc = cnt + (1 + gi) * kLine;
+    if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == quota - 1) {
+      __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)kGo - 1) {
+        __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        top = 1;
+      }
+    }
+  }
+  top = __builtin_amdgcn_readfirstlane(top);
+  gen = __builtin_amdgcn_readfirstlane(gen);         // thread 0's value (lane 0 of wave 0)
+  if (top) {
+    if (lane < kGo) store_coherent(sync + (kOneGo + lane) * kLine, gen);
+    if (lane == kGo) store_coherent(sync + kOneGen * kLine, gen);
+  }
+}
+
+// Thread 0 polls its flag until it holds gen (or the poll limit raises the error word); then the workgroup meets.
+NA_DEVICE void one_wait(const uint32_t* go, uint32_t gen, uint32_t* err) {
+  if (threadIdx.x == 0) {
+    uint32_t polls = 0;
+    while (load_coherent(go) != gen) {
+      if (++polls > kSpinLimit) {
+        __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void k_moe_one_t950(
+    const int64_t* __restrict__ ids, const uint8_t* __restrict__ pool, long long slot_bytes,
+    const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ x,
+    const uint16_t* __restrict__ bias_gu, const uint16_t* __restrict__ bias_dn, const uint16_t* __restrict__ wts,
+    uint8_t* __restrict__ h8, uint16_t* __restrict__ yw, uint16_t* __restrict__ out, float alpha, float limit,
+    uint32_t h8_sc, uint32_t* __restrict__ sync) {
+  __shared__ DecodeLds<4, 1> L;
+  const long long rid = route_ids_load(ids, 4);
+  args_at_entry(x, bias_gu, bias_dn, wts, h8, yw, out, alpha, limit, (int)h8_sc, sync);
+  const int blk = blockIdx.x, item = blk & 3, b = blk >> 2;
+  const int tid = threadIdx.x, lane = tid & 63;
+  uint32_t* err = sync + kOneErr * kLine;
+  const uint32_t gen = tid == 0 ? load_coherent(sync + kOneGen * kLine) + 1u : 0u;   // used by thread 0 only
+  gate_up_body<4, 1, true>(L, item, b, rid, 1, pool, slot_bytes, slot_tab, expert_base, x, bias_gu, h8, alpha, limit,
+                           h8_sc);
+  if (tid < 64) one_publish(sync, blk, gen);
+  down_body<4, 1, true>(L, item, b, rid, 1, pool, slot_bytes, slot_tab, expert_base, h8, wts, bias_dn, yw, h8_sc,
+                        [&]() { one_wait(sync + (kOneGo + b % kGo) * kLine, gen, err); });
+  if (tid >= 64) return;
+  // wave 0: yw stores acknowledged, count block b; the fourth arrival sums the block (k_combine_t950's arithmetic)
+  __builtin_amdgcn_s_waitcnt(0);
+  uint32_t* bc = one_block_counter(sync, b);
+  int last = 0;
+  if (lane == 0) {
+    last = __hip_atomic_fetch_add(bc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 3u;
+    if (last) __hip_atomic_store(bc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  last = __builtin_amdgcn_readfirstlane(last);
+  if (!last || lane >= kTRows / 2) return;
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t v = load_coherent(reinterpret_cast<const uint32_t*>(yw + (long long)k * kH + 16 * b) + lane);
+    a0 += bf16_to_f32((uint16_t)(v & 0xffff));
+    a1 += bf16_to_f32((uint16_t)(v >> 16));
+  }
+  reinterpret_cast<uint32_t*>(out + 16 * b)[lane] = (uint32_t)f32_to_bf16(a0) | ((uint32_t)f32_to_bf16(a1) << 16);
 }
 
 template <typename... KArgs, typename... Args>
@@ -874,6 +1043,24 @@ static void* scratch_address() {
   return addr[dev];
 }
 
+// Whether the current device holds all kOneWgs workgroups of k_moe_one_t950 at once (the occupancy query times the
+// CU count), asked once per device.
+static bool one_resident_ok() {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static int8_t ok[kMaxDevices] = {};                 // 0 unknown, 1 yes, -1 no
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ok[dev]) {
+    int per_cu = 0, cus = 0;
+    const bool q = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_one_t950, 256, 0) == hipSuccess &&
+                   hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess;
+    ok[dev] = q && (long long)per_cu * cus >= kOneWgs ? 1 : -1;
+  }
+  return ok[dev] > 0;
+}
+
 }  // namespace na
 
 using namespace na;
@@ -914,6 +1101,28 @@ int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
                        int k_split, int down_mode, void* const* events, hipStream_t stream) {
   return decode_t950(x, topk_ids, topk_w, B, pool, slot_bytes, slot_tab, expert_base, bias_gu, bias_dn, h_scratch,
                      yw_scratch, out, alpha, limit, k_split, down_mode, events, stream);
+}
+
+long long na_moe_one_sync_words(void) { return (long long)kOneSyncLines * kLine; }
+
+int na_moe_decode_t950_one(const void* x, const int64_t* topk_ids, const void* topk_w, const void* pool,
+                           long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
+                           const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha,
+                           float limit, unsigned int* sync, void* const* events, hipStream_t stream) {
+  if (!x || !topk_ids || !topk_w || !pool || !h_scratch || !yw_scratch || !out || !sync) return kErrArgs;
+  if (slot_bytes < kTSlot || (slot_bytes & 15) || (reinterpret_cast<uintptr_t>(pool) & 15)) return kErrArgs;
+  if ((reinterpret_cast<uintptr_t>(h_scratch) | reinterpret_cast<uintptr_t>(yw_scratch) |
+       reinterpret_cast<uintptr_t>(out)) & 15)
+    return kErrArgs;
+  const uint32_t h8_sc = h8_scale_bytes(alpha, limit);
+  if (!h8_sc) return kErrArgs;
+  if (!one_resident_ok()) return kErrResident;
+  launch_t(k_moe_one_t950, dim3(kOneWgs), dim3(256), stream, events ? (hipEvent_t)events[0] : nullptr,
+           events ? (hipEvent_t)events[1] : nullptr, topk_ids, (const uint8_t*)pool, slot_bytes, slot_tab,
+           expert_base, (const uint16_t*)x, (const uint16_t*)bias_gu, (const uint16_t*)bias_dn,
+           (const uint16_t*)topk_w, (uint8_t*)h_scratch, (uint16_t*)yw_scratch, (uint16_t*)out, alpha, limit, h8_sc,
+           (uint32_t*)sync);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
 int na_moe_decode_t950_noalloc(const void* x, const int64_t* topk_ids, const void* topk_w, int B, const void* pool,

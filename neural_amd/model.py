@@ -395,8 +395,9 @@ class DecodeModel:
 
     # ------------------------------------------------------------------------------------------------ graphs
     def sync_error(self) -> bool:
-        """Whether a fused attention block ever gave up a wait (its outputs were then invalid).  Reads the device."""
-        return bool(int(self.sync[0].item()))
+        """Whether a fused attention block or a single-launch expert body ever gave up a wait (its outputs were then
+        invalid).  Reads the device."""
+        return bool(int(self.sync[0].item())) or self.rx.sync_error()
 
     def capture(self) -> torch.cuda.CUDAGraph:
         """Capture one step as a hipGraph (replay = one greedy step at the device-side position).  The capture itself

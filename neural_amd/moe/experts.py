@@ -21,11 +21,12 @@ class ResidentExperts:
     def __init__(self, pool: torch.Tensor, layout: ExpertLayout = GPTOSS_LAYOUT, bias_gu: torch.Tensor | None = None,
                  bias_dn: torch.Tensor | None = None, slot_tab: torch.Tensor | None = None,
                  max_batch: int = MAX_DECODE_TOKENS, gu_pairs_per_wave: int = 4, dn_pairs_per_wave: int = 2,
-                 k_split: int = 0, combine_in_down: bool = True):
+                 k_split: int = 0, combine_in_down: bool = True, one_launch: bool = True):
         """pool: uint8 [n, layout.slot_bytes] in the raw, PS4 or t950 (gfx950 tile) layout.  The t950 layout runs the
         block-scaled MFMA decode kernels (k_split waves per workgroup split K; 0 = automatic, 4); with
         combine_in_down, a single token takes two launches (the down kernel holds every expert of an output block
-        and sums the top-k itself) instead of three.  The store layouts run the VALU kernels (gu/dn_pairs_per_wave
+        and sums the top-k itself) instead of three, and with one_launch as well (and the automatic k_split) a single
+        launch (na_moe_decode_t950_one: the same bits).  The store layouts run the VALU kernels (gu/dn_pairs_per_wave
         row pairs per wavefront)."""
         if layout.weight_repr not in ("mxfp4_g32", "mxfp4_g32_ps4", TILE_REPR):
             raise ValueError(f"ResidentExperts serves the raw, PS4 and t950 slot layouts, not {layout.weight_repr}")
@@ -59,6 +60,14 @@ class ResidentExperts:
         self.down_mode = 0 if combine_in_down else 1
         self.h = torch.empty(max_batch * layout.top_k, layout.down_k, dtype=torch.bfloat16, device=dev)
         self.yw = torch.empty(max_batch * layout.top_k, layout.down_n, dtype=torch.bfloat16, device=dev)
+        # the single-launch path's handoff words (zero before its first call; every call leaves them reusable)
+        self.one = self.tiled and combine_in_down and one_launch and self.k_split in (0, 4)
+        self.sync = (torch.zeros(N.lib().na_moe_one_sync_words(), dtype=torch.int32, device=dev) if self.one
+                     else None)
+
+    def sync_error(self) -> bool:
+        """Whether a wait of the single-launch path ever gave up (reads one device word: synchronises)."""
+        return bool(self.sync is not None and int(self.sync[0].item()) != 0)
 
     def forward_decode(self, layer: int, hidden: torch.Tensor, router_indices: torch.Tensor,
                        routing_weights: torch.Tensor, out: torch.Tensor | None = None, events=None) -> torch.Tensor:
@@ -86,6 +95,13 @@ class ResidentExperts:
             out = torch.empty(B, L.hidden, dtype=torch.bfloat16, device=hidden.device)
         elif out.dtype is not torch.bfloat16 or tuple(out.shape) != (B, L.hidden) or not out.is_contiguous():
             raise ValueError("out must be contiguous bf16 [B, hidden]")
+        if self.one and B == 1:
+            N.call("na_moe_decode_t950_one", hidden.data_ptr(), router_indices.data_ptr(), routing_weights.data_ptr(),
+                   self.pool.data_ptr(), L.slot_bytes, N.ptr(self.slot_tab), layer * L.n_experts,
+                   N.ptr(self.bias_gu), N.ptr(self.bias_dn), self.h.data_ptr(), self.yw.data_ptr(), out.data_ptr(),
+                   float(L.act_alpha), float(L.act_limit), self.sync.data_ptr(), N.events_array(events),
+                   N.stream(hidden.device))
+            return out
         if self.tiled:
             N.call("na_moe_decode_t950", hidden.data_ptr(), router_indices.data_ptr(), routing_weights.data_ptr(), B,
                    self.pool.data_ptr(), L.slot_bytes, N.ptr(self.slot_tab), layer * L.n_experts,
@@ -143,6 +159,8 @@ class ResidentExperts:
 
     def launches(self, batch: int, with_out: bool = True) -> tuple:
         """Names of the kernels one forward_decode call launches, in order (two timing events per launch)."""
+        if self.one and with_out and batch == 1:
+            return ("experts",)
         if self.tiled and self.down_mode == 0 and with_out and batch == 1:
             return ("gate_up", "down_combine")
         return ("gate_up", "down", "combine") if with_out else ("gate_up", "down")

@@ -242,8 +242,10 @@ def test_down_with_combine_matches_expert_major_path(B):
     tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
     tiles.repack_to_t950(raw, tp)
     tabd, bg, bd = torch.from_numpy(tab).to(dev), bgu.to(dev), bdn.to(dev)
-    two = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=True)
+    one = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4)      # single launch at B = 1
+    two = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=True, one_launch=False)
     three = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=False)
+    assert one.launches(B) == (("experts",) if B == 1 else ("gate_up", "down", "combine"))
     assert two.launches(B) == (("gate_up", "down_combine") if B == 1 else ("gate_up", "down", "combine"))
     assert len(three.launches(B)) == 3
     rng = np.random.default_rng(B)
@@ -260,6 +262,8 @@ def test_down_with_combine_matches_expert_major_path(B):
         layer = 3 + call
         a = two.forward_decode(layer, xd, idd, wd).float().cpu().numpy()
         c = three.forward_decode(layer, xd, idd, wd).float().cpu().numpy()
+        o = one.forward_decode(layer, xd, idd, wd).float().cpu().numpy()
+        assert np.array_equal(o, a if B == 1 else c), call
         if B == 1:
             assert np.array_equal(a, c), call
         for b in range(B):
@@ -282,6 +286,57 @@ def test_down_with_combine_matches_expert_major_path(B):
                 assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale, (name, call, b, d.max(), scale)
                 prof = ulp_profile(arr, want)
                 assert prof[1] >= T950_FRAC2 and prof[2] >= T950_FRAC4, (name, call, b, prof)
+    assert not one.sync_error()
+
+
+@pytest.mark.gpu
+def test_one_launch_graph_replays_and_layer_chain():
+    """The single-launch expert body (B = 1) captured in a hipGraph: every replay (new token, new routing, the
+    launch's generation word advancing on the device) equals the two-launch path's eager result bit for bit; then 36
+    back-to-back launches over chained layers (each output the next input, as in a decode step) equal the two-launch
+    chain bit for bit, and no wait ever gave up."""
+    import torch
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
+    dev = _dev()
+    slots, x, ids, w, tab, bgu, bdn = _t950_case(1, 4242, True, nslot=8)
+    print("case one-launch graph replay", flush=True)
+    raw = torch.from_numpy(np.stack(slots)).to(dev)
+    tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
+    tiles.repack_to_t950(raw, tp)
+    tabd, bg, bd = torch.from_numpy(tab).to(dev), bgu.to(dev), bdn.to(dev)
+    one = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd)
+    two = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, one_launch=False)
+    assert one.launches(1) == ("experts",)
+    xd, idd = x.to(dev), torch.from_numpy(ids).to(dev)
+    wd = torch.from_numpy(w).to(torch.bfloat16).to(dev)
+    out = torch.empty(1, 2880, dtype=torch.bfloat16, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        one.forward_decode(5, xd, idd, wd, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        one.forward_decode(5, xd, idd, wd, out=out)
+    rng = np.random.default_rng(11)
+    for rep in range(4):
+        xd.copy_(synth.bf16_normal(rng, (1, 2880)).to(dev))
+        idd.copy_(torch.from_numpy(rng.choice(128, (1, 4), replace=False)).to(dev))
+        g.replay()
+        torch.cuda.synchronize()
+        want = two.forward_decode(5, xd, idd, wd)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), rep
+    # a decode step's chain: layer l's output is layer l + 1's input
+    ida = torch.from_numpy(rng.choice(128, (36, 1, 4)).astype(np.int64)).to(dev)
+    ya, yb = xd.clone(), xd.clone()
+    for layer in range(36):
+        ya = one.forward_decode(layer, ya, ida[layer], wd)
+        yb = two.forward_decode(layer, yb, ida[layer], wd)
+    torch.cuda.synchronize()
+    assert torch.equal(ya, yb)
+    assert not one.sync_error()
 
 
 def _e4m3_table():
@@ -412,7 +467,8 @@ def test_duplicate_ids_in_a_token(B):
     tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
     tiles.repack_to_t950(raw, tp)
     tabd, bg, bd = torch.from_numpy(tab).to(dev), bgu.to(dev), bdn.to(dev)
-    paths = {"two": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4),   # down + combine's K split
+    paths = {"one": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4),   # a single launch at B = 1
+             "two": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, one_launch=False),
              "three": ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, combine_in_down=False),
              "store": ResidentExperts(raw, GPTOSS_LAYOUT, bg, bd, tabd)}
     xd, idd = x.to(dev), torch.from_numpy(ids).to(dev)
@@ -421,6 +477,7 @@ def test_duplicate_ids_in_a_token(B):
     got = {nm: rx.forward_decode(layer, xd, idd, wd).float().cpu().numpy() for nm, rx in paths.items()}
     torch.cuda.synchronize()
     assert np.array_equal(got["two"], got["three"])
+    assert np.array_equal(got["one"], got["two"])
     cache = {}
     for b in range(B):
         ys = []
