@@ -12,8 +12,9 @@ uniform E2M1 codes, E8M0 exponents uniform in [119, 125]) serves two measurement
                 routing weight, top-k combine) of all 36 layers per step, random top-4 routing from 16 routing sets
                 cycled so the 256 MB Infinity Cache never serves a repeated expert; batch 1 plus the batch 2 / 4 / 8
                 sweep; whole-step HBM GB/s.
-  roofline      the dominant expert kernel (gate_up) of configuration 1 at batch 1: algorithmic bytes per launch
-                (4 experts x 8,812,800 B of E2M1 codes + E8M0 scales) / its average launch duration, from events
+  roofline      the dominant expert kernel of configuration 1 at batch 1, the single-launch expert body
+                k_moe_one_t950: algorithmic bytes per launch (4 experts x 13,219,200 B of E2M1 codes + E8M0 scales,
+                gate_up and down) / its average launch duration, from events
                 timestamped by the dispatches themselves on the launch stream (eager steps queued behind a spin
                 kernel, so the launches run back to back as in the graph replays); peak 8 TB/s; traffic = HBM bytes
                 per launch from the committed rocprofv3 --pmc table (null when the kernel sources changed since).
@@ -491,27 +492,35 @@ def run_model(A, pool, dev):
            **({"context_prefill_ms": round(t_ctx * 1e3, 1), "prefill_tok_s": round(ctx / t_ctx, 1),
                "prefill_chunk": A.prefill_chunk} if A.context_mode == "prefill" else
               {"context_steps_per_s": round((ctx - 1) / t_ctx, 1)})}
-    out = {"tok_s": tok_s, "ms_per_step": el / n_new * 1e3, "config": cfg, "gate_up_us": avg[names[0]]}
+    out = {"tok_s": tok_s, "ms_per_step": el / n_new * 1e3, "config": cfg, "gate_up_us": avg[names[0]],
+           "expert_label": names[0]}
     del model, w, rx
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return out
 
 
-def gate_up_roofline(avg_us, k_split):
-    """The roofline object of the gate_up kernel at batch 1 (4 distinct experts per launch)."""
-    gu_bytes = TOPK * GATE_UP_BYTES
-    gbps = gu_bytes / (avg_us * 1e-6) / 1e9
-    kname = "k_moe_gate_up_t950"
+# bench kernel label -> (symbol, algorithmic bytes per distinct expert) of the batch-1 t950 expert launches
+EXPERT_KERNELS = {"experts": ("k_moe_one_t950", GATE_UP_BYTES + DOWN_BYTES),
+                  "gate_up": ("k_moe_gate_up_t950", GATE_UP_BYTES)}
+
+
+def expert_roofline(label, avg_us, k_split):
+    """The roofline object of the dominant batch-1 expert launch (4 distinct experts per launch): the single-launch
+    expert body ("experts": gate_up, SwiGLU, down and the top-4 sum; 4 x 13,219,200 B) where the library runs it,
+    else the gate_up kernel (4 x 8,812,800 B)."""
+    kname, per_expert = EXPERT_KERNELS[label]
+    nbytes = TOPK * per_expert
+    gbps = nbytes / (avg_us * 1e-6) / 1e9
     traffic, why = measured_traffic(kname, "t950", 1, effective_k_split(k_split, 1))
     log(f"traffic: {traffic} ({why})")
     return {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kname,
-            "avg_launch_us": round(avg_us, 3), "algorithmic_bytes_per_launch": gu_bytes}
+            "avg_launch_us": round(avg_us, 3), "algorithmic_bytes_per_launch": nbytes}
 
 
 def bench_model(A):
-    """Configuration 4 alone (see run_model); roofline: gate_up inside the decode step."""
+    """Configuration 4 alone (see run_model); roofline: the expert body inside the decode step."""
     import torch
 
     from neural_amd import synth
@@ -523,7 +532,8 @@ def bench_model(A):
     res = {"metric": METRIC, "value": round(m["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": A.steps,
            "warmup": A.warmup, "ms_per_step": round(m["ms_per_step"], 4), "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic", "config": m["config"],
-           "roofline": {**gate_up_roofline(m["gate_up_us"], A.k_split), "workload": "config4 decode step"},
+           "roofline": {**expert_roofline(m["expert_label"], m["gate_up_us"], A.k_split),
+                        "workload": "config4 decode step"},
            "cpu_baseline": None}
     print(json.dumps(res), flush=True)
 
@@ -744,9 +754,9 @@ def bench_decode(A):
     c1 = config1_summary(m1, L, 1)
     if not A.no_batch_sweep:
         c1["batch_sweep"] = batch_sweep(rx, dev, A, 1)
-    roof = gate_up_roofline(m1["kern"][m1["dom"]]["avg_us"], A.k_split)
+    roof = expert_roofline(m1["dom"], m1["kern"][m1["dom"]]["avg_us"], A.k_split)
     roof.update(workload="config1 batch 1 (the expert GEMV stream the metric's GB/s half names)",
-                config4_gate_up_avg_launch_us=round(m4["gate_up_us"], 3))
+                config4_avg_launch_us=round(m4["gate_up_us"], 3))
     cpu = None
     if not A.skip_cpu:
         try:
@@ -1015,7 +1025,8 @@ def bench_experts(A):
     c1 = config1_summary(m, L, B)
     if not A.no_batch_sweep:
         c1["batch_sweep"] = batch_sweep(rx, dev, A, B)
-    kname = "k_moe_gate_up_t950" if A.layout == "t950" else "k_moe_gate_up"
+    kname = ({"experts": "k_moe_one_t950", "gate_up": "k_moe_gate_up_t950"}[m["dom"]] if A.layout == "t950"
+             else "k_moe_gate_up")
     traffic, why = measured_traffic(kname, A.layout, B, effective_k_split(A.k_split, B))
     log(f"traffic: {traffic} ({why})")
     top = m["kern"][m["dom"]]

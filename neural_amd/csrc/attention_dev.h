@@ -89,6 +89,12 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
   // A operand: query rows (row n of the head for lanes n < 8, zero rows otherwise), d = 8g.. and 32 + 8g..
   const uint16_t* qrow = q + ((long long)b * kNQ + h * kRep + min(n, kRep - 1)) * kHD;
   uint4 qa0 = make_uint4(0, 0, 0, 0), qa1 = make_uint4(0, 0, 0, 0);
+  // the sinks of the rows this thread finishes (constant weights), read now so that no dependent load waits at the end
+  const uint16_t* sk = sinks + h * kRep;
+  float sink_r[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sink_r[r] = bf16_to_f32(sk[4 * min(g, 1) + r]);
+  const float sink_c = bf16_to_f32(sk[(2 * tid) / kHD]);
   if constexpr (!FUSED) {
     qa0 = *reinterpret_cast<const uint4*>(qrow + 8 * g);
     qa1 = *reinterpret_cast<const uint4*>(qrow + 32 + 8 * g);
@@ -217,26 +223,27 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
       m_run[r] = m_new[r];
       acc[r] *= alpha[r];
     }
-    const int nks = (min(kSub, c1 - k0) + 31) / 32;     // 32-key steps holding live keys (P is 0 past c1)
+    // every 32-key step of the sub-chunk, with no branch, so that all the LDS reads are in flight together: P is
+    // +0 past c1 (and V^T holds finite cache rows there), so those steps add exact zeros to acc (never -0)
+    uint4 pa[kSub / 32], vb[kSub / 32];
 #pragma unroll
     for (int ks = 0; ks < kSub / 32; ++ks) {
-      if (ks < nks) {                                  // uniform
-        const uint4 pa = *reinterpret_cast<const uint4*>(L.p + (n & (kRep - 1)) * kPPitch + 2 * (32 * ks + 8 * g));
-        const uint4 vb = *reinterpret_cast<const uint4*>(L.vt + (16 * wave + n) * kVtPitch + 2 * (32 * ks + 8 * g));
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pa), as_bf16x8(vb), acc, 0, 0, 0);
-      }
+      pa[ks] = *reinterpret_cast<const uint4*>(L.p + (n & (kRep - 1)) * kPPitch + 2 * (32 * ks + 8 * g));
+      vb[ks] = *reinterpret_cast<const uint4*>(L.vt + (16 * wave + n) * kVtPitch + 2 * (32 * ks + 8 * g));
     }
+#pragma unroll
+    for (int ks = 0; ks < kSub / 32; ++ks)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pa[ks]), as_bf16x8(vb[ks]), acc, 0, 0, 0);
     __syncthreads();                               // LDS is rewritten by the next sub-chunk
   }
 
   // ---- finish: a single chunk writes the output; otherwise publish the partial, the last arriver combines
-  const uint16_t* sk = sinks + h * kRep;
   uint16_t* orow = out + ((long long)b * kNQ + h * kRep) * kHD;
   if (ns == 1) {
     if (g < 2) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float sink = bf16_to_f32(sk[4 * g + r]);
+        const float sink = sink_r[r];
         const float m = fmaxf(sink, m_run[r]);
         const float a = m_run[r] == kNegInf ? 0.f : expf(m_run[r] - m);
         const float S = expf(sink - m) + s_run[r] * a;   // the combine's formula, so one chunk == split at pos < 64
@@ -274,50 +281,67 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
   }
   __syncthreads();
   if (!last) return;
-  // Combine.  One acquire fence (the partials were published with device-coherent stores before the count), then
-  // one round of plain loads, all in flight together: thread tid's two outputs i = 2 tid, 2 tid + 1 (row i / 64) of
-  // the first 32 chunks into registers, every chunk's maxima and sums into LDS.  Then each thread forms its row's
+  // Combine.  One round of device-coherent loads (the partials were published with device-coherent stores before
+  // the count), all in flight together: thread tid's two outputs i = 2 tid, 2 tid + 1 (row i / 64) of the first 32
+  // chunks into registers, every chunk's maxima and sums into LDS.  Then each thread forms its row's
   // maximum m, weights w_c = exp(m_c - m) and S itself (in chunk order) and out[row][d] = sum_c acc_c[row][d] w_c / S.
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   const float* pbase = work + (long long)bh * ns * kPartFloats;
   const int i = 2 * tid, row = i / kHD;
   float2 v[32];
 #pragma unroll
   for (int j = 0; j < 32; ++j)
-    v[j] = j < ns ? *reinterpret_cast<const float2*>(pbase + j * kPartFloats + 2 * kRep + i) : make_float2(0.f, 0.f);
-  for (int k = tid; k < ns * kRep; k += 256) {
-    const int cc = k / kRep, r = k - cc * kRep;
-    L.cm[cc][r] = pbase[cc * kPartFloats + r];
-    L.cs[cc][r] = pbase[cc * kPartFloats + kRep + r];
-  }
-  __syncthreads();
-  const float sink = bf16_to_f32(sk[row]);
-  float m = sink;
-  for (int cc = 0; cc < ns; ++cc) m = fmaxf(m, L.cm[cc][row]);
-  float S = expf(sink - m), o0 = 0.f, o1 = 0.f;
+    v[j] = j < ns ? load8_coherent(pbase + j * kPartFloats + 2 * kRep + i) : make_float2(0.f, 0.f);
+  // every chunk's maxima and sums (ns x 8 <= 512 of each): both loads of both rounds issued before the LDS stores
+  float lm[2], ls[2];
 #pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    if (j < ns) {
-      const float mc = L.cm[j][row];
-      const float w = mc == kNegInf ? 0.f : expf(mc - m);
-      S += L.cs[j][row] * w;
-      o0 += v[j].x * w;
-      o1 += v[j].y * w;
+  for (int it = 0; it < 2; ++it) {
+    const int k = min(tid + 256 * it, ns * kRep - 1), cc = k / kRep, r = k - cc * kRep;
+    lm[it] = loadf_coherent(pbase + cc * kPartFloats + r);
+    ls[it] = loadf_coherent(pbase + cc * kPartFloats + kRep + r);
+  }
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int k = tid + 256 * it, cc = k / kRep, r = k - cc * kRep;
+    if (k < ns * kRep) {
+      L.cm[cc][r] = lm[it];
+      L.cs[cc][r] = ls[it];
     }
   }
-  for (int cb = 32; cb < ns; cb += 32) {               // uniform; ns <= 64
-#pragma unroll
-    for (int j = 0; j < 32; ++j)
-      v[j] = cb + j < ns ? *reinterpret_cast<const float2*>(pbase + (cb + j) * kPartFloats + 2 * kRep + i)
-                         : make_float2(0.f, 0.f);
+  __syncthreads();
+  // Branch-free over 32 chunks at a time: every LDS read of a round is issued before the first use (a branch per
+  // chunk would wait out the LDS latency 32 times in a row).  Chunks past ns read in-bounds rows of cm / cs and are
+  // masked: they add fmaf(0, 0, x) = x, so the sums equal the ones over the live chunks, in chunk order.
+  const float sink = sink_c;
+  float m = sink;
+  for (int cb = 0; cb < ns; cb += 32) {                // uniform; ns <= 64
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
-      if (cb + j < ns) {
-        const float mc = L.cm[cb + j][row];
-        const float w = mc == kNegInf ? 0.f : expf(mc - m);
-        S += L.cs[cb + j][row] * w;
-        o0 += v[j].x * w;
-        o1 += v[j].y * w;
+      const float mc = L.cm[cb + j][row];
+      m = fmaxf(m, cb + j < ns ? mc : kNegInf);
+    }
+  }
+  float S = expf(sink - m), o0 = 0.f, o1 = 0.f;
+  for (int cb = 0; cb < ns; cb += 32) {                // uniform; ns <= 64
+    if (cb > 0) {
+#pragma unroll
+      for (int j = 0; j < 32; ++j)
+        v[j] = cb + j < ns ? load8_coherent(pbase + (cb + j) * kPartFloats + 2 * kRep + i) : make_float2(0.f, 0.f);
+    }
+#pragma unroll
+    for (int j0 = 0; j0 < 32; j0 += 8) {               // 8 chunks' LDS reads in flight, then their arithmetic
+      float mcv[8], csv[8], wv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        mcv[j] = L.cm[cb + j0 + j][row];
+        csv[j] = L.cs[cb + j0 + j][row];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) wv[j] = (cb + j0 + j >= ns || mcv[j] == kNegInf) ? 0.f : expf(mcv[j] - m);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        S = fmaf(cb + j0 + j < ns ? csv[j] : 0.f, wv[j], S);
+        o0 = fmaf(v[j0 + j].x, wv[j], o0);
+        o1 = fmaf(v[j0 + j].y, wv[j], o1);
       }
     }
   }

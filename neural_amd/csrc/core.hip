@@ -91,11 +91,14 @@ struct NormIn {
       const int ch = min((int)threadIdx.x + 256 * i, kH / 8 - 1);
       m[i] = *reinterpret_cast<const uint4*>(mid + 8 * ch);
       w[i] = *reinterpret_cast<const uint4*>(wp + 8 * ch);
-      // absent inputs read mid's chunk (a valid address) and are replaced by zero at use
-      g[i] = *reinterpret_cast<const uint4*>((gp ? gp : mid) + 8 * ch);
-      const float* cc = cp ? cp + 8 * ch : reinterpret_cast<const float*>(mid);
-      c[i][0] = *reinterpret_cast<const uint4*>(cc);
-      c[i][1] = *reinterpret_cast<const uint4*>(cc + 4);
+      // absent inputs are not read (uniform branches: every workgroup of a launch reads the same inputs, and these
+      // requests queue in the L2 with the launch's weight stream); their values are unused
+      g[i] = c[i][0] = c[i][1] = make_uint4(0, 0, 0, 0);
+      if (gp) g[i] = *reinterpret_cast<const uint4*>(gp + 8 * ch);
+      if (cp) {
+        c[i][0] = *reinterpret_cast<const uint4*>(cp + 8 * ch);
+        c[i][1] = *reinterpret_cast<const uint4*>(cp + 8 * ch + 4);
+      }
     }
   }
 };

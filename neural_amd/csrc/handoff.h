@@ -38,6 +38,14 @@ NA_DEVICE void store_coherent(uint32_t* p, uint32_t v) {
 NA_DEVICE uint32_t load_coherent(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// 8 bytes with one device-coherent load (p 8-byte aligned).
+NA_DEVICE float2 load8_coherent(const float* p) {
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
+NA_DEVICE float loadf_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 // 16 bytes as four coherent dword loads (p 4-byte aligned).
 NA_DEVICE uint4 load16_coherent(const void* p) {
   const uint32_t* w = reinterpret_cast<const uint32_t*>(p);
