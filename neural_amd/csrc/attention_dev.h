@@ -30,17 +30,6 @@ struct AttnLds {
   uint32_t last;                                   // split-K: this workgroup combines
 };
 
-// Wave-wide max / sum over the 16 lanes of a row group (lanes 16 q .. 16 q + 15).
-NA_DEVICE float group16_max(float v) {
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-NA_DEVICE float group16_sum(float v) {
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o);
-  return v;
-}
 
 NA_DEVICE bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
@@ -165,7 +154,7 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
       }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) wmax[r] = group16_max(wmax[r]);
+    for (int r = 0; r < 4; ++r) wmax[r] = row16_max(wmax[r]);
     if (n == 0 && g < 2) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) L.mx[wave][4 * g + r] = wmax[r];
@@ -208,7 +197,7 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
       }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) psum[r] = group16_sum(psum[r]);
+    for (int r = 0; r < 4; ++r) psum[r] = row16_sum(psum[r]);   // exact in lane n = 0, the one stored
     if (n == 0 && g < 2) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) L.sm[wave][4 * g + r] = psum[r];

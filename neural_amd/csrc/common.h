@@ -128,15 +128,47 @@ NA_DEVICE float e8m0_scale(float v, int s) {
   return s == 255 ? v * __builtin_inff() : __builtin_amdgcn_ldexpf(v, s - 127);
 }
 
-NA_DEVICE float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
 template <int CTRL>
 NA_DEVICE float dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// The value of lane i ^ 16 (v_permlane16_swap with v as both operands: odd rows <-> even rows) and of lane i ^ 32
+// (v_permlane32_swap: upper half <-> lower half).  VALU permutations, no LDS round trip.  Must run with all lanes
+// active.
+NA_DEVICE float lane_xor16(float v) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  const auto p = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  return __builtin_bit_cast(float, ((threadIdx.x >> 4) & 1) ? p[0] : p[1]);
+}
+NA_DEVICE float lane_xor32(float v) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  const auto p = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+  return __builtin_bit_cast(float, ((threadIdx.x >> 5) & 1) ? p[0] : p[1]);
+}
+
+// Sums by DPP and lane permutations.  Each returns, in the lanes stated, exactly the value of the xor butterfly
+// v += v(lane ^ o) over the offsets in the order named (the same pairs, the same association), so the result does not
+// depend on which of these implementations computed it; the other lanes hold partial or differently associated sums.
+// row_shl:N (lane i reads lane i + N of its row) equals the xor partner for the lanes that the following levels read.
+// Must run with all lanes active.
+
+// Offsets 1, 2, 4, 8: exact in lane 0 of each row of 16.
+NA_DEVICE float row16_sum(float v) {
+  v += dpp<0xB1>(v);      // quad_perm [1,0,3,2]: lane i ^ 1
+  v += dpp<0x4E>(v);      // quad_perm [2,3,0,1]: lane i ^ 2
+  v += dpp<0x104>(v);     // row_shl:4: lane i + 4 (= i ^ 4 for lanes 0..3 of the row)
+  return v + dpp<0x108>(v);   // row_shl:8: lane i + 8 (= i ^ 8 for lanes 0..7)
+}
+
+// Offsets 32, 16, 8, 4, 2, 1 (a whole wavefront): exact in lane 0.
+NA_DEVICE float wave_sum_lane0(float v) {
+  v += lane_xor32(v);
+  v += lane_xor16(v);
+  v += dpp<0x108>(v);     // row_shl:8: exact for lanes 0..7
+  v += dpp<0x104>(v);     // row_shl:4: exact for lanes 0..3
+  v += dpp<0x4E>(v);      // quad xor 2
+  return v + dpp<0xB1>(v);    // quad xor 1
 }
 
 // Largest value over the 16 lanes of each row of the wavefront (lanes 16 r .. 16 r + 15), returned to all 16: DPP

@@ -25,11 +25,14 @@ constexpr int kHq = 64 * 64;             // query width (NQ x HD)
 constexpr int kQkvRows = (64 + 2 * 8) * 64;   // 5120
 constexpr int kNE = 128;
 
-// Sum over the TPR lanes of a row group (TPR a power of two <= 64, groups aligned to TPR lanes).
+// Sum over the TPR lanes of a row group (TPR = 16, 32 or 64, groups aligned to TPR lanes), exact in the group's first
+// lane (the xor butterfly over offsets 1, 2, 4, .., TPR / 2; common.h): the only lane whose result is used.
 template <int TPR>
 NA_DEVICE float sum_group(float v) {
-#pragma unroll
-  for (int o = 1; o < TPR; o <<= 1) v += __shfl_xor(v, o);
+  static_assert(TPR == 16 || TPR == 32 || TPR == 64, "row groups of 16, 32 or 64 lanes");
+  v = row16_sum(v);
+  if constexpr (TPR >= 32) v += lane_xor16(v);
+  if constexpr (TPR >= 64) v += lane_xor32(v);
   return v;
 }
 
@@ -52,6 +55,7 @@ struct RowChunks {
 #pragma unroll
     for (int i = 0; i < IT; ++i) w[i] = load16<true>(wrow + 8 * min(j + TPR * i, NCH - 1));
   }
+  // the row's dot product, in the row group's first lane (j == 0; the other lanes hold partial sums)
   NA_DEVICE float dot(const uint16_t* hc, int j) const {
     float a = 0.f;
 #pragma unroll
@@ -135,7 +139,7 @@ NA_DEVICE void norm_finish(const NormIn& in, bool has_g, bool has_c, float eps, 
       if (tid + 256 * i < kH / 8) ss += x * x;
     }
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_lane0(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   const float var = ((red[0] + red[1]) + (red[2] + red[3])) * (1.0f / kH);
@@ -350,25 +354,44 @@ __global__ __launch_bounds__(256) void k_oproj(const uint16_t* __restrict__ att,
 // writes ids / weights and resets the count.
 // Top 4 of 128 logits held by one wave (lane l: logits l and l + 64) by repeated argmax, lowest index on ties; lanes
 // 0..3 write ids[k] and the weights bf16(exp(v_k - v_0) / sum_k exp(v_k - v_0)) (the reference's softmax over the
-// four, fused_core.py:486-502).
+// four, fused_core.py:486-502).  The logits are bf16 values (the router rounds them), so (value, index) fits one
+// 32-bit key that orders exactly as the comparison "larger value, then smaller index" (-0 as +0): each round is one
+// wavefront maximum of keys by DPP and four lane reads, with no LDS round trip.
+NA_DEVICE uint32_t top_key(float v, int idx) {
+  uint32_t b = __float_as_uint(v) >> 16;
+  if (b == 0x8000u) b = 0;
+  const uint32_t ord = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+  return (ord << 16) | (uint32_t)(0xFFFF - idx);
+}
+NA_DEVICE float top_key_value(uint32_t key) {
+  const uint32_t ord = key >> 16;
+  return bf16_to_f32((uint16_t)((ord & 0x8000u) ? (ord & 0x7FFFu) : (~ord & 0xFFFFu)));
+}
+template <int CTRL>
+NA_DEVICE uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+// The largest key of the wavefront, in every lane: DPP maxima within each row of 16, then the four rows'.
+NA_DEVICE uint32_t wave_max_key(uint32_t k) {
+  k = max(k, dpp_u32<0xB1>(k));
+  k = max(k, dpp_u32<0x4E>(k));
+  k = max(k, dpp_u32<0x124>(k));
+  k = max(k, dpp_u32<0x128>(k));
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)k, 0), r1 = (uint32_t)__builtin_amdgcn_readlane((int)k, 16);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)k, 32), r3 = (uint32_t)__builtin_amdgcn_readlane((int)k, 48);
+  return max(max(r0, r1), max(r2, r3));
+}
 NA_DEVICE void top4_softmax(float v0, float v1, int lane, int64_t* __restrict__ ids, uint16_t* __restrict__ wts) {
+  uint32_t k0 = top_key(v0, lane), k1 = top_key(v1, lane + 64);
   float tv[4];
   int ti[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    float bvv = v0;
-    int bi = lane;
-    if (v1 > bvv) { bvv = v1; bi = lane + 64; }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bvv, off);
-      const int oi = __shfl_xor(bi, off);
-      if (ov > bvv || (ov == bvv && oi < bi)) { bvv = ov; bi = oi; }
-    }
-    tv[k] = bvv;
-    ti[k] = bi;
-    if (bi == lane) v0 = -__builtin_inff();
-    if (bi == lane + 64) v1 = -__builtin_inff();
+    const uint32_t best = wave_max_key(max(k0, k1));
+    tv[k] = top_key_value(best);
+    ti[k] = 0xFFFF - (int)(best & 0xFFFFu);
+    if (k0 == best) k0 = 0;                          // every real key is above 0
+    if (k1 == best) k1 = 0;
   }
   if (lane < 4) {
     float ex[4];
@@ -615,7 +638,7 @@ __global__ __launch_bounds__(256) void k_rows_norm(uint16_t* __restrict__ x, con
       if (tid + 256 * i < kH / 8) ss += v * v;
     }
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_lane0(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   const float r = rsqrtf(((red[0] + red[1]) + (red[2] + red[3])) * (1.0f / kH) + eps);

@@ -429,7 +429,7 @@ __global__ __launch_bounds__(kThreads) void k_router(const uint16_t* __restrict_
         a = dot2_bf16(w4.z, x4.z, a);
         a = dot2_bf16(w4.w, x4.w, a);
       }
-      a = wave_sum(a);
+      a = wave_sum_lane0(a);
       if (lane == 0) logits[b * n_exp + e] = rb(a + (br ? bf16_to_f32(br[e]) : 0.f));
     }
   }
