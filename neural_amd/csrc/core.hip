@@ -72,7 +72,7 @@ struct RowChunks {
 #define NA_QKV_TPR 32
 #endif
 #ifndef NA_OPROJ_TPR
-#define NA_OPROJ_TPR 64
+#define NA_OPROJ_TPR 32
 #endif
 #ifndef NA_ROUTER_TPR
 #define NA_ROUTER_TPR 64
