@@ -287,11 +287,14 @@ int na_core_route_pack(const void* hn, const float* logits, const int64_t* ids, 
 /* The attention block of one decode layer in ONE launch: na_core_qkv, na_decode_attention (B = 1), na_core_oproj and
  * na_core_router, with their arguments and results (fused_core.py:581-629: k_qkv, k_attn / SplitAttn, k_oproj,
  * k_router + k_topk), as four phases of one grid.  Each phase issues its loads (weights; the cache rows of earlier
- * positions) before it waits for the phase it needs (device-coherent counters, bounded waits), so weight streams and
+ * positions) before it waits for the phase it needs, whose results it reads as tagged words (each 64-bit word a
+ * 32-bit payload and the launch's generation number, polled by the reader; bounded waits), so weight streams and
  * cache reads overlap the phases before them.  Differences from the four calls: c and g feed o_proj's residual too
  * (it is recomputed per row, not read from xbuf); mid is updated in place; results are bit-identical.
- *   sync   uint32 [na_core_attn_block_sync_words()] (23,552 bytes: counters and release flags, each on its own 256-byte
- *          line), zero before the first call; every completed call leaves it zero except word 0, an error flag that
+ *   sync   uint32 [na_core_attn_block_sync_words()] (51,968 bytes: the error word, the generation word, the
+ *          attention's split counters and the tagged words of the phases' results, on 256-byte lines), zero before
+ *          the first call and owned by one stream (calls that overlap on one buffer race); every completed call
+ *          leaves the counters zero and advances the generation word (uint32 64) by one; word 0 is an error flag that
  *          a wait which gave up after its poll limit raises (and nothing clears): that call's outputs are not
  *          valid.
  *   n_split chunks of the attention (1..64); attn_work: na_attn_workspace_floats(1, n_split) floats (n_split > 1)

@@ -31,7 +31,7 @@ __global__ __launch_bounds__(256) void k_decode_attn(
   __shared__ AttnLds L;
   args_at_entry(q, kc, vc, cache_rows, sinks, pos_p, out, scaling, window, ring, ns, work, counters);
   decode_attn_body<false>(L, blockIdx.x, q, kc, vc, cache_rows, sinks, pos_p, out, scaling, window, ring, ns, work,
-                          counters, AttnHandoff{nullptr, nullptr, 0, nullptr, nullptr});
+                          counters, AttnHandoff{nullptr, nullptr, 0, nullptr});
 }
 
 }  // namespace na

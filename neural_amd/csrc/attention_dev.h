@@ -42,18 +42,42 @@ NA_DEVICE void chunk_range(int lo, int hi, int c, int ns, int& c0, int& c1) {
   c1 = min(c0 + bps * 64, hi + 1);
 }
 
-// The attention of workgroup `blk` (grid B x 8 x ns).  FUSED: q, and the K / V row of the step's own position, are
-// written earlier in the same launch (see handoff.h): the first sub-chunk's K / V loads are issued, then the
-// workgroup waits for its release flag `go`, then reads q, and that row with coherent loads; the output is written
-// with coherent stores and counted in *done (one count per sequence and KV head, done_n in all), whose completion
-// raises the flags `next`.
+// The attention of workgroup `blk` (grid B x 8 x ns).  FUSED (B = 1): q, and the K / V row of the step's own
+// position, are produced earlier in the same launch as tagged words (handoff.h; word 32 r + d holds dims d and d + 32
+// of QKV row r = head, q heads 0..63, K heads 64..71, V heads 72..79): the first sub-chunk's K / V loads are issued,
+// then thread 0 polls the group's last word (V head h, dims 31 / 63, from the group's last QKV workgroup), then each
+// lane reads its words.  The output is also written as tagged words (word i: elements 2i, 2i + 1 of the 4096).
 struct AttnHandoff {
-  const uint32_t* go;
-  uint32_t* done;
-  uint32_t done_n;
-  uint32_t* next;
+  const uint64_t* qkv;
+  uint64_t* att;
+  uint32_t gen;                                    // the generation word as loaded at entry (launch_tag)
   uint32_t* err;
 };
+
+// The KV group's 320 tagged QKV words (q heads 8h .. 8h + 7, then K head h, then V head h; 32 words each) read by
+// the workgroup's threads (thread t: words t and 256 + t) into bf16 rows in LDS: [0, 512) the 8 q rows, [512, 576)
+// K's row, [576, 640) V's row.
+NA_DEVICE void tagged_group_rows(const uint64_t* qkv, int h, uint32_t gen, uint32_t* err, uint16_t* rows) {
+  const int t = threadIdx.x;
+  const int n = t + 256 < (kRep + 2) * 32 ? 2 : 1;
+  const uint64_t* src[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int k = min(t + 256 * i, (kRep + 2) * 32 - 1);
+    const int r = k >> 5, head = r < kRep ? h * kRep + r : r == kRep ? kNQ + h : kNQ + kNKV + h;
+    src[i] = qkv + head * 32 + (k & 31);
+  }
+  uint32_t w[2];
+  tag_read_at<2>(src, gen, w, err);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (i < n) {
+      const int k = t + 256 * i, r = k >> 5, d = k & 31;
+      rows[r * kHD + d] = (uint16_t)(w[i] & 0xffffu);
+      rows[r * kHD + 32 + d] = (uint16_t)(w[i] >> 16);
+    }
+  }
+}
 
 template <bool FUSED>
 NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
@@ -117,23 +141,29 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
     }
     if (FUSED && !waited) {
       // every load above reads keys older than the step (or is replaced below); now the step's own q, K and V
-      wait_go(hs.go, hs.err);
+      // (staged in the P rows' LDS, which the sub-chunk writes only after its next barrier)
+      uint16_t* rows = reinterpret_cast<uint16_t*>(L.p);
+      const uint32_t tg = launch_tag(hs.gen);
+      if (tid == 0) tag_wait1(hs.qkv + (kNQ + kNKV + h) * 32 + 31, tg, hs.err);
+      __syncthreads();
+      tagged_group_rows(hs.qkv, h, tg, hs.err, rows);
+      __syncthreads();
       waited = true;
-      if (n < kRep) {                              // q: read by nothing in the launch before (ordinary loads)
-        qa0 = *reinterpret_cast<const uint4*>(qrow + 8 * g);
-        qa1 = *reinterpret_cast<const uint4*>(qrow + 32 + 8 * g);
+      if (n < kRep) {
+        qa0 = *reinterpret_cast<const uint4*>(rows + n * kHD + 8 * g);
+        qa1 = *reinterpret_cast<const uint4*>(rows + n * kHD + 32 + 8 * g);
       }
+      // the step's row, where the QKV phase stored it in the cache (a position outside a linear cache is stored
+      // nowhere: the clamped row loaded above is what the cache holds)
+      if (ring > 0 || hi < cache_rows) {
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        if (kw + 16 * kb + n == hi) {
-          long long row = ring > 0 ? (long long)hi % ring : hi;
-          row = min(row, cache_rows - 1);
-          const uint16_t* kp = kbase + row * kHD + 8 * g;
-          const uint16_t* vp = vbase + row * kHD + 8 * g;
-          kr[kb][0] = load16_coherent(kp);
-          kr[kb][1] = load16_coherent(kp + 32);
-          vr[kb][0] = load16_coherent(vp);
-          vr[kb][1] = load16_coherent(vp + 32);
+        for (int kb = 0; kb < 4; ++kb) {
+          if (kw + 16 * kb + n == hi) {
+            kr[kb][0] = *reinterpret_cast<const uint4*>(rows + kRep * kHD + 8 * g);
+            kr[kb][1] = *reinterpret_cast<const uint4*>(rows + kRep * kHD + 32 + 8 * g);
+            vr[kb][0] = *reinterpret_cast<const uint4*>(rows + (kRep + 1) * kHD + 8 * g);
+            vr[kb][1] = *reinterpret_cast<const uint4*>(rows + (kRep + 1) * kHD + 32 + 8 * g);
+          }
         }
       }
     }
@@ -237,11 +267,15 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
         const float a = m_run[r] == kNegInf ? 0.f : expf(m_run[r] - m);
         const float S = expf(sink - m) + s_run[r] * a;   // the combine's formula, so one chunk == split at pos < 64
         const uint16_t o = f32_to_bf16((0.f + acc[r] * a) * (1.f / S));
-        if constexpr (FUSED) store_coherent(orow + (4 * g + r) * kHD + 16 * wave + n, o);
-        else orow[(4 * g + r) * kHD + 16 * wave + n] = o;
+        orow[(4 * g + r) * kHD + 16 * wave + n] = o;
+        if constexpr (FUSED) {                     // even lanes: (own, lane n + 1) = dims d, d + 1 of the row
+          const uint32_t nb = __builtin_bit_cast(uint32_t, dpp<0xB1>(__builtin_bit_cast(float, (uint32_t)o)));
+          if (!(n & 1))
+            tag_store(hs.att + bh * (kRep * kHD / 2) + ((4 * g + r) * kHD + 16 * wave + n) / 2,
+                      (uint32_t)o | (nb << 16), launch_tag(hs.gen));
+        }
       }
     }
-    if constexpr (FUSED) publish_done(hs.done, bh, hs.done_n, hs.next);
     return;
   }
   float* part = work + ((long long)bh * ns + c) * kPartFloats;
@@ -337,10 +371,9 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
   {
     const float inv = 1.f / S;
     const uint32_t o = (uint32_t)f32_to_bf16(o0 * inv) | ((uint32_t)f32_to_bf16(o1 * inv) << 16);
-    if constexpr (FUSED) store_coherent(reinterpret_cast<uint32_t*>(orow + i), o);
-    else *reinterpret_cast<uint32_t*>(orow + i) = o;
+    *reinterpret_cast<uint32_t*>(orow + i) = o;
+    if constexpr (FUSED) tag_store(hs.att + bh * (kRep * kHD / 2) + tid, o, launch_tag(hs.gen));
   }
-  if constexpr (FUSED) publish_done(hs.done, bh, hs.done_n, hs.next);
 }
 
 }  // namespace na

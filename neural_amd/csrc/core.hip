@@ -193,31 +193,26 @@ __global__ __launch_bounds__(256) void k_embed(const uint16_t* __restrict__ emb,
 }
 
 // Lines (kLine words) of the fused attention block's sync buffer (handoff.h): each counter and flag on its own line.
-constexpr int kSyncErr = 0, kSyncRouter = 1;
+// The attention block's sync buffer, in 256-byte lines: the error word; the generation number of the last completed
+// launch (each launch reads it at entry and tags its words with it + 1; the router's last workgroup stores that
+// number once every workgroup of the launch has read the old one); the split counters of the attention's chunks;
+// the tagged words (handoff.h) of the phases' results: QKV rows (word 32 r + d: dims d and d + 32 of row r = head,
+// 80 heads), the attention output (word i: elements 2i, 2i + 1), o_proj's mid (word i: rows 2i, 2i + 1) and the
+// router's logits (word e: the fp32 logit of expert e).
+constexpr int kSyncErr = 0, kSyncGen = 1;
 constexpr int kSyncSplit = 2;                                   // 8 lines: the attention's split counters
-constexpr int kSyncQkvCnt = 10, kSyncQkvGo = 18;               // 8 lines each: QKV counts and release per KV group
-constexpr int kSyncCnt = 26;                                    // 2 phases (attention, o_proj) x (top + kGo groups)
-constexpr int kSyncGo = kSyncCnt + 2 * (1 + kGo);               // 2 phases x kGo release flags (o_proj, router)
-constexpr int kSyncLines = kSyncGo + 2 * kGo;                   // 92 lines, 23,552 bytes
+constexpr int kTagQkv = 10;                                     // 2560 words, 80 lines
+constexpr int kTagAtt = kTagQkv + kQkvRows / 2 / 32;            // 2048 words, 64 lines
+constexpr int kTagMid = kTagAtt + kHq / 2 / 32;                 // 1440 words, 45 lines
+constexpr int kTagLogit = kTagMid + kH / 2 / 32;                // 128 words, 4 lines
+constexpr int kSyncLines = kTagLogit + kNE / 32;                // 203 lines, 51,968 bytes
 constexpr int kSyncWords = kSyncLines * kLine;
-NA_DEVICE constexpr int sync_qkv_cnt(int grp) { return (kSyncQkvCnt + grp) * kLine; }
-NA_DEVICE constexpr int sync_qkv_go(int grp) { return (kSyncQkvGo + grp) * kLine; }
-NA_DEVICE constexpr int sync_cnt(int phase) { return (kSyncCnt + phase * (1 + kGo)) * kLine; }
-NA_DEVICE constexpr int sync_go(int phase, int i) { return (kSyncGo + phase * kGo + i) * kLine; }
-
-// The router's last workgroup returns every release flag to zero (lanes of one wave): every waiter has passed its
-// wait by then (the router's counter is complete only after every router workgroup waited, the router's flags were
-// raised only after every o_proj workgroup finished, which each waited for the attention's, and so on).
-NA_DEVICE void sync_reset(uint32_t* sync, int lane) {
-  for (int i = lane; i < 8 + 2 * kGo; i += 64)
-    store_coherent(sync + (i < 8 ? sync_qkv_go(i) : sync_go((i - 8) / kGo, (i - 8) % kGo)), 0u);
-}
+NA_DEVICE uint64_t* sync_tags(uint32_t* sync, int line) { return reinterpret_cast<uint64_t*>(sync + line * kLine); }
 
 // QKV: ROWS = 256 / TPR rows per workgroup, grid 5120 / ROWS; workgroup (head, c) computes the rows of dims
 // d = c * ROWS/2 + (0 .. ROWS/2 - 1) (row groups 0 .. ROWS/2 - 1) and of their RoPE partners d + 32 (the other row
-// groups) of head `head` (0..63 q, 64..71 k, 72..79 v).  FUSED (the first phase of k_attn_block): q and the K / V
-// row at pos are written with coherent stores and the workgroup is counted in *done.  hc: kH bf16 of LDS, ys: ROWS
-// floats of LDS.
+// groups) of head `head` (0..63 q, 64..71 k, 72..79 v).  FUSED (the first phase of k_attn_block): each (d, d + 32)
+// pair is also written as tagged word 32 head + d (gen: the generation word as loaded at entry).  hc: kH bf16 of LDS, ys: ROWS floats of LDS.
 template <int TPR, bool FUSED>
 NA_DEVICE void qkv_body(int blk, uint16_t* hc, float* ys, const uint16_t* __restrict__ mid,
                         const uint16_t* __restrict__ g, const float* __restrict__ cext, uint16_t* __restrict__ xbuf,
@@ -225,7 +220,7 @@ NA_DEVICE void qkv_body(int blk, uint16_t* hc, float* ys, const uint16_t* __rest
                         const uint16_t* __restrict__ bias, const int64_t* __restrict__ pos_p,
                         const float* __restrict__ inv_freq, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
                         long long rows, int ring, uint16_t* __restrict__ qout, float eps, float att_scale,
-                        uint32_t* sync) {
+                        uint64_t* tags, uint32_t gen) {
   constexpr int ROWS = 256 / TPR, HALF = ROWS / 2, PER_HEAD = 64 / ROWS;
   const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
   const int head = blk / PER_HEAD, c = blk % PER_HEAD;
@@ -263,19 +258,12 @@ NA_DEVICE void qkv_body(int blk, uint16_t* hc, float* ys, const uint16_t* __rest
         dst = (head < 72 ? kc + (long long)(head - 64) * rows * 64 : vc + (long long)(head - 72) * rows * 64) +
               slot * 64;
     }
+    const uint16_t b1 = f32_to_bf16(o1), b2 = f32_to_bf16(o2);
     if (dst) {
-      if constexpr (FUSED) {
-        store_coherent(dst + dd, f32_to_bf16(o1));
-        store_coherent(dst + 32 + dd, f32_to_bf16(o2));
-      } else {
-        dst[dd] = f32_to_bf16(o1);
-        dst[32 + dd] = f32_to_bf16(o2);
-      }
+      dst[dd] = b1;
+      dst[32 + dd] = b2;
     }
-  }
-  if constexpr (FUSED) {                             // KV group of this head: its 8 q heads, its k and v heads
-    const int grp = head < 64 ? head / 8 : head < 72 ? head - 64 : head - 72;
-    publish_group(sync + sync_qkv_cnt(grp), 10 * PER_HEAD, sync + sync_qkv_go(grp));
+    if constexpr (FUSED) tag_store(tags + head * 32 + dd, (uint32_t)b1 | ((uint32_t)b2 << 16), launch_tag(gen));
   }
 }
 
@@ -290,19 +278,21 @@ __global__ __launch_bounds__(256) void k_qkv(const uint16_t* __restrict__ mid, c
   __shared__ __align__(16) uint16_t hc[kH];
   __shared__ float ys[256 / TPR];
   qkv_body<TPR, false>(blockIdx.x, hc, ys, mid, g, cext, xbuf, in_w, W, bias, pos_p, inv_freq, kc, vc, rows, ring,
-                       qout, eps, att_scale, nullptr);
+                       qout, eps, att_scale, nullptr, 0);
 }
 
 // o_proj + residual: 256 / TPR rows per workgroup: mid[n] = bf16(x[n] + bf16(att . Wo[n] + bo[n])), x = xbuf.
-// FUSED (the third phase of k_attn_block): the weight rows are loaded first, the workgroup then waits until
-// *ready >= ready_target (the attention output is complete), reads att with coherent loads, recomputes its rows of x
-// from mid, g and c (the residual the QKV phase normalised), and writes mid with coherent stores, counted in *done.
+// FUSED (the third phase of k_attn_block): the weight rows are loaded first, then threads 0..7 poll a tagged word of
+// each head's attention output (att_tags; gen: the generation word as loaded at entry), each thread reads its 8 words (16 of the 4096 elements), the
+// workgroup recomputes its rows of x from mid, g and c (the residual the QKV phase normalised), and writes mid, also
+// as tagged words (mid_tags: rows 2i, 2i + 1 in word i, from lanes 0 and 32 of each wave).
 template <int TPR, bool FUSED>
 NA_DEVICE void oproj_body(int blk, uint16_t* hc, const uint16_t* __restrict__ att, const uint16_t* __restrict__ Wo,
                           const uint16_t* __restrict__ bo, const uint16_t* __restrict__ xbuf,
                           const uint16_t* __restrict__ g, const float* __restrict__ cext, uint16_t* __restrict__ mid,
-                          const uint32_t* go, uint32_t* done, uint32_t done_n, uint32_t* next, uint32_t* err) {
+                          const uint64_t* att_tags, uint64_t* mid_tags, uint32_t gen, uint32_t* err) {
   constexpr int ROWS = 256 / TPR;
+  static_assert(!FUSED || TPR == 32, "tagged mid words pair the rows of lanes 0 and 32");
   const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
   const int row = ROWS * blk + r;
   VecIn<kHq> a;
@@ -324,17 +314,25 @@ NA_DEVICE void oproj_body(int blk, uint16_t* hc, const uint16_t* __restrict__ at
   float x = bf16_to_f32(xv);
   if constexpr (FUSED) {
     if (g) x = rb(x + rb(gx + (cext ? rb(cx) : 0.f)));
-    wait_go(go, err);
-    // ordinary loads: nothing in this launch reads att before its producers finish, and a kernel boundary leaves
-    // no stale copy in any L2, so the first read of a line on an XCD fetches the final bytes and later ones hit
-    a.load(att);
+    gen = launch_tag(gen);
+    // threads 0..7 poll the last word of each head's output, then every thread reads its 8 words (ordinary loads
+    // first: the L2 of the XCD serves all but its first o_proj workgroup)
+    if (tid < kNKV) tag_wait1(att_tags + (tid + 1) * (kHq / kNKV / 2) - 1, gen, err);
+    __syncthreads();
+    uint32_t w[8];
+    tag_read<8, true>(att_tags + 8 * tid, gen, w, err);
+    *reinterpret_cast<uint4*>(hc + 16 * tid) = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint4*>(hc + 16 * tid + 8) = make_uint4(w[4], w[5], w[6], w[7]);
+    __syncthreads();
+  } else {
+    a.store(hc);
   }
-  a.store(hc);
   const float s = rw.dot(hc, j);
   const uint16_t o = f32_to_bf16(x + rb(s + bf16_to_f32(bv)));
   if constexpr (FUSED) {
     if (j == 0) store_coherent(mid + row, o);
-    publish_done(done, blk, done_n, next);
+    const uint32_t o2 = (uint32_t)__builtin_amdgcn_readlane((int)o, 32);   // row 2 wave + 1
+    if ((tid & 63) == 0) tag_store(mid_tags + ROWS / 2 * blk + (tid >> 6), (uint32_t)o | (o2 << 16), gen);
   } else {
     if (j == 0) mid[row] = o;
   }
@@ -345,8 +343,7 @@ __global__ __launch_bounds__(256) void k_oproj(const uint16_t* __restrict__ att,
                                                const uint16_t* __restrict__ bo, const uint16_t* __restrict__ xbuf,
                                                uint16_t* __restrict__ mid) {
   __shared__ __align__(16) uint16_t hc[kHq];
-  oproj_body<TPR, false>(blockIdx.x, hc, att, Wo, bo, xbuf, nullptr, nullptr, mid, nullptr, nullptr, 0, nullptr,
-                         nullptr);
+  oproj_body<TPR, false>(blockIdx.x, hc, att, Wo, bo, xbuf, nullptr, nullptr, mid, nullptr, nullptr, 0, nullptr);
 }
 
 // post-attention RMSNorm + router + top-4: 256 / TPR experts per workgroup, grid 128 / (256 / TPR).  Workgroup 0 writes hn (the experts' input);
@@ -405,15 +402,18 @@ NA_DEVICE void top4_softmax(float v0, float v1, int lane, int64_t* __restrict__ 
 }
 
 // Router phase: NR = 128 / (256 / TPR) workgroups; workgroup `blk` computes 256 / TPR logits.  FUSED (the last phase
-// of k_attn_block): the weights and the norm weight are loaded first, then the workgroup waits until
-// *ready >= ready_target (o_proj has written mid) and reads mid with coherent loads; the workgroup that selects the
-// top 4 also returns the launch's phase counters (reset, 3 words) to zero: every waiter has passed by then.
+// of k_attn_block): the weights and the norm weight are loaded first, then thread 0 polls one tagged word of mid
+// (mid_tags; gen: the generation word as loaded at entry) and every thread reads its 8 words; the logits are also written as tagged words
+// (logit_tags), and the last workgroup (blk = NR - 1) reads all 128 of them, selects the top 4 and stores gen into
+// *gen_word: every workgroup of the launch has read the old number by then (each one's result is an input of the
+// router's logits, and each read the number before it produced anything).
 template <int TPR, bool FUSED>
 NA_DEVICE void router_body(int blk, int nr, uint16_t* hc, uint32_t& last, const uint16_t* __restrict__ mid,
                            const uint16_t* __restrict__ post_w, float eps, const uint16_t* __restrict__ Wr,
                            const uint16_t* __restrict__ br, uint16_t* __restrict__ hn, float* __restrict__ logits,
                            uint32_t* __restrict__ counter, int64_t* __restrict__ ids, uint16_t* __restrict__ wts,
-                           const uint32_t* go, uint32_t* sync, uint32_t* err) {
+                           const uint64_t* mid_tags, uint64_t* logit_tags, uint32_t* gen_word, uint32_t gen,
+                           uint32_t* err) {
   constexpr int ROWS = 256 / TPR;
   const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
   const int e = ROWS * blk + r;
@@ -430,15 +430,36 @@ NA_DEVICE void router_body(int blk, int nr, uint16_t* hc, uint32_t& last, const 
   rw.load(Wr + (long long)e * kH, j);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (FUSED) {
-    wait_go(go, err);
+    gen = launch_tag(gen);
+    if (tid == 0) tag_wait1(mid_tags + (kH / 2 - 1) - (kH / 2 / 32) * blk, gen, err);   // a word per workgroup
+    __syncthreads();
+    const uint64_t* src[8];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) ni.m[i] = load16_coherent(mid + 8 * min(tid + 256 * i, kH / 8 - 1));
+    for (int k = 0; k < 8; ++k) src[k] = mid_tags + 4 * min(tid + 256 * (k >> 2), kH / 8 - 1) + (k & 3);
+    uint32_t w[8];
+    tag_read_at<8>(src, gen, w, err);
+    ni.m[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    ni.m[1] = make_uint4(w[4], w[5], w[6], w[7]);
   }
   norm_finish(ni, false, false, eps, hc, nullptr);
   if (blk == 0)
     for (int i = tid; i < kH / 8; i += 256)
       *reinterpret_cast<uint4*>(hn + 8 * i) = *reinterpret_cast<const uint4*>(hc + 8 * i);
   const float s = rw.dot(hc, j);
+  if constexpr (FUSED) {
+    const float v = rb(s + bf16_to_f32(bv));
+    if (j == 0) {
+      logits[e] = v;
+      tag_store(logit_tags + e, __float_as_uint(v), gen);
+    }
+    if (blk != nr - 1 || tid >= 64) return;
+    const uint64_t* src[2] = {logit_tags + tid, logit_tags + tid + 64};
+    uint32_t l[2];
+    tag_read_at<2>(src, gen, l, err);
+    top4_softmax(__uint_as_float(l[0]), __uint_as_float(l[1]), tid, ids, wts);
+    if (tid == 0) store_coherent(gen_word, gen);
+    return;
+  }
   if (j == 0) __hip_atomic_store(logits + e, rb(s + bf16_to_f32(bv)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -448,7 +469,6 @@ NA_DEVICE void router_body(int blk, int nr, uint16_t* hc, uint32_t& last, const 
   }
   __syncthreads();
   if (!last || tid >= 64) return;
-  if constexpr (FUSED) sync_reset(sync, tid);
   top4_softmax(__hip_atomic_load(logits + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
                __hip_atomic_load(logits + tid + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), tid, ids, wts);
 }
@@ -462,7 +482,7 @@ __global__ __launch_bounds__(256) void k_router_norm(const uint16_t* __restrict_
   __shared__ __align__(16) uint16_t hc[kH];
   __shared__ uint32_t last;
   router_body<TPR, false>(blockIdx.x, gridDim.x, hc, last, mid, post_w, eps, Wr, br, hn, logits, counter, ids, wts,
-                          nullptr, nullptr, nullptr);
+                          nullptr, nullptr, nullptr, 0, nullptr);
 }
 
 // Tail 1: x = bf16(mid + bf16(g + bf16(c))); hn = bf16(w * (x * r)) (one workgroup).
@@ -772,11 +792,13 @@ __global__ __launch_bounds__(256) void k_route_pack(const uint16_t* __restrict__
 
 
 // ---------------------------------------------------------------- the attention block of a decode layer, one launch
-// Phases by workgroup id (see handoff.h): [QKV: 640][attention: 8 ns][o_proj: 720][router: 32].  Each phase issues
-// its own loads first (weights, the older keys of the cache) and then waits for what it needs: the attention of KV
-// head h for the 80 QKV workgroups of its group (query heads 8h .. 8h + 7, K and V head h: q and the step's K / V
-// row), o_proj for the 8 attention heads, the router for every o_proj row.  sync: kSyncWords uint32 (the layout above), zero before the first launch and left zero except the error
-// flag (line kSyncErr), which a wait that gave up raises and nothing clears.
+// Phases by workgroup id (see handoff.h): [QKV: 640][attention: 8 ns][o_proj: 360][router: 32].  Each phase issues
+// its own loads first (weights, the older keys of the cache) and then waits for what it needs, reading the earlier
+// phases' results as tagged words: the attention of KV head h the 80 QKV rows of its group (query heads 8h .. 8h + 7,
+// K and V head h: q and the step's K / V row), o_proj the 8 attention heads' output, the router every o_proj row,
+// the router's last workgroup every logit.  sync: kSyncWords uint32 (the layout above), zero before the first launch;
+// a launch leaves the split counters zero, the generation word advanced by one and the error word (line kSyncErr)
+// as it was unless a wait gave up, which raises it (nothing clears it).
 constexpr int kBlkQkv = kQkvRows / (256 / kQkvTpr);
 constexpr int kBlkOproj = kH / (256 / kOprojTpr);
 constexpr int kBlkRouter = kNE / (256 / kRouterTpr);
@@ -829,32 +851,32 @@ __global__ __launch_bounds__(256, 4) void k_attn_block(AttnBlockArgs a) {
   __shared__ AttnBlockLds L;
   uint32_t* sync = a.sync;
   uint32_t* err = sync + kSyncErr * kLine;
+  const uint32_t gen = load_coherent(sync + kSyncGen * kLine);   // raw: each phase forms its tag where it needs it
   int blk = blockIdx.x;
-  if (blk < kBlkQkv) {                                  // QKV -> the release of its KV group
+  if (blk < kBlkQkv) {                                  // QKV -> tagged q, K, V rows
     qkv_body<kQkvTpr, true>(blk, L.core.hc, L.core.ys, a.mid, a.g, a.c, a.xbuf, a.in_w, a.Wqkv, a.bqkv, a.pos,
-                            a.inv_freq, a.kc, a.vc, a.cache_rows, a.ring, a.q, a.eps, a.att_scale, sync);
+                            a.inv_freq, a.kc, a.vc, a.cache_rows, a.ring, a.q, a.eps, a.att_scale,
+                            sync_tags(sync, kTagQkv), gen);
     return;
   }
   blk -= kBlkQkv;
   const int natt = kNKV * a.ns;
-  if (blk < natt) {                                     // attention (one count per head) -> o_proj's flags
+  if (blk < natt) {                                     // attention (chunks counted per head) -> tagged att
     decode_attn_body<true>(L.attn, blk, a.q, a.kc, a.vc, a.cache_rows, a.sinks, a.pos, a.att, a.scaling, a.window,
                            a.ring, a.ns, a.work, sync + kSyncSplit * kLine,
-                           AttnHandoff{sync + sync_qkv_go((blk / a.ns) % kNKV), sync + sync_cnt(0), (uint32_t)kNKV,
-                                       sync + sync_go(0, 0), err});
+                           AttnHandoff{sync_tags(sync, kTagQkv), sync_tags(sync, kTagAtt), gen, err});
     return;
   }
   blk -= natt;
-  if (blk < kBlkOproj) {                                // o_proj -> the router's flags
-    oproj_body<kOprojTpr, true>(blk, L.core.hc, a.att, a.Wo, a.bo, nullptr, a.g, a.c, a.mid,
-                                sync + sync_go(0, blk % kGo), sync + sync_cnt(1), (uint32_t)kBlkOproj,
-                                sync + sync_go(1, 0), err);
+  if (blk < kBlkOproj) {                                // o_proj -> tagged mid
+    oproj_body<kOprojTpr, true>(blk, L.core.hc, a.att, a.Wo, a.bo, nullptr, a.g, a.c, a.mid, sync_tags(sync, kTagAtt),
+                                sync_tags(sync, kTagMid), gen, err);
     return;
   }
   blk -= kBlkOproj;
   router_body<kRouterTpr, true>(blk, kBlkRouter, L.core.hc, L.core.last, a.mid, a.post_w, a.eps, a.Wr, a.br, a.hn,
-                                a.logits, sync + kSyncRouter * kLine, a.ids, a.wts, sync + sync_go(1, blk % kGo), sync,
-                                err);
+                                a.logits, nullptr, a.ids, a.wts, sync_tags(sync, kTagMid), sync_tags(sync, kTagLogit),
+                                sync + kSyncGen * kLine, gen, err);
 }
 }  // namespace na
 

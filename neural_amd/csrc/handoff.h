@@ -3,23 +3,21 @@
 //
 // * Data crosses workgroups (and XCDs, whose L2 caches are not coherent with each other for ordinary device
 //   memory) through agent-scope relaxed atomic stores, which gfx950 issues with the sc1 bit (written through to the
-//   coherent point).  A consumer reads with agent-scope atomic loads (sc1) what the launch read before the handoff
-//   (an L2 could hold the old bytes), and with ordinary loads what nothing in the launch read before: a kernel
-//   boundary leaves no stale line in any L2, so an XCD's first read fetches the final bytes and the L2 serves the
-//   rest.
-// * Completion: after its stores are acknowledged (s_waitcnt 0) and the workgroup's waves meet at a barrier, one
-//   thread counts the workgroup (two-level counters, publish_done); the workgroup that completes the count raises
-//   the phase's release flags, kGo words on separate 256-byte lines; a consumer polls the flag of its group (thread
-//   0, a short sleep between reads), then the workgroup meets at a barrier.  Hundreds of consumers polling one word,
-//   or hundreds of producers incrementing one, would queue every access to that line; spread over kGo lines they
-//   do not.
+//   coherent point), and agent-scope loads (sc1).  A kernel boundary leaves no stale line in any L2, so what nothing
+//   in the launch read before can also be read with ordinary loads once it is complete.
+// * Tagged words (the attention block, core.hip): each 64-bit word holds a 32-bit payload and the launch's
+//   generation number, written by one store; the consumer polls the words it needs until they carry its number.
+//   No acknowledgement, count or flag stands between the producer's store and the consumer's read.
+// * Counters and flags (the single-launch expert body, tiles.hip): after its stores are acknowledged (s_waitcnt 0)
+//   a workgroup counts itself in two levels (kGo group counters, then a top counter, so no counter takes more than
+//   a few dozen increments); the one that completes the count raises kGo release flags on separate 256-byte lines,
+//   which consumers poll (thread 0, a short sleep between reads).  Hundreds of workgroups polling one word, or
+//   incrementing one, would queue every access to that line; spread over kGo lines they do not.
 // * Progress: the hardware dispatches a grid's workgroups in increasing id order on each XCD, so every producer
 //   has been dispatched before any consumer that waits for it, and producers never wait for consumers: every wait
-//   ends.  The wait is bounded anyway: after kSpinLimit polls the workgroup raises an error flag the host can read
-//   and goes on with whatever the buffers hold, so a broken assumption shows up as a flagged wrong result, never as
-//   a hung GPU.
-// * Counters return themselves to zero; the flags are returned to zero inside the launch by the phase that knows
-//   every waiter has passed (see the kernels), so a launch starts from zeros and leaves zeros.
+//   ends.  The waits are bounded anyway: after kSpinLimit polls the workgroup raises an error flag the host can
+//   read and goes on with whatever the buffers hold, so a broken assumption shows up as a flagged wrong result,
+//   never as a hung GPU.
 #pragma once
 #include "common.h"
 
@@ -46,64 +44,74 @@ NA_DEVICE float2 load8_coherent(const float* p) {
 NA_DEVICE float loadf_coherent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// 16 bytes as four coherent dword loads (p 4-byte aligned).
-NA_DEVICE uint4 load16_coherent(const void* p) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(p);
-  return make_uint4(load_coherent(w), load_coherent(w + 1), load_coherent(w + 2), load_coherent(w + 3));
+// ---- tagged words: a 64-bit word holds a 32-bit payload (low half) and the generation number of the launch that
+// wrote it (high half), written by one 64-bit device-coherent store and read by one 64-bit device-coherent load, so
+// a reader that sees its launch's number sees that launch's payload.  Every word of a tagged area is written once
+// per launch; a launch's number differs from the previous launch's (it is advanced by one per launch), so the area
+// needs no clearing and the producer no acknowledgement, count or flag: the consumer polls the data itself.
+NA_DEVICE void tag_store(uint64_t* p, uint32_t payload, uint32_t gen) {
+  __hip_atomic_store(p, ((uint64_t)gen << 32) | payload, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+NA_DEVICE uint64_t tag_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+NA_DEVICE bool tag_is(uint64_t w, uint32_t gen) { return (uint32_t)(w >> 32) == gen; }
+// A launch's number from the generation word as loaded at entry (raw + 1).  Call it where the number is first needed:
+// the empty asm keeps the compiler from moving the addition, and with it the wait for that load, to the kernel's
+// start, ahead of the loads a phase issues first.
+NA_DEVICE uint32_t launch_tag(uint32_t raw) {
+  asm volatile("" : "+v"(raw));
+  return raw + 1u;
 }
 
-// Every thread of the workgroup calls it after its last coherent store of the phase (workgroup `blk` of the phase's
-// n).  Counting is two-level: workgroup blk counts in group counter cnt[(1 + blk % kGo) * kLine], and the workgroup
-// that completes its group counts in the top counter cnt[0]; the one that completes the top (min(n, kGo) groups)
-// raises the kGo release flags go[i * kLine].  Hundreds of increments of one word would queue behind each other for
-// microseconds; each counter here takes at most ceil(n / kGo).  A counter's last arrival returns it to zero: nobody
-// waits on a counter, consumers wait on the flags.
-NA_DEVICE void publish_done(uint32_t* cnt, int blk, uint32_t n, uint32_t* go) {
-  __shared__ uint32_t completes;
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t gi = (uint32_t)blk % kGo;
-    const uint32_t quota = (n - gi + kGo - 1) / kGo;
-    const uint32_t groups = n < (uint32_t)kGo ? n : (uint32_t)kGo;
-    uint32_t* gc = cnt + (1 + gi) * kLine;
-    bool top = false;
-    if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == quota - 1) {
-      __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      top = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1;
-      if (top) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// One thread: poll *p (a short sleep between reads) until it carries gen, or raise *err after kSpinLimit polls.
+NA_DEVICE void tag_wait1(const uint64_t* p, uint32_t gen, uint32_t* err) {
+  uint32_t polls = 0;
+  while (!tag_is(tag_load(p), gen)) {
+    if (++polls > kSpinLimit) {
+      __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
     }
-    completes = top;
-  }
-  __syncthreads();
-  if (completes && threadIdx.x < kGo) store_coherent(go + threadIdx.x * kLine, 1u);
-}
-
-// A release by group: every thread of the workgroup calls it after its last coherent store; the workgroup that
-// completes the group's n counts in *cnt returns the counter to zero and raises the one flag *go.
-NA_DEVICE void publish_group(uint32_t* cnt, uint32_t n, uint32_t* go) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0 && __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n - 1) {
-    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    store_coherent(go, 1u);
+    __builtin_amdgcn_s_sleep(2);
   }
 }
 
-// Every thread of the workgroup calls it; returns when the release flag *go is raised (or the poll limit raised
-// *err).
-NA_DEVICE void wait_go(const uint32_t* go, uint32_t* err) {
-  if (threadIdx.x == 0) {
-    uint32_t polls = 0;
-    while (load_coherent(go) == 0) {
-      if (++polls > kSpinLimit) {
-        __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
+// The payloads of the N words *p[0] .. *p[N - 1]: all loaded at once, then the ones not yet carrying gen polled
+// again with device-coherent loads (bounded as above).  CACHED: the first loads are ordinary ones (64-bit, so still
+// single-copy atomic), which an XCD's L2 serves once one of its workgroups has fetched the line: for words that
+// many workgroups read.  A line fetched before all its words were written holds older tags, so those words are
+// polled again device-coherently: a stale copy costs a round trip, never a wrong payload.
+template <int N, bool CACHED = false>
+NA_DEVICE void tag_read_at(const uint64_t* const (&p)[N], uint32_t gen, uint32_t (&out)[N], uint32_t* err) {
+  uint64_t w[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k)
+    w[k] = CACHED ? __hip_atomic_load(p[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) : tag_load(p[k]);
+  uint32_t polls = 0;
+  for (;;) {
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < N; ++k) ok = ok && tag_is(w[k], gen);
+    if (ok) break;
+    if (++polls > kSpinLimit) {
+      __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
     }
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+      if (!tag_is(w[k], gen)) w[k] = tag_load(p[k]);
   }
-  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < N; ++k) out[k] = (uint32_t)w[k];
+}
+// ... of the N consecutive words p[0 .. N - 1].
+template <int N, bool CACHED = false>
+NA_DEVICE void tag_read(const uint64_t* p, uint32_t gen, uint32_t (&out)[N], uint32_t* err) {
+  const uint64_t* q[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) q[k] = p + k;
+  tag_read_at<N, CACHED>(q, gen, out, err);
 }
 
 }  // namespace na

@@ -851,7 +851,7 @@ NA_DEVICE uint32_t* one_block_counter(uint32_t* sync, int b) {
 }
 
 // Wave 0 of workgroup blk after its last h store (the other waves stored nothing): its stores acknowledged, lane 0
-// counts the workgroup two-level (handoff.h publish_done's counters); the wave that completes the count raises the
+// counts the workgroup two-level (kGo group counters, then the top one); the wave that completes the count raises the
 // kGo flags and the generation word to gen.  Only thread 0 read the generation word, before this count, so every
 // workgroup has read it before it advances.
 NA_DEVICE void one_publish(uint32_t* sync, int blk, uint32_t gen) {

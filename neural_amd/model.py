@@ -186,7 +186,7 @@ class DecodeModel:
         self.attn_work = z(max(N.lib().na_attn_workspace_floats(1, ns_max), 1), dt=torch.float32)
         self.attn_counters = z(NKV, dt=torch.int32)
         self.fused_attn = bool(fused_attn)
-        self.sync = z(N.lib().na_core_attn_block_sync_words(), dt=torch.int32)   # fused block's counters and flags
+        self.sync = z(N.lib().na_core_attn_block_sync_words(), dt=torch.int32)   # fused block's handoff state
         self.graph = None
 
     def _check_weights(self):
