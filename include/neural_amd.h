@@ -125,17 +125,18 @@ int na_moe_decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
                        const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha, float limit,
                        int k_split, int down_mode, void* const* events, hipStream_t stream);
 
-/* Words (uint32) of the sync buffer na_moe_decode_t950_one needs (32,000 bytes). */
+/* Words (uint32) of the sync buffer na_moe_decode_t950_one needs (95,488 bytes). */
 long long na_moe_one_sync_words(void);
 
 /* The expert body of one token (B = 1) over a t950 pool in a single launch: the same contract and the same bits as
  * na_moe_decode_t950 (server.py:508-518, b_body; seam neural/moe/gptoss_adapter.py:267-284), out required.  720
- * workgroups each run one (expert, 16-row block) of gate_up, publish their h (device-coherent stores, counted), load
- * the matching down row block, wait for every workgroup's h, run the down block, and the last of each output block's
- * four workgroups sums the top-k.  h_scratch and yw_scratch hold 4 x 5,760 bytes each.  sync: na_moe_one_sync_words
- * uint32, zero before the first call, owned by one stream (calls that overlap on one sync buffer race); word 0 (a
- * wait that gave up) stays set once raised.  Returns -4 where the device cannot hold the 720 workgroups at once.
- * events: NULL or 2 recorded events (the launch's start and stop). */
+ * workgroups each run one (expert, 16-row block) of gate_up and write their h as tagged words (a 32-bit payload and
+ * the launch's number per 64-bit word), load the matching down row block, read their expert's h row once it carries
+ * the launch's number, run the down block and write its weighted outputs the same way; one workgroup of each output
+ * block sums the top-k.  h_scratch and yw_scratch are not used (NULL allowed): h and the weighted outputs live in
+ * sync.  sync: na_moe_one_sync_words uint32, zero before the first call, owned by one stream (calls that overlap on
+ * one sync buffer race); word 0 (a wait that gave up) stays set once raised.  Returns -4 where the device cannot hold
+ * the 720 workgroups at once.  events: NULL or 2 recorded events (the launch's start and stop). */
 int na_moe_decode_t950_one(const void* x, const int64_t* topk_ids, const void* topk_w, const void* pool,
                            long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
                            const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha,

@@ -257,23 +257,44 @@ NA_DEVICE void h8_codes(uint16_t hv, uint32_t sh, uint32_t sl, uint8_t& hi, uint
   lo = (uint8_t)(__builtin_bit_cast(uint32_t, o2) & 0xff);
 }
 
-// h of D column n = lane % 16 (output row 16b + n) of `pair` -> its hi and lo bytes (a byte store each).  COH: the
-// stores are device-coherent (written through to the coherent point), for a reader in the same launch on another XCD.
-template <bool COH = false>
+// h of D column n = lane % 16 (output row 16b + n) of `pair` -> its hi and lo bytes (a byte store each).
 NA_DEVICE void store_h8(uint8_t* h8, int pair, int b, uint16_t hv, uint32_t sh, uint32_t sl, bool ok) {
   uint8_t hi, lo;
   h8_codes(hv, sh, sl, hi, lo);
   uint8_t* row = h8 + (long long)pair * kH8Row + 16 * b + (threadIdx.x & 15);
   if (ok) {
-    if constexpr (COH) {
-      __hip_atomic_store(row, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(row + kI, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      row[0] = hi;
-      row[kI] = lo;
-    }
+    row[0] = hi;
+    row[kI] = lo;
   }
 }
+
+// ---- the single-launch expert body's handoffs as tagged words (handoff.h): h of pair p, row block b in the 8 words
+// (p x 180 + b) x 8 + k (k < 4: hi codes 16b + 4k .. 16b + 4k + 3, k >= 4: lo codes 16b + 4(k - 4) ..; byte i of the
+// payload = code i), the weighted output yw of pair p, block b in the 8 words (p x 180 + b) x 8 + k (outputs 16b + 2k,
+// 16b + 2k + 1).  raw: the workgroup's launch count as thread 0 read it (other threads: 0), from which one_tag forms
+// the launch's number (the kernel's comment below); err: the error word a wait that gives up raises.
+constexpr int kOneWgs = 4 * kTDownBlocks;       // 720 workgroups
+struct OneTags {
+  uint64_t* h;
+  uint64_t* y;
+  uint32_t raw;
+  uint32_t* err;
+};
+// What the single-launch body loads at entry, before its routing ids arrive (batch 1): the token's x (pieces of
+// k_moe_gate_up_t950<4, 1>'s x_load) and the expert's pool slot, picked from the layer's 128 slot-table entries
+// (-1: no slot table, slot = the global id).
+struct OnePre {
+  XRegs<1, 256> x;
+  long long slot;
+};
+
+// The launch's number, in every lane of wave 0 (call it where lane 0 is active).  The empty asm keeps the division,
+// and so the wait for the entry count, at the point of use.
+NA_DEVICE uint32_t one_tag(const OneTags& tg) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)launch_tag(tg.raw));
+}
+NA_DEVICE uint64_t* one_h_words(const OneTags& tg, int pair, int b) { return tg.h + ((long long)pair * kTDownBlocks + b) * 8; }
+NA_DEVICE uint64_t* one_y_words(const OneTags& tg, int pair, int b) { return tg.y + ((long long)pair * kTDownBlocks + b) * 8; }
 
 // The pairs' h8 rows of up to XT staged tokens through registers: piece p = tid + NTH k < nt x 360; piece q = p % 360
 // of token t = p / 360 is bytes 16 (q % 180) .. of its hi (q < 180) or lo row.
@@ -286,16 +307,13 @@ NA_DEVICE uint4 load16_sc1(const void* base, uint32_t off) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-template <int XT, int NTH, typename PairOf, bool COH = false>
+template <int XT, int NTH, typename PairOf>
 NA_DEVICE void h8_load(int tid, const uint8_t* h8, PairOf pair_of, int nt, XRegs<XT, NTH>& xr) {
 #pragma unroll
   for (int k = 0; k < XRegs<XT, NTH>::XP; ++k) {
     const int p = tid + NTH * k;
     const int t = p / kH8Pieces, q = p - t * kH8Pieces;
-    if (p < nt * kH8Pieces) {
-      const uint32_t off = (uint32_t)pair_of(t) * kH8Row + 16 * q;
-      xr.v[k] = COH ? load16_sc1(h8, off) : load16(h8 + off);
-    }
+    if (p < nt * kH8Pieces) xr.v[k] = load16(h8 + (long long)pair_of(t) * kH8Row + 16 * q);
   }
 }
 
@@ -377,15 +395,16 @@ NA_DEVICE void token_sums(const f32x4_t& acc, float& y0, float& y1) {
 
 // Store the bf16 values v held as D columns n = lane % 16 (16 lanes per D row) as 32-bit pairs: even lanes write
 // (v[n], v[n + 1]) to row_ptr + n.  All lanes must call it (it exchanges values between neighbouring lanes).
-template <bool COH = false>
 NA_DEVICE void store_row_pairs(uint16_t* row_ptr, uint16_t v, bool ok) {
   const int lane = threadIdx.x & 63;
   const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
-  if (ok && !(lane & 1)) {
-    uint32_t* d = reinterpret_cast<uint32_t*>(row_ptr + (lane & 15));
-    if constexpr (COH) store_coherent(d, (uint32_t)v | (hi << 16));
-    else *d = (uint32_t)v | (hi << 16);
-  }
+  if (ok && !(lane & 1)) *reinterpret_cast<uint32_t*>(row_ptr + (lane & 15)) = (uint32_t)v | (hi << 16);
+}
+// ... as tagged words: even lanes write (v[n], v[n + 1]) as word n / 2 of w.
+NA_DEVICE void tag_row_pairs(uint64_t* w, uint16_t v, bool ok, uint32_t tag) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
+  if (ok && !(lane & 1)) tag_store(w + ((lane & 15) >> 1), (uint32_t)v | (hi << 16), tag);
 }
 
 // The id of this lane's pair (lanes past the pairs re-read the last one): the first read of a decode kernel, issued
@@ -451,7 +470,6 @@ NA_DEVICE int pair_at(uint64_t users, int u) {
 // The duplicate pairs' h: for token u = 2 (lane / 16) + e < nt (user pair p), the same value v[e] also goes to every
 // other pair of p's token that `all` routes to the expert (columns 16b .. 16b + 15).  Kept out of line of the common
 // path, which stores only the users' rows.
-template <bool COH>
 __device__ __noinline__ void dup_rows_store_h8(uint8_t* h8, uint64_t users, uint64_t all, int nt, int b, uint16_t v0,
                                                uint16_t v1, uint32_t sh, uint32_t sl) {
   const int lane = threadIdx.x & 63;
@@ -461,14 +479,15 @@ __device__ __noinline__ void dup_rows_store_h8(uint8_t* h8, uint64_t users, uint
     const int u = 2 * (lane >> 4) + e;
     const int p = pair_at(users, min(u, nt - 1));
     const uint32_t dm = token_dups(all, p) & ~(1u << (p & 3));
-    for (int k = 0; k < 4; ++k) store_h8<COH>(h8, (p & ~3) + k, b, v[e], sh, sl, u < nt && ((dm >> k) & 1));
+    for (int k = 0; k < 4; ++k) store_h8(h8, (p & ~3) + k, b, v[e], sh, sl, u < nt && ((dm >> k) & 1));
   }
 }
 
-// As dup_rows_store for the down outputs: pair q gets bf16(y[e] x w[q]) with its own routing weight.
-template <bool COH>
+// As dup_rows_store for the down outputs: pair q gets bf16(y[e] x w[q]) with its own routing weight (TAG: as tagged
+// words of tg, in place of yw).
+template <bool TAG>
 __device__ __noinline__ void dup_rows_store_w(uint16_t* yw, uint64_t users, uint64_t all, int nt, int b, float y0,
-                                              float y1, const uint16_t* wts) {
+                                              float y1, const uint16_t* wts, OneTags tg, uint32_t tag) {
   const int lane = threadIdx.x & 63;
   const float y[2] = {y0, y1};
 #pragma unroll
@@ -478,8 +497,9 @@ __device__ __noinline__ void dup_rows_store_w(uint16_t* yw, uint64_t users, uint
     const uint32_t dm = token_dups(all, p) & ~(1u << (p & 3));
     for (int k = 0; k < 4; ++k) {
       const int q = (p & ~3) + k;
-      store_row_pairs<COH>(yw + (long long)q * kH + 16 * b, f32_to_bf16(y[e] * bf16_to_f32(wts[q])),
-                           u < nt && ((dm >> k) & 1));
+      const uint16_t v = f32_to_bf16(y[e] * bf16_to_f32(wts[q]));
+      if constexpr (TAG) tag_row_pairs(one_y_words(tg, q, b), v, u < nt && ((dm >> k) & 1), tag);
+      else store_row_pairs(yw + (long long)q * kH + 16 * b, v, u < nt && ((dm >> k) & 1));
     }
   }
 }
@@ -515,13 +535,15 @@ struct DecodeLds {
 // barrier -> one MFMA per tile (each waits only for its own codes) -> fixed-order sum of the KS partial sums through
 // LDS -> epilogue in wave 0, which reads nothing from global memory.
 // The body of workgroup (item, b); every wave returns from it (waves past the first right after the K reduction).
-// COH: h is stored device-coherently (the single-launch expert body reads it in the same launch).
-template <int KS, int XT, bool COH>
+// TAG (the single-launch expert body, batch 1): h is written as tagged words of tg (the users' rows only: down reads
+// an expert's first user's row), not to h8.
+template <int KS, int XT, bool TAG>
 NA_DEVICE void gate_up_body(DecodeLds<KS, XT>& L, int item, int b, long long rid, int B,
                             const uint8_t* __restrict__ pool, long long slot_bytes,
                             const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ x,
                             const uint16_t* __restrict__ bias_gu, uint8_t* __restrict__ h8, float alpha, float limit,
-                            uint32_t h8_sc) {
+                            uint32_t h8_sc, const OneTags& tg = OneTags{}, const OnePre* pre = nullptr) {
+  static_assert(!TAG || XT == 1, "tagged h: one token");
   constexpr int MT = (kTTiles + KS - 1) / KS;
   constexpr int NTH = 64 * KS;
   int nt, distinct, valid;
@@ -530,7 +552,7 @@ NA_DEVICE void gate_up_body(DecodeLds<KS, XT>& L, int item, int b, long long rid
   if (e < 0 || e == 128) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const long long gid = expert_base + e;
-  const long long slot = slot_tab ? slot_tab[gid] : gid;
+  const long long slot = TAG ? (pre->slot >= 0 ? pre->slot : gid) : slot_tab ? slot_tab[gid] : gid;
   const uint8_t* gblk = pool + slot * slot_bytes + (long long)b * kTBlock;
   const uint8_t* ublk = gblk + (long long)kTUpBlock0 * kTBlock;
   int t0, t1;
@@ -538,7 +560,8 @@ NA_DEVICE void gate_up_body(DecodeLds<KS, XT>& L, int item, int b, long long rid
   ScaleRegs<2, NTH> sr;
   scale_load<2, NTH>(tid, gblk, ublk, sr);
   XRegs<XT, NTH> xr;
-  x_load<XT, NTH>(tid, x, kH, [users](int t) { return pair_at(users, t) >> 2; }, nt, xr);
+  if constexpr (TAG) xr = pre->x;                      // batch 1: token 0's row, loaded at the kernel's entry
+  else x_load<XT, NTH>(tid, x, kH, [users](int t) { return pair_at(users, t) >> 2; }, nt, xr);
   const int j = 16 * b + (lane & 15);
   const uint16_t* bg = bias_gu ? bias_gu + gid * kGU : nullptr;
   // epilogue operands are loaded now and converted at their use, so no wait is placed before the barrier
@@ -600,9 +623,24 @@ NA_DEVICE void gate_up_body(DecodeLds<KS, XT>& L, int item, int b, long long rid
       ub = rb(ub + bf16_to_f32(buj));
     }
     hv[q] = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
-    store_h8<COH>(h8, pair_at(users, min(u, nt - 1)), b, hv[q], h8_sc & 0xff, h8_sc >> 8, u < nt);
+    if constexpr (!TAG) store_h8(h8, pair_at(users, min(u, nt - 1)), b, hv[q], h8_sc & 0xff, h8_sc >> 8, u < nt);
   }
-  if (all != users) dup_rows_store_h8<COH>(h8, users, all, nt, b, hv[0], hv[1], h8_sc & 0xff, h8_sc >> 8);   // rare
+  if constexpr (TAG) {
+    // lanes 0..15 hold the token's 16 values; lane k < 8 gathers the codes of word k (hi for k < 4, lo above)
+    uint8_t hi, lo;
+    h8_codes(hv[0], h8_sc & 0xff, h8_sc >> 8, hi, lo);
+    const int src = 4 * (lane & 3);
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t hb = (uint32_t)__shfl((int)hi, src + i), lb = (uint32_t)__shfl((int)lo, src + i);
+      w |= ((lane < 4 ? hb : lb) & 0xffu) << (8 * i);
+    }
+    const uint32_t tag = one_tag(tg);
+    if (lane < 8) tag_store(one_h_words(tg, pair_at(users, 0), b) + lane, w, tag);
+  } else if (all != users) {
+    dup_rows_store_h8(h8, users, all, nt, b, hv[0], hv[1], h8_sc & 0xff, h8_sc >> 8);   // rare
+  }
 }
 
 template <int KS, int XT>
@@ -621,14 +659,18 @@ __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
 // token's own h row (E4M3 from the gate_up kernel), + bias, x routing weight -> yw[pair, n].  An invalid id (128)
 // writes +0 for its pairs and reads no weights.  The top-k sum is left to k_combine_t950.  Load order as in the
 // gate_up kernel.  Every wave returns from the body (waves past the first right after the K reduction).
-// COH (the single-launch expert body): h was written earlier in the same launch, so the weight rows are loaded first,
-// then wait() (the release of h), then h with device-coherent loads; yw is stored device-coherently, and only by
-// wave 0 (whose acknowledged stores the caller counts).
-template <int KS, int XT, bool COH, typename Wait>
+// TAG (the single-launch expert body, batch 1): h was written earlier in the same launch as tagged words of tg, so
+// the weight rows are loaded first, then thread 0 polls the last word of the expert's h row (from its last gate_up
+// workgroup), then every thread reads its 8 words of the row (ordinary loads first: all 180 down workgroups of the
+// expert read that row, and an XCD's L2 serves all but the first), polling again any word not yet tagged; yw is
+// written as tagged words of tg (by wave 0), not to yw.
+template <int KS, int XT, bool TAG>
 NA_DEVICE void down_body(DecodeLds<KS, XT>& L, int item, int b, long long rid, int B, const uint8_t* __restrict__ pool,
                          long long slot_bytes, const int64_t* __restrict__ slot_tab, long long expert_base,
                          const uint8_t* __restrict__ h8, const uint16_t* __restrict__ wts,
-                         const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw, uint32_t h8_sc, Wait wait) {
+                         const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw, uint32_t h8_sc,
+                         const OneTags& tg = OneTags{}, const OnePre* pre = nullptr) {
+  static_assert(!TAG || XT == 1, "tagged h: one token");
   constexpr int MT = (kTTiles + KS - 1) / KS;
   constexpr int NTH = 64 * KS;
   int nt, distinct, valid;
@@ -637,19 +679,21 @@ NA_DEVICE void down_body(DecodeLds<KS, XT>& L, int item, int b, long long rid, i
   if (e < 0) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (e == 128) {                                      // invalid ids: each of their pairs contributes +0
-    if (COH && wave != 0) return;
-    for (int i = COH ? lane : tid; i < 4 * B * (kTRows / 2); i += COH ? 64 : NTH) {
+    if constexpr (TAG) {
+      if (wave != 0) return;
+      const uint32_t tag = one_tag(tg);
+      if (lane < 4 * (kTRows / 2) && ((all >> (lane >> 3)) & 1))
+        tag_store(one_y_words(tg, lane >> 3, b) + (lane & 7), 0u, tag);
+      return;
+    }
+    for (int i = tid; i < 4 * B * (kTRows / 2); i += NTH) {
       const int q = i / (kTRows / 2), c = i - q * (kTRows / 2);
-      uint32_t* d = reinterpret_cast<uint32_t*>(yw + (long long)q * kH + 16 * b + 2 * c);
-      if ((all >> q) & 1) {
-        if constexpr (COH) store_coherent(d, 0u);
-        else *d = 0u;
-      }
+      if ((all >> q) & 1) *reinterpret_cast<uint32_t*>(yw + (long long)q * kH + 16 * b + 2 * c) = 0u;
     }
     return;
   }
   const long long gid = expert_base + e;
-  const long long slot = slot_tab ? slot_tab[gid] : gid;
+  const long long slot = TAG ? (pre->slot >= 0 ? pre->slot : gid) : slot_tab ? slot_tab[gid] : gid;
   const uint8_t* blk = pool + slot * slot_bytes + kTDownOff + (long long)b * kTBlock;
   int t0, t1;
   ktile_range<KS>(wave, t0, t1);
@@ -657,7 +701,7 @@ NA_DEVICE void down_body(DecodeLds<KS, XT>& L, int item, int b, long long rid, i
   scale_load<1, NTH>(tid, blk, blk, sr);
   XRegs<XT, NTH> xr;
   const auto pair_of = [users](int t) { return pair_at(users, t); };
-  if constexpr (!COH) h8_load<XT, NTH>(tid, h8, pair_of, nt, xr);
+  if constexpr (!TAG) h8_load<XT, NTH>(tid, h8, pair_of, nt, xr);
   const int n = 16 * b + (lane & 15);
   // epilogue operands are loaded now and converted at their use, so no wait is placed before the barrier
   const uint16_t bdn = (bias_dn ? bias_dn + gid * kH : wts)[bias_dn ? n : 0];   // unconditional load
@@ -666,9 +710,30 @@ NA_DEVICE void down_body(DecodeLds<KS, XT>& L, int item, int b, long long rid, i
   for (int q = 0; q < 2; ++q) wr[q] = wts[pair_at(users, min(2 * (lane >> 4) + q, nt - 1))];
   CodeRegs<MT> rd;
   code_load<MT>(blk, lane, t0, t1, rd);
-  if constexpr (COH) {
-    wait();
-    h8_load<XT, NTH, decltype(pair_of), true>(tid, h8, pair_of, nt, xr);
+  if constexpr (TAG) {
+    static_assert(XRegs<XT, NTH>::XP == 2, "two 16-byte pieces of the h row per thread");
+    __shared__ uint32_t tag_lds;                       // thread 0's number, for every thread after the barrier
+    const uint64_t* hrow = one_h_words(tg, pair_at(users, 0), 0);
+    if (tid == 0) {
+      const uint32_t t0 = one_tag(tg);
+      tag_wait1(hrow + (kTDownBlocks - 1) * 8 + 7, t0, tg.err);
+      tag_lds = t0;
+    }
+    __syncthreads();
+    const uint32_t tag = tag_lds;
+    // piece p < 180 = hi codes of block p (words 0..3 of its 8), p >= 180 = lo codes of block p - 180 (words 4..7)
+    const uint64_t* src[8];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int p = min(tid + NTH * k, kH8Pieces - 1);
+      const uint64_t* w = hrow + (p < kTDownBlocks ? p * 8 : (p - kTDownBlocks) * 8 + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) src[4 * k + i] = w + i;
+    }
+    uint32_t hw[8];
+    tag_read_at<8, true>(src, tag, hw, tg.err);
+    xr.v[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    xr.v[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
   }
   __builtin_amdgcn_sched_barrier(0);
   h8_store<XT, NTH>(tid, L.x, nt, xr, h8_sc & 0xff, h8_sc >> 8);
@@ -698,21 +763,20 @@ NA_DEVICE void down_body(DecodeLds<KS, XT>& L, int item, int b, long long rid, i
     }
   }
   float yb[2];
+  const uint32_t ytag = TAG ? one_tag(tg) : 0u;
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int u = 2 * (lane >> 4) + q;
     float y = rb(y2[q]);
     if (bias_dn) y = rb(y + bf16_to_f32(bdn));
     yb[q] = y;
-    store_row_pairs<COH>(yw + (long long)pair_at(users, min(u, nt - 1)) * kH + 16 * b,
-                         f32_to_bf16(y * bf16_to_f32(wr[q])), u < nt);
+    const uint16_t v = f32_to_bf16(y * bf16_to_f32(wr[q]));
+    const int pr = pair_at(users, min(u, nt - 1));
+    if constexpr (TAG) tag_row_pairs(one_y_words(tg, pr, b), v, u < nt, ytag);
+    else store_row_pairs(yw + (long long)pr * kH + 16 * b, v, u < nt);
   }
-  if (all != users) dup_rows_store_w<COH>(yw, users, all, nt, b, yb[0], yb[1], wts);   // uniform, rare
+  if (all != users) dup_rows_store_w<TAG>(yw, users, all, nt, b, yb[0], yb[1], wts, tg, ytag);   // uniform, rare
 }
-
-struct NoWait {
-  NA_DEVICE void operator()() const {}
-};
 
 template <int KS, int XT>
 __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
@@ -723,7 +787,7 @@ __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
   const long long rid = route_ids_load(ids, 4 * B);
   args_at_entry(h8, wts, bias_dn, yw, (int)h8_sc);    // past the preloaded arguments: fetched while the ids fly
   down_body<KS, XT, false>(L, blockIdx.x, blockIdx.y, rid, B, pool, slot_bytes, slot_tab, expert_base, h8, wts,
-                           bias_dn, yw, h8_sc, NoWait{});
+                           bias_dn, yw, h8_sc);
 }
 
 __global__ __launch_bounds__(256) void k_combine_t950(const uint32_t* __restrict__ yw, int B,
@@ -827,110 +891,82 @@ __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
   }
 }
 
-// ---- the expert body of one token in a single launch (na_moe_decode_t950_one): 720 workgroups, workgroup blk = 4b +
-// item runs k_moe_gate_up_t950<4, 1>'s (item, gate_up row block b) with h stored device-coherently, then
-// k_moe_down_t950<4, 1>'s (item, down row block b) and, for the last of block b's four workgroups, k_combine_t950's sum
-// of block b.  The arithmetic is those kernels', so the output equals the two- and three-launch paths bit for bit.
-// Handoffs (handoff.h): wave 0 of each workgroup (the only wave that stores h) counts the workgroup once its h stores
-// are acknowledged, two-level; the count's completion raises kGo release flags to this launch's generation number.
-// Each workgroup issues its down row block's loads (weights, scales, bias) before it waits for the release, then
-// reads h device-coherently.  The generation (line kOneGen, read by thread 0 at entry) advances by one per launch,
-// so the flags never need clearing.  Block b's workgroups count on block b's counter after their yw stores are
-// acknowledged; the fourth reads the four slices device-coherently and writes out.
-// Every workgroup waits for every other's gate_up part, so all 720 must be resident at once: the host launches this
-// kernel only where the occupancy query allows it (3 workgroups per CU x 256 CUs = 768 on MI355X).  The waits are
-// bounded (handoff.h): a broken assumption shows as the error word, never as a hang.
-// sync: kOneSyncLines lines of kLine uint32, zero before the first launch; line 0 = the error word (raised by a wait
-// that gave up, never cleared here).
-constexpr int kOneWgs = 4 * kTDownBlocks;       // 720
-constexpr int kOneErr = 0, kOneGen = 1, kOneCnt = 2, kOneGo = kOneCnt + 1 + kGo, kOneBlk = kOneGo + kGo;
-constexpr int kOneSyncLines = kOneBlk + kTDownBlocks / 2;   // 125 lines, 32,000 bytes (two block counters a line)
-
-NA_DEVICE uint32_t* one_block_counter(uint32_t* sync, int b) {
-  return sync + (kOneBlk + b / 2) * kLine + (b & 1) * (kLine / 2);
-}
-
-// Wave 0 of workgroup blk after its last h store (the other waves stored nothing): its stores acknowledged, lane 0
-// counts the workgroup two-level (kGo group counters, then the top one); the wave that completes the count raises the
-// kGo flags and the generation word to gen.  Only thread 0 read the generation word, before this count, so every
-// workgroup has read it before it advances.
-NA_DEVICE void one_publish(uint32_t* sync, int blk, uint32_t gen) {
-  __builtin_amdgcn_s_waitcnt(0);
-  const int lane = threadIdx.x & 63;
-  uint32_t* cnt = sync + kOneCnt * kLine;
-  int top = 0;
-  if (lane == 0) {
-    const uint32_t gi = (uint32_t)blk % kGo;
-    const uint32_t quota = ((uint32_t)kOneWgs - gi + kGo - 1) / kGo;
-    uint32_t* gc = cnt + (1 + gi) * kLine;
-    if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == quota - 1) {
-      __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)kGo - 1) {
-        __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        top = 1;
-      }
-    }
-  }
-  top = __builtin_amdgcn_readfirstlane(top);
-  gen = __builtin_amdgcn_readfirstlane(gen);         // thread 0's value (lane 0 of wave 0)
-  if (top) {
-    if (lane < kGo) store_coherent(sync + (kOneGo + lane) * kLine, gen);
-    if (lane == kGo) store_coherent(sync + kOneGen * kLine, gen);
-  }
-}
-
-// Thread 0 polls its flag until it holds gen (or the poll limit raises the error word); then the workgroup meets.
-NA_DEVICE void one_wait(const uint32_t* go, uint32_t gen, uint32_t* err) {
-  if (threadIdx.x == 0) {
-    uint32_t polls = 0;
-    while (load_coherent(go) != gen) {
-      if (++polls > kSpinLimit) {
-        __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-  }
-  __syncthreads();
-}
+// ---- the expert body of one token in a single launch (na_moe_decode_t950_one): 720 workgroups.  Workgroup blk =
+// 4b + i runs k_moe_gate_up_t950<4, 1>'s (i-th distinct expert, gate_up row block b), writing its 16 h values as
+// tagged words (handoff.h), then k_moe_down_t950<4, 1>'s (i-th expert, down row block b): its weight rows are loaded
+// before it polls the expert's h row, and its weighted outputs are written as tagged words; workgroup 4b + 3 then
+// reads the four pairs' outputs of block b and sums them in k_combine_t950's order.  Bit-identical to the two- and
+// three-launch paths.  The launch's number: workgroup blk owns counter word blk, reads it at entry (n after n
+// launches), tags with n + 1 and stores n + 1 back before it ends: the same number in every workgroup of a launch,
+// one more than the previous launch's, with no atomic, no shared word and nothing to reset.
+// A down workgroup waits for the gate_up parts of its expert's 180 workgroups, so all 720 must be resident at once:
+// the host launches this kernel only where the occupancy query allows it (3 workgroups per CU x 256 CUs = 768 on
+// MI355X).  The waits are bounded (handoff.h): a broken assumption shows as the error word, never as a hang.
+// sync: kOneSyncLines lines of kLine uint32, zero before the first launch: line 0 the error word (raised by a wait
+// that gave up, never cleared here), the workgroups' counter words (720 uint32), then the tagged words of h
+// (4 x 180 x 8) and of the weighted outputs (4 x 180 x 8).
+constexpr int kOneErr = 0, kOneCtr = 1, kOneTagH = kOneCtr + (kOneWgs + kLine - 1) / kLine;
+constexpr int kOneTagWords = 4 * kTDownBlocks * 8;                     // 5760 per area
+constexpr int kOneTagY = kOneTagH + kOneTagWords * 2 / kLine;
+constexpr int kOneSyncLines = kOneTagY + kOneTagWords * 2 / kLine;     // 373 lines, 95,488 bytes
 
 __global__ __launch_bounds__(256) void k_moe_one_t950(
     const int64_t* __restrict__ ids, const uint8_t* __restrict__ pool, long long slot_bytes,
     const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ x,
     const uint16_t* __restrict__ bias_gu, const uint16_t* __restrict__ bias_dn, const uint16_t* __restrict__ wts,
-    uint8_t* __restrict__ h8, uint16_t* __restrict__ yw, uint16_t* __restrict__ out, float alpha, float limit,
-    uint32_t h8_sc, uint32_t* __restrict__ sync) {
+    uint16_t* __restrict__ out, float alpha, float limit, uint32_t h8_sc, uint32_t* __restrict__ sync) {
   __shared__ DecodeLds<4, 1> L;
   const long long rid = route_ids_load(ids, 4);
-  args_at_entry(x, bias_gu, bias_dn, wts, h8, yw, out, alpha, limit, (int)h8_sc, sync);
+  args_at_entry(x, bias_gu, bias_dn, wts, out, alpha, limit, (int)h8_sc, sync);
   const int blk = blockIdx.x, item = blk & 3, b = blk >> 2;
   const int tid = threadIdx.x, lane = tid & 63;
-  uint32_t* err = sync + kOneErr * kLine;
-  const uint32_t gen = tid == 0 ? load_coherent(sync + kOneGen * kLine) + 1u : 0u;   // used by thread 0 only
-  gate_up_body<4, 1, true>(L, item, b, rid, 1, pool, slot_bytes, slot_tab, expert_base, x, bias_gu, h8, alpha, limit,
-                           h8_sc);
-  if (tid < 64) one_publish(sync, blk, gen);
-  down_body<4, 1, true>(L, item, b, rid, 1, pool, slot_bytes, slot_tab, expert_base, h8, wts, bias_dn, yw, h8_sc,
-                        [&]() { one_wait(sync + (kOneGo + b % kGo) * kLine, gen, err); });
-  if (tid >= 64) return;
-  // wave 0: yw stores acknowledged, count block b; the fourth arrival sums the block (k_combine_t950's arithmetic)
-  __builtin_amdgcn_s_waitcnt(0);
-  uint32_t* bc = one_block_counter(sync, b);
-  int last = 0;
-  if (lane == 0) {
-    last = __hip_atomic_fetch_add(bc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 3u;
-    if (last) __hip_atomic_store(bc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // loads that do not depend on the routing, issued while the ids are in flight: token 0's x, the layer's slots
+  OnePre pre;
+  x_load<1, 256>(tid, x, kH, [](int) { return 0; }, 1, pre.x);
+  int64_t srow[2] = {0, 0};
+  if (slot_tab) {
+    srow[0] = slot_tab[expert_base + lane];
+    srow[1] = slot_tab[expert_base + 64 + lane];
   }
-  last = __builtin_amdgcn_readfirstlane(last);
-  if (!last || lane >= kTRows / 2) return;
+  // the launch count: loaded by thread 0 now, first needed at the end of the gate_up part (one_tag)
+  uint32_t* ctr = sync + kOneCtr * kLine + blk;
+  const uint32_t raw = tid == 0 ? load_coherent(ctr) : 0u;
+  const OneTags tg{reinterpret_cast<uint64_t*>(sync + kOneTagH * kLine),
+                   reinterpret_cast<uint64_t*>(sync + kOneTagY * kLine), raw, sync + kOneErr * kLine};
+  {                                                    // this workgroup's expert -> its slot (a lane read, uniform)
+    int nt, distinct, valid;
+    uint64_t users, all;
+    const int e = __builtin_amdgcn_readfirstlane(route_t950<4>(rid, 4, item, nt, users, all, distinct, valid));
+    pre.slot = -1;
+    if (slot_tab && e >= 0 && e < 128) {
+      const int64_t v = srow[e >> 6];
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, e & 63);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), e & 63);
+      pre.slot = (long long)(((uint64_t)hi << 32) | lo);
+    }
+  }
+  gate_up_body<4, 1, true>(L, item, b, rid, 1, pool, slot_bytes, slot_tab, expert_base, x, bias_gu, nullptr, alpha,
+                           limit, h8_sc, tg, &pre);
+  down_body<4, 1, true>(L, item, b, rid, 1, pool, slot_bytes, slot_tab, expert_base, nullptr, wts, bias_dn, nullptr,
+                        h8_sc, tg, &pre);
+  if (tid >= 64) return;
+  const uint32_t tag = one_tag(tg);
+  if (tid == 0) store_coherent(ctr, tag);              // the count for the next launch
+  if (item != 3) return;
+  // block b's sum: thread t < 8 reads word t of the four pairs' outputs (k_combine_t950's arithmetic)
+  if (tid >= kTRows / 2) return;
+  const uint64_t* src[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) src[k] = one_y_words(tg, k, b) + tid;
+  uint32_t w[4];
+  tag_read_at<4>(src, tag, w, tg.err);
   float a0 = 0.f, a1 = 0.f;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const uint32_t v = load_coherent(reinterpret_cast<const uint32_t*>(yw + (long long)k * kH + 16 * b) + lane);
-    a0 += bf16_to_f32((uint16_t)(v & 0xffff));
-    a1 += bf16_to_f32((uint16_t)(v >> 16));
+    a0 += bf16_to_f32((uint16_t)(w[k] & 0xffff));
+    a1 += bf16_to_f32((uint16_t)(w[k] >> 16));
   }
-  reinterpret_cast<uint32_t*>(out + 16 * b)[lane] = (uint32_t)f32_to_bf16(a0) | ((uint32_t)f32_to_bf16(a1) << 16);
+  reinterpret_cast<uint32_t*>(out + 16 * b)[tid] = (uint32_t)f32_to_bf16(a0) | ((uint32_t)f32_to_bf16(a1) << 16);
 }
 
 template <typename... KArgs, typename... Args>
@@ -1109,19 +1145,18 @@ int na_moe_decode_t950_one(const void* x, const int64_t* topk_ids, const void* t
                            long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
                            const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha,
                            float limit, unsigned int* sync, void* const* events, hipStream_t stream) {
-  if (!x || !topk_ids || !topk_w || !pool || !h_scratch || !yw_scratch || !out || !sync) return kErrArgs;
+  (void)h_scratch;                                     // h and the weighted outputs travel as tagged words in sync
+  (void)yw_scratch;
+  if (!x || !topk_ids || !topk_w || !pool || !out || !sync) return kErrArgs;
   if (slot_bytes < kTSlot || (slot_bytes & 15) || (reinterpret_cast<uintptr_t>(pool) & 15)) return kErrArgs;
-  if ((reinterpret_cast<uintptr_t>(h_scratch) | reinterpret_cast<uintptr_t>(yw_scratch) |
-       reinterpret_cast<uintptr_t>(out)) & 15)
-    return kErrArgs;
+  if ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(sync)) & 15) return kErrArgs;
   const uint32_t h8_sc = h8_scale_bytes(alpha, limit);
   if (!h8_sc) return kErrArgs;
   if (!one_resident_ok()) return kErrResident;
   launch_t(k_moe_one_t950, dim3(kOneWgs), dim3(256), stream, events ? (hipEvent_t)events[0] : nullptr,
            events ? (hipEvent_t)events[1] : nullptr, topk_ids, (const uint8_t*)pool, slot_bytes, slot_tab,
            expert_base, (const uint16_t*)x, (const uint16_t*)bias_gu, (const uint16_t*)bias_dn,
-           (const uint16_t*)topk_w, (uint8_t*)h_scratch, (uint16_t*)yw_scratch, (uint16_t*)out, alpha, limit, h8_sc,
-           (uint32_t*)sync);
+           (const uint16_t*)topk_w, (uint16_t*)out, alpha, limit, h8_sc, (uint32_t*)sync);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
