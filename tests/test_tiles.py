@@ -499,3 +499,38 @@ def test_duplicate_ids_in_a_token(B):
             assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale, (nm, b, d.max(), scale)
             prof = ulp_profile(arr[b], want)
             assert prof[1] >= T950_FRAC2 and prof[2] >= T950_FRAC4, (nm, b, prof)
+
+
+@pytest.mark.gpu
+def test_one_launch_sparse_routing_lists():
+    """The single-launch body at B = 1 on top-4 lists with fewer than four distinct experts, so that some of the four
+    workgroups of an output block have no expert of their own (the one that sums the block among them): one expert
+    four times, an invalid id and a valid one twice each, two experts twice each, all four invalid.  Consecutive calls
+    on one sync buffer (each launch's tags differ from the last); bit for bit equal to the two-launch path, which the
+    other tests hold to the oracle."""
+    import torch
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
+    dev = _dev()
+    slots, x, ids, w, tab, bgu, bdn = _t950_case(1, 1400, True, nslot=8)
+    print("case one-launch sparse routing lists", flush=True)
+    raw = torch.from_numpy(np.stack(slots)).to(dev)
+    tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
+    tiles.repack_to_t950(raw, tp)
+    tabd, bg, bd = torch.from_numpy(tab).to(dev), bgu.to(dev), bdn.to(dev)
+    one = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4)
+    two = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4, one_launch=False)
+    assert one.launches(1) == ("experts",)
+    e0, e1 = int(ids[0, 0]), int(ids[0, 1])
+    lists = [[e0, e0, e0, e0], [200, e1, 200, e1], [e0, e1, e0, e1], [-1, 200, 128, -5], [e1, e0, 300, e0]]
+    xd = x.to(dev)
+    wd = torch.from_numpy(w).to(torch.bfloat16).to(dev)
+    for rep in range(2):
+        for i, lst in enumerate(lists):
+            idd = torch.tensor([lst], dtype=torch.int64, device=dev)
+            a = one.forward_decode(6, xd, idd, wd).float().cpu().numpy()
+            b = two.forward_decode(6, xd, idd, wd).float().cpu().numpy()
+            assert np.array_equal(a, b), (rep, lst)
+            if all(not 0 <= e < 128 for e in lst):
+                assert not np.any(a), lst                    # every pair contributes +0
+    assert not one.sync_error()
