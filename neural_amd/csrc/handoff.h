@@ -5,14 +5,13 @@
 //   memory) through agent-scope relaxed atomic stores, which gfx950 issues with the sc1 bit (written through to the
 //   coherent point), and agent-scope loads (sc1).  A kernel boundary leaves no stale line in any L2, so what nothing
 //   in the launch read before can also be read with ordinary loads once it is complete.
-// * Tagged words (the attention block, core.hip): each 64-bit word holds a 32-bit payload and the launch's
-//   generation number, written by one store; the consumer polls the words it needs until they carry its number.
-//   No acknowledgement, count or flag stands between the producer's store and the consumer's read.
-// * Counters and flags (the single-launch expert body, tiles.hip): after its stores are acknowledged (s_waitcnt 0)
-//   a workgroup counts itself in two levels (kGo group counters, then a top counter, so no counter takes more than
-//   a few dozen increments); the one that completes the count raises kGo release flags on separate 256-byte lines,
-//   which consumers poll (thread 0, a short sleep between reads).  Hundreds of workgroups polling one word, or
-//   incrementing one, would queue every access to that line; spread over kGo lines they do not.
+// * Tagged words (the attention block, core.hip; the single-launch expert body, tiles.hip): each 64-bit word holds
+//   a 32-bit payload and the launch's generation number, written by one store; the consumer polls the words it
+//   needs until they carry its number.  No acknowledgement, count or flag stands between the producer's store and
+//   the consumer's read.  One thread per awaited producer polls a single word first (with a short sleep between
+//   reads), so that waiting workgroups do not flood the memory system with reads of whole areas.
+// * Last-arriver counts (the attention's chunks, attention_dev.h): after its stores are acknowledged (s_waitcnt 0)
+//   a workgroup increments its group's counter; the one that completes it reads the others' results.
 // * Progress: the hardware dispatches a grid's workgroups in increasing id order on each XCD, so every producer
 //   has been dispatched before any consumer that waits for it, and producers never wait for consumers: every wait
 //   ends.  The waits are bounded anyway: after kSpinLimit polls the workgroup raises an error flag the host can
@@ -25,7 +24,6 @@ namespace na {
 
 constexpr uint32_t kSpinLimit = 1u << 16;   // polls (about 1 us each) before a wait gives up
 constexpr int kLine = 64;                    // uint32 words per 256-byte line
-constexpr int kGo = 16;                      // release flags per phase
 
 NA_DEVICE void store_coherent(uint16_t* p, uint16_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
