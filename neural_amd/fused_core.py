@@ -37,77 +37,102 @@ from .attention import (H, HD, HP, K, MAX_SPLIT, NE, NKV, NQ, REP, SplitAttn, de
 _PACK_BASE = H + 3 * K        # h_norm | 4 weights | 4 ids | 4 resident flags (server.py:471), + 4 near-miss ids
 
 
+# Rows of the fused Q|K|V product that each projection owns (q: 64 heads, k and v: 8 heads each, 64 dims per head).
+_QKV_ROWS = (("q_proj", 0, NQ * HD), ("k_proj", NQ * HD, (NQ + NKV) * HD),
+             ("v_proj", (NQ + NKV) * HD, (NQ + 2 * NKV) * HD))
+# The reference's Triton tiling knobs: accepted and recorded in FusedCore.cfg, no meaning for these kernels.
+_TILING_KNOBS = ("qkv_bk", "qkv_warps", "o_rows", "o_bk", "o_warps", "r_rows", "r_bk", "attn_bn")
+
+
+def _fuse_projections(attn):
+    """Gather attn.{q,k,v}_proj into one weight buffer [5120, 2880] and one bias buffer [5120] (rows in _QKV_ROWS
+    order), then point each projection's weight and bias at its rows: the module computes exactly what it did, on
+    storage the fused QKV kernel reads in one pass."""
+    n_rows = _QKV_ROWS[-1][2]
+    w_like, b_like = attn.q_proj.weight, attn.q_proj.bias
+    if w_like.dtype is not torch.bfloat16:
+        raise AssertionError(f"q/k/v weights must be bf16 and stack to [{n_rows}, {H}]")
+    W = torch.empty(n_rows, H, dtype=w_like.dtype, device=w_like.device)
+    Bv = torch.empty(n_rows, dtype=b_like.dtype, device=b_like.device)
+    with torch.no_grad():
+        for name, lo, hi in _QKV_ROWS:
+            proj = getattr(attn, name)
+            if tuple(proj.weight.shape) != (hi - lo, H) or proj.weight.dtype is not torch.bfloat16:
+                raise AssertionError(f"q/k/v weights must be bf16 and stack to [{n_rows}, {H}]")
+            W[lo:hi].copy_(proj.weight)
+            Bv[lo:hi].copy_(proj.bias)
+            proj.weight.data, proj.bias.data = W[lo:hi], Bv[lo:hi]
+    return W, Bv
+
+
 class FusedCore:
-    """Per-layer decode launcher (reference fused_core.py:505-629).  Concatenates each layer's q/k/v weights and
-    biases into one buffer and re-points the modules' tensors at views of it; with ring=R > 0 replaces every sliding
-    layer's K/V cache by a rolling [1, NKV, R, HD] cache (slot = pos % R) and sets lg.ring on every layer; with
-    split_k = NS > 1 full-attention layers run chunked attention (NS chunks) on one shared workspace.  The Triton
-    tiling arguments (qkv_bk, qkv_warps, o_rows, o_bk, o_warps, r_rows, r_bk, attn_bn, split_bn, split_cache_s) are
-    accepted and recorded; the kernels' tilings are their own.  Construct before any graph capture."""
+    """Per-layer decode launcher with the reference's constructor and run() signature (fused_core.py:505-629).
+
+    Side effects of construction on ``cg`` (the drop-in contract; construct before any graph capture):
+      * every layer's q/k/v projection weights and biases are re-pointed at row ranges of one fused buffer per
+        layer (``self.W[L]`` [5120, 2880] bf16, ``self.B[L]`` [5120]); the module's own forward is unchanged;
+      * ``lg.ring`` is set on every layer: ``ring`` for sliding layers when ring > 0, else 0;
+      * with ring > 0, each sliding layer's ``lg.k`` / ``lg.v`` become new zeroed rolling caches [1, NKV, ring, HD]
+        (position p in slot p % ring); ring must cover the layer's window;
+      * with split_k = NS > 1, the full-attention layers share one chunked-attention workspace (SplitAttn over NS
+        chunks); they must then share one smax.
+    The Triton tiling knobs are accepted and recorded in ``cfg``; the kernels' tilings are their own."""
 
     def __init__(self, cg, dev, qkv_bk=128, qkv_warps=4, o_rows=16, o_bk=256, o_warps=4, r_rows=8, r_bk=256,
                  attn_bn=64, ring=0, split_k=1, split_bn=64, split_cache_s=True, near_miss=False):
         self.cg, self.dev = cg, torch.device(dev)
-        self.ring, self.split_k = int(ring), int(split_k)
-        self.near_miss = bool(near_miss)
+        self.ring, self.split_k, self.near_miss = int(ring), int(split_k), bool(near_miss)
         if not 1 <= self.split_k <= MAX_SPLIT:
             raise AssertionError(f"split_k must be in [1, {MAX_SPLIT}]")
-        self.cfg = dict(qkv_bk=qkv_bk, qkv_warps=qkv_warps, o_rows=o_rows, o_bk=o_bk, o_warps=o_warps,
-                        r_rows=r_rows, r_bk=r_bk, attn_bn=attn_bn, ring=self.ring, split_k=self.split_k,
-                        split_bn=split_bn, split_cache_s=bool(split_cache_s), near_miss=self.near_miss)
-        self.W, self.B = [], []
-        for lg in cg.layers:
-            a = lg.layer.self_attn
-            with torch.no_grad():
-                W = torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]).contiguous()
-                B = torch.cat([a.q_proj.bias, a.k_proj.bias, a.v_proj.bias]).contiguous()
-                a.q_proj.weight.data = W[:NQ * HD]
-                a.k_proj.weight.data = W[NQ * HD:(NQ + NKV) * HD]
-                a.v_proj.weight.data = W[(NQ + NKV) * HD:]
-                a.q_proj.bias.data = B[:NQ * HD]
-                a.k_proj.bias.data = B[NQ * HD:(NQ + NKV) * HD]
-                a.v_proj.bias.data = B[(NQ + NKV) * HD:]
-            if W.dtype is not torch.bfloat16 or tuple(W.shape) != ((NQ + 2 * NKV) * HD, H):
-                raise AssertionError(f"q/k/v weights must be bf16 and stack to [{(NQ + 2 * NKV) * HD}, {H}]")
-            self.W.append(W)
-            self.B.append(B)
-        for lg in cg.layers:
-            if self.ring and lg.sliding:
-                if self.ring < int(lg.sliding):
-                    raise AssertionError(f"ring {self.ring} is smaller than the sliding window {lg.sliding}")
-                lg.k = torch.zeros(1, NKV, self.ring, HD, dtype=torch.bfloat16, device=self.dev)
-                lg.v = torch.zeros_like(lg.k)
-                lg.ring = self.ring
-            else:
-                lg.ring = 0
-        z = lambda *s, dt=torch.bfloat16: torch.zeros(*s, dtype=dt, device=self.dev)  # noqa: E731
-        self.xbuf = z(H)
-        self.q = z(NQ * HD)
-        self.att = z(NQ * HD)
-        self.logits = z(NE, dt=torch.float32)
-        self.counter = z(1, dt=torch.int32)
-        self.split = None
-        if self.split_k > 1:
-            full = {int(lg.smax) for lg in cg.layers if not lg.sliding}
-            if len(full) > 1:
-                raise AssertionError(f"full-attention layers with different smax {full}")
-            if full:
-                self.split = SplitAttn(self.split_k, full.pop(), self.dev, bn=split_bn, cache_s=split_cache_s)
+        knobs = (qkv_bk, qkv_warps, o_rows, o_bk, o_warps, r_rows, r_bk, attn_bn)
+        self.cfg = {**dict(zip(_TILING_KNOBS, knobs)), "ring": self.ring, "split_k": self.split_k,
+                    "split_bn": split_bn, "split_cache_s": bool(split_cache_s), "near_miss": self.near_miss}
+        fused = [_fuse_projections(lg.layer.self_attn) for lg in cg.layers]
+        self.W = [w for w, _ in fused]
+        self.B = [b for _, b in fused]
+        self._install_rings()
+        self.xbuf, self.q, self.att = (torch.zeros(n, dtype=torch.bfloat16, device=self.dev)
+                                       for n in (H, NQ * HD, NQ * HD))
+        self.logits = torch.zeros(NE, dtype=torch.float32, device=self.dev)
+        self.counter = torch.zeros(1, dtype=torch.int32, device=self.dev)
+        full_rows = sorted({int(lg.smax) for lg in cg.layers if not lg.sliding})
+        if self.split_k > 1 and len(full_rows) > 1:
+            raise AssertionError(f"full-attention layers with different smax {set(full_rows)}")
+        self.split = (SplitAttn(self.split_k, full_rows[0], self.dev, bn=split_bn, cache_s=split_cache_s)
+                      if self.split_k > 1 and full_rows else None)
+
+    def _install_rings(self):
+        for lg in self.cg.layers:
+            r = self.ring if (self.ring and lg.sliding) else 0
+            if r and r < int(lg.sliding):
+                raise AssertionError(f"ring {r} is smaller than the sliding window {lg.sliding}")
+            if r:
+                lg.k, lg.v = (torch.zeros(1, NKV, r, HD, dtype=torch.bfloat16, device=self.dev) for _ in "kv")
+            lg.ring = r
 
     def layer_ring(self, L):
         """Ring size of layer L's cache (0 = linear)."""
-        return self.ring if (self.ring and self.cg.layers[L].sliding) else 0
+        return int(self.cg.layers[L].ring)
 
     def snapshot_rings(self):
-        """Copy of every sliding layer's ring (None for the other layers), to resume a prompt at this position."""
-        return [(lg.k.clone(), lg.v.clone()) if (self.ring and lg.sliding) else None for lg in self.cg.layers]
+        """Per layer, a copy (k, v) of its rolling cache, or None for a linear layer: the state to resume a prompt
+        at this position (ring_reuse_ok says when that is valid)."""
+        return [None if not lg.ring else (lg.k.clone(), lg.v.clone()) for lg in self.cg.layers]
 
     def restore_rings(self, snap):
-        """In-place restore of snapshot_rings() (addresses unchanged: captured graphs stay valid)."""
-        for lg, kv in zip(self.cg.layers, snap):
-            if kv is not None:
-                lg.k.copy_(kv[0])
-                lg.v.copy_(kv[1])
+        """Copy a snapshot_rings() result back into the same cache tensors (addresses unchanged, so captured graphs
+        stay valid)."""
+        for lg, saved in zip(self.cg.layers, snap):
+            for dst, src in zip((lg.k, lg.v), saved or ()):
+                dst.copy_(src)
+
+    def _cache(self, L, name, override, default, rows, ring):
+        t = default if override is None else override
+        if not (tuple(t.shape) == (1, NKV, rows, HD) and t.dtype == torch.bfloat16 and t.is_contiguous()):
+            raise AssertionError(f"layer {L}: {name} must be a contiguous bf16 [1, {NKV}, {rows}, {HD}] "
+                                 f"({'ring' if ring else 'linear'} layout), got {tuple(t.shape)} {t.dtype} "
+                                 f"stride {t.stride()}")
+        return t
 
     def run(self, L, mid, g_out, c_out, slot_tab, bx, bslots, bgids, bw, pack, kc=None, vc=None, hn_o=None,
             sc_o=None, idx_o=None):
@@ -121,17 +146,12 @@ class FusedCore:
         lg = cg.layers[L]
         ly = lg.layer
         a = ly.self_attn
-        kc = lg.k if kc is None else kc
-        vc = lg.v if vc is None else vc
-        hn_o = lg.h_norm if hn_o is None else hn_o
-        sc_o = lg.r_scores if sc_o is None else sc_o
-        idx_o = lg.r_idx if idx_o is None else idx_o
         ring = self.layer_ring(L)
         rows = ring or int(lg.smax)
-        for t, nm in ((kc, "kc"), (vc, "vc")):
-            assert tuple(t.shape) == (1, NKV, rows, HD) and t.dtype == torch.bfloat16 and t.is_contiguous(), (
-                f"layer {L}: {nm} must be a contiguous bf16 [1, {NKV}, {rows}, {HD}] "
-                f"({'ring' if ring else 'linear'} layout), got {tuple(t.shape)} {t.dtype} stride {t.stride()}")
+        kc = self._cache(L, "kc", kc, lg.k, rows, ring)
+        vc = self._cache(L, "vc", vc, lg.v, rows, ring)
+        hn_o, sc_o, idx_o = (d if o is None else o for o, d in ((hn_o, lg.h_norm), (sc_o, lg.r_scores),
+                                                                 (idx_o, lg.r_idx)))
         _need(mid, H, torch.bfloat16, "mid")
         _need(bx, H, torch.bfloat16, "bx")
         _need(hn_o, H, torch.bfloat16, "hn_o")

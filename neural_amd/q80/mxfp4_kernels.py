@@ -22,6 +22,7 @@ from __future__ import annotations
 import operator
 import os
 
+import numpy as np
 import torch
 
 from .. import _native as N
@@ -42,18 +43,22 @@ GK_SUPPORTED = 90          # K = 2880: the GPT-OSS-120B geometry these kernels a
 
 
 def _scale_layout(scales: torch.Tensor, GK: int, packed) -> bool:
-    """True when ``scales`` (..., N, w) holds PS4 rows (w == GK//2 + 1), False for raw rows (w == GK); ``packed``
-    (None = infer) is checked against the view (reference mxfp4_kernels.py:72-84)."""
-    w = scales.shape[-1]
-    inferred = (w == GK // 2 + 1)
-    if not (inferred or w == GK):
-        raise ValueError(f"scales view has row width {w}: want {GK} (raw E8M0) or {GK // 2 + 1} (packed 4-bit)")
-    if packed is not None and bool(packed) != inferred:
-        raise ValueError(f"packed={packed} but the scales view row width {w} says "
-                         f"{'packed' if inferred else 'raw'} (GK={GK})")
-    if scales.stride(-1) != 1 or scales.stride(-2) != w:
-        raise ValueError(f"scales rows must be contiguous (strides {tuple(scales.stride())}, row width {w})")
-    return inferred
+    """Whether ``scales`` (..., N, w) holds PS4 rows (reference mxfp4_kernels.py:72-84).
+
+    The row width decides: GK bytes is a raw E8M0 row, GK // 2 + 1 a PS4 row (a base byte and GK / 2 bytes of two
+    4-bit deltas).  ``packed`` (None = infer) must agree with what the width says: a flag never overrides the
+    view.  The rows must be dense (unit stride inside a row, rows back to back)."""
+    row_kinds = {GK: False, GK // 2 + 1: True}
+    width = int(scales.shape[-1])
+    if width not in row_kinds:
+        raise ValueError(f"scales view has row width {width}: want {GK} (raw E8M0) or {GK // 2 + 1} (packed 4-bit)")
+    is_ps4 = row_kinds[width]
+    if packed is not None and bool(packed) is not is_ps4:
+        raise ValueError(f"packed={packed} but the scales view row width {width} says "
+                         f"{'packed' if is_ps4 else 'raw'} (GK={GK})")
+    if (scales.stride(-2), scales.stride(-1)) != (width, 1):
+        raise ValueError(f"scales rows must be contiguous (strides {tuple(scales.stride())}, row width {width})")
+    return is_ps4
 
 
 def _check_pool_views(blocks: torch.Tensor, scales: torch.Tensor, x: torch.Tensor, slots: torch.Tensor):
@@ -122,82 +127,124 @@ def mxfp4_gemv_masked(x: torch.Tensor, blocks: torch.Tensor, scales: torch.Tenso
 
 
 # ------------------------------------------------------------------------------------------ prefill planning
-def _grouped_tile_rows(pair_descriptors, block_m):
-    """Host plan builder (reference mxfp4_kernels.py:298-315): (x address, y address, slot, M) per pair ->
-    pair-local tiles (x, y, slot, M, pm) for pm in range(ceil(M / block_m)); empty pairs give no tile."""
-    block_m = operator.index(block_m)
-    if block_m < 16 or block_m & (block_m - 1):
+_I31 = 2 ** 31 - 1
+
+
+def _tile_height(block_m) -> int:
+    bm = operator.index(block_m)
+    if bm < 16 or bm & (bm - 1):
         raise ValueError("block_m must be a power of two >= 16")
-    rows = []
+    return bm
+
+
+def _descriptor_table(pair_descriptors) -> np.ndarray:
+    """The (x address, y address, slot, M) descriptors as an int64 [P, 4] table, each entry an integer
+    (operator.index), addresses and slots non-negative, 0 <= M <= 2^31 - 1."""
+    table = []
     for desc in pair_descriptors:
+        desc = tuple(desc)
         if len(desc) != 4:
             raise ValueError("pair descriptor must have four integers")
-        xptr, yptr, slot, m = (operator.index(v) for v in desc)
-        if xptr < 0 or yptr < 0 or slot < 0 or not 0 <= m <= 2 ** 31 - 1:
-            raise ValueError("invalid pointer, slot or pair row count")
-        rows.extend((xptr, yptr, slot, m, pm) for pm in range(-(-m // block_m)))
-    return rows
+        table.append([operator.index(v) for v in desc])
+    arr = np.array(table, dtype=object).reshape(-1, 4)
+    if arr.size and ((arr[:, :3] < 0).any() or (arr[:, 3] < 0).any() or (arr[:, 3] > _I31).any()):
+        raise ValueError("invalid pointer, slot or pair row count")
+    return arr.astype(np.int64)
+
+
+def _tile_table(descs: np.ndarray, bm: int) -> np.ndarray:
+    """int64 [ntiles, 5]: pair by pair in the given order, one row (x, y, slot, M, pm) per block of bm rows of the
+    pair, pm = 0 .. ceil(M / bm) - 1; a pair with M = 0 has no row."""
+    per_pair = -(-descs[:, 3] // bm)
+    first = np.cumsum(per_pair) - per_pair                 # index of each pair's first tile
+    out = np.empty((int(per_pair.sum()), 5), dtype=np.int64)
+    out[:, :4] = np.repeat(descs, per_pair, axis=0)
+    out[:, 4] = np.arange(out.shape[0]) - np.repeat(first, per_pair)
+    return out
+
+
+def _grouped_tile_rows(pair_descriptors, block_m):
+    """Tile rows of a ragged launch (reference mxfp4_kernels.py:298-315): for descriptors (x address, y address,
+    slot, M), the tuples (x, y, slot, M, pm), pm = 0 .. ceil(M / block_m) - 1 per pair, pairs in the given order.
+    Tiles never span two pairs; an empty pair has none.  ValueError for a block_m that is not a power of two >= 16
+    and for a malformed descriptor."""
+    bm = _tile_height(block_m)
+    return [tuple(r) for r in _tile_table(_descriptor_table(pair_descriptors), bm).tolist()]
+
+
+def _byte_spans(tensors) -> np.ndarray:
+    """[n, 2] int64 half-open byte ranges [start, end) of contiguous tensors, sorted by start."""
+    spans = np.array([(t.data_ptr(), t.data_ptr() + t.numel() * t.element_size()) for t in tensors],
+                     dtype=np.int64).reshape(-1, 2)
+    return spans[np.argsort(spans[:, 0], kind="stable")]
+
+
+def _check_disjoint_outputs(xs, outs):
+    """Outputs must not overlap one another, and no output may overlap any input (inputs may repeat)."""
+    w = _byte_spans(outs)
+    if (w[1:, 0] < w[:-1, 1]).any():
+        raise ValueError("grouped output slices overlap")
+    r = _byte_spans(xs)
+    if len(w) and len(r):
+        # w is sorted and disjoint, so its ends are sorted too: the first output ending after a read's start is the
+        # only one that can reach into it from below; any later one starts after it.
+        k = np.searchsorted(w[:, 1], r[:, 0], side="right")
+        hit = k < len(w)
+        if (w[np.minimum(k, len(w) - 1), 0][hit] < r[hit, 1]).any():
+            raise ValueError("grouped outputs overlap an input slice")
+
+
+def _aligned16(x, out) -> bool:
+    return all(v % 16 == 0 for v in (x.data_ptr(), out.data_ptr(), x.shape[1] * x.element_size(),
+                                     out.shape[1] * out.element_size()))
 
 
 class GroupedGemmPlan:
     """Owned metadata of one ragged grouped GEMM launch (reference mxfp4_kernels.py:318-382).
 
     ``pairs``: iterable of (contiguous bf16 x[M, K], physical slot, contiguous bf16 out[M, N]).  Inputs may repeat;
-    outputs must be disjoint and may not overlap any input.  The tile table [ntiles, 5] int64 (x address, out
-    address, slot, M, pm) is uploaded once from pinned memory; the plan keeps the upload source and every pair tensor
-    alive.  A CPU plan can be built for validation; launching needs a GPU."""
+    outputs must be disjoint and may not overlap any input.  Fields: ``pairs`` (the tuple, which keeps every pair
+    tensor alive), ``metadata_host`` / ``metadata`` (the tile table [ntiles, 5] int64 of x address, out address,
+    slot, M, pm: pinned host memory and its one asynchronous upload for a CUDA plan, the same CPU tensor otherwise),
+    ``block_m``, ``K``, ``N``, ``device``, ``slots``, ``ntiles`` and ``aligned`` (every non-empty pair's addresses and
+    row pitches are multiples of 16 bytes).  A CPU plan can be built for validation; launching needs a GPU."""
     __slots__ = ("pairs", "metadata_host", "metadata", "block_m", "K", "N",
                  "device", "slots", "ntiles", "aligned")
 
     def __init__(self, pairs, *, block_m=64):
         self.pairs = tuple(pairs)
-        self.block_m = operator.index(block_m)
-        _grouped_tile_rows((), self.block_m)
-        self.K = self.N = None
-        self.device = None
-        self.aligned = True
-        descs, reads, writes, slots = [], [], [], []
-        for x, slot, out in self.pairs:
-            slot = operator.index(slot)
-            if x.ndim != 2 or out.ndim != 2 or x.shape[0] != out.shape[0]:
-                raise ValueError("each grouped pair needs x[M,K] and out[M,N]")
-            if x.dtype is not torch.bfloat16 or out.dtype is not torch.bfloat16:
-                raise ValueError("grouped GEMM inputs and outputs must be bf16")
-            if not x.is_contiguous() or not out.is_contiguous():
-                raise ValueError("grouped GEMM pair matrices must be contiguous")
-            if x.device != out.device:
-                raise ValueError("a grouped pair's input/output must share a device")
-            if self.device is None:
-                self.device, self.K, self.N = x.device, x.shape[1], out.shape[1]
+        self.block_m = _tile_height(block_m)
+        self.slots = tuple(operator.index(slot) for _, slot, _ in self.pairs)
+        for x, _, out in self.pairs:
+            self._check_pair(x, out)
+        first = self.pairs[0] if self.pairs else None
+        self.device = first[0].device if first else None
+        self.K = first[0].shape[1] if first else None
+        self.N = first[2].shape[1] if first else None
+        for x, _, out in self.pairs:
             if (x.device != self.device or x.shape[1] != self.K or out.shape[1] != self.N
                     or self.K < 32 or self.K % 32 or self.N < 1):
                 raise ValueError("grouped pairs need one device, common K (multiple of 32), and common N")
-            m = x.shape[0]
-            descs.append((x.data_ptr(), out.data_ptr(), slot, m))
-            slots.append(slot)
-            if m:
-                self.aligned &= (x.data_ptr() % 16 == 0 and out.data_ptr() % 16 == 0
-                                 and x.shape[1] * x.element_size() % 16 == 0
-                                 and out.shape[1] * out.element_size() % 16 == 0)
-                reads.append((x.data_ptr(), x.data_ptr() + x.numel() * x.element_size()))
-                writes.append((out.data_ptr(), out.data_ptr() + out.numel() * out.element_size()))
-        ordered = sorted(writes)
-        if any(a[1] > b[0] for a, b in zip(ordered, ordered[1:])):
-            raise ValueError("grouped output slices overlap")
-        wi = 0
-        for lo, hi in sorted(reads):                 # sweep: no input may overlap any output
-            while wi < len(ordered) and ordered[wi][1] <= lo:
-                wi += 1
-            if wi < len(ordered) and ordered[wi][0] < hi:
-                raise ValueError("grouped outputs overlap an input slice")
-        tiles = _grouped_tile_rows(descs, self.block_m)
-        self.slots = tuple(slots)
-        self.ntiles = len(tiles)
-        on_gpu = self.device is not None and self.device.type == "cuda"
-        self.metadata_host = torch.empty((self.ntiles, 5), dtype=torch.int64, pin_memory=on_gpu)
-        if tiles:
-            self.metadata_host.copy_(torch.tensor(tiles, dtype=torch.int64))
-        self.metadata = (self.metadata_host.to(self.device, non_blocking=True) if on_gpu else self.metadata_host)
+        live = [(x, out) for x, _, out in self.pairs if x.shape[0]]
+        self.aligned = all(_aligned16(x, out) for x, out in live)
+        _check_disjoint_outputs([x for x, _ in live], [out for _, out in live])
+        descs = _descriptor_table((x.data_ptr(), out.data_ptr(), slot, x.shape[0]) for x, slot, out in self.pairs)
+        table = torch.from_numpy(_tile_table(descs, self.block_m))
+        self.ntiles = table.shape[0]
+        cuda = self.device is not None and self.device.type == "cuda"
+        self.metadata_host = table.pin_memory() if cuda else table
+        self.metadata = self.metadata_host.to(self.device, non_blocking=True) if cuda else self.metadata_host
+
+    @staticmethod
+    def _check_pair(x, out):
+        if x.ndim != 2 or out.ndim != 2 or x.shape[0] != out.shape[0]:
+            raise ValueError("each grouped pair needs x[M,K] and out[M,N]")
+        if x.dtype is not torch.bfloat16 or out.dtype is not torch.bfloat16:
+            raise ValueError("grouped GEMM inputs and outputs must be bf16")
+        if not (x.is_contiguous() and out.is_contiguous()):
+            raise ValueError("grouped GEMM pair matrices must be contiguous")
+        if x.device != out.device:
+            raise ValueError("a grouped pair's input/output must share a device")
 
 
 # ------------------------------------------------------------------------------------------ prefill products
@@ -263,35 +310,46 @@ def mxfp4_gemm_into(x: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor,
     return out
 
 
-def mxfp4_gemm_grouped_into(pairs_or_plan, blocks: torch.Tensor, scales: torch.Tensor, *, block_n=128, block_m=64,
-                            packed=None):
-    """One ragged GEMM launch writing each pair's own output slice (reference mxfp4_kernels.py:385-419).  Returns the
-    GroupedGemmPlan so a caller can reuse it.  Each output row gets exactly mxfp4_gemm's arithmetic."""
-    plan = (pairs_or_plan if isinstance(pairs_or_plan, GroupedGemmPlan)
-            else GroupedGemmPlan(pairs_or_plan, block_m=block_m))
-    if plan.block_m != block_m:
-        raise ValueError("plan block_m differs from the requested launch")
-    if not plan.ntiles:
-        return plan
+def _grouped_pool(plan, blocks, scales, packed):
+    """Check the pool views against a plan; returns the PS4 flag.  The messages are the reference's
+    (mxfp4_kernels.py:398-413), with this build's own limits (K = 2880, N a multiple of 192, aligned pairs)."""
     if blocks.ndim != 4 or blocks.shape[-1] != 16:
         raise ValueError("grouped blocks must have shape [capacity,N,GK,16]")
     cap, n, gk, _ = blocks.shape
-    if plan.K != gk * 32 or plan.N != n or max(plan.slots) >= cap:
+    if (plan.K, plan.N) != (gk * 32, n) or max(plan.slots) >= cap:
         raise ValueError("grouped plan dimensions or slots do not match the pool")
-    if (plan.device != blocks.device or scales.device != blocks.device or blocks.device.type != "cuda"):
+    if blocks.device.type != "cuda" or {plan.device, scales.device} != {blocks.device}:
         raise ValueError("grouped launch needs plan, blocks and scales on the same CUDA device")
-    if blocks.dtype is not torch.uint8 or scales.dtype is not torch.uint8:
+    if {blocks.dtype, scales.dtype} != {torch.uint8}:
         raise ValueError("grouped blocks and scales must be uint8")
-    if tuple(blocks.stride()[1:]) != (gk * 16, 16, 1) or scales.shape[:2] != (cap, n):
+    if blocks.stride()[1:] != (gk * 16, 16, 1) or tuple(scales.shape[:2]) != (cap, n):
         raise ValueError("grouped pool matrix rows must be contiguous and scales must match")
-    block_n = operator.index(block_n)
-    if block_n < 16 or block_n & (block_n - 1):
-        raise ValueError("block_n must be a power of two >= 16")
     if gk != GK_SUPPORTED or n % 192:
         raise ValueError(f"these kernels serve K = {GK_SUPPORTED * 32} and N a multiple of 192")
     if not plan.aligned:
         raise ValueError("pair rows must be 16-byte aligned (x and out addresses and row pitches)")
-    pk = _scale_layout(scales, gk, packed)
+    return _scale_layout(scales, gk, packed)
+
+
+def mxfp4_gemm_grouped_into(pairs_or_plan, blocks: torch.Tensor, scales: torch.Tensor, *, block_n=128, block_m=64,
+                            packed=None):
+    """One ragged GEMM launch writing each pair's own output slice (reference mxfp4_kernels.py:385-419).  Returns the
+    GroupedGemmPlan (built here from pairs, or the one passed in, whose block_m must match) so a caller can reuse
+    it.  Each output row gets exactly mxfp4_gemm's arithmetic.  block_n is validated as the reference does and
+    otherwise unused (the kernel tiles 192 weight rows)."""
+    if isinstance(pairs_or_plan, GroupedGemmPlan):
+        plan = pairs_or_plan
+        if plan.block_m != block_m:
+            raise ValueError("plan block_m differs from the requested launch")
+    else:
+        plan = GroupedGemmPlan(pairs_or_plan, block_m=block_m)
+    if plan.ntiles == 0:
+        return plan
+    bn = operator.index(block_n)
+    if bn < 16 or bn & (bn - 1):
+        raise ValueError("block_n must be a power of two >= 16")
+    pk = _grouped_pool(plan, blocks, scales, packed)
     N.call("na_mxfp4_gemm_grouped", blocks.data_ptr(), blocks.stride(0), scales.data_ptr(), scales.stride(0), int(pk),
-           plan.metadata.data_ptr(), plan.ntiles, plan.block_m, n, gk * 32, N.stream(blocks.device))
+           plan.metadata.data_ptr(), plan.ntiles, plan.block_m, blocks.shape[1], blocks.shape[2] * 32,
+           N.stream(blocks.device))
     return plan

@@ -9,8 +9,8 @@ The descriptor (neural_amd.moe.layout.prepacked_descriptor) is the store's ident
 fields, kernel and weight_repr strictly (a raw store is never opened with the PS4 layout or the other way round); the
 human-readable ``row`` label is informational.  Incompatible stores are rejected, never coerced.
 
-Layer files are memory-mapped read-only (copy-on-write private mappings); rows are handed out as views, so a
-retrieval is one contiguous copy.  No GPU work happens here: neural_amd.moe.gptoss_adapter.load_resident_store
+Layer files are memory-mapped (numpy memmaps, copy-on-write private pages by default); rows are handed out as views,
+so a retrieval is one contiguous copy.  No GPU work happens here: neural_amd.moe.gptoss_adapter.load_resident_store
 streams the rows into HBM and repacks them into the gfx950 tile layout.
 """
 from __future__ import annotations
@@ -25,6 +25,10 @@ from ..moe.layout import ExpertLayout, prepacked_descriptor
 
 FORMAT_MAGIC = "Q80-PREPACKED-SLOTS"
 FORMAT_VERSION = 1
+
+
+def _fail(reason: str, **extra) -> dict[str, Any]:
+    return {"status": "fail", "reason": reason, **extra}
 
 
 class Q80PrepackedStore:
@@ -95,61 +99,83 @@ class Q80PrepackedStore:
         return meta
 
     # ---- access --------------------------------------------------------------------------------------------------
+    def _read_metadata(self):
+        """(metadata dict, None) or (None, failure status)."""
+        path = self.root / "metadata.json"
+        if not path.is_file():
+            return None, _fail("no metadata.json")
+        try:
+            meta = json.loads(path.read_text(encoding="utf-8"))
+        except ValueError:
+            return None, _fail("metadata.json is not JSON")
+        if meta.get("magic") != FORMAT_MAGIC:
+            return None, _fail("bad magic")
+        if meta.get("version") != FORMAT_VERSION:
+            return None, _fail(f"version {meta.get('version')} != {FORMAT_VERSION}")
+        return meta, None
+
+    def _compare_descriptor(self, recorded):
+        """(note or None, None) when every field but the informational ``row`` label equals this runtime's layout
+        descriptor, else (None, failure status naming the differing fields, and both representations when the
+        weight_repr differs)."""
+        current = prepacked_descriptor(self.layout)
+        if not isinstance(recorded, dict):
+            return None, _fail("layout descriptor mismatch (no descriptor)")
+        structural = (set(current) | set(recorded)) - {"row"}
+        differs = sorted(k for k in structural if current.get(k) != recorded.get(k))
+        if differs:
+            status = _fail("layout descriptor mismatch (kernel/layout change)", differs=differs)
+            if "weight_repr" in differs:
+                status.update(store_weight_repr=recorded.get("weight_repr"),
+                              runtime_weight_repr=current.get("weight_repr"))
+            return None, status
+        if current.get("row") == recorded.get("row"):
+            return None, None
+        return (f"row label differs (store {recorded.get('row')!r} vs current {current.get('row')!r}); structural "
+                "fields, kernel and weight_repr all match"), None
+
+    def _map_layer(self, li: int, shared: bool):
+        """Layer li's file as a uint8 tensor view [n_experts, slot_bytes] over a memory map, or None when the file
+        is missing or not exactly n_experts * slot_bytes long."""
+        import numpy as np
+        import torch
+
+        L = self.layout
+        path = self.root / f"layer_{li}.slots"
+        if not path.is_file() or path.stat().st_size != L.n_experts * L.slot_bytes:
+            return None
+        # "c": private copy-on-write pages (the file is never written); "r+": a shared writable mapping
+        mm = np.memmap(path, dtype=np.uint8, mode="r+" if shared else "c", shape=(L.n_experts, L.slot_bytes))
+        return torch.from_numpy(mm)
+
     def open(self, *, expect_model_id: str | None = None, shared: bool = False) -> dict[str, Any]:
         """Validate and map the store (reference prepacked_store.py:149-207).  Returns {"status": "ok", "layers",
         "size_gib"[, "descriptor_note"]} or {"status": "fail", "reason", ...}: missing metadata, bad magic or
         version, a descriptor that differs in any structural field, kernel or weight_repr ("differs" names the
         fields; "store_weight_repr" / "runtime_weight_repr" when the representation differs), a different model
-        id, a layer file missing or of the wrong size.  shared=False maps copy-on-write (the file is never written)."""
-        import torch
-
-        mp = self.root / "metadata.json"
-        if not mp.is_file():
-            return {"status": "fail", "reason": "no metadata.json"}
-        try:
-            meta = json.loads(mp.read_text(encoding="utf-8"))
-        except ValueError:
-            return {"status": "fail", "reason": "metadata.json is not JSON"}
-        if meta.get("magic") != FORMAT_MAGIC:
-            return {"status": "fail", "reason": "bad magic"}
-        if meta.get("version") != FORMAT_VERSION:
-            return {"status": "fail", "reason": f"version {meta.get('version')} != {FORMAT_VERSION}"}
-        want = prepacked_descriptor(self.layout)
-        have = meta.get("layout")
-        if not isinstance(have, dict):
-            return {"status": "fail", "reason": "layout descriptor mismatch (no descriptor)"}
-        w = {k: v for k, v in want.items() if k != "row"}
-        h = {k: v for k, v in have.items() if k != "row"}
-        if w != h:
-            out = {"status": "fail", "reason": "layout descriptor mismatch (kernel/layout change)",
-                   "differs": sorted(k for k in set(w) | set(h) if w.get(k) != h.get(k))}
-            if w.get("weight_repr") != h.get("weight_repr"):
-                out["store_weight_repr"] = h.get("weight_repr")
-                out["runtime_weight_repr"] = w.get("weight_repr")
-            return out
-        note = None
-        if want.get("row") != have.get("row"):
-            note = (f"row label differs (store {have.get('row')!r} vs current {want.get('row')!r}); structural "
-                    "fields, kernel and weight_repr all match")
+        id, a layer file missing or of the wrong size.  shared=False maps copy-on-write (the file is never written).
+        Nothing is mapped unless every check passes."""
+        meta, failed = self._read_metadata()
+        if failed:
+            return failed
+        note, failed = self._compare_descriptor(meta.get("layout"))
+        if failed:
+            return failed
         if expect_model_id is not None and meta.get("model_id") != expect_model_id:
-            return {"status": "fail", "reason": "model identity mismatch"}
-        L = self.layout
-        expected = L.n_experts * L.slot_bytes
+            return _fail("model identity mismatch")
         maps = {}
-        for li in range(L.n_layers):
-            p = self.root / f"layer_{li}.slots"
-            if not p.is_file() or p.stat().st_size != expected:
-                return {"status": "fail", "reason": f"layer {li} missing/size"}
-            storage = torch.UntypedStorage.from_file(str(p), shared=shared, nbytes=expected)
-            t = torch.empty(0, dtype=torch.uint8)
-            t.set_(storage)
-            maps[li] = t.view(L.n_experts, L.slot_bytes)
-        self._maps = maps
-        self.meta = meta
-        out = {"status": "ok", "layers": L.n_layers, "size_gib": round(L.n_layers * expected / 1024 ** 3, 2)}
+        for li in range(self.layout.n_layers):
+            view = self._map_layer(li, shared)
+            if view is None:
+                return _fail(f"layer {li} missing/size")
+            maps[li] = view
+        self._maps, self.meta = maps, meta
+        L = self.layout
+        status = {"status": "ok", "layers": L.n_layers,
+                  "size_gib": round(L.n_layers * L.n_experts * L.slot_bytes / 2 ** 30, 2)}
         if note:
-            out["descriptor_note"] = note
-        return out
+            status["descriptor_note"] = note
+        return status
 
     def _layer(self, layer: int):
         if layer not in self._maps:
@@ -169,17 +195,18 @@ class Q80PrepackedStore:
         return self._layer(layer)
 
     def verify_layer(self, layer: int) -> bool:
-        """Re-hash a layer file against metadata.json's SHA-256 (corruption check)."""
+        """Re-read a layer file from disk and compare its SHA-256 with the one metadata.json records (a corruption
+        check; False also when no hash is recorded for the layer)."""
         if self.meta is None:
             raise RuntimeError("store not opened")
-        h = hashlib.sha256()
-        with open(self.root / f"layer_{layer}.slots", "rb") as f:
-            while True:
-                chunk = f.read(1 << 24)
-                if not chunk:
-                    break
-                h.update(chunk)
-        return h.hexdigest() == self.meta.get("sha256_per_layer", {}).get(str(layer))
+        recorded = self.meta.get("sha256_per_layer", {}).get(str(layer))
+        digest = hashlib.sha256()
+        block = bytearray(16 << 20)
+        view = memoryview(block)
+        with open(self.root / f"layer_{layer}.slots", "rb", buffering=0) as f:
+            while n := f.readinto(block):
+                digest.update(view[:n])
+        return digest.hexdigest() == recorded
 
     def biases(self):
         """(bias_gu, bias_dn) from expert_biases.pt, loaded with torch.load(weights_only=True) (nothing in the file

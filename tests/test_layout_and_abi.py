@@ -1,7 +1,9 @@
-"""CPU: store geometry and pool views (the reference's tests/test_scale_layout.py:44-116 restated for this
-package), ragged tile plans (tests/test_grouped_gemm_plan.py), and the C-ABI library: it loads and exports every
+"""CPU: slot geometry and pool views against the byte format (neural_amd/moe/layout.py; the reference's
+neural/moe/layout.py:17-212 and tools/scale_pack.py:6-12 define it), ragged tile plans (the contract of the
+reference's mxfp4_kernels.py:298-382), and the C-ABI library: it loads and exports every
 symbol include/neural_amd.h declares (no compute call: there is no GPU here)."""
 import ctypes
+import dataclasses
 import os
 import re
 
@@ -11,8 +13,8 @@ import torch
 
 from neural_amd import scale_pack as sp
 from neural_amd import synth
-from neural_amd.moe.layout import (GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4, ExpertLayout, gptoss_layout_for_repr,
-                                   mxfp4_pool_views, prepacked_descriptor)
+from neural_amd.moe.layout import (GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4, GPTOSS_LAYOUT_T950, MXFP4_REPRS, TILE_REPR,
+                                   ExpertLayout, gptoss_layout_for_repr, mxfp4_pool_views, prepacked_descriptor)
 from neural_amd.q80.mxfp4_kernels import GroupedGemmPlan, _grouped_tile_rows, _scale_layout
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -22,69 +24,125 @@ RAW_STORE_DESCRIPTOR = {"slot_bytes": 13219200, "n_layers": 36, "n_experts": 128
                         "kernel": "neural.q80.mxfp4_kernels (Triton, fp32-accum)", "weight_repr": "mxfp4_g32"}
 
 
-def test_layout_arithmetic():
-    assert GPTOSS_LAYOUT.slot_bytes == 13_219_200 == sp.RAW_SLOT_BYTES
-    assert GPTOSS_LAYOUT_PS4.slot_bytes == 12_839_040 == sp.PS4_SLOT_BYTES
-    assert GPTOSS_LAYOUT_PS4.gate_saz_bytes == 5760 * 46 and GPTOSS_LAYOUT_PS4.down_saz_bytes == 2880 * 46
-    assert GPTOSS_LAYOUT.gate_pack_bytes == GPTOSS_LAYOUT_PS4.gate_pack_bytes == 5760 * 1440
-    assert (GPTOSS_LAYOUT.scale_layout_mode, GPTOSS_LAYOUT_PS4.scale_layout_mode) == (0, 1)
-    assert GPTOSS_LAYOUT.is_mxfp4 and GPTOSS_LAYOUT_PS4.is_mxfp4
-    assert gptoss_layout_for_repr("mxfp4_g32") is GPTOSS_LAYOUT
-    assert gptoss_layout_for_repr("mxfp4_g32_ps4") is GPTOSS_LAYOUT_PS4
-    assert round(100 * (1 - 12_839_040 / 13_219_200), 2) == 2.88
-    with pytest.raises(KeyError):
-        gptoss_layout_for_repr("int4_g32")
-    with pytest.raises(ValueError):
-        ExpertLayout("q", 1, 1, 1, 64, 64, 64, 32, weight_repr="int4_g32")
+# Slot byte counts derived by hand from the format: a row of K = 2880 inputs has 90 groups of 32 E2M1 codes
+# (16 bytes each, 1,440 bytes per row), and either 90 E8M0 bytes (raw) or 1 base byte + 45 delta bytes (PS4).
+GATE_CODES = 5760 * 90 * 16            # 8,294,400
+DOWN_CODES = 2880 * 90 * 16            # 4,147,200
+RAW_SCALES = (5760 + 2880) * 90        # 777,600
+PS4_SCALES = (5760 + 2880) * (1 + 45)  # 397,440
+T950_SLOT = (5760 + 2880) // 16 * (22 * 1024 + 512 + 16 * 96)   # 540 blocks of 16 rows x 24,576 B
+
+
+def test_slot_bytes_derived_from_the_format():
+    assert GPTOSS_LAYOUT.slot_bytes == GATE_CODES + DOWN_CODES + RAW_SCALES == 13_219_200
+    assert GPTOSS_LAYOUT_PS4.slot_bytes == GATE_CODES + DOWN_CODES + PS4_SCALES == 12_839_040
+    assert GPTOSS_LAYOUT_T950.slot_bytes == T950_SLOT == 13_271_040
+    assert (sp.RAW_SLOT_BYTES, sp.PS4_SLOT_BYTES) == (13_219_200, 12_839_040)
+    for L, scale_row in ((GPTOSS_LAYOUT, 90), (GPTOSS_LAYOUT_PS4, 46)):
+        assert (L.off_down_codes, L.off_gate_scales) == (GATE_CODES, GATE_CODES + DOWN_CODES)
+        assert L.off_down_scales == GATE_CODES + DOWN_CODES + 5760 * scale_row
+        assert L.off_down_scales + L.down_saz_bytes == L.slot_bytes
+        assert (L.gate_groups, L.down_groups) == (90, 90)
+    assert GPTOSS_LAYOUT_PS4.scale_layout_mode == 1 and GPTOSS_LAYOUT.scale_layout_mode == 0
+    assert not GPTOSS_LAYOUT_T950.is_mxfp4            # not a store representation the views or the CPU kernels read
+
+
+def test_layout_rules_on_small_geometries():
+    # hidden 64 (2 groups), intermediate 96 (3 groups): raw is fine, PS4 needs an even group count per row
+    small = ExpertLayout("s", 1, 4, 2, hidden=64, gate_up_n=192, down_n=64, down_k=96)
+    assert small.slot_bytes == 192 * 2 * 16 + 64 * 3 * 16 + 192 * 2 + 64 * 3 == 9_792
+    with pytest.raises(AssertionError):
+        ExpertLayout("s", 1, 4, 2, hidden=64, gate_up_n=192, down_n=64, down_k=96, weight_repr="mxfp4_g32_ps4")
+    even = ExpertLayout("e", 1, 4, 2, hidden=128, gate_up_n=128, down_n=128, down_k=64, weight_repr="mxfp4_g32_ps4")
+    assert even.slot_bytes == 128 * 4 * 16 + 128 * 2 * 16 + 128 * 3 + 128 * 2 == 12_928
+    with pytest.raises(AssertionError):               # gate_up must stack gate | up over the intermediate
+        ExpertLayout("g", 1, 4, 2, hidden=64, gate_up_n=100, down_n=64, down_k=64)
+    with pytest.raises(ValueError):                   # the int4 / int8 representations are outside this path
+        ExpertLayout("q", 1, 4, 2, hidden=64, gate_up_n=128, down_n=64, down_k=64, weight_repr="int8_g32")
+    for bad in ("int4_g32", TILE_REPR, ""):            # only the two store representations have a gpt-oss layout
+        with pytest.raises(KeyError):
+            gptoss_layout_for_repr(bad)
+    assert [gptoss_layout_for_repr(r).weight_repr for r in MXFP4_REPRS] == list(MXFP4_REPRS)
 
 
 def test_descriptors():
     raw = prepacked_descriptor(GPTOSS_LAYOUT)
+    assert raw["row"] == "gate_codes|down_codes|gate_scales|down_scales"
     assert {k: v for k, v in raw.items() if k != "row"} == RAW_STORE_DESCRIPTOR
-    ps4 = prepacked_descriptor(GPTOSS_LAYOUT_PS4)
-    assert ps4["weight_repr"] == "mxfp4_g32_ps4" and ps4["slot_bytes"] == 12_839_040
-    diff = {k for k in set(raw) | set(ps4) if raw.get(k) != ps4.get(k)}
-    assert {"slot_bytes", "weight_repr", "kernel"} <= diff
+    ps4, t950 = prepacked_descriptor(GPTOSS_LAYOUT_PS4), prepacked_descriptor(GPTOSS_LAYOUT_T950)
+    assert set(raw) == set(ps4) == set(t950)
+    for d, L in ((ps4, GPTOSS_LAYOUT_PS4), (t950, GPTOSS_LAYOUT_T950)):
+        assert d["slot_bytes"] == L.slot_bytes and d["weight_repr"] == L.weight_repr
+        assert {k for k in raw if raw[k] != d[k]} == {"slot_bytes", "weight_repr", "kernel", "row"}
+    fewer = dataclasses.replace(GPTOSS_LAYOUT, n_experts=64)
+    assert {k for k, v in prepacked_descriptor(fewer).items() if raw[k] != v} == {"n_experts"}
 
 
-def _pools(cap=3, seed=1):
-    rng = np.random.default_rng(seed)
-    raws = [synth.slot_raw(rng) for _ in range(cap)]
-    return torch.from_numpy(np.stack(raws)), torch.from_numpy(np.stack([sp.pack_slot(r) for r in raws]))
+def test_pool_views_cover_each_slot_byte_once():
+    """Each view's offset, shape and strides, from the byte order gate codes | down codes | gate scales | down
+    scales, and the four views together tile the slot without a gap or an overlap."""
+    for L, w in ((GPTOSS_LAYOUT, 90), (GPTOSS_LAYOUT_PS4, 46)):
+        pool = torch.empty(3, L.slot_bytes, dtype=torch.uint8)
+        views = mxfp4_pool_views(pool, L)
+        want = [(0, (3, 5760, 90, 16), (L.slot_bytes, 1440, 16, 1)),
+                (GATE_CODES, (3, 2880, 90, 16), (L.slot_bytes, 1440, 16, 1)),
+                (GATE_CODES + DOWN_CODES, (3, 5760, w), (L.slot_bytes, w, 1)),
+                (GATE_CODES + DOWN_CODES + 5760 * w, (3, 2880, w), (L.slot_bytes, w, 1))]
+        spans = []
+        for v, (off, shape, stride) in zip(views, want):
+            assert (v.storage_offset(), tuple(v.shape), v.stride()) == (off, shape, stride)
+            assert v.untyped_storage().data_ptr() == pool.untyped_storage().data_ptr()
+            spans.append((off, off + int(np.prod(shape[1:]))))
+        assert [a for a, _ in spans[1:]] == [b for _, b in spans[:-1]] and spans[-1][1] == L.slot_bytes
+    with pytest.raises(AssertionError):                # a pool whose rows are not the layout's slot size
+        mxfp4_pool_views(torch.empty(2, GPTOSS_LAYOUT.slot_bytes, dtype=torch.uint8), GPTOSS_LAYOUT_PS4)
+    with pytest.raises(AssertionError):                # the tile layout has no store views
+        mxfp4_pool_views(torch.empty(1, T950_SLOT, dtype=torch.uint8), GPTOSS_LAYOUT_T950)
 
 
-def test_pool_views_place_the_scales():
-    raw_pool, pk_pool = _pools()
-    gb, db, gs, ds = mxfp4_pool_views(raw_pool, GPTOSS_LAYOUT)
-    gb2, db2, gs2, ds2 = mxfp4_pool_views(pk_pool, GPTOSS_LAYOUT_PS4)
-    assert gs.shape == (3, 5760, 90) and ds.shape == (3, 2880, 90)
-    assert gs2.shape == (3, 5760, 46) and ds2.shape == (3, 2880, 46)
-    assert gb.shape == gb2.shape == (3, 5760, 90, 16) and db.shape == db2.shape == (3, 2880, 90, 16)
-    assert gs.stride(0) == 13_219_200 and gs2.stride(0) == 12_839_040 and gs2.stride(1) == 46 and gs2.stride(2) == 1
-    for i in range(3):
-        assert torch.equal(gb[i], gb2[i]) and torch.equal(db[i], db2[i])
-        assert np.array_equal(sp.unpack_scale_rows(gs2[i].numpy()), gs[i].numpy())
-        assert np.array_equal(sp.unpack_scale_rows(ds2[i].numpy()), ds[i].numpy())
-    with pytest.raises(AssertionError):
-        mxfp4_pool_views(raw_pool, GPTOSS_LAYOUT_PS4)
+def test_pool_views_read_the_bytes_the_format_names():
+    """Individual codes and scales read through the views are the bytes at their hand-computed slot offsets; a PS4
+    row's base is its smallest exponent."""
+    rng = np.random.default_rng(2027)
+    raw = synth.slot_raw(rng)
+    pool = torch.from_numpy(np.stack([np.zeros_like(raw), raw]))
+    gb, db, gs, ds = mxfp4_pool_views(pool, GPTOSS_LAYOUT)
+    for n, g, b in ((0, 0, 0), (5759, 89, 15), (2880, 44, 7), (17, 3, 9)):
+        assert int(gb[1, n, g, b]) == raw[n * 1440 + g * 16 + b]
+        assert int(gs[1, n, g]) == raw[GATE_CODES + DOWN_CODES + n * 90 + g]
+    for n, g, b in ((0, 0, 0), (2879, 89, 15), (1234, 60, 1)):
+        assert int(db[1, n, g, b]) == raw[GATE_CODES + n * 1440 + g * 16 + b]
+        assert int(ds[1, n, g]) == raw[GATE_CODES + DOWN_CODES + 5760 * 90 + n * 90 + g]
+    ps4 = torch.from_numpy(sp.pack_slot(raw)[None])
+    _, _, gs2, ds2 = mxfp4_pool_views(ps4, GPTOSS_LAYOUT_PS4)
+    for n in (0, 777, 5759):
+        row = gs[1, n].numpy().astype(int)
+        base = int(gs2[0, n, 0])
+        assert base == row.min()
+        deltas = [(int(gs2[0, n, 1 + j // 2]) >> (4 * (j % 2))) & 15 for j in range(90)]
+        assert [base + d for d in deltas] == row.tolist()
+    assert int(ds2[0, 2879, 0]) == int(ds[1, 2879].min())
 
 
-def test_launchers_infer_the_layout_from_the_view():
-    raw_pool, pk_pool = _pools(cap=2)
-    _, _, gs, ds = mxfp4_pool_views(raw_pool, GPTOSS_LAYOUT)
-    _, _, gs2, ds2 = mxfp4_pool_views(pk_pool, GPTOSS_LAYOUT_PS4)
-    GK = 90
-    assert _scale_layout(gs, GK, None) is False and _scale_layout(ds, GK, None) is False
-    assert _scale_layout(gs2, GK, None) is True and _scale_layout(ds2, GK, None) is True
-    assert _scale_layout(gs, GK, False) is False and _scale_layout(gs2, GK, True) is True
-    with pytest.raises(ValueError):
-        _scale_layout(gs, GK, True)
-    with pytest.raises(ValueError):
-        _scale_layout(gs2, GK, False)
-    with pytest.raises(ValueError):
-        _scale_layout(torch.zeros(2, 8, 47, dtype=torch.uint8), GK, None)
-    with pytest.raises(ValueError):
-        _scale_layout(torch.zeros(2, 8, 180, dtype=torch.uint8)[:, :, ::2], GK, None)
+def test_scale_layout_reads_the_row_width():
+    GK = 4                                              # raw rows 4 bytes wide, PS4 rows 1 + 2
+    raw2d, ps42d = torch.zeros(7, 4, dtype=torch.uint8), torch.zeros(7, 3, dtype=torch.uint8)
+    assert _scale_layout(raw2d, GK, None) is False and _scale_layout(ps42d, GK, None) is True
+    assert _scale_layout(raw2d, GK, 0) is False and _scale_layout(ps42d, GK, 1) is True
+    with pytest.raises(ValueError, match="says raw"):
+        _scale_layout(raw2d, GK, True)
+    with pytest.raises(ValueError, match="says packed"):
+        _scale_layout(ps42d, GK, False)
+    with pytest.raises(ValueError, match="row width 5"):
+        _scale_layout(torch.zeros(7, 5, dtype=torch.uint8), GK, None)
+    with pytest.raises(ValueError, match="contiguous"):  # rows of 3 inside a pitch of 8
+        _scale_layout(torch.zeros(7, 8, dtype=torch.uint8)[:, :3], GK, None)
+    with pytest.raises(ValueError, match="contiguous"):  # a transposed view: unit stride across rows
+        _scale_layout(torch.zeros(3, 7, dtype=torch.uint8).t(), GK, None)
+    # the GPT-OSS pool views: 90 raw, 46 PS4, whatever the slot stride between experts
+    for L, want in ((GPTOSS_LAYOUT, False), (GPTOSS_LAYOUT_PS4, True)):
+        _, _, gs, ds = mxfp4_pool_views(torch.empty(2, L.slot_bytes, dtype=torch.uint8), L)
+        assert _scale_layout(gs, 90, None) is want and _scale_layout(ds, 90, want) is want
 
 
 # ------------------------------------------------------------------- ragged tile plans (contract: mxfp4_kernels.py:298-382)
@@ -220,6 +278,12 @@ def test_library_rejects_bad_arguments_without_launching():
     assert lib.na_mxfp4_gemv(None, 0, None, 0, None, 0, 0, None, 4, None, 0, None, 5760, 2880, 0, None, None) == -1
     assert lib.na_moe_decode(None, None, None, 1, None, 0, 0, None, 0, None, None, None, None, None,
                              ctypes.c_float(1.702), ctypes.c_float(7.0), 0, 0, None, None) == -1
+    # the fused attention block: every argument valid except a sync buffer that is not 16-byte aligned (its handoff
+    # words are 64-bit atomics), and a misaligned q; neither call reaches a launch
+    a, f = 1 << 20, ctypes.c_float
+    blk = lambda q, sync: lib.na_core_attn_block(a, None, None, a, a, a, a, a, a, a, a, 4352, 0, q, f(1e-5), f(1.0),  # noqa: E731
+                                                 a, f(0.125), 0, 32, a, a, a, a, a, a, a, a, a, a, a, sync, None, None)
+    assert blk(a, a + 8) == -1 and blk(a, a + 4) == -1 and blk(a + 2, a) == -1
 
 
 def test_product_code_never_touches_the_oracle():

@@ -1,8 +1,9 @@
 """The prepacked store reader/writer (neural_amd/q80/prepacked_store.py) and the gpt-oss adapter helpers
 (neural_amd/moe/gptoss_adapter.py) on the CPU.
 
-Mirrors the reference's store tests (tests/test_scale_layout.py:130-170, 300-370): layout_for_store on raw, PS4,
-missing, foreign and self-contradicting descriptors; a raw and a PS4 store of the same slots open with their own
+The contract is the reference's store behaviour (neural/q80/prepacked_store.py:149-230, gptoss_adapter.py:34-52):
+layout_for_store names the layout from the descriptor alone and refuses missing, unreadable, foreign and
+self-contradicting descriptors; a raw and a PS4 store of the same slots open with their own
 layout and are refused with the other one (naming both representations); strict identity checks (magic, version,
 model id, layer files); verify_layer catches a flipped byte; biases load through torch.load(weights_only=True).
 The dequant helper is bit-exact against the oracle's dequant; the installer dispatches one token to decode and more
@@ -20,42 +21,56 @@ import torch
 from neural_amd import scale_pack as sp
 from neural_amd import synth
 from neural_amd.moe import gptoss_adapter as GA
-from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4, prepacked_descriptor
-from neural_amd.q80.prepacked_store import FORMAT_MAGIC, FORMAT_VERSION, Q80PrepackedStore
+from neural_amd.moe.layout import GPTOSS_LAYOUT, GPTOSS_LAYOUT_PS4, GPTOSS_LAYOUT_T950
+from neural_amd.q80.prepacked_store import Q80PrepackedStore
 from oracle import mxfp4_oracle as mo
 
 MID = GA.GPTOSS_MODEL_ID
 
 
-def _write_meta(root, layout, model_id=MID):
-    os.makedirs(root, exist_ok=True)
-    meta = {"magic": FORMAT_MAGIC, "version": FORMAT_VERSION, "model_id": model_id,
-            "layout": prepacked_descriptor(layout), "sha256_per_layer": {}, "built_unix": 1, "build_seconds": 1.0}
-    with open(os.path.join(root, "metadata.json"), "w") as f:
-        json.dump(meta, f)
+def _metadata_only(root, layout, edit=None):
+    """A store directory holding only metadata.json for ``layout`` (build() over no layers), optionally edited."""
+    Q80PrepackedStore.build(root, None, model_id=MID, layout=layout, layers=())
+    if edit is not None:
+        p = os.path.join(root, "metadata.json")
+        meta = json.load(open(p))
+        edit(meta)
+        json.dump(meta, open(p, "w"))
+    return str(root)
 
 
-def test_layout_for_store(tmp_path):
-    _write_meta(str(tmp_path / "raw"), GPTOSS_LAYOUT)
-    _write_meta(str(tmp_path / "ps4"), GPTOSS_LAYOUT_PS4)
-    assert GA.layout_for_store(str(tmp_path / "raw")) is GPTOSS_LAYOUT
-    assert GA.layout_for_store(str(tmp_path / "ps4")) is GPTOSS_LAYOUT_PS4
-    with pytest.raises(RuntimeError):
-        GA.layout_for_store(str(tmp_path / "missing"))
-    bad = tmp_path / "bad"
-    _write_meta(str(bad), GPTOSS_LAYOUT)
-    meta = json.load(open(bad / "metadata.json"))
-    meta["layout"]["weight_repr"] = "int4_g32"                        # not a gpt-oss store representation
-    json.dump(meta, open(bad / "metadata.json", "w"))
-    with pytest.raises(RuntimeError):
-        GA.layout_for_store(str(bad))
-    lie = tmp_path / "lie"
-    _write_meta(str(lie), GPTOSS_LAYOUT_PS4)
-    meta = json.load(open(lie / "metadata.json"))
-    meta["layout"]["slot_bytes"] = 13_219_200                         # the descriptor contradicts itself
-    json.dump(meta, open(lie / "metadata.json", "w"))
-    with pytest.raises(RuntimeError):
-        GA.layout_for_store(str(lie))
+def test_layout_for_store_reads_the_descriptor_only(tmp_path):
+    raw = _metadata_only(tmp_path / "raw", GPTOSS_LAYOUT)
+    ps4 = _metadata_only(tmp_path / "ps4", GPTOSS_LAYOUT_PS4)
+    assert os.listdir(raw) == ["metadata.json"]          # no layer files: the layout comes from the metadata alone
+    assert GA.layout_for_store(raw) is GPTOSS_LAYOUT and GA.layout_for_store(ps4) is GPTOSS_LAYOUT_PS4
+    # a smaller store of the same representation still names the gpt-oss layout of that representation
+    few = _metadata_only(tmp_path / "few", dataclasses.replace(GPTOSS_LAYOUT_PS4, n_layers=2))
+    assert GA.layout_for_store(few) is GPTOSS_LAYOUT_PS4
+
+
+def test_layout_for_store_refuses_what_it_cannot_name(tmp_path):
+    os.makedirs(tmp_path / "empty")
+    (tmp_path / "garbled").mkdir()
+    (tmp_path / "garbled" / "metadata.json").write_text("{not json")
+    cases = {
+        "empty": str(tmp_path / "empty"),                                   # no metadata.json
+        "garbled": str(tmp_path / "garbled"),                               # unreadable JSON
+        "tiles": _metadata_only(tmp_path / "tiles", GPTOSS_LAYOUT_T950),    # this build's tile layout is no store
+        "no_layout": _metadata_only(tmp_path / "nl", GPTOSS_LAYOUT, lambda m: m.update(layout="mxfp4_g32")),
+        "no_repr": _metadata_only(tmp_path / "nr", GPTOSS_LAYOUT, lambda m: m["layout"].pop("weight_repr")),
+        # raw slot size under the PS4 name, and the other way round: the descriptor contradicts itself
+        "ps4_raw_size": _metadata_only(tmp_path / "c1", GPTOSS_LAYOUT_PS4,
+                                       lambda m: m["layout"].update(slot_bytes=13_219_200)),
+        "raw_ps4_size": _metadata_only(tmp_path / "c2", GPTOSS_LAYOUT,
+                                       lambda m: m["layout"].update(slot_bytes=12_839_040)),
+    }
+    for name, root in cases.items():
+        with pytest.raises(RuntimeError) as e:
+            GA.layout_for_store(root)
+        assert root in str(e.value), name
+    with pytest.raises(RuntimeError, match="12839040 != 13219200"):
+        GA.layout_for_store(cases["raw_ps4_size"])
 
 
 @pytest.fixture(scope="module")
