@@ -91,10 +91,21 @@ def lib() -> ctypes.CDLL:
     return _LIB
 
 
+ERR_RESIDENT = -4
+
+
 def call(name: str, *args) -> None:
     rc = getattr(lib(), name)(*args)
     if rc != 0:
         raise RuntimeError(f"{name}: {ERRORS.get(rc, 'error')} (status {rc})")
+
+
+def call_status(name: str, *args, allow=()) -> int:
+    """call() that returns the status instead of raising for the codes in ``allow``."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0 and rc not in allow:
+        raise RuntimeError(f"{name}: {ERRORS.get(rc, 'error')} (status {rc})")
+    return rc
 
 
 def stream(device=None) -> int:

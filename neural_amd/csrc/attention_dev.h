@@ -158,7 +158,7 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
       if (ring > 0 || hi < cache_rows) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-          if (kw + 16 * kb + n == hi) {
+          if (kw + 16 * kb + n >= hi) {   // every lane clamped to hi takes the step's row, as the cache read would
             kr[kb][0] = *reinterpret_cast<const uint4*>(rows + kRep * kHD + 8 * g);
             kr[kb][1] = *reinterpret_cast<const uint4*>(rows + kRep * kHD + 32 + 8 * g);
             vr[kb][0] = *reinterpret_cast<const uint4*>(rows + (kRep + 1) * kHD + 8 * g);

@@ -945,8 +945,9 @@ int na_core_attn_block(void* mid, const void* g, const float* c, void* xbuf, con
   if (c && !g) return kErrArgs;
   if (ring > 0 && (window <= 0 || ring < window || cache_rows != ring)) return kErrArgs;
   if (n_split <= 0 || n_split > kAttnMaxSplit || window < 0 || (n_split > 1 && !attn_work)) return kErrArgs;
+  // 16-byte rows for the vector accesses; the handoff words in sync are 64-bit device-coherent atomics
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc) |
-       reinterpret_cast<uintptr_t>(att)) & 15)
+       reinterpret_cast<uintptr_t>(att) | reinterpret_cast<uintptr_t>(sync)) & 15)
     return kErrArgs;
   AttnBlockArgs a{(uint16_t*)mid, (const uint16_t*)g, c, (uint16_t*)xbuf, (const uint16_t*)in_w,
                   (const uint16_t*)Wqkv, (const uint16_t*)bqkv, pos, inv_freq, (uint16_t*)kc, (uint16_t*)vc,

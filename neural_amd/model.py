@@ -187,6 +187,7 @@ class DecodeModel:
         self.attn_counters = z(NKV, dt=torch.int32)
         self.fused_attn = bool(fused_attn)
         self.sync = z(N.lib().na_core_attn_block_sync_words(), dt=torch.int32)   # fused block's handoff state
+        self.sync_redos = 0                  # generate() calls redone with the multi-launch path (sync_error())
         self.graph = None
 
     def _check_weights(self):
@@ -395,9 +396,17 @@ class DecodeModel:
 
     # ------------------------------------------------------------------------------------------------ graphs
     def sync_error(self) -> bool:
-        """Whether a fused attention block or a single-launch expert body ever gave up a wait (its outputs were then
-        invalid).  Reads the device."""
+        """Whether a fused attention block or a single-launch expert body gave up a wait since the last
+        clear_sync_error() (the outputs of that step are then invalid).  Reads the device (synchronises).  The
+        waits rely on every workgroup of a launch being resident together, which a kernel of another stream or
+        process on the same GPU can break; a caller replaying captured steps (run(), capture()) polls this after
+        its replays and redoes them with the multi-launch path on True, as generate() does."""
         return bool(int(self.sync[0].item())) or self.rx.sync_error()
+
+    def clear_sync_error(self) -> None:
+        """Zero the error words (the kernels only ever set them)."""
+        self.sync[:1].zero_()
+        self.rx.clear_sync_error()
 
     def capture(self) -> torch.cuda.CUDAGraph:
         """Capture one step as a hipGraph (replay = one greedy step at the device-side position).  The capture itself
@@ -409,7 +418,8 @@ class DecodeModel:
         return g
 
     def run(self, n_steps: int, graph: bool = True) -> None:
-        """n_steps decode steps from the current device state (graph replays when a graph was captured)."""
+        """n_steps decode steps from the current device state (graph replays when a graph was captured).  Nothing is
+        checked here: the caller reads sync_error() afterwards (generate() does, and redoes the steps)."""
         if graph:
             if self.graph is None:
                 self.capture()
@@ -425,7 +435,24 @@ class DecodeModel:
         p = torch.as_tensor(prompt, dtype=torch.int64).reshape(-1)
         if p.numel() < 1 or p.numel() + n_new > self.smax:
             raise ValueError("prompt must be non-empty and prompt + n_new must fit smax")
+        n_steps = p.numel() - 1 + n_new
         self.reset(p)
-        self.run(p.numel() - 1 + n_new, graph)
+        self.run(n_steps, graph)
         torch.cuda.synchronize(self.dev)
+        if self.sync_error():
+            # a bounded wait gave up somewhere, so some step used stale data: decode again from the prompt with the
+            # multi-launch path (separate QKV / attention / o_proj / router launches and the two-launch expert
+            # body: the same bits, and no wait between workgroups)
+            self.sync_redos += 1
+            self.clear_sync_error()
+            fused, one = self.fused_attn, self.rx.one
+            self.fused_attn, self.rx.one = False, False
+            try:
+                self.reset(p)
+                self.run(n_steps, graph=False)
+                torch.cuda.synchronize(self.dev)
+            finally:
+                self.fused_attn, self.rx.one = fused, one
+            if self.sync_error():
+                raise RuntimeError("the multi-launch decode path flagged its error word (it has no waits to give up)")
         return self.seq[:p.numel() + n_new].cpu()

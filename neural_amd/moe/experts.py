@@ -66,8 +66,16 @@ class ResidentExperts:
                      else None)
 
     def sync_error(self) -> bool:
-        """Whether a wait of the single-launch path ever gave up (reads one device word: synchronises)."""
+        """Whether a wait of the single-launch path ever gave up, so that some output since the last
+        clear_sync_error() may be wrong (reads one device word: synchronises).  The waits can give up only if the
+        launch's 720 workgroups are not all resident at once, e.g. under another process's kernels on the same
+        GPU; callers that replay captured graphs poll this after their replays."""
         return bool(self.sync is not None and int(self.sync[0].item()) != 0)
+
+    def clear_sync_error(self) -> None:
+        """Zero the error word (the kernels only ever set it); stream-ordered, capturable."""
+        if self.sync is not None:
+            self.sync[:1].zero_()
 
     def forward_decode(self, layer: int, hidden: torch.Tensor, router_indices: torch.Tensor,
                        routing_weights: torch.Tensor, out: torch.Tensor | None = None, events=None) -> torch.Tensor:
@@ -96,12 +104,17 @@ class ResidentExperts:
         elif out.dtype is not torch.bfloat16 or tuple(out.shape) != (B, L.hidden) or not out.is_contiguous():
             raise ValueError("out must be contiguous bf16 [B, hidden]")
         if self.one and B == 1:
-            N.call("na_moe_decode_t950_one", hidden.data_ptr(), router_indices.data_ptr(), routing_weights.data_ptr(),
-                   self.pool.data_ptr(), L.slot_bytes, N.ptr(self.slot_tab), layer * L.n_experts,
-                   N.ptr(self.bias_gu), N.ptr(self.bias_dn), self.h.data_ptr(), self.yw.data_ptr(), out.data_ptr(),
-                   float(L.act_alpha), float(L.act_limit), self.sync.data_ptr(), N.events_array(events),
-                   N.stream(hidden.device))
-            return out
+            rc = N.call_status("na_moe_decode_t950_one", hidden.data_ptr(), router_indices.data_ptr(),
+                               routing_weights.data_ptr(), self.pool.data_ptr(), L.slot_bytes, N.ptr(self.slot_tab),
+                               layer * L.n_experts, N.ptr(self.bias_gu), N.ptr(self.bias_dn), self.h.data_ptr(),
+                               self.yw.data_ptr(), out.data_ptr(), float(L.act_alpha), float(L.act_limit),
+                               self.sync.data_ptr(), N.events_array(events), N.stream(hidden.device),
+                               allow=(N.ERR_RESIDENT,))
+            if rc == 0:
+                return out
+            # the device cannot hold all 720 workgroups at once (a smaller partition): nothing was launched; from
+            # now on this object takes the two-launch form, which gives the same bits
+            self.one = False
         if self.tiled:
             N.call("na_moe_decode_t950", hidden.data_ptr(), router_indices.data_ptr(), routing_weights.data_ptr(), B,
                    self.pool.data_ptr(), L.slot_bytes, N.ptr(self.slot_tab), layer * L.n_experts,

@@ -130,18 +130,20 @@ def test_sliding_ring_equals_linear_and_oracle():
     assert not bad, bad[:10]
 
 
-@pytest.mark.parametrize("sliding,ns", [(0, 16), (128, 1)])
-def test_batched_sequences(sliding, ns):
+@pytest.mark.parametrize("S,sliding,ns", [(4096, 0, 16), (4096, 128, 1), (8192, 0, 16), (8192, 0, 32),
+                                          (8192, 128, 1)])
+def test_batched_sequences(S, sliding, ns):
+    """Configuration 3's batch of 4 sequences, each at its own position (up to the last row of an 8192-row cache)."""
     import torch
     from neural_amd import attention as A
     dev = _dev()
-    B, S = 4, 4096
-    rng = np.random.default_rng(21 + ns)
+    B = 4
+    rng = np.random.default_rng(21 + ns + S)
     k, v = _cache(rng, B, S)
     sinks = rb(rng.standard_normal(NQ).astype(np.float32))
     q = rb(rng.standard_normal((B, NQ * HD)).astype(np.float32))
-    pos = np.array([4095, 17, 1024, 3000], np.int64)
-    print(f"case attention batched B={B} sliding={sliding} ns={ns}", flush=True)
+    pos = np.array([4095, 17, 1024, 3000] if S == 4096 else [8191, 63, 5000, 8128], np.int64)
+    print(f"case attention batched B={B} S={S} sliding={sliding} ns={ns}", flush=True)
     out = torch.empty(B, NQ * HD, dtype=torch.bfloat16, device=dev)
     split = A.SplitAttn(ns, S, dev, batch=B) if ns > 1 else None
     A.decode_attention_batched(_t(q, dev), _t(k, dev), _t(v, dev), _t(sinks, dev), torch.from_numpy(pos).to(dev),

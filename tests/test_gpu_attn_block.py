@@ -5,7 +5,8 @@ Bar: bit-identical outputs (q, the K / V rows, xbuf, att, mid, hn, router logits
 over consecutive decode steps of a 2-layer model with a sliding layer on a 16-row ring and a full layer, for the full
 layer's attention in 1, 4 and 32 chunks (chunks past the position are empty), across the ring wrap; each launch
 leaves its split counters at zero, advances its generation word (the tag of its handoff words) by one and leaves the
-error flag clear; graph replays equal eager steps.
+error flag clear; graph replays equal eager steps.  The same bar at configuration 4's geometry (window 128 on a
+128-row ring, 4360 cache rows, 32 chunks) after a 4090-token prefill, across two ring wraps.
 """
 import numpy as np
 import pytest
@@ -86,3 +87,43 @@ def test_fused_block_graph_replay_equals_eager(parts):
     assert torch.equal(eager, first) and torch.equal(first, again)
     err, gen, counters = _sync_state(fa.sync)
     assert not fa.sync_error() and err == 0 and counters == 0 and gen > 0
+
+
+def test_fused_block_equals_four_launches_at_model_size(parts):
+    """Configuration 4's attention geometry: a sliding layer with window 128 on a 128-row ring and a full layer of
+    4360 cache rows whose attention runs in 32 chunks.  A 4090-token context is prefilled into both models' caches
+    (the same kernels, so the caches start equal), then 140 greedy steps at positions 4090 .. 4229 (the ring wraps
+    at 4096 and 4224): every output of every layer and the caches bit for bit, the error word clear."""
+    import torch
+    from neural_amd.model import DecodeModel, random_weights
+    print("case attention block fused vs 4 launches at window 128, smax 4360, n_split 32", flush=True)
+    w = random_weights(n_layers=2, vocab=VOCAB, device="cpu", seed=23, window=128, norm_std=0.1).to(parts["dev"])
+    assert [ly.sliding for ly in w.layers] == [128, 0]
+    fa = DecodeModel(w, parts["rx"], smax=4360, n_split=32, fused_attn=True)
+    fb = DecodeModel(w, parts["rx"], smax=4360, n_split=32, fused_attn=False)
+    assert fa.ring == 128 and tuple(fa.kc[0].shape) == (1, 8, 128, 64) and tuple(fa.kc[1].shape) == (1, 8, 4360, 64)
+    prompt = np.random.default_rng(4090).integers(0, VOCAB, 4090)
+    for m in (fa, fb):
+        m.prefill(prompt)
+    torch.cuda.synchronize()
+    for li in range(2):
+        assert torch.equal(fa.kc[li], fb.kc[li]) and torch.equal(fa.vc[li], fb.vc[li]), li
+    assert int(fa.pos.item()) == 4090 and torch.equal(fa.seq, fb.seq)
+    for step in range(140):
+        for m in (fa, fb):
+            m.embed()
+        for li in range(2):
+            fa.layer(li)
+            fb.layer(li)
+            torch.cuda.synchronize()
+            for nm in ("q", "att", "xbuf", "mid", "hn", "ids", "wts", "g"):
+                assert torch.equal(getattr(fa, nm), getattr(fb, nm)), (4090 + step, li, nm)
+            assert torch.equal(fa.kc[li], fb.kc[li]) and torch.equal(fa.vc[li], fb.vc[li]), (4090 + step, li)
+        for m in (fa, fb):
+            m.tail()
+        torch.cuda.synchronize()
+        assert int(fa.tok.item()) == int(fb.tok.item()), 4090 + step
+    assert torch.equal(fa.seq, fb.seq) and int(fa.pos.item()) == 4230
+    assert not fa.sync_error()
+    err, _, counters = _sync_state(fa.sync)
+    assert err == 0 and counters == 0

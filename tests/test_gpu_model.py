@@ -345,3 +345,20 @@ def test_graph_replay_matches_eager(tiny):
     again = m.generate(prompt, NEW, graph=True)          # replays of the same graph from a reset state
     assert torch.equal(eager, first) and torch.equal(first, again)
     assert int(m.attn_counters.abs().sum()) == 0 and int(m.r_counter.item()) == 0
+
+
+def test_generate_redoes_a_flagged_decode(tiny):
+    """An error word raised by a bounded wait makes generate() decode again with the multi-launch path; the words
+    are planted from the host (no kernel is made to give up a wait), and the tokens equal the unflagged run's."""
+    import torch
+    m = tiny["model"]
+    print("case generate with a planted error word", flush=True)
+    prompt = np.random.default_rng(82).integers(0, VOCAB, PROMPT)
+    want = m.generate(prompt, NEW, graph=True)
+    assert not m.sync_error() and m.sync_redos == 0
+    for words in (m.sync, m.rx.sync):
+        words[:1].fill_(1)
+        got = m.generate(prompt, NEW, graph=True)
+        assert torch.equal(got, want)
+        assert not m.sync_error() and m.fused_attn and m.rx.one
+    assert m.sync_redos == 2
