@@ -31,11 +31,19 @@ and mfma (the matrix cores' issue rate for the scaled FP8 x FP4 and the bf16 ins
 """
 from __future__ import annotations
 
-import argparse
-import json
 import os
-import sys
-import time
+
+# The reference server's OpenMP settings for its CPU expert kernels (server.py:25 sets GOMP_SPINCOUNT before torch
+# loads libgomp); threads bound close to the master.  They must be in the environment before libgomp is loaded,
+# i.e. before torch is imported, or they have no effect on the CPU baseline below.
+os.environ.setdefault("GOMP_SPINCOUNT", "20000000")
+os.environ.setdefault("OMP_PROC_BIND", "close")
+
+import argparse  # noqa: E402
+import json  # noqa: E402
+import statistics  # noqa: E402
+import sys  # noqa: E402
+import time  # noqa: E402
 
 import numpy as np
 
@@ -73,13 +81,30 @@ def measured_traffic(kernel, layout, batch, k_split):
             tab = json.load(fh)
     except (OSError, ValueError):
         return None, "no traffic table"
+    e = traffic_entry(tab, kernel, layout, batch, k_split)
+    if e is None:
+        return None, "workload not in traffic table, or measured on other kernel sources"
+    return int(e["hbm_bytes_per_launch"]), "ok"
+
+
+def traffic_entry(tab, kernel, layout, batch, k_split):
+    """The committed profile entry of a workload, if it was measured on the current kernel sources."""
     sha = sources_sha256()
     for e in tab.get("entries", []):
         if (e["kernel"], e["layout"], e["batch"], e["k_split"]) == (kernel, layout, batch, k_split):
-            if e["sources_sha256"] != sha:
-                return None, "traffic table measured on other kernel sources"
-            return int(e["hbm_bytes_per_launch"]), "ok"
-    return None, "workload not in traffic table"
+            return e if e["sources_sha256"] == sha else None
+    return None
+
+
+def rocprof_avg_us(kernel, layout, batch, k_split):
+    """The kernel's average duration from the committed rocprofv3 --kernel-trace --stats run of the same workload on
+    the current kernel sources (profiles/traffic.json, "rocprof_avg_us"), or None."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            e = traffic_entry(json.load(fh), kernel, layout, batch, k_split)
+    except (OSError, ValueError):
+        return None
+    return e.get("rocprof_avg_us") if e else None
 
 
 def effective_k_split(k_split, batch):
@@ -135,7 +160,8 @@ def cpu_info():
                 quota = max(1, int(int(q) // int(per)))
     except (OSError, ValueError):
         pass
-    return {"model": model, "sockets": len(sockets) or None, "socket0_physical_cores": len(cores0) or None,
+    return {"model": model, "model_name_line": f"model name\t: {model}" if model else None,
+            "sockets": len(sockets) or None, "socket0_physical_cores": len(cores0) or None,
             "affinity_cpus": usable, "cgroup_cpus": quota, "usable_cpus": min(usable, quota or usable)}
 
 
@@ -168,55 +194,69 @@ def host_expert_slots(pool_dev, ids, n=160):
     return out
 
 
-def cpu_baseline(host, threads, seconds=10.0):
-    """The reference C kernel on ``threads`` host cores: gptoss_experts(4, ...) per token per layer (the reference has
-    no batched CPU decode), rotating over the host expert copies so that every call reads cold slots."""
+def cpu_baselines(pool_dev, ids, seconds):
+    """The reference's C expert kernel on this host: configuration 1's expert body, gptoss_experts(4, ...) per token
+    per layer (the reference has no batched CPU decode), over a 160-expert host copy (2.1 GB) rotated per call so
+    that every call reads cold slots.  Timed as the reference's own A/B tool times kernels
+    (tools/kernel_tuning_ab.py:130-158): every configuration once per round, rounds interleaved (the order reversed
+    on odd rounds), 6 rounds of warm-up, then the median wall-clock time per call over at least 30 rounds (as many as
+    fit ``seconds``).  Configurations: the AVX-512 build of gptoss_cpu_multi.c (the server's library) and the
+    portable AVX2 build (gptoss_cpu_portable.c), each at all physical cores of the first socket (capped at the CPUs
+    this process may use) and at 8 threads (the reference server's default, server.py:107).  OMP_PROC_BIND and
+    GOMP_SPINCOUNT are set at the top of this file, before libgomp loads."""
     from oracle.refkernels import RefExperts, cpu_has
 
-    name = "multi" if cpu_has("avx512f") else "portable"
-    ref = RefExperts(name)
+    info = cpu_info()
+    host = host_expert_slots(pool_dev, ids)
+    t_sock = min(info["socket0_physical_cores"] or info["usable_cpus"], info["usable_cpus"])
+    libs = (["multi"] if cpu_has("avx512f") else []) + ["portable"]
+    configs = [(lib, t) for lib in libs for t in ([t_sock] + ([8] if t_sock != 8 else []))]
+    refs = {lib: RefExperts(lib) for lib in libs}
     rng = np.random.default_rng(5)
     x = rng.standard_normal(H).astype(np.float32)
     bgu = [np.zeros(5760, np.float32)] * 4
     bdn = [np.zeros(2880, np.float32)] * 4
     w = np.full(4, 0.25, np.float32)
     scratch = np.zeros(4 * (5760 + 3 * H) + H + 64, np.float32)
-    ref.experts(host[:4], x, bgu, bdn, w, threads=threads, scratch=scratch)      # warm-up (thread pool start)
-    n, t0 = 0, time.perf_counter()
+    times = {c: [] for c in configs}
+    k, rounds, t_start, warm = 0, 0, time.perf_counter(), 6
     while True:
-        sel = [host[(4 * n + j) % len(host)] for j in range(4)]
-        ref.experts(sel, x, bgu, bdn, w, threads=threads, scratch=scratch)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and n >= N_LAYERS:
+        for c in (configs if rounds % 2 == 0 else configs[::-1]):
+            sel = [host[(k + j) % len(host)] for j in range(4)]
+            k += 4
+            t0 = time.perf_counter()
+            refs[c[0]].experts(sel, x, bgu, bdn, w, threads=c[1], scratch=scratch)
+            dt = time.perf_counter() - t0
+            if rounds >= warm:
+                times[c].append(dt)
+        rounds += 1
+        if rounds >= warm + 30 and time.perf_counter() - t_start >= seconds:
             break
-    t_call = el / n
-    return {"value": round(1.0 / (N_LAYERS * t_call), 3), "unit": "tok/s", "cores": threads, "kind": "reference",
-            "library": f"libgptoss_{name}.so",
-            "sample": f"{n} calls of gptoss_experts(E=4) ({threads} OpenMP threads) over a {len(host)}-expert host "
-                      f"copy rotated per call; one call = the expert body of one layer for one token; "
-                      f"{t_call * 1e3:.3f} ms/call; tok/s = 1 / (36 x ms/call) (experts only: the reference has no "
-                      f"CPU dense core)",
-            "ms_per_call": round(t_call * 1e3, 4), "gbps": round(4 * SLOT_ALGO_BYTES / t_call / 1e9, 2)}
 
+    def summary(c):
+        med = statistics.median(times[c])
+        return {"value": round(1.0 / (N_LAYERS * med), 3), "cores": c[1], "ms_per_call": round(med * 1e3, 4),
+                "mean_ms_per_call": round(statistics.fmean(times[c]) * 1e3, 4),
+                "gbps": round(4 * SLOT_ALGO_BYTES / med / 1e9, 2), "calls": len(times[c])}
 
-def cpu_baselines(pool_dev, ids, seconds):
-    """cpu_baseline at all physical cores of the first socket (capped at the usable CPUs) and at 8 threads (the
-    reference server's default, server.py:107), with the host CPU described."""
-    info = cpu_info()
-    host = host_expert_slots(pool_dev, ids)
-    t_sock = min(info["socket0_physical_cores"] or info["usable_cpus"], info["usable_cpus"])
-    os.environ.setdefault("OMP_PROC_BIND", "close")
-    main = cpu_baseline(host, t_sock, seconds)
-    res = dict(main)
+    main_c = configs[0]
+    res = {**summary(main_c), "unit": "tok/s", "kind": "reference", "library": f"libgptoss_{main_c[0]}.so",
+           "sample": (f"median of {len(times[main_c])} interleaved calls of gptoss_experts(E=4) ({main_c[1]} OpenMP "
+                      f"threads) over a {len(host)}-expert host copy rotated per call, after {warm} warm-up rounds; "
+                      "one call = the expert body of one layer for one token; tok/s = 1 / (36 x median ms/call) "
+                      "(experts only: the reference has no CPU dense core)")}
+    for c in configs[1:]:
+        key = ("threads_8" if c[1] == 8 else "all_cores") if c[0] == main_c[0] else \
+            (f"{c[0]}_threads_8" if c[1] == 8 else f"{c[0]}_all_cores")
+        res[key] = {**summary(c), "library": f"libgptoss_{c[0]}.so"}
     res["cpu"] = info
+    res["omp_env"] = {k: os.environ.get(k) for k in ("OMP_PROC_BIND", "GOMP_SPINCOUNT")}
     res["threads_rule"] = (f"min(physical cores of socket 0 = {info['socket0_physical_cores']}, CPUs this process "
                            f"may use = {info['usable_cpus']})")
-    res["build"] = ("oracle/Makefile from the reference's kernels/*.c, gcc -O3 -fopenmp; libgptoss_multi.so adds "
-                    "-Dsb_inited=1, a declaration kernels/gptoss_cpu_cap2.c:113 makes only on Win32")
-    if t_sock != 8:
-        t8 = cpu_baseline(host, 8, seconds)
-        res["threads_8"] = {k: t8[k] for k in ("value", "cores", "ms_per_call", "gbps")}
+    res["build"] = ("oracle/Makefile from the reference's kernels/*.c: gptoss_cpu_multi.c with gcc -O3 -fopenmp "
+                    "-mavx2 -mfma -mavx512{f,bw,dq,vl} -Dsb_inited=1 (a declaration kernels/gptoss_cpu_cap2.c:113 "
+                    "makes only on Win32); gptoss_cpu_portable.c with the reference's flags -O3 -ffp-contract=off "
+                    "-fopenmp -mavx2 -mfma")
     return res
 
 
@@ -472,6 +512,24 @@ def run_model(A, pool, dev):
     avg = {nm: acc[nm] / n_l for nm in names}
     log("model: per launch " + ", ".join(f"{nm} {v:.2f} us" for nm, v in avg.items())
         + f", attention full {att_full / (n_l / 2):.2f} us, sliding {att_slide / (n_l / 2):.2f} us")
+    attn_roof = None
+    if not A.unfused_attn:
+        # the attention block's algorithmic bytes: Q|K|V, o_proj and router weights with their biases, the two norm
+        # weights and the sinks, plus the K and V cache rows its attention reads (128 ring rows on a sliding layer,
+        # positions 0 .. p on a full layer, p averaged over the R timed steps)
+        blk_w = 2 * (5120 * 2880 + 5120 + 2880 * 4096 + 2880 + 128 * 2880 + 128 + 2 * 2880 + 64)
+        p_avg = ctx + (R - 1) / 2
+        kinds = {"sliding": (att_slide / (n_l / 2), blk_w + 2 * 2 * 8 * 64 * 128),
+                 "full": (att_full / (n_l / 2), blk_w + 2 * 2 * 8 * 64 * (p_avg + 1))}
+        per = {k: {"avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": int(b),
+                   "gbps": round(b / us / 1e3, 1), "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+               for k, (us, b) in kinds.items()}
+        tot_b, tot_us = sum(b for _, b in kinds.values()), sum(us for us, _ in kinds.values())
+        attn_roof = {"kernel": "k_attn_block", "bound": "hbm", "achieved": round(tot_b / tot_us / 1e3, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
+                     "traffic": None, **per,
+                     "workload": f"config4 decode step at context {ctx}: one sliding and one full layer's block "
+                                 "(18 of each per token), dispatch-stamped events over eager steps"}
     dense = N_LAYERS * 2 * (5120 * 2880 + 2880 * 4096 + 128 * 2880) + 2 * 201088 * 2880
     experts = N_LAYERS * TOPK * SLOT_ALGO_BYTES
     kv = 2 * 2 * 8 * 64 * (18 * (ctx + n_new / 2) + 18 * 128)
@@ -493,7 +551,7 @@ def run_model(A, pool, dev):
                "prefill_chunk": A.prefill_chunk} if A.context_mode == "prefill" else
               {"context_steps_per_s": round((ctx - 1) / t_ctx, 1)})}
     out = {"tok_s": tok_s, "ms_per_step": el / n_new * 1e3, "config": cfg, "gate_up_us": avg[names[0]],
-           "expert_label": names[0]}
+           "expert_label": names[0], "attn_roofline": attn_roof}
     del model, w, rx
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
@@ -514,9 +572,12 @@ def expert_roofline(label, avg_us, k_split):
     gbps = nbytes / (avg_us * 1e-6) / 1e9
     traffic, why = measured_traffic(kname, "t950", 1, effective_k_split(k_split, 1))
     log(f"traffic: {traffic} ({why})")
+    rp = rocprof_avg_us(kname, "t950", 1, effective_k_split(k_split, 1))
     return {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kname,
-            "avg_launch_us": round(avg_us, 3), "algorithmic_bytes_per_launch": nbytes}
+            "avg_launch_us": round(avg_us, 3), "algorithmic_bytes_per_launch": nbytes,
+            # the same bytes over rocprofv3's average duration of the kernel (includes its per-dispatch cost)
+            "rocprof_avg_launch_us": rp, "frac_rocprof": round(nbytes / (rp * 1e3) / HBM_PEAK_GBS, 4) if rp else None}
 
 
 def bench_model(A):
@@ -534,7 +595,7 @@ def bench_model(A):
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic", "config": m["config"],
            "roofline": {**expert_roofline(m["expert_label"], m["gate_up_us"], A.k_split),
                         "workload": "config4 decode step"},
-           "cpu_baseline": None}
+           "roofline_config4_attention": m["attn_roofline"], "cpu_baseline": None}
     print(json.dumps(res), flush=True)
 
 
@@ -774,7 +835,8 @@ def bench_decode(A):
     res = {"metric": METRIC, "value": round(m4["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": A.steps,
            "warmup": A.warmup, "ms_per_step": round(m4["ms_per_step"], 4), "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "numerics": NUMERICS, "data": "synthetic",
-           "config": cfg, "roofline": roof, "cpu_baseline": cpu}
+           "config": cfg, "roofline": roof, "roofline_config4_attention": m4["attn_roofline"],
+           "cpu_baseline": cpu}
     print(json.dumps(res), flush=True)
 
 
