@@ -38,6 +38,9 @@ import os
 # i.e. before torch is imported, or they have no effect on the CPU baseline below.
 os.environ.setdefault("GOMP_SPINCOUNT", "20000000")
 os.environ.setdefault("OMP_PROC_BIND", "close")
+# The CPUs this process may use, read before libgomp loads: with OMP_PROC_BIND set, libgomp binds the main thread to
+# one CPU when it initialises, after which the main thread's affinity mask names only that CPU.
+START_AFFINITY = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
 
 import argparse  # noqa: E402
 import json  # noqa: E402
@@ -151,7 +154,7 @@ def cpu_info():
                     cores0.add(v)
     except OSError:
         pass
-    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    usable = START_AFFINITY
     quota = None
     try:
         with open("/sys/fs/cgroup/cpu.max") as fh:
