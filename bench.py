@@ -793,9 +793,9 @@ def config1_summary(m, L, B):
 
 
 NUMERICS = ("weights MXFP4 (E2M1 codes x E8M0 scales, consumed as stored by the block-scaled MFMA, exact); activations "
-            "bf16, fed to the MFMA as two exact E4M3 rows (hi + lo) per bf16 row: exact for every element within 2^13 "
-            "of its 32-element block's largest magnitude (x), and for every |h| >= 2^-9 between the expert products "
-            "(fixed scales); fp32 accumulation, bf16 outputs at the reference's rounding points")
+            "bf16 (x, and h between the expert products), fed to the MFMA as two E4M3 rows (hi + lo) per bf16 row "
+            "with one E8M0 scale per 32-element block: exact for every element within 2^13 of its block's largest "
+            "magnitude; fp32 accumulation, bf16 outputs at the reference's rounding points")
 
 
 def bench_decode(A):

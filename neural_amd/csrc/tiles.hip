@@ -235,43 +235,15 @@ NA_DEVICE void x_load(int tid, const uint16_t* base, long long row_stride, RowOf
   }
 }
 
-// ---- h between the gate_up and down kernels, as E4M3 with two fixed scales.  The clamped SwiGLU bounds |h| by
-// (limit + 1) x max(limit, 1 / alpha) (gate <= limit, |up + 1| <= limit + 1, and |gate sigma(alpha gate)| < 0.28 /
-// alpha for gate < 0), so s_hi = 2^(e - 7) of that bound (x8_scale_byte) keeps every |h| / s_hi below 256, and the
-// remainder h - hi s_hi (at most 8 s_hi) over s_lo = s_hi / 32 stays at most 256.  hi s_hi + lo s_lo equals h exactly
-// when h's lowest bit lies on lo's grid (s_hi 2^-14; for limit 7, alpha 1.702: every |h| >= 2^-9) and to within half
-// of it below.  Per pair: one row of 2880 hi codes, then one of 2880 lo codes (the bytes of a 2880 x bf16 row).
-constexpr int kH8Row = 2 * kI;               // bytes per pair
-constexpr int kH8Pieces = kH8Row / 16;       // 360 16-byte pieces per pair (= kChunks)
-
-// Both E4M3 codes of one h value (a bf16) under the fixed scale bytes sh, sl.
-NA_DEVICE void h8_codes(uint16_t hv, uint32_t sh, uint32_t sl, uint8_t& hi, uint8_t& lo) {
-  const float f = bf16_to_f32(hv), s_hi = e8m0_f32(sh), s_lo = e8m0_f32(sl);
-  fp8x2_t o = {0, 0};
-  o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o, f, 0.f, s_hi, false);
-  const uint32_t c = __builtin_bit_cast(uint32_t, o) & 0xff;
-  const float r = f - __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(c, s_hi, false)[0];
-  fp8x2_t o2 = {0, 0};
-  o2 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o2, r, 0.f, s_lo, false);
-  hi = (uint8_t)c;
-  lo = (uint8_t)(__builtin_bit_cast(uint32_t, o2) & 0xff);
-}
-
-// h of D column n = lane % 16 (output row 16b + n) of `pair` -> its hi and lo bytes (a byte store each).
-NA_DEVICE void store_h8(uint8_t* h8, int pair, int b, uint16_t hv, uint32_t sh, uint32_t sl, bool ok) {
-  uint8_t hi, lo;
-  h8_codes(hv, sh, sl, hi, lo);
-  uint8_t* row = h8 + (long long)pair * kH8Row + 16 * b + (threadIdx.x & 15);
-  if (ok) {
-    row[0] = hi;
-    row[kI] = lo;
-  }
-}
+// ---- h between the gate_up and down parts: the bf16 values of the reference's h, one 2880-element row per pair.  The
+// down part quantises each row into E4M3 hi + lo rows with one E8M0 scale per 32-element block while it stages it
+// (x8_store, as gate_up does with x), which holds every element within 2^13 of its block's largest magnitude exactly.
+constexpr int kHRow = 2 * kI;               // bytes per pair
+constexpr int kHPieces = kHRow / 16;        // 360 16-byte pieces per pair (= kChunks)
 
 // ---- the single-launch expert body's handoffs as tagged words (handoff.h): h of pair p, row block b in the 8 words
-// (p x 180 + b) x 8 + k (k < 4: hi codes 16b + 4k .. 16b + 4k + 3, k >= 4: lo codes 16b + 4(k - 4) ..; byte i of the
-// payload = code i), the weighted output yw of pair p, block b in the 8 words (p x 180 + b) x 8 + k (outputs 16b + 2k,
-// 16b + 2k + 1).  raw: the workgroup's launch count as thread 0 read it (other threads: 0), from which one_tag forms
+// (p x 180 + b) x 8 + k (bf16 values 16b + 2k, 16b + 2k + 1), the weighted output yw of pair p, block b in the 8
+// words (p x 180 + b) x 8 + k (outputs 16b + 2k, 16b + 2k + 1).  raw: the workgroup's launch count as thread 0 read it (other threads: 0), from which one_tag forms
 // the launch's number (the kernel's comment below); err: the error word a wait that gives up raises.
 constexpr int kOneWgs = 4 * kTDownBlocks;       // 720 workgroups
 struct OneTags {
@@ -296,8 +268,8 @@ NA_DEVICE uint32_t one_tag(const OneTags& tg) {
 NA_DEVICE uint64_t* one_h_words(const OneTags& tg, int pair, int b) { return tg.h + ((long long)pair * kTDownBlocks + b) * 8; }
 NA_DEVICE uint64_t* one_y_words(const OneTags& tg, int pair, int b) { return tg.y + ((long long)pair * kTDownBlocks + b) * 8; }
 
-// The pairs' h8 rows of up to XT staged tokens through registers: piece p = tid + NTH k < nt x 360; piece q = p % 360
-// of token t = p / 360 is bytes 16 (q % 180) .. of its hi (q < 180) or lo row.
+// The pairs' h rows of up to XT staged tokens through registers: piece p = tid + NTH k < nt x 360; piece q = p % 360
+// of token t = p / 360 is values 8q .. 8q + 7 of its row.
 // 16 bytes at base + off with one device-coherent (sc1) load: what the same launch wrote on another XCD.  base is
 // uniform across the wave (a buffer resource is scalar), off per lane and 16-byte aligned.
 NA_DEVICE uint4 load16_sc1(const void* base, uint32_t off) {
@@ -312,26 +284,9 @@ NA_DEVICE void h8_load(int tid, const uint8_t* h8, PairOf pair_of, int nt, XRegs
 #pragma unroll
   for (int k = 0; k < XRegs<XT, NTH>::XP; ++k) {
     const int p = tid + NTH * k;
-    const int t = p / kH8Pieces, q = p - t * kH8Pieces;
-    if (p < nt * kH8Pieces) xr.v[k] = load16(h8 + (long long)pair_of(t) * kH8Row + 16 * q);
+    const int t = p / kHPieces, q = p - t * kHPieces;
+    if (p < nt * kHPieces) xr.v[k] = load16(h8 + (long long)pair_of(t) * kHRow + 16 * q);
   }
-}
-
-// ... into the staged rows 2t (hi) / 2t + 1 (lo), every scale byte of a row set to its fixed value, and the zero strip.
-template <int XT, int NTH>
-NA_DEVICE void h8_store(int tid, X8Lds<2 * XT>& L, int nt, const XRegs<XT, NTH>& xr, uint32_t sh, uint32_t sl) {
-#pragma unroll
-  for (int k = 0; k < XRegs<XT, NTH>::XP; ++k) {
-    const int p = tid + NTH * k;
-    const int t = p / kH8Pieces, q = p - t * kH8Pieces, half = q >= kH8Pieces / 2 ? 1 : 0;
-    if (p < nt * kH8Pieces)
-      *reinterpret_cast<uint4*>(L.row[2 * t + half] + 16 * (q - half * (kH8Pieces / 2))) = xr.v[k];
-  }
-  for (int i = tid; i < 2 * nt * (kX8ScPitch / 4); i += NTH) {
-    const int r = i / (kX8ScPitch / 4), c = i - r * (kX8ScPitch / 4);
-    reinterpret_cast<uint32_t*>(L.sc[r])[c] = ((r & 1) ? sl : sh) * 0x01010101u;
-  }
-  if (tid < 8) reinterpret_cast<uint4*>(L.zero)[tid] = make_uint4(0, 0, 0, 0);
 }
 
 // Quantise the loaded pieces into the E4M3 rows 2t (hi) / 2t + 1 (lo) of staged token t < nt and their scales, and
@@ -400,6 +355,11 @@ NA_DEVICE void store_row_pairs(uint16_t* row_ptr, uint16_t v, bool ok) {
   const uint32_t hi = (uint32_t)__shfl_xor((int)v, 1) & 0xffff;
   if (ok && !(lane & 1)) *reinterpret_cast<uint32_t*>(row_ptr + (lane & 15)) = (uint32_t)v | (hi << 16);
 }
+// h of D column n = lane % 16 (row 16b + n) of `pair` as bf16 pairs (store_row_pairs: every lane calls it).
+NA_DEVICE void store_h(uint8_t* h, int pair, int b, uint16_t hv, bool ok) {
+  store_row_pairs(reinterpret_cast<uint16_t*>(h + (long long)pair * kHRow) + 16 * b, hv, ok);
+}
+
 // ... as tagged words: even lanes write (v[n], v[n + 1]) as word n / 2 of w.
 NA_DEVICE void tag_row_pairs(uint64_t* w, uint16_t v, bool ok, uint32_t tag) {
   const int lane = threadIdx.x & 63;
@@ -470,8 +430,8 @@ NA_DEVICE int pair_at(uint64_t users, int u) {
 // The duplicate pairs' h: for token u = 2 (lane / 16) + e < nt (user pair p), the same value v[e] also goes to every
 // other pair of p's token that `all` routes to the expert (columns 16b .. 16b + 15).  Kept out of line of the common
 // path, which stores only the users' rows.
-__device__ __noinline__ void dup_rows_store_h8(uint8_t* h8, uint64_t users, uint64_t all, int nt, int b, uint16_t v0,
-                                               uint16_t v1, uint32_t sh, uint32_t sl) {
+__device__ __noinline__ void dup_rows_store_h(uint8_t* h, uint64_t users, uint64_t all, int nt, int b, uint16_t v0,
+                                              uint16_t v1) {
   const int lane = threadIdx.x & 63;
   const uint16_t v[2] = {v0, v1};
 #pragma unroll
@@ -479,7 +439,7 @@ __device__ __noinline__ void dup_rows_store_h8(uint8_t* h8, uint64_t users, uint
     const int u = 2 * (lane >> 4) + e;
     const int p = pair_at(users, min(u, nt - 1));
     const uint32_t dm = token_dups(all, p) & ~(1u << (p & 3));
-    for (int k = 0; k < 4; ++k) store_h8(h8, (p & ~3) + k, b, v[e], sh, sl, u < nt && ((dm >> k) & 1));
+    for (int k = 0; k < 4; ++k) store_h(h, (p & ~3) + k, b, v[e], u < nt && ((dm >> k) & 1));
   }
 }
 
@@ -530,7 +490,7 @@ struct DecodeLds {
 };
 
 // gate_up: output block b (rows j = 16b .. 16b + 15 of gate and of up) of the item-th distinct expert -> h[pair, j]
-// (E4M3, see h8_codes; h8_sc = the two scale bytes, hi | lo << 8).
+// (bf16).
 // Order: route and slot -> every global load (codes, scales, x, bias) -> x quantised to E4M3 and the scales to LDS,
 // barrier -> one MFMA per tile (each waits only for its own codes) -> fixed-order sum of the KS partial sums through
 // LDS -> epilogue in wave 0, which reads nothing from global memory.
@@ -542,7 +502,7 @@ NA_DEVICE void gate_up_body(DecodeLds<KS, XT>& L, int item, int b, long long rid
                             const uint8_t* __restrict__ pool, long long slot_bytes,
                             const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ x,
                             const uint16_t* __restrict__ bias_gu, uint8_t* __restrict__ h8, float alpha, float limit,
-                            uint32_t h8_sc, const OneTags& tg = OneTags{}, const OnePre* pre = nullptr) {
+                            const OneTags& tg = OneTags{}, const OnePre* pre = nullptr) {
   static_assert(!TAG || XT == 1, "tagged h: one token");
   constexpr int MT = (kTTiles + KS - 1) / KS;
   constexpr int NTH = 64 * KS;
@@ -623,23 +583,13 @@ NA_DEVICE void gate_up_body(DecodeLds<KS, XT>& L, int item, int b, long long rid
       ub = rb(ub + bf16_to_f32(buj));
     }
     hv[q] = f32_to_bf16(swiglu_clamp_bf16(gb, ub, alpha, limit));
-    if constexpr (!TAG) store_h8(h8, pair_at(users, min(u, nt - 1)), b, hv[q], h8_sc & 0xff, h8_sc >> 8, u < nt);
+    if constexpr (!TAG) store_h(h8, pair_at(users, min(u, nt - 1)), b, hv[q], u < nt);
   }
   if constexpr (TAG) {
-    // lanes 0..15 hold the token's 16 values; lane k < 8 gathers the codes of word k (hi for k < 4, lo above)
-    uint8_t hi, lo;
-    h8_codes(hv[0], h8_sc & 0xff, h8_sc >> 8, hi, lo);
-    const int src = 4 * (lane & 3);
-    uint32_t w = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t hb = (uint32_t)__shfl((int)hi, src + i), lb = (uint32_t)__shfl((int)lo, src + i);
-      w |= ((lane < 4 ? hb : lb) & 0xffu) << (8 * i);
-    }
-    const uint32_t tag = one_tag(tg);
-    if (lane < 8) tag_store(one_h_words(tg, pair_at(users, 0), b) + lane, w, tag);
+    // lanes 0..15 hold the token's 16 values: even lanes write them as 8 words of bf16 pairs
+    tag_row_pairs(one_h_words(tg, pair_at(users, 0), b), hv[0], lane < 16, one_tag(tg));
   } else if (all != users) {
-    dup_rows_store_h8(h8, users, all, nt, b, hv[0], hv[1], h8_sc & 0xff, h8_sc >> 8);   // rare
+    dup_rows_store_h(h8, users, all, nt, b, hv[0], hv[1]);   // rare
   }
 }
 
@@ -647,16 +597,17 @@ template <int KS, int XT>
 __global__ __launch_bounds__(64 * KS) void k_moe_gate_up_t950(
     const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
     const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ x,
-    const uint16_t* __restrict__ bias_gu, uint8_t* __restrict__ h8, float alpha, float limit, uint32_t h8_sc) {
+    const uint16_t* __restrict__ bias_gu, uint8_t* __restrict__ h8, float alpha, float limit) {
   __shared__ DecodeLds<KS, XT> L;
   const long long rid = route_ids_load(ids, 4 * B);
-  args_at_entry(x, bias_gu, h8, alpha, limit, (int)h8_sc);   // past the preloaded arguments: fetched while ids fly
+  args_at_entry(x, bias_gu, h8, alpha, limit);       // past the preloaded arguments: fetched while ids fly
   gate_up_body<KS, XT, false>(L, blockIdx.x, blockIdx.y, rid, B, pool, slot_bytes, slot_tab, expert_base, x, bias_gu,
-                              h8, alpha, limit, h8_sc);
+                              h8, alpha, limit);
 }
 
 // down, expert-major: output block b (rows n = 16b .. 16b + 15) of the item-th distinct expert from each routed
-// token's own h row (E4M3 from the gate_up kernel), + bias, x routing weight -> yw[pair, n].  An invalid id (128)
+// token's own h row (bf16 from the gate_up kernel, quantised to E4M3 hi + lo rows while staged), + bias, x routing
+// weight -> yw[pair, n].  An invalid id (128)
 // writes +0 for its pairs and reads no weights.  The top-k sum is left to k_combine_t950.  Load order as in the
 // gate_up kernel.  Every wave returns from the body (waves past the first right after the K reduction).
 // TAG (the single-launch expert body, batch 1): h was written earlier in the same launch as tagged words of tg, so
@@ -668,7 +619,7 @@ template <int KS, int XT, bool TAG>
 NA_DEVICE void down_body(DecodeLds<KS, XT>& L, int item, int b, long long rid, int B, const uint8_t* __restrict__ pool,
                          long long slot_bytes, const int64_t* __restrict__ slot_tab, long long expert_base,
                          const uint8_t* __restrict__ h8, const uint16_t* __restrict__ wts,
-                         const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw, uint32_t h8_sc,
+                         const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw,
                          const OneTags& tg = OneTags{}, const OnePre* pre = nullptr) {
   static_assert(!TAG || XT == 1, "tagged h: one token");
   constexpr int MT = (kTTiles + KS - 1) / KS;
@@ -721,12 +672,12 @@ NA_DEVICE void down_body(DecodeLds<KS, XT>& L, int item, int b, long long rid, i
     }
     __syncthreads();
     const uint32_t tag = tag_lds;
-    // piece p < 180 = hi codes of block p (words 0..3 of its 8), p >= 180 = lo codes of block p - 180 (words 4..7)
+    // piece q (values 8q .. 8q + 7 of the row) = words 4 (q % 2) .. 4 (q % 2) + 3 of block q / 2
     const uint64_t* src[8];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int p = min(tid + NTH * k, kH8Pieces - 1);
-      const uint64_t* w = hrow + (p < kTDownBlocks ? p * 8 : (p - kTDownBlocks) * 8 + 4);
+      const int q = min(tid + NTH * k, kHPieces - 1);
+      const uint64_t* w = hrow + (q >> 1) * 8 + 4 * (q & 1);
 #pragma unroll
       for (int i = 0; i < 4; ++i) src[4 * k + i] = w + i;
     }
@@ -736,7 +687,7 @@ NA_DEVICE void down_body(DecodeLds<KS, XT>& L, int item, int b, long long rid, i
     xr.v[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
   }
   __builtin_amdgcn_sched_barrier(0);
-  h8_store<XT, NTH>(tid, L.x, nt, xr, h8_sc & 0xff, h8_sc >> 8);
+  x8_store<XT, NTH>(tid, L.x, nt, xr);
   scale_store<1, NTH>(tid, L.sc, sr);
   __syncthreads();
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -782,12 +733,12 @@ template <int KS, int XT>
 __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
     const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
     const int64_t* __restrict__ slot_tab, long long expert_base, const uint8_t* __restrict__ h8,
-    const uint16_t* __restrict__ wts, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw, uint32_t h8_sc) {
+    const uint16_t* __restrict__ wts, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw) {
   __shared__ DecodeLds<KS, XT> L;
   const long long rid = route_ids_load(ids, 4 * B);
-  args_at_entry(h8, wts, bias_dn, yw, (int)h8_sc);    // past the preloaded arguments: fetched while the ids fly
+  args_at_entry(h8, wts, bias_dn, yw);                // past the preloaded arguments: fetched while the ids fly
   down_body<KS, XT, false>(L, blockIdx.x, blockIdx.y, rid, B, pool, slot_bytes, slot_tab, expert_base, h8, wts,
-                           bias_dn, yw, h8_sc);
+                           bias_dn, yw);
 }
 
 __global__ __launch_bounds__(256) void k_combine_t950(const uint32_t* __restrict__ yw, int B,
@@ -807,7 +758,7 @@ __global__ __launch_bounds__(256) void k_combine_t950(const uint32_t* __restrict
 
 // down + combine, row-block-major, for one token: one workgroup of 16 waves per output block b holds the token's
 // (up to 4) distinct experts (4 groups of KSD = 4 waves; group g serves the g-th distinct expert), so the top-k sum
-// needs no third kernel and no cross-workgroup exchange.  The 4 pairs' E4M3 h rows are staged in LDS once;
+// needs no third kernel and no cross-workgroup exchange.  The 4 pairs' h rows are staged in LDS once (as E4M3 hi + lo);
 // each group runs the expert-major down arithmetic on its pair's rows; the group leaders leave each pair's
 // bf16(y x w) slice in LDS; after a barrier, out[16b + n] = bf16(sum_k yw[k][n]) in top-k order.
 constexpr int kDcWaves = 16, kDcKS = 4;
@@ -822,14 +773,13 @@ struct DownCombLds {
 __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
     const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
     const int64_t* __restrict__ slot_tab, long long expert_base, const uint8_t* __restrict__ h8,
-    const uint16_t* __restrict__ wts, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ out,
-    uint32_t h8_sc) {
+    const uint16_t* __restrict__ wts, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ out) {
   constexpr int MT = (kTTiles + kDcKS - 1) / kDcKS;
   constexpr int NTH = 64 * kDcWaves;
   constexpr int GTH = 64 * kDcKS;
   __shared__ DownCombLds L;
   const long long rid = route_ids_load(ids, 4);
-  args_at_entry(h8, wts, bias_dn, out, (int)h8_sc);   // past the preloaded arguments: fetched while the ids fly
+  args_at_entry(h8, wts, bias_dn, out);               // past the preloaded arguments: fetched while the ids fly
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = wave / kDcKS, kw = wave - g * kDcKS, gtid = tid - g * GTH;
   const int b = blockIdx.x;
@@ -854,7 +804,7 @@ __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
   CodeRegs<MT> rd;
   code_load<MT>(blk, lane, t0, live ? t1 : t0, rd);
   __builtin_amdgcn_sched_barrier(0);
-  h8_store<4, NTH>(tid, L.x, 4, xr, h8_sc & 0xff, h8_sc >> 8);
+  x8_store<4, NTH>(tid, L.x, 4, xr);
   scale_store<1, GTH>(gtid, L.sc[g], sr);
   if (e == 128 && kw == 0) {                           // invalid ids: each of their pairs contributes +0
     for (int i = lane; i < 4 * kTRows; i += 64)
@@ -914,10 +864,10 @@ __global__ __launch_bounds__(256) void k_moe_one_t950(
     const int64_t* __restrict__ ids, const uint8_t* __restrict__ pool, long long slot_bytes,
     const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ x,
     const uint16_t* __restrict__ bias_gu, const uint16_t* __restrict__ bias_dn, const uint16_t* __restrict__ wts,
-    uint16_t* __restrict__ out, float alpha, float limit, uint32_t h8_sc, uint32_t* __restrict__ sync) {
+    uint16_t* __restrict__ out, float alpha, float limit, uint32_t* __restrict__ sync) {
   __shared__ DecodeLds<4, 1> L;
   const long long rid = route_ids_load(ids, 4);
-  args_at_entry(x, bias_gu, bias_dn, wts, out, alpha, limit, (int)h8_sc, sync);
+  args_at_entry(x, bias_gu, bias_dn, wts, out, alpha, limit, sync);
   const int blk = blockIdx.x, item = blk & 3, b = blk >> 2;
   const int tid = threadIdx.x, lane = tid & 63;
   // loads that do not depend on the routing, issued while the ids are in flight: token 0's x, the layer's slots
@@ -946,9 +896,9 @@ __global__ __launch_bounds__(256) void k_moe_one_t950(
     }
   }
   gate_up_body<4, 1, true>(L, item, b, rid, 1, pool, slot_bytes, slot_tab, expert_base, x, bias_gu, nullptr, alpha,
-                           limit, h8_sc, tg, &pre);
-  down_body<4, 1, true>(L, item, b, rid, 1, pool, slot_bytes, slot_tab, expert_base, nullptr, wts, bias_dn, nullptr,
-                        h8_sc, tg, &pre);
+                           limit, tg, &pre);
+  down_body<4, 1, true>(L, item, b, rid, 1, pool, slot_bytes, slot_tab, expert_base, nullptr, wts, bias_dn, nullptr, tg,
+                        &pre);
   if (tid >= 64) return;
   const uint32_t tag = one_tag(tg);
   if (tid == 0) store_coherent(ctr, tag);              // the count for the next launch
@@ -979,20 +929,13 @@ static void launch_t(void (*kern)(KArgs...), dim3 grid, dim3 block, hipStream_t 
 }
 
 typedef void (*GateUpT)(const int64_t*, int, const uint8_t*, long long, const int64_t*, long long, const uint16_t*,
-                        const uint16_t*, uint8_t*, float, float, uint32_t);
+                        const uint16_t*, uint8_t*, float, float);
 typedef void (*DownT)(const int64_t*, int, const uint8_t*, long long, const int64_t*, long long, const uint8_t*,
-                      const uint16_t*, const uint16_t*, uint16_t*, uint32_t);
+                      const uint16_t*, const uint16_t*, uint16_t*);
 
-// The fixed E8M0 bytes of h (hi | lo << 8, see h8_codes) for the activation's alpha and limit; 0 when the bound
-// (limit + 1) x max(limit, 1 / alpha) is not a positive finite float far enough from the E8M0 range's ends.
-static uint32_t h8_scale_bytes(float alpha, float limit) {
-  if (!(alpha > 0.f) || !(limit > 0.f)) return 0;
-  const double bound = ((double)limit + 1.0) * (limit > 1.0 / alpha ? (double)limit : 1.0 / alpha);
-  if (!(bound < 1e30) || !(bound > 1e-30)) return 0;
-  int e = 0;
-  std::frexp(bound, &e);                               // bound = m 2^e, 0.5 <= m < 1: 2^(e-1) <= bound < 2^e
-  const int hi = (e - 1) - 7 + 127;                    // s_hi = 2^((e - 1) - 7)
-  return (uint32_t)hi | ((uint32_t)(hi - 5) << 8);
+// The clamped SwiGLU's parameters: positive and finite (the decode kernels' argument check).
+static bool act_args_ok(float alpha, float limit) {
+  return alpha > 0.f && limit > 0.f && std::isfinite(alpha) && std::isfinite(limit);
 }
 
 template <int KS>
@@ -1012,7 +955,7 @@ static DownT pick_down_t950(int ks, int xt) {
   return ks == 4 ? down_t950_xt<4>(xt) : down_t950_xt<8>(xt);
 }
 
-// The t950 decode expert body of na_moe_decode_t950 with its scratch given: h (E4M3 hi + lo rows of the 4 B pairs,
+// The t950 decode expert body of na_moe_decode_t950 with its scratch given: h (bf16 rows of the 4 B pairs,
 // 5,760 B each) and yw (bf16 weighted expert outputs of the pairs, 5,760 B each).
 static int decode_t950(const void* x, const int64_t* topk_ids, const void* topk_w, int B, const void* pool,
                        long long slot_bytes, const int64_t* slot_tab, long long expert_base, const void* bias_gu,
@@ -1030,24 +973,23 @@ static int decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
   hipEvent_t ev[6] = {};
   if (events)
     for (int i = 0; i < (two ? 4 : 6); ++i) ev[i] = (hipEvent_t)events[i];
-  const uint32_t h8_sc = h8_scale_bytes(alpha, limit);
-  if (!h8_sc) return kErrArgs;
+  if (!act_args_ok(alpha, limit)) return kErrArgs;
   const int items = 4 * B;
   const dim3 g1(items, kTDownBlocks);
   const dim3 blk(64 * k_split);
   const int xt = B <= 1 ? 1 : B <= 2 ? 2 : B <= 4 ? 4 : 8;
   launch_t(pick_gate_up_t950(k_split, xt), g1, blk, stream, ev[0], ev[1], topk_ids, B, (const uint8_t*)pool,
            slot_bytes, slot_tab, expert_base, (const uint16_t*)x, (const uint16_t*)bias_gu, (uint8_t*)h_scratch,
-           alpha, limit, h8_sc);
+           alpha, limit);
   if (two) {
     launch_t(k_moe_down_comb_t950, dim3(kTDownBlocks), dim3(64 * kDcWaves), stream, ev[2], ev[3], topk_ids, B,
              (const uint8_t*)pool, slot_bytes, slot_tab, expert_base, (const uint8_t*)h_scratch,
-             (const uint16_t*)topk_w, (const uint16_t*)bias_dn, (uint16_t*)out, h8_sc);
+             (const uint16_t*)topk_w, (const uint16_t*)bias_dn, (uint16_t*)out);
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
   }
   launch_t(pick_down_t950(k_split, xt), g1, blk, stream, ev[2], ev[3], topk_ids, B, (const uint8_t*)pool, slot_bytes,
            slot_tab, expert_base, (const uint8_t*)h_scratch, (const uint16_t*)topk_w, (const uint16_t*)bias_dn,
-           (uint16_t*)yw_scratch, h8_sc);
+           (uint16_t*)yw_scratch);
   if (out)
     launch_t(k_combine_t950, dim3((B * kH / 2 + 255) / 256), dim3(256), stream, ev[4], ev[5],
              (const uint32_t*)yw_scratch, B, (uint32_t*)out);
@@ -1150,13 +1092,12 @@ int na_moe_decode_t950_one(const void* x, const int64_t* topk_ids, const void* t
   if (!x || !topk_ids || !topk_w || !pool || !out || !sync) return kErrArgs;
   if (slot_bytes < kTSlot || (slot_bytes & 15) || (reinterpret_cast<uintptr_t>(pool) & 15)) return kErrArgs;
   if ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(sync)) & 15) return kErrArgs;
-  const uint32_t h8_sc = h8_scale_bytes(alpha, limit);
-  if (!h8_sc) return kErrArgs;
+  if (!act_args_ok(alpha, limit)) return kErrArgs;
   if (!one_resident_ok()) return kErrResident;
   launch_t(k_moe_one_t950, dim3(kOneWgs), dim3(256), stream, events ? (hipEvent_t)events[0] : nullptr,
            events ? (hipEvent_t)events[1] : nullptr, topk_ids, (const uint8_t*)pool, slot_bytes, slot_tab,
            expert_base, (const uint16_t*)x, (const uint16_t*)bias_gu, (const uint16_t*)bias_dn,
-           (const uint16_t*)topk_w, (uint16_t*)out, alpha, limit, h8_sc, (uint32_t*)sync);
+           (const uint16_t*)topk_w, (uint16_t*)out, alpha, limit, (uint32_t*)sync);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

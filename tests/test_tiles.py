@@ -13,9 +13,10 @@ from neural_amd import synth
 from neural_amd import tiles
 from tolerance import ulp_profile
 
-# per element against the oracle: the body's bf16 rounding points, and h between the two products as E4M3 hi + lo
-# under fixed scales (exact for |h| >= 2^-9), leave rounding flips that the next product carries: at least 97.5 %
-# of outputs within 2 bf16 ulps and 99 % within 4 (measured on the GPU: 98.4 % / 99.3 % at worst)
+# per element against the oracle: the body's bf16 rounding points leave rounding flips in gate_up's outputs (the
+# block-scaled MFMA sums the hi and lo activation rows' products separately, 128 at a time) that the down product
+# carries: at least 97.5 % of outputs within 2 bf16 ulps and 99 % within 4 (measured on the GPU: 98.4 % / 99.3 % at
+# worst, the same with h crossing as bf16 and quantised per 32-element block as with the earlier fixed-scale E4M3 h)
 T950_FRAC2, T950_FRAC4 = 0.975, 0.99
 
 
@@ -188,6 +189,7 @@ def test_moe_decode_t950_matches_oracle_and_store_path(B, k_split, bias):
             d = np.abs(arr - want)
             assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale, (name, b, d.max(), d.mean(), scale)
             prof = ulp_profile(arr, want)
+            print(f"  t950 decode {name} B={b}: ulp profile {prof}", flush=True)
             assert prof[1] >= T950_FRAC2 and prof[2] >= T950_FRAC4, (name, b, prof)
 
 
@@ -285,6 +287,7 @@ def test_down_with_combine_matches_expert_major_path(B):
                 d = np.abs(arr - want)
                 assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale, (name, call, b, d.max(), scale)
                 prof = ulp_profile(arr, want)
+                print(f"  t950 decode {name} call {call} B={b}: ulp profile {prof}", flush=True)
                 assert prof[1] >= T950_FRAC2 and prof[2] >= T950_FRAC4, (name, call, b, prof)
     assert not one.sync_error()
 
@@ -498,6 +501,7 @@ def test_duplicate_ids_in_a_token(B):
             d = np.abs(arr[b] - want)
             assert d.max() <= 2e-2 + 1e-2 * scale and d.mean() <= 1e-3 * scale, (nm, b, d.max(), scale)
             prof = ulp_profile(arr[b], want)
+            print(f"  t950 decode {nm} b={b}: ulp profile {prof}", flush=True)
             assert prof[1] >= T950_FRAC2 and prof[2] >= T950_FRAC4, (nm, b, prof)
 
 
