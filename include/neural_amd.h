@@ -142,6 +142,23 @@ int na_moe_decode_t950_one(const void* x, const int64_t* topk_ids, const void* t
                            const void* bias_dn, void* h_scratch, void* yw_scratch, void* out, float alpha,
                            float limit, unsigned int* sync, void* const* events, hipStream_t stream);
 
+/* na_moe_decode_t950_one routed by the layer's 128 router logits instead of ids and weights (the router's output
+ * in the reference's decode core, fused_core.py:417-502, before k_topk): every workgroup selects the top 4 and their
+ * softmax weights itself with the router's own rule (largest bf16 value first, lowest index on ties; weights
+ * bf16(exp(v_k - v_0) / sum)), so the selection costs no separate step between the router and the expert body.
+ * logits: fp32 [128] (bf16 values, as the router rounds them).  ids_out (int64 [4]) and wts_out (bf16 [4]) receive
+ * the selection when given (both or neither).  Otherwise the contract of na_moe_decode_t950_one, on the same sync
+ * buffer layout; the same bits as na_moe_decode_t950_one given the router's ids and weights. */
+int na_moe_decode_t950_one_logits(const void* x, const float* logits, int64_t* ids_out, void* wts_out,
+                                  const void* pool, long long slot_bytes, const int64_t* slot_tab,
+                                  long long expert_base, const void* bias_gu, const void* bias_dn, void* out,
+                                  float alpha, float limit, unsigned int* sync, void* const* events,
+                                  hipStream_t stream);
+
+/* 1 when the current device holds the single-launch expert body's 720 workgroups at once (both forms), else 0:
+ * the condition under which na_moe_decode_t950_one(_logits) launch instead of returning -4. */
+int na_moe_one_resident(void);
+
 /* na_moe_decode_t950 that allocates nothing and takes no scratch: h and the weighted expert outputs live in a
  * file-scope device array of the library (368,640 bytes per device, for B <= 8; its address is looked up once per
  * device on the first call there, with that device current).  No counterpart in the reference: it is for callers
@@ -291,9 +308,12 @@ int na_core_route_pack(const void* hn, const float* logits, const int64_t* ids, 
  * positions) before it waits for the phase it needs, whose results it reads as tagged words (each 64-bit word a
  * 32-bit payload and the launch's generation number, polled by the reader; bounded waits), so weight streams and
  * cache reads overlap the phases before them.  Differences from the four calls: c and g feed o_proj's residual too
- * (it is recomputed per row, not read from xbuf); mid is updated in place; results are bit-identical.
- *   sync   uint32 [na_core_attn_block_sync_words()] (51,968 bytes: the error word, the generation word, the
- *          attention's split counters and the tagged words of the phases' results, on 256-byte lines), zero before
+ * (it is recomputed per row, not read from xbuf); mid is updated in place; results are bit-identical.  ids and wts
+ * may both be NULL: the block then stops at the router's logits (and hn), leaving the top-4 selection to the expert
+ * body that reads them (na_moe_decode_t950_one_logits), which saves the wait for every logit at the block's end.
+ *   sync   uint32 [na_core_attn_block_sync_words()] (52,224 bytes: the error word, the generation word, the
+ *          attention's split counters, the tagged words of the phases' results and the router's entry count, on
+ *          256-byte lines), zero before
  *          the first call and owned by one stream (calls that overlap on one buffer race); every completed call
  *          leaves the counters zero and advances the generation word (uint32 64) by one; word 0 is an error flag that
  *          a wait which gave up after its poll limit raises (and nothing clears): that call's outputs are not

@@ -35,6 +35,8 @@ SIGNATURES = {
     "na_moe_decode_t950": [VP, VP, VP, I32, VP, I64, VP, I64, VP, VP, VP, VP, VP, F32, F32, I32, I32, VP, VP],
     "na_moe_decode_t950_noalloc": [VP, VP, VP, I32, VP, I64, VP, I64, VP, VP, VP, F32, F32, I32, I32, VP],
     "na_moe_decode_t950_one": [VP, VP, VP, VP, I64, VP, I64, VP, VP, VP, VP, VP, F32, F32, VP, VP, VP],
+    "na_moe_decode_t950_one_logits": [VP, VP, VP, VP, VP, I64, VP, I64, VP, VP, VP, F32, F32, VP, VP, VP],
+    "na_moe_one_resident": [],
     "na_moe_one_sync_words": [],
     "na_attn_workspace_floats": [I32, I32],
     "na_moe_prefill_workspace_bytes": [I32],

@@ -16,6 +16,7 @@
 #include "attention_dev.h"
 #include "common.h"
 #include "handoff.h"
+#include "topk.h"
 
 #include <hip/hip_ext.h>
 
@@ -198,14 +199,17 @@ __global__ __launch_bounds__(256) void k_embed(const uint16_t* __restrict__ emb,
 // number once every workgroup of the launch has read the old one); the split counters of the attention's chunks;
 // the tagged words (handoff.h) of the phases' results: QKV rows (word 32 r + d: dims d and d + 32 of row r = head,
 // 80 heads), the attention output (word i: elements 2i, 2i + 1), o_proj's mid (word i: rows 2i, 2i + 1) and the
-// router's logits (word e: the fp32 logit of expert e).
+// router's logits (word e: the fp32 logit of expert e); and, when the block leaves the top-4 selection to the expert
+// body, the count of router workgroups that have read the generation word (the last one waits for it instead of for
+// every logit before it advances the word, and returns it to zero).
 constexpr int kSyncErr = 0, kSyncGen = 1;
 constexpr int kSyncSplit = 2;                                   // 8 lines: the attention's split counters
 constexpr int kTagQkv = 10;                                     // 2560 words, 80 lines
 constexpr int kTagAtt = kTagQkv + kQkvRows / 2 / 32;            // 2048 words, 64 lines
 constexpr int kTagMid = kTagAtt + kHq / 2 / 32;                 // 1440 words, 45 lines
 constexpr int kTagLogit = kTagMid + kH / 2 / 32;                // 128 words, 4 lines
-constexpr int kSyncLines = kTagLogit + kNE / 32;                // 203 lines, 51,968 bytes
+constexpr int kSyncEntered = kTagLogit + kNE / 32;              // router workgroups that have read the generation word
+constexpr int kSyncLines = kSyncEntered + 1;                    // 204 lines, 52,224 bytes
 constexpr int kSyncWords = kSyncLines * kLine;
 NA_DEVICE uint64_t* sync_tags(uint32_t* sync, int line) { return reinterpret_cast<uint64_t*>(sync + line * kLine); }
 
@@ -349,74 +353,32 @@ __global__ __launch_bounds__(256) void k_oproj(const uint16_t* __restrict__ att,
 // post-attention RMSNorm + router + top-4: 256 / TPR experts per workgroup, grid 128 / (256 / TPR).  Workgroup 0 writes hn (the experts' input);
 // every workgroup publishes its 16 logits (device-coherent stores, then a count); the last one selects the top 4,
 // writes ids / weights and resets the count.
-// Top 4 of 128 logits held by one wave (lane l: logits l and l + 64) by repeated argmax, lowest index on ties; lanes
-// 0..3 write ids[k] and the weights bf16(exp(v_k - v_0) / sum_k exp(v_k - v_0)) (the reference's softmax over the
-// four, fused_core.py:486-502).  The logits are bf16 values (the router rounds them), so (value, index) fits one
-// 32-bit key that orders exactly as the comparison "larger value, then smaller index" (-0 as +0): each round is one
-// wavefront maximum of keys by DPP and four lane reads, with no LDS round trip.
-NA_DEVICE uint32_t top_key(float v, int idx) {
-  uint32_t b = __float_as_uint(v) >> 16;
-  if (b == 0x8000u) b = 0;
-  const uint32_t ord = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
-  return (ord << 16) | (uint32_t)(0xFFFF - idx);
-}
-NA_DEVICE float top_key_value(uint32_t key) {
-  const uint32_t ord = key >> 16;
-  return bf16_to_f32((uint16_t)((ord & 0x8000u) ? (ord & 0x7FFFu) : (~ord & 0xFFFFu)));
-}
-template <int CTRL>
-NA_DEVICE uint32_t dpp_u32(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
-}
-// The largest key of the wavefront, in every lane: DPP maxima within each row of 16, then the four rows'.
-NA_DEVICE uint32_t wave_max_key(uint32_t k) {
-  k = max(k, dpp_u32<0xB1>(k));
-  k = max(k, dpp_u32<0x4E>(k));
-  k = max(k, dpp_u32<0x124>(k));
-  k = max(k, dpp_u32<0x128>(k));
-  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)k, 0), r1 = (uint32_t)__builtin_amdgcn_readlane((int)k, 16);
-  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)k, 32), r3 = (uint32_t)__builtin_amdgcn_readlane((int)k, 48);
-  return max(max(r0, r1), max(r2, r3));
-}
-NA_DEVICE void top4_softmax(float v0, float v1, int lane, int64_t* __restrict__ ids, uint16_t* __restrict__ wts) {
-  uint32_t k0 = top_key(v0, lane), k1 = top_key(v1, lane + 64);
-  float tv[4];
-  int ti[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const uint32_t best = wave_max_key(max(k0, k1));
-    tv[k] = top_key_value(best);
-    ti[k] = 0xFFFF - (int)(best & 0xFFFFu);
-    if (k0 == best) k0 = 0;                          // every real key is above 0
-    if (k1 == best) k1 = 0;
-  }
-  if (lane < 4) {
-    float ex[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) ex[k] = expf(tv[k] - tv[0]);
-    const float sum = ((ex[0] + ex[1]) + ex[2]) + ex[3];
-    const float mine = lane == 0 ? ex[0] : lane == 1 ? ex[1] : lane == 2 ? ex[2] : ex[3];
-    ids[lane] = lane == 0 ? ti[0] : lane == 1 ? ti[1] : lane == 2 ? ti[2] : ti[3];
-    wts[lane] = f32_to_bf16(mine / sum);
-  }
-}
-
 // Router phase: NR = 128 / (256 / TPR) workgroups; workgroup `blk` computes 256 / TPR logits.  FUSED (the last phase
 // of k_attn_block): the weights and the norm weight are loaded first, then thread 0 polls one tagged word of mid
-// (mid_tags; gen: the generation word as loaded at entry) and every thread reads its 8 words; the logits are also written as tagged words
-// (logit_tags), and the last workgroup (blk = NR - 1) reads all 128 of them, selects the top 4 and stores gen into
-// *gen_word: every workgroup of the launch has read the old number by then (each one's result is an input of the
-// router's logits, and each read the number before it produced anything).
+// (mid_tags; gen: the generation word as loaded at entry) and every thread reads its 8 words.  With ids (select):
+// the logits are also written as tagged words (logit_tags), and the last workgroup (blk = NR - 1) reads all 128 of
+// them, selects the top 4 and stores gen into *gen_word: every workgroup of the launch has read the old number by
+// then (each one's result is an input of the router's logits, and each read the number before it produced
+// anything).  Without ids the logits go to `logits` only, for the next launch (the expert body selects the top 4
+// itself): each workgroup counts itself into *entered once its read of the generation word is complete, and the
+// last workgroup, once its own logits are stored, waits for all NR counts (the other phases' workgroups have read
+// the word, since their results fed its mid), returns the count to zero and advances the word.
 template <int TPR, bool FUSED>
 NA_DEVICE void router_body(int blk, int nr, uint16_t* hc, uint32_t& last, const uint16_t* __restrict__ mid,
                            const uint16_t* __restrict__ post_w, float eps, const uint16_t* __restrict__ Wr,
                            const uint16_t* __restrict__ br, uint16_t* __restrict__ hn, float* __restrict__ logits,
                            uint32_t* __restrict__ counter, int64_t* __restrict__ ids, uint16_t* __restrict__ wts,
                            const uint64_t* mid_tags, uint64_t* logit_tags, uint32_t* gen_word, uint32_t gen,
-                           uint32_t* err) {
+                           uint32_t* err, uint32_t* entered = nullptr) {
   constexpr int ROWS = 256 / TPR;
   const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
   const int e = ROWS * blk + r;
+  const bool select = ids != nullptr;
+  if (FUSED && !select && tid == 0) {
+    uint32_t one = 1u;
+    asm volatile("; counted after the generation word %1 is read" : "+v"(one) : "v"(gen));
+    __hip_atomic_fetch_add(entered, one, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   NormIn ni;
   if constexpr (FUSED) {
 #pragma unroll
@@ -448,6 +410,20 @@ NA_DEVICE void router_body(int blk, int nr, uint16_t* hc, uint32_t& last, const 
   const float s = rw.dot(hc, j);
   if constexpr (FUSED) {
     const float v = rb(s + bf16_to_f32(bv));
+    if (!select) {
+      if (j == 0) logits[e] = v;
+      if (blk != nr - 1 || tid != 0) return;
+      for (uint32_t n = 0; load_coherent(entered) < (uint32_t)nr; ++n) {
+        if (n >= kSpinLimit) {
+          __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      store_coherent(entered, 0u);
+      store_coherent(gen_word, gen);
+      return;
+    }
     if (j == 0) {
       logits[e] = v;
       tag_store(logit_tags + e, __float_as_uint(v), gen);
@@ -876,7 +852,7 @@ __global__ __launch_bounds__(256, 4) void k_attn_block(AttnBlockArgs a) {
   blk -= kBlkOproj;
   router_body<kRouterTpr, true>(blk, kBlkRouter, L.core.hc, L.core.last, a.mid, a.post_w, a.eps, a.Wr, a.br, a.hn,
                                 a.logits, nullptr, a.ids, a.wts, sync_tags(sync, kTagMid), sync_tags(sync, kTagLogit),
-                                sync + kSyncGen * kLine, gen, err);
+                                sync + kSyncGen * kLine, gen, err, sync + kSyncEntered * kLine);
 }
 }  // namespace na
 
@@ -940,7 +916,7 @@ int na_core_attn_block(void* mid, const void* g, const float* c, void* xbuf, con
                        const void* bo, const void* post_w, const void* Wr, const void* br, void* hn, float* logits,
                        int64_t* ids, void* wts, unsigned int* sync, void* const* events, hipStream_t stream) {
   if (!mid || !xbuf || !in_w || !Wqkv || !bqkv || !pos || !inv_freq || !kc || !vc || !q || !sinks || !att || !Wo ||
-      !bo || !post_w || !Wr || !br || !hn || !logits || !ids || !wts || !sync || cache_rows <= 0 || ring < 0)
+      !bo || !post_w || !Wr || !br || !hn || !logits || !ids != !wts || !sync || cache_rows <= 0 || ring < 0)
     return kErrArgs;
   if (c && !g) return kErrArgs;
   if (ring > 0 && (window <= 0 || ring < window || cache_rows != ring)) return kErrArgs;

@@ -15,6 +15,7 @@
 #include "common.h"
 #include "handoff.h"
 #include "t950.h"
+#include "topk.h"
 
 #include <hip/hip_ext.h>
 
@@ -860,14 +861,27 @@ constexpr int kOneTagWords = 4 * kTDownBlocks * 8;                     // 5760 p
 constexpr int kOneTagY = kOneTagH + kOneTagWords * 2 / kLine;
 constexpr int kOneSyncLines = kOneTagY + kOneTagWords * 2 / kLine;     // 373 lines, 95,488 bytes
 
+// LOGITS (na_moe_decode_t950_one_logits): the routing comes from the layer's 128 router logits instead of ids and
+// weights: every wave selects the top 4 itself (topk.h, the router's own selection and softmax), the weights go to
+// LDS for the down part, and workgroup 0 writes the ids and weights out (ids_out / wts_out, when given).
+template <bool LOGITS>
 __global__ __launch_bounds__(256) void k_moe_one_t950(
     const int64_t* __restrict__ ids, const uint8_t* __restrict__ pool, long long slot_bytes,
     const int64_t* __restrict__ slot_tab, long long expert_base, const uint16_t* __restrict__ x,
     const uint16_t* __restrict__ bias_gu, const uint16_t* __restrict__ bias_dn, const uint16_t* __restrict__ wts,
-    uint16_t* __restrict__ out, float alpha, float limit, uint32_t* __restrict__ sync) {
+    uint16_t* __restrict__ out, float alpha, float limit, uint32_t* __restrict__ sync, const float* __restrict__ logits,
+    int64_t* __restrict__ ids_out, uint16_t* __restrict__ wts_out) {
   __shared__ DecodeLds<4, 1> L;
-  const long long rid = route_ids_load(ids, 4);
-  args_at_entry(x, bias_gu, bias_dn, wts, out, alpha, limit, sync);
+  __shared__ uint16_t wts_lds[4];
+  long long rid;
+  float lv0 = 0.f, lv1 = 0.f;
+  if constexpr (LOGITS) {
+    lv0 = logits[threadIdx.x & 63];
+    lv1 = logits[64 + (threadIdx.x & 63)];
+  } else {
+    rid = route_ids_load(ids, 4);
+  }
+  args_at_entry(x, bias_gu, bias_dn, wts, out, alpha, limit, sync, ids_out, wts_out);
   const int blk = blockIdx.x, item = blk & 3, b = blk >> 2;
   const int tid = threadIdx.x, lane = tid & 63;
   // loads that do not depend on the routing, issued while the ids are in flight: token 0's x, the layer's slots
@@ -883,6 +897,21 @@ __global__ __launch_bounds__(256) void k_moe_one_t950(
   const uint32_t raw = tid == 0 ? load_coherent(ctr) : 0u;
   const OneTags tg{reinterpret_cast<uint64_t*>(sync + kOneTagH * kLine),
                    reinterpret_cast<uint64_t*>(sync + kOneTagY * kLine), raw, sync + kOneErr * kLine};
+  if constexpr (LOGITS) {                              // the top 4 of the logits, in every wave
+    float tv[4];
+    int ti[4];
+    top4_select(lv0, lv1, lane, tv, ti);
+    rid = top4_id(ti, min(lane, 3));
+    if (tid < 4) {
+      const uint16_t wv = top4_weight(tv, tid);
+      wts_lds[tid] = wv;                               // read by the down part, after gate_up's first barrier
+      if (blk == 0 && ids_out) {
+        ids_out[tid] = rid;
+        wts_out[tid] = wv;
+      }
+    }
+    wts = wts_lds;
+  }
   {                                                    // this workgroup's expert -> its slot (a lane read, uniform)
     int nt, distinct, valid;
     uint64_t users, all;
@@ -1031,10 +1060,11 @@ static bool one_resident_ok() {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
   std::lock_guard<std::mutex> lock(mu);
   if (!ok[dev]) {
-    int per_cu = 0, cus = 0;
-    const bool q = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_one_t950, 256, 0) == hipSuccess &&
+    int per_cu = 0, per_cu_l = 0, cus = 0;               // both forms (ids, logits) of the kernel
+    const bool q = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_one_t950<false>, 256, 0) == hipSuccess &&
+                   hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_l, k_moe_one_t950<true>, 256, 0) == hipSuccess &&
                    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess;
-    ok[dev] = q && (long long)per_cu * cus >= kOneWgs ? 1 : -1;
+    ok[dev] = q && (long long)min(per_cu, per_cu_l) * cus >= kOneWgs ? 1 : -1;
   }
   return ok[dev] > 0;
 }
@@ -1094,12 +1124,31 @@ int na_moe_decode_t950_one(const void* x, const int64_t* topk_ids, const void* t
   if ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(sync)) & 15) return kErrArgs;
   if (!act_args_ok(alpha, limit)) return kErrArgs;
   if (!one_resident_ok()) return kErrResident;
-  launch_t(k_moe_one_t950, dim3(kOneWgs), dim3(256), stream, events ? (hipEvent_t)events[0] : nullptr,
+  launch_t(k_moe_one_t950<false>, dim3(kOneWgs), dim3(256), stream, events ? (hipEvent_t)events[0] : nullptr,
            events ? (hipEvent_t)events[1] : nullptr, topk_ids, (const uint8_t*)pool, slot_bytes, slot_tab,
            expert_base, (const uint16_t*)x, (const uint16_t*)bias_gu, (const uint16_t*)bias_dn,
-           (const uint16_t*)topk_w, (uint16_t*)out, alpha, limit, (uint32_t*)sync);
+           (const uint16_t*)topk_w, (uint16_t*)out, alpha, limit, (uint32_t*)sync, nullptr, nullptr, nullptr);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
+
+int na_moe_decode_t950_one_logits(const void* x, const float* logits, int64_t* ids_out, void* wts_out,
+                                  const void* pool, long long slot_bytes, const int64_t* slot_tab,
+                                  long long expert_base, const void* bias_gu, const void* bias_dn, void* out,
+                                  float alpha, float limit, unsigned int* sync, void* const* events,
+                                  hipStream_t stream) {
+  if (!x || !logits || !pool || !out || !sync || !ids_out != !wts_out) return kErrArgs;
+  if (slot_bytes < kTSlot || (slot_bytes & 15) || (reinterpret_cast<uintptr_t>(pool) & 15)) return kErrArgs;
+  if ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(sync)) & 15) return kErrArgs;
+  if (!act_args_ok(alpha, limit)) return kErrArgs;
+  if (!one_resident_ok()) return kErrResident;
+  launch_t(k_moe_one_t950<true>, dim3(kOneWgs), dim3(256), stream, events ? (hipEvent_t)events[0] : nullptr,
+           events ? (hipEvent_t)events[1] : nullptr, nullptr, (const uint8_t*)pool, slot_bytes, slot_tab, expert_base,
+           (const uint16_t*)x, (const uint16_t*)bias_gu, (const uint16_t*)bias_dn, nullptr, (uint16_t*)out, alpha,
+           limit, (uint32_t*)sync, logits, ids_out, (uint16_t*)wts_out);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+int na_moe_one_resident(void) { return one_resident_ok() ? 1 : 0; }
 
 int na_moe_decode_t950_noalloc(const void* x, const int64_t* topk_ids, const void* topk_w, int B, const void* pool,
                                long long slot_bytes, const int64_t* slot_tab, long long expert_base,

@@ -235,16 +235,24 @@ class DecodeModel:
         rows = kc.shape[2]
         ns = self.sliding_split if ly.sliding else self.n_split
         if self.fused_attn:
+            # with the single-launch expert body, the block stops at the router's logits and the expert body selects
+            # the top 4 itself (no wait for every logit at the block's end); otherwise the block selects them
+            select_here = not self.rx.one
             N.call("na_core_attn_block", self.mid.data_ptr(), self.g.data_ptr() if li else None, None,
                    self.xbuf.data_ptr(), ly.in_w.data_ptr(), ly.Wqkv.data_ptr(), ly.bqkv.data_ptr(),
                    self.pos.data_ptr(), self.inv_freq.data_ptr(), kc.data_ptr(), vc.data_ptr(), rows, ring,
                    self.q.data_ptr(), EPS, float(self.att_scale), ly.sinks.data_ptr(), float(self.scaling),
                    int(ly.sliding), ns, self.attn_work.data_ptr(), self.att.data_ptr(), ly.Wo.data_ptr(),
                    ly.bo.data_ptr(), ly.post_w.data_ptr(), ly.Wr.data_ptr(), ly.br.data_ptr(), self.hn.data_ptr(),
-                   self.r_logits.data_ptr(), self.ids.data_ptr(), self.wts.data_ptr(), self.sync.data_ptr(),
+                   self.r_logits.data_ptr(), self.ids.data_ptr() if select_here else None,
+                   self.wts.data_ptr() if select_here else None, self.sync.data_ptr(),
                    N.events_array(events.get("attn")) if events else None, s)
-            self.rx.forward_decode(li, self.hn, self.ids, self.wts, out=self.g,
-                                   events=events.get("experts") if events else None)
+            if select_here:
+                self.rx.forward_decode(li, self.hn, self.ids, self.wts, out=self.g,
+                                       events=events.get("experts") if events else None)
+            else:
+                self.rx.forward_decode_logits(li, self.hn, self.r_logits, self.g, ids_out=self.ids,
+                                              wts_out=self.wts, events=events.get("experts") if events else None)
             return
         N.call("na_core_qkv", self.mid.data_ptr(), self.g.data_ptr() if li else None, None, self.xbuf.data_ptr(),
                ly.in_w.data_ptr(), ly.Wqkv.data_ptr(), ly.bqkv.data_ptr(), self.pos.data_ptr(),

@@ -61,7 +61,8 @@ class ResidentExperts:
         self.h = torch.empty(max_batch * layout.top_k, layout.down_k, dtype=torch.bfloat16, device=dev)
         self.yw = torch.empty(max_batch * layout.top_k, layout.down_n, dtype=torch.bfloat16, device=dev)
         # the single-launch path's handoff words (zero before its first call; every call leaves them reusable)
-        self.one = self.tiled and combine_in_down and one_launch and self.k_split in (0, 4)
+        self.one = (self.tiled and combine_in_down and one_launch and self.k_split in (0, 4)
+                    and bool(N.lib().na_moe_one_resident()))
         self.sync = (torch.zeros(N.lib().na_moe_one_sync_words(), dtype=torch.int32, device=dev) if self.one
                      else None)
 
@@ -129,6 +130,43 @@ class ResidentExperts:
                N.stream(hidden.device))
         return out
 
+
+    def forward_decode_logits(self, layer: int, hidden: torch.Tensor, logits: torch.Tensor, out: torch.Tensor,
+                              ids_out: torch.Tensor | None = None, wts_out: torch.Tensor | None = None,
+                              events=None) -> torch.Tensor:
+        """One token's expert body routed by the layer's 128 router logits (fp32, bf16 values): the top 4 and their
+        softmax weights by the router's own rule (na_moe_decode_t950_one_logits selects them in the same launch),
+        written to ids_out [1, 4] int64 / wts_out [1, 4] bf16 when given.  The same bits as forward_decode with the
+        router's ids and weights.  Without the single-launch body (other layouts, or a device that cannot hold its
+        720 workgroups) the selection runs as its own launch first."""
+        L = self.layout
+        if hidden.dtype is not torch.bfloat16 or tuple(hidden.shape) != (1, L.hidden) or not hidden.is_contiguous():
+            raise ValueError("hidden must be contiguous bf16 [1, hidden]")
+        if logits.dtype is not torch.float32 or logits.numel() != L.n_experts or not logits.is_contiguous():
+            raise ValueError(f"logits must be contiguous fp32 [{L.n_experts}]")
+        if out.dtype is not torch.bfloat16 or tuple(out.shape) != (1, L.hidden) or not out.is_contiguous():
+            raise ValueError("out must be contiguous bf16 [1, hidden]")
+        if (ids_out is None) != (wts_out is None):
+            raise ValueError("ids_out and wts_out go together")
+        for t, dt, nm in ((ids_out, torch.int64, "ids_out"), (wts_out, torch.bfloat16, "wts_out")):
+            if t is not None and (t.dtype is not dt or t.numel() != L.top_k or not t.is_contiguous()):
+                raise ValueError(f"{nm} must be contiguous {dt} [1, {L.top_k}]")
+        if not 0 <= layer < L.n_layers:
+            raise ValueError(f"layer {layer} outside [0, {L.n_layers})")
+        if self.one:
+            rc = N.call_status("na_moe_decode_t950_one_logits", hidden.data_ptr(), logits.data_ptr(),
+                               N.ptr(ids_out), N.ptr(wts_out), self.pool.data_ptr(), L.slot_bytes,
+                               N.ptr(self.slot_tab), layer * L.n_experts, N.ptr(self.bias_gu), N.ptr(self.bias_dn),
+                               out.data_ptr(), float(L.act_alpha), float(L.act_limit), self.sync.data_ptr(),
+                               N.events_array(events), N.stream(hidden.device), allow=(N.ERR_RESIDENT,))
+            if rc == 0:
+                return out
+            self.one = False
+        ids = ids_out if ids_out is not None else torch.empty(1, L.top_k, dtype=torch.int64, device=hidden.device)
+        wts = wts_out if wts_out is not None else torch.empty(1, L.top_k, dtype=torch.bfloat16, device=hidden.device)
+        lb = logits.to(torch.bfloat16)                   # exact: the router's logits are bf16 values
+        N.call("na_rows_topk", lb.data_ptr(), 1, ids.data_ptr(), wts.data_ptr(), N.stream(hidden.device))
+        return self.forward_decode(layer, hidden, ids.view(1, L.top_k), wts.view(1, L.top_k), out=out, events=events)
 
     def forward_prefill(self, layer: int, hidden: torch.Tensor, router_indices: torch.Tensor,
                         routing_weights: torch.Tensor, out: torch.Tensor | None = None, events=None) -> torch.Tensor:

@@ -1,7 +1,8 @@
 """The fused attention block of a decode layer (na_core_attn_block: QKV, attention, o_proj and router as four phases
 of one launch, reference fused_core.py:581-629) against the four separate launches it replaces, on the GPU.
 
-Bar: bit-identical outputs (q, the K / V rows, xbuf, att, mid, hn, router logits' selection and weights) and caches
+Bar: bit-identical outputs (q, the K / V rows, xbuf, att, mid, hn, router logits' selection and weights, here made
+by the single-launch expert body from the block's logits) and caches
 over consecutive decode steps of a 2-layer model with a sliding layer on a 16-row ring and a full layer, for the full
 layer's attention in 1, 4 and 32 chunks (chunks past the position are empty), across the ring wrap; each launch
 leaves its split counters at zero, advances its generation word (the tag of its handoff words) by one and leaves the
@@ -15,11 +16,14 @@ pytestmark = pytest.mark.gpu
 
 H, NE, VOCAB, WIN, N_SLOTS, SMAX = 2880, 128, 4096, 16, 8, 64
 LINE = 64                                   # uint32 words per line of the sync buffer: 0 error, 1 generation, 2-9 split
+ENTERED = 203                               # the router workgroups' entry count (the expert body selects the top 4)
 
 
 def _sync_state(sync):
+    """(error word, generation word, split counters + router entry count): every completed launch leaves the
+    counters at zero."""
     s = sync.cpu().numpy().view(np.uint32)
-    return int(s[0]), int(s[LINE]), int(s[2 * LINE:10 * LINE].sum())
+    return int(s[0]), int(s[LINE]), int(s[2 * LINE:10 * LINE].sum()) + int(s[ENTERED * LINE])
 
 
 @pytest.fixture(scope="module")

@@ -538,3 +538,64 @@ def test_one_launch_sparse_routing_lists():
             if all(not 0 <= e < 128 for e in lst):
                 assert not np.any(a), lst                    # every pair contributes +0
     assert not one.sync_error()
+
+
+@pytest.mark.gpu
+def test_one_launch_routed_by_logits():
+    """na_moe_decode_t950_one_logits: the expert body selecting its top 4 from the router's 128 logits.  The
+    selection equals the oracle's router_top4 (ids exactly, lowest index on ties; weights within one bf16 ulp) and
+    the prompt path's na_rows_topk bit for bit (the router's own selection code), on logits with planted ties, an
+    all-equal row and -0 / +0; the output equals na_moe_decode_t950_one given those ids and weights, bit for bit,
+    over consecutive calls on one sync buffer."""
+    import torch
+    from neural_amd import _native as N
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
+    from oracle.mxfp4_oracle import router_top4
+    dev = _dev()
+    slots, x, _, _, tab, bgu, bdn = _t950_case(1, 1500, True, nslot=8)
+    print("case one-launch routed by logits", flush=True)
+    raw = torch.from_numpy(np.stack(slots)).to(dev)
+    tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
+    tiles.repack_to_t950(raw, tp)
+    tabd, bg, bd = torch.from_numpy(tab).to(dev), bgu.to(dev), bdn.to(dev)
+    rx = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bg, bd, tabd, k_split=4)
+    assert rx.one
+    rng = np.random.default_rng(77)
+    rows = []
+    for kind in range(6):
+        v = mo.rb(rng.standard_normal(128).astype(np.float32) * 2)
+        if kind == 1:
+            v[[3, 90, 17]] = v.max() + 1.0                         # a three-way tie for the top, lowest index first
+        elif kind == 2:
+            v[:] = mo.rb(np.float32(0.5))                          # all equal: experts 0..3
+        elif kind == 3:
+            v[:] = -1.0
+            v[[5, 9]] = np.float32(-0.0)
+            v[[7, 11]] = np.float32(0.0)                           # -0 ranks as +0: experts 5, 7, 9, 11
+        elif kind == 4:
+            v[[40, 41]] = v.max() + 2.0
+            v[[2, 127]] = v.max() + 1.0                            # ties at ranks 1-2 and 3-4
+        rows.append(v)
+    xd = x.to(dev)
+    ids_o = torch.empty(1, 4, dtype=torch.int64, device=dev)
+    wts_o = torch.empty(1, 4, dtype=torch.bfloat16, device=dev)
+    ids_r = torch.empty(1, 4, dtype=torch.int64, device=dev)
+    wts_r = torch.empty(1, 4, dtype=torch.bfloat16, device=dev)
+    for rep in range(2):
+        for i, v in enumerate(rows):
+            lg = torch.from_numpy(v).to(dev)
+            layer = (3 * i + rep) % 36
+            a = rx.forward_decode_logits(layer, xd, lg, torch.empty(1, 2880, dtype=torch.bfloat16, device=dev),
+                                         ids_out=ids_o, wts_out=wts_o)
+            lb = lg.to(torch.bfloat16)
+            N.call("na_rows_topk", lb.data_ptr(), 1, ids_r.data_ptr(), wts_r.data_ptr(), N.stream(dev))
+            b = rx.forward_decode(layer, xd, ids_o.clone(), wts_o.clone())
+            torch.cuda.synchronize()
+            assert torch.equal(ids_o, ids_r) and torch.equal(wts_o, wts_r), (rep, i)
+            want_ids, want_w = router_top4(v.astype(np.float64))
+            assert ids_o.cpu().numpy()[0].tolist() == [int(e) for e in want_ids], (i, ids_o, want_ids)
+            gw = wts_o.float().cpu().numpy()[0]
+            assert np.all(np.abs(gw - want_w) <= 2.0 ** -8 * np.abs(want_w)), (i, gw, want_w)
+            assert torch.equal(a, b), (rep, i)
+    assert not rx.sync_error()
