@@ -63,7 +63,7 @@ N_LAYERS, N_EXPERTS, TOPK, H = 36, 128, 4, 2880
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 KERNEL_SOURCES = ("neural_amd/csrc/common.h", "neural_amd/csrc/t950.h", "neural_amd/csrc/handoff.h",
-                  "neural_amd/csrc/tiles.hip", "neural_amd/csrc/moe_decode.hip")
+                  "neural_amd/csrc/topk.h", "neural_amd/csrc/tiles.hip", "neural_amd/csrc/moe_decode.hip")
 
 
 def sources_sha256():

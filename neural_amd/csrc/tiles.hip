@@ -843,10 +843,13 @@ __global__ __launch_bounds__(64 * kDcWaves) void k_moe_down_comb_t950(
 }
 
 // ---- the expert body of one token in a single launch (na_moe_decode_t950_one): 720 workgroups.  Workgroup blk =
-// 4b + i runs k_moe_gate_up_t950<4, 1>'s (i-th distinct expert, gate_up row block b), writing its 16 h values as
+// 180 i + b runs k_moe_gate_up_t950<4, 1>'s (i-th distinct expert, gate_up row block b), writing its 16 h values as
 // tagged words (handoff.h), then k_moe_down_t950<4, 1>'s (i-th expert, down row block b): its weight rows are loaded
-// before it polls the expert's h row, and its weighted outputs are written as tagged words; workgroup 4b + 3 then
-// reads the four pairs' outputs of block b and sums them in k_combine_t950's order.  Bit-identical to the two- and
+// before it polls the expert's h row, and its weighted outputs are written as tagged words; workgroup 540 + b (the
+// fourth expert's) then reads the four pairs' outputs of block b and sums them in k_combine_t950's order.  The order
+// is expert-major: workgroups are dispatched, and their weight loads served, roughly in id order, so the first
+// experts' h rows are complete (and their down parts run) while the later experts' gate_up rows still stream, where
+// an interleaved order released every expert's h only near the end of the stream (0.9 us slower per launch).  Bit-identical to the two- and
 // three-launch paths.  The launch's number: workgroup blk owns counter word blk, reads it at entry (n after n
 // launches), tags with n + 1 and stores n + 1 back before it ends: the same number in every workgroup of a launch,
 // one more than the previous launch's, with no atomic, no shared word and nothing to reset.
@@ -882,7 +885,7 @@ __global__ __launch_bounds__(256) void k_moe_one_t950(
     rid = route_ids_load(ids, 4);
   }
   args_at_entry(x, bias_gu, bias_dn, wts, out, alpha, limit, sync, ids_out, wts_out);
-  const int blk = blockIdx.x, item = blk & 3, b = blk >> 2;
+  const int blk = blockIdx.x, item = blk / kTDownBlocks, b = blk - item * kTDownBlocks;   // expert-major
   const int tid = threadIdx.x, lane = tid & 63;
   // loads that do not depend on the routing, issued while the ids are in flight: token 0's x, the layer's slots
   OnePre pre;
