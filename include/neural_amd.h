@@ -96,8 +96,9 @@ int na_bench_mfma_rate(int kind, int blocks, int iters, float* out, void* const*
 
 /* ---- gfx950 tile layout ("t950", weight_repr "mxfp4_g32_t950").  No counterpart in the reference's store; it is
  * this build's resident layout, a lossless permutation of the reference's slot (neural/moe/layout.py:143-186,
- * tools/scale_pack.py:6-12): 540 blocks of 16 rows, each 22.5 KiB of codes in v_mfma_f32_16x16x32_bf16 B-operand
- * order followed by 16 x 96-byte E8M0 scale rows.  13,271,040 bytes per slot. */
+ * tools/scale_pack.py:6-12): 540 blocks of 16 rows, each 22.5 KiB of codes group-major (byte 256 g + 16 n + b = code
+ * byte b of row n, group g: one 16-byte load per lane of a 1024-byte k-tile is the FP4 B operand of
+ * v_mfma_scale_f32_16x16x128_f8f6f4) followed by 16 x 96-byte E8M0 scale rows.  13,271,040 bytes per slot. */
 long long na_t950_slot_bytes(void);
 
 /* Repack n_slots store slots (raw, or PS4 with src_ps4 = 1; row stride src_stride) into t950 (row stride dst_stride).

@@ -73,8 +73,8 @@ __global__ __launch_bounds__(384) void k_selftest_x8(const uint16_t* __restrict_
 }
 
 // One v_mfma_scale_f32_16x16x128_f8f6f4 in the decode kernels' operand order: A = E4M3 codes a[m][k] (16 x 128 bytes)
-// with E8M0 bytes sa[m][kb] (16 x 4); B = one full t950 k-tile (1024 bytes: lane 16 q + n holds bytes 4q .. 4q + 3 of
-// groups 0..3 of row n), rearranged by tile_to_mfma_b, with E8M0 bytes sb[n][kb] (16 x 4).  d[m * 16 + n] = D[m][n].
+// with E8M0 bytes sa[m][kb] (16 x 4); B = one full t950 k-tile (1024 bytes: lane 16 kb + n holds the 16 code bytes of
+// group kb of row n), as loaded, with E8M0 bytes sb[n][kb] (16 x 4).  d[m * 16 + n] = D[m][n].
 __global__ void k_selftest_mfma8(const uint8_t* __restrict__ a, const uint8_t* __restrict__ sa,
                                  const uint8_t* __restrict__ tile, const uint8_t* __restrict__ sb,
                                  float* __restrict__ d) {
@@ -82,10 +82,8 @@ __global__ void k_selftest_mfma8(const uint8_t* __restrict__ a, const uint8_t* _
   const uint4 a0 = *reinterpret_cast<const uint4*>(a + m * 128 + 16 * kb);
   const uint4 a1 = *reinterpret_cast<const uint4*>(a + m * 128 + 64 + 16 * kb);
   const uint4 c = *reinterpret_cast<const uint4*>(tile + 16 * l);
-  uint32_t w0 = c.x, w1 = c.y, w2 = c.z, w3 = c.w;
-  tile_to_mfma_b(w0, w1, w2, w3);
   const mfma_i32x8_t A = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-  const mfma_i32x8_t Bv = {(int)w0, (int)w1, (int)w2, (int)w3, 0, 0, 0, 0};
+  const mfma_i32x8_t Bv = {(int)c.x, (int)c.y, (int)c.z, (int)c.w, 0, 0, 0, 0};
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, Bv, acc, 0, 4, 0, (int)sa[m * 4 + kb], 0,
                                                         (int)sb[m * 4 + kb]);

@@ -16,7 +16,7 @@
 //
 // Weight layouts (template W): the store's raw and PS4 slots (row r: 1,440 code bytes, then a raw 90-byte or PS4
 // 46-byte scale row; lane (q, n) reads the 16 bytes of group 4t + q of row n, already the MFMA's B order) and the t950
-// tiles (lane (q, n) reads the 16 bytes of its tile, transposed across the lane quarters into the B order).
+// tiles (lane (q, n) reads the 16 bytes at 1024 t + 16 (16 q + n) of the row block: the same operand).
 #include "common.h"
 #include "t950.h"
 
@@ -36,28 +36,20 @@ struct WSrc {
   const uint8_t* scales;    // raw/PS4: row 0's scale row (pitch 90 or 46); t950: unused
 };
 
-// Codes (4 dwords, one per MFMA j) and E8M0 scales (one byte per MFMA j) of k-tile t for lane (q, n) of row block rblk.
+// Store layouts (raw, PS4): the 16 code bytes of (row n, group 4t + q) of row block rblk for lane 16 q + n, and that
+// group's E8M0 scale.
 template <int W>
 NA_DEVICE void w_load(const WSrc& s, int rblk, int t, int lane, uint4& c, uint32_t& sc) {
   const int q = lane >> 4, n = lane & 15;
-  if constexpr (W == kWT950) {
-    const uint8_t* blk = s.codes + (long long)rblk * kTBlock;
-    const int off = t < kTFull ? t * 1024 + 16 * lane : kTFull * 1024 + 8 * lane;   // half tile: 16 B at 8 B stride
-    c = load16<true>(blk + off);
-    sc = *reinterpret_cast<const uint32_t*>(blk + kTCodes + n * kTScalePitch + 4 * t);
+  const int r = rblk * 16 + n;
+  const int g = min(4 * t + q, kGK - 1);             // groups 90, 91 of the last k-tile: zeroed at the use
+  c = load16<true>(s.codes + (long long)r * kRowBytes + 16 * g);
+  if constexpr (W == kWRaw) {
+    sc = s.scales[(long long)r * kGK + g];
   } else {
-    const int r = rblk * 16 + n;
-    const int g = min(4 * t + q, kGK - 1);           // groups 90, 91 of the last k-tile: zeroed at the use
-    c = load16<true>(s.codes + (long long)r * kRowBytes + 16 * g);
-    uint32_t e;
-    if constexpr (W == kWRaw) {
-      e = s.scales[(long long)r * kGK + g];
-    } else {
-      const uint8_t* row = s.scales + (long long)r * kPs4Row;
-      const uint32_t nib = row[1 + (g >> 1)];
-      e = row[0] + ((g & 1) ? (nib >> 4) : (nib & 15));
-    }
-    sc = e;
+    const uint8_t* row = s.scales + (long long)r * kPs4Row;
+    const uint32_t nib = row[1 + (g >> 1)];
+    sc = row[0] + ((g & 1) ? (nib >> 4) : (nib & 15));
   }
 }
 
@@ -266,18 +258,9 @@ struct XRows {
 };
 
 // FP4 B operand of k-tile t in the MFMA order (lane 16 kb + n: the 16 code bytes of group 4t + kb of row n), groups
-// beyond K zeroed.  The raw and PS4 loads already are in that order; the t950 tiles are transposed across the lanes.
-template <int W>
+// beyond K zeroed.  Every layout's load already is in that order.
 NA_DEVICE mfma_i32x8_t w_operand8(uint4 c, int t, int lane) {
-  if constexpr (W == kWT950) {
-    if (t == kTFull) {                                 // half tile: the lane's 8 bytes are groups 88, 89
-      c.z = 0;
-      c.w = 0;
-    }
-    tile_to_mfma_b(c.x, c.y, c.z, c.w);
-  } else {
-    if (4 * t + (lane >> 4) >= kGK) c = make_uint4(0, 0, 0, 0);
-  }
+  if (4 * t + (lane >> 4) >= kGK) c = make_uint4(0, 0, 0, 0);
   return mfma_i32x8_t{(int)c.x, (int)c.y, (int)c.z, (int)c.w, 0, 0, 0, 0};
 }
 
@@ -298,7 +281,7 @@ struct WStream {
     for (int nb = 0; nb < NB; ++nb) {
       if constexpr (W == kWT950) {
         const uint8_t* bk = src.codes + (long long)blk[nb] * kTBlock;
-        c[nb] = load16(bk + (t < kTFull ? t * 1024 + 16 * lane : kTFull * 1024 + 8 * lane));
+        c[nb] = load16(bk + t * 1024 + 16 * lane);
         sc[nb] = 0;
       } else {
         w_load<W>(src, blk[nb], t, lane, c[nb], sc[nb]);
@@ -331,7 +314,7 @@ NA_DEVICE void gemm8_step(int t, const WStream<W, NB>& ws, bool live, const S& s
     int sb[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      b[nb] = w_operand8<W>(c[nb], t, lane);
+      b[nb] = w_operand8(c[nb], t, lane);
       sb[nb] = ws.scale(t, nb, sc[nb]);
     }
     __builtin_amdgcn_s_setprio(1);                     // the MFMA burst issues ahead of the other wave's staging

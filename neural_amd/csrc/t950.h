@@ -2,10 +2,10 @@
 //
 // 13,271,040 B per slot: 540 row blocks of 16 rows (gate_up rows 0..5759 = blocks 0..359, the up half from block 180;
 // down rows 0..2879 = blocks 360..539), each 24,576 B:
-//   codes  [0, 23040):  22 full k-tiles of 1024 B (groups 4t..4t+3) and one half k-tile of 512 B (groups 88, 89).
-//          In a full tile, lane l = 16 q + n owns bytes [16 l, 16 l + 16) = for j = 0..3 the 4 code bytes 4q..4q+3 of
-//          (row n, group 4t + j), i.e. E2M1 elements 32 (4t + j) + 8q .. + 7 of row n.  In the half tile lane l owns
-//          8 bytes at 8 l: the same for j = 0, 1 (groups 88, 89).
+//   codes  [0, 23040):  90 groups of 256 B, group-major: byte 256 g + 16 n + b = code byte b of (row n, group g).
+//          k-tile t (groups 4t..4t+3; the last, t = 22, only groups 88 and 89 in 512 B) is the 1024 B at 1024 t, and
+//          lane l = 16 kb + n owns its bytes [16 l, 16 l + 16) = E2M1 elements 32 (4t + kb) .. + 31 of row n: one
+//          128-bit load per lane is the FP4 B operand of v_mfma_scale_f32_16x16x128_f8f6f4 as it stands.
 //   scales [23040, 24576): 16 rows x 96 B, byte n * 96 + g = E8M0 of (row n, group g), bytes 90..95 of a row = 0.
 #pragma once
 #include "common.h"
@@ -97,24 +97,6 @@ NA_DEVICE void x8_quant_chunk(uint4 v, uint2& hi, uint2& lo, uint32_t& sh, uint3
   }
   hi = make_uint2(hc[0], hc[1]);
   lo = make_uint2(lc[0], lc[1]);
-}
-
-// t950 code dwords (lane 16 q + n holds bytes 4q .. 4q + 3 of groups 4t + j in dword j) -> the FP4 B operand order of
-// v_mfma_scale_f32_16x16x128_f8f6f4 (lane 16 kb + n holds the 16 bytes of group 4t + kb of row n, i.e. B[k = 32 kb ..
-// 32 kb + 31][n]): a 4 x 4 transpose across the lane quarters, two v_permlane32_swap then two v_permlane16_swap.
-NA_DEVICE void tile_to_mfma_b(uint32_t& w0, uint32_t& w1, uint32_t& w2, uint32_t& w3) {
-  auto p = __builtin_amdgcn_permlane32_swap(w0, w2, false, false);
-  w0 = p[0];
-  w2 = p[1];
-  p = __builtin_amdgcn_permlane32_swap(w1, w3, false, false);
-  w1 = p[0];
-  w3 = p[1];
-  p = __builtin_amdgcn_permlane16_swap(w0, w1, false, false);
-  w0 = p[0];
-  w1 = p[1];
-  p = __builtin_amdgcn_permlane16_swap(w2, w3, false, false);
-  w2 = p[0];
-  w3 = p[1];
 }
 
 }  // namespace na

@@ -3,13 +3,12 @@
 //
 // Layout of one slot (13,271,040 B): 540 row blocks of 16 rows (gate_up rows 0..5759 = blocks 0..359, down rows
 // 0..2879 = blocks 360..539), each 24,576 B:
-//   codes  [0, 23040):  22 full k-tiles of 1024 B (groups 4t..4t+3) and one half k-tile of 512 B (groups 88, 89).
-//          In a full tile, lane l = 16 q + n owns bytes [16 l, 16 l + 16) = for j = 0..3 the 4 code bytes 4q..4q+3 of
-//          (row n, group 4t + j), i.e. E2M1 elements 32 (4t + j) + 8q .. + 7 of row n.  In the half tile lane l owns
-//          8 bytes at 8 l: the same for j = 0, 1 (groups 88, 89).
+//   codes  [0, 23040):  90 groups of 256 B, group-major: byte 256 g + 16 n + b = code byte b of (row n, group g).
+//          k-tile t (groups 4t..4t+3; the last, t = 22, only groups 88 and 89) is the 1024 B at 1024 t, and lane
+//          l = 16 kb + n owns its bytes [16 l, 16 l + 16) = E2M1 elements 32 (4t + kb) .. + 31 of row n.
 //   scales [23040, 24576): 16 rows x 96 B, byte n * 96 + g = E8M0 of (row n, group g), bytes 90..95 of a row = 0.
-// One 128-bit load per lane of a full tile is exactly the B operands of four v_mfma_f32_16x16x32_bf16 (one per group:
-// lane l supplies B[k = 8 (l / 16) + 0..7][n = l % 16]) for the 16 rows of the block.  The codes are the store's
+// One 128-bit load per lane of a k-tile is exactly the FP4 B operand of one v_mfma_scale_f32_16x16x128_f8f6f4 (lane
+// l supplies B[k = 32 (l / 16) + 0..31][n = l % 16]) for the 16 rows of the block.  The codes are the store's
 // E2M1 nibbles unchanged and the scales the store's E8M0 bytes unchanged (PS4 rows are expanded), so the repack is a
 // byte permutation plus padding and round-trips exactly (na_repack_from_t950).
 #include "common.h"
@@ -38,8 +37,8 @@ NA_DEVICE int store_scale(const uint8_t* slot, int ps4, int mat, int row, int g)
   return s[0] + ((g & 1) ? (b >> 4) : (b & 15));
 }
 
-// One thread per 16 bytes of destination.  Per row block: 1440 code pieces (22 x 64 full-tile pieces, then 32 pieces
-// of the half tile, two lanes' 8 bytes each) and 96 scale pieces (16 rows x 6).
+// One thread per 16 bytes of destination.  Per row block: 1440 code pieces (piece 16 g + n = the 16 code bytes of row
+// n, group g) and 96 scale pieces (16 rows x 6).
 constexpr int kTPiecesPerBlock = kTCodes / 16 + kTRows * kTScalePitch / 16;   // 1440 + 96 = 1536
 
 __global__ __launch_bounds__(256) void k_repack_to_t950(const uint8_t* __restrict__ src, long long src_stride, int ps4,
@@ -54,20 +53,11 @@ __global__ __launch_bounds__(256) void k_repack_to_t950(const uint8_t* __restric
   const int row0 = (mat == 0 ? blk : blk - kTGateBlocks) * kTRows;
   const uint8_t* slot = src + (long long)s * src_stride;
   uint32_t out[4];
-  if (pc < kTFull * 64) {                               // full tile t, lane l
-    const int t = pc >> 6, l = pc & 63, n = l & 15, q = l >> 4;
-    const uint8_t* row = store_code_row(slot, mat, row0 + n);
+  if (pc < kTCodes / 16) {                              // codes of (row n, group g)
+    const int g = pc >> 4, n = pc & 15;
+    const uint8_t* row = store_code_row(slot, mat, row0 + n) + 16 * g;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) out[j] = *reinterpret_cast<const uint32_t*>(row + (4 * t + j) * 16 + 4 * q);
-  } else if (pc < kTCodes / 16) {                       // half tile: two lanes (2 x 8 bytes)
-    const int lp = 2 * (pc - kTFull * 64);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int l = lp + h, n = l & 15, q = l >> 4;
-      const uint8_t* row = store_code_row(slot, mat, row0 + n);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) out[2 * h + j] = *reinterpret_cast<const uint32_t*>(row + (88 + j) * 16 + 4 * q);
-    }
+    for (int j = 0; j < 4; ++j) out[j] = *reinterpret_cast<const uint32_t*>(row + 4 * j);
   } else {                                              // scales: row n, bytes 16c .. 16c + 15
     const int sp = pc - kTCodes / 16, n = sp / 6, c = sp - 6 * (sp / 6);
     uint8_t b[16];
@@ -100,24 +90,13 @@ __global__ __launch_bounds__(256) void k_repack_from_t950(const uint8_t* __restr
   const int row0 = (mat == 0 ? blk : blk - kTGateBlocks) * kTRows;
   const uint8_t* b = src + (long long)s * src_stride + (long long)blk * kTBlock;
   uint8_t* slot = dst + (long long)s * dst_stride;
-  if (pc < kTFull * 64) {
-    const int t = pc >> 6, l = pc & 63, n = l & 15, q = l >> 4;
+  if (pc < kTCodes / 16) {                              // codes of (row n, group g)
+    const int g = pc >> 4, n = pc & 15;
     const uint4 v = *reinterpret_cast<const uint4*>(b + 16 * pc);
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    uint8_t* row = slot + (mat == 0 ? 0 : kOffDownCodes) + (long long)(row0 + n) * kRowBytes;
+    uint8_t* row = slot + (mat == 0 ? 0 : kOffDownCodes) + (long long)(row0 + n) * kRowBytes + 16 * g;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<uint32_t*>(row + (4 * t + j) * 16 + 4 * q) = w[j];
-  } else if (pc < kTCodes / 16) {
-    const int lp = 2 * (pc - kTFull * 64);
-    const uint4 v = *reinterpret_cast<const uint4*>(b + 16 * pc);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int l = lp + h, n = l & 15, q = l >> 4;
-      uint8_t* row = slot + (mat == 0 ? 0 : kOffDownCodes) + (long long)(row0 + n) * kRowBytes;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) *reinterpret_cast<uint32_t*>(row + (88 + j) * 16 + 4 * q) = w[2 * h + j];
-    }
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<uint32_t*>(row + 4 * j) = w[j];
   } else {
     const int n = pc - kTCodes / 16;
     const uint8_t* sr = b + kTCodes + n * kTScalePitch;
@@ -140,8 +119,8 @@ __global__ __launch_bounds__(256) void k_repack_from_t950(const uint8_t* __restr
 // scales, consumed as stored (no dequantisation instruction); A = the activations of the expert's tokens as E4M3 with
 // one E8M0 scale per 32-element block, two A rows per token (hi and lo, see x8_quant_chunk), so that one MFMA serves up
 // to 8 tokens.  The KS partial tiles are summed in a fixed order through LDS.  Code tiles are read with non-temporal
-// 128-bit loads (each weight byte is used once per step) and put into the MFMA's operand order by four lane-swap
-// instructions; a row block's 1,536 scale bytes are read by the workgroup with coalesced 16-byte loads and staged in
+// 128-bit loads (each weight byte is used once per step), one load per lane and k-tile being the MFMA's B operand as
+// it stands; a row block's 1,536 scale bytes are read by the workgroup with coalesced 16-byte loads and staged in
 // LDS, so that each wave reads its scales from LDS instead of issuing one scattered 64-lane load per tile.
 constexpr int kMaxTokT = 8;                  // tokens per expert the MFMA M dimension holds (two A rows each)
 constexpr int kScPitch = 112;                // LDS bytes per staged weight scale row: 28 dwords, 16 rows hit 16 banks
@@ -163,9 +142,9 @@ struct CodeRegs {
 
 // Branch-free: every wave issues exactly MT loads, all before any wait.  Slot i holds tile t0 + i when that is below
 // t1, else a copy of tile t0 whose codes block_compute replaces by zeros (E2M1 code 0 is +0, so the slot adds
-// nothing).  The half tile is read as 16 bytes per lane at 8-byte stride (the last lane's excess bytes fall in the
-// block's scale rows) and block_compute zeroes its groups 90 and 91.  The zeroing happens at the use, so that no
-// wait for the codes is placed before the first barrier.
+// nothing).  In the half tile (t = 22) lanes 32..63 (groups 90, 91, past K) read the first 512 bytes of the block's
+// scale rows, which block_compute replaces by zeros.  The zeroing happens at the use, so that no wait for the codes
+// is placed before the first barrier.
 NA_DEVICE int slot_tile(int t0, int t1, int i) { return t0 + i < t1 ? t0 + i : t0; }
 
 template <int MT>
@@ -173,8 +152,7 @@ NA_DEVICE void code_load(const uint8_t* blk, int lane, int t0, int t1, CodeRegs<
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
     const int t = slot_tile(t0, t1, i);
-    const int off = t < kTFull ? t * 1024 + 16 * lane : kTFull * 1024 + 8 * lane;
-    r.c[i] = load16<true>(blk + off);
+    r.c[i] = load16<true>(blk + t * 1024 + 16 * lane);
   }
 }
 
@@ -327,10 +305,9 @@ NA_DEVICE void block_compute(const CodeRegs<MT>& r, const uint8_t* wsc, const ui
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
     const int t = slot_tile(t0, t1, i);
-    const bool live = t0 + i < t1, full = live && t < kTFull;
-    uint32_t w0 = live ? r.c[i].x : 0u, w1 = live ? r.c[i].y : 0u, w2 = full ? r.c[i].z : 0u, w3 = full ? r.c[i].w : 0u;
-    tile_to_mfma_b(w0, w1, w2, w3);
     const int g = 4 * t + kb;                              // B: this lane's group; A: this lane's first K block
+    const bool ok = t0 + i < t1 && g < kGK;
+    const uint32_t w0 = ok ? r.c[i].x : 0u, w1 = ok ? r.c[i].y : 0u, w2 = ok ? r.c[i].z : 0u, w3 = ok ? r.c[i].w : 0u;
     const int sb = wsc[g];                                 // groups 90, 91: the row's zero padding (codes are 0)
     const int sa = arow ? asc[min(g, kGK - 1)] : 127;
     const uint8_t* ap = arow ? arow + 128 * t : zero;

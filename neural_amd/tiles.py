@@ -3,13 +3,14 @@ repack launchers.
 
 A t950 slot (13,271,040 B) holds the same logical data as a raw store slot (13,219,200 B): 540 row blocks of 16 rows
 (gate_up blocks 0..359, down blocks 360..539), each 24,576 B =
-    codes  22 full k-tiles x 1024 B (groups 4t..4t+3) + 1 half k-tile x 512 B (groups 88, 89);
-           full tile: byte 16 l + 4 j + b (lane l = 16 q + n) = code byte 4q + b of (row n, group 4t + j)
-           half tile: byte  8 l + 4 j + b                      = code byte 4q + b of (row n, group 88 + j)
+    codes  90 groups x 256 B, group-major: byte 256 g + 16 n + b = code byte b of (row n, group g), i.e. k-tile t
+           (groups 4t..4t+3, the last one groups 88, 89 only) is the 1024 B at 1024 t and the 16 B at 1024 t + 16 l
+           are the code bytes of (row n, group 4t + kb) for lane l = 16 kb + n;
     scales 16 rows x 96 B: byte 96 n + g = E8M0 of (row n, group g) for g < 90, 0 for g = 90..95.
-A lane's 16 bytes of a full tile are exactly the B operands of four v_mfma_f32_16x16x32_bf16 for the block's 16 rows,
-and a lane's scales are one aligned row.  The repack is a byte permutation (plus PS4 expansion and zero padding), so
-raw -> t950 -> raw and PS4 -> t950 -> PS4 (canonical PS4, base = row minimum) are exact.
+One 128-bit load per lane of a k-tile is exactly the FP4 B operand of one v_mfma_scale_f32_16x16x128_f8f6f4 for the
+block's 16 rows (lane 16 kb + n: B[32 kb .. 32 kb + 31][n]), and a lane's scales are one aligned row.  The repack
+is a byte permutation (plus PS4 expansion and zero padding), so raw -> t950 -> raw and PS4 -> t950 -> PS4 (canonical
+PS4, base = row minimum) are exact.
 """
 from __future__ import annotations
 
@@ -30,24 +31,15 @@ assert SLOT_T950 == 13_271_040
 
 # ------------------------------------------------------------------------------------------- host codec (numpy)
 def _codes_to_blocks(codes: np.ndarray) -> np.ndarray:
-    """codes u8 [N, 90, 16] -> [N / 16, 23040] tile bytes."""
+    """codes u8 [N, 90, 16] -> [N / 16, 23040] tile bytes (per row block: [group][row][16 bytes])."""
     nrb = codes.shape[0] // ROWS
-    c = codes.reshape(nrb, ROWS, sp.GROUPS, 16)
-    full = c[:, :, :88, :].reshape(nrb, ROWS, FULL_TILES, 4, 4, 4)        # rb, n, t, j, q, b
-    full = full.transpose(0, 2, 4, 1, 3, 5).reshape(nrb, FULL_TILES * 1024)  # rb, t, q, n, j, b
-    tail = c[:, :, 88:, :].reshape(nrb, ROWS, 2, 4, 4)                   # rb, n, j, q, b
-    tail = tail.transpose(0, 3, 1, 2, 4).reshape(nrb, 512)                # rb, q, n, j, b
-    return np.concatenate([full, tail], axis=1)
+    return np.ascontiguousarray(codes.reshape(nrb, ROWS, sp.GROUPS, 16).transpose(0, 2, 1, 3)).reshape(nrb, CODE_BYTES)
 
 
 def _blocks_to_codes(blk: np.ndarray) -> np.ndarray:
     nrb = blk.shape[0]
-    full = blk[:, :FULL_TILES * 1024].reshape(nrb, FULL_TILES, 4, ROWS, 4, 4).transpose(0, 3, 1, 4, 2, 5)
-    tail = blk[:, FULL_TILES * 1024:CODE_BYTES].reshape(nrb, 4, ROWS, 2, 4).transpose(0, 2, 3, 1, 4)
-    c = np.empty((nrb, ROWS, sp.GROUPS, 16), np.uint8)
-    c[:, :, :88, :] = full.reshape(nrb, ROWS, 88, 16)
-    c[:, :, 88:, :] = tail.reshape(nrb, ROWS, 2, 16)
-    return c.reshape(nrb * ROWS, sp.GROUPS, 16)
+    c = blk.reshape(nrb, sp.GROUPS, ROWS, 16).transpose(0, 2, 1, 3)
+    return np.ascontiguousarray(c).reshape(nrb * ROWS, sp.GROUPS, 16)
 
 
 def _scales_to_blocks(sc: np.ndarray) -> np.ndarray:

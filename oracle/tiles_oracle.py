@@ -15,15 +15,14 @@ SLOT_T950 = (GU // ROWS + H // ROWS) * BLOCK
 
 
 def code_dest(mat: int, row: int, g: int, byte: int) -> int:
-    """t950 offset of code byte `byte` of (row, group g) of matrix mat (0 = gate_up, 1 = down)."""
+    """t950 offset of code byte `byte` of (row, group g) of matrix mat (0 = gate_up, 1 = down).  k-tile t holds groups
+    4t .. 4t + 3 in 1024 bytes at 1024 t (the last, t = 22, only groups 88 and 89 in 512 bytes), in which the 16 bytes
+    of MFMA lane l = 16 kb + n, at 16 l, are the code bytes 0..15 of (row n, group 4t + kb)."""
     blk = (0 if mat == 0 else GU // ROWS) + row // ROWS
     n = row % ROWS
-    q, b = byte // 4, byte % 4
-    lane = 16 * q + n
-    if g < 88:
-        t, j = g // 4, g % 4
-        return blk * BLOCK + t * 1024 + 16 * lane + 4 * j + b
-    return blk * BLOCK + FULL * 1024 + 8 * lane + 4 * (g - 88) + b
+    t, kb = g // 4, g % 4
+    lane = 16 * kb + n
+    return blk * BLOCK + t * 1024 + 16 * lane + byte
 
 
 def scale_dest(mat: int, row: int, g: int) -> int:
@@ -37,11 +36,8 @@ def source_to_dest_map() -> np.ndarray:
     for mat, rows, off in ((0, GU, 0), (1, H, OFF_DC)):
         r, g, byte = np.meshgrid(np.arange(rows), np.arange(GK), np.arange(16), indexing="ij")
         blk = (0 if mat == 0 else GU // ROWS) + r // ROWS
-        n, q, b = r % ROWS, byte // 4, byte % 4
-        lane = 16 * q + n
-        full = blk * BLOCK + (g // 4) * 1024 + 16 * lane + 4 * (g % 4) + b
-        tail = blk * BLOCK + FULL * 1024 + 8 * lane + 4 * (g - 88) + b
-        out[off:off + rows * GK * 16] = np.where(g < 88, full, tail).reshape(-1)
+        lane = 16 * (g % 4) + r % ROWS
+        out[off:off + rows * GK * 16] = (blk * BLOCK + (g // 4) * 1024 + 16 * lane + byte).reshape(-1)
     rows = np.arange(GU + H)
     mat = (rows >= GU).astype(np.int64)
     r_in = np.where(mat == 0, rows, rows - GU)

@@ -38,9 +38,10 @@ def test_byte_map_is_a_bijection_onto_non_padding_bytes():
     off = pad % to.BLOCK
     assert (off >= to.CODE).all() and ((off - to.CODE) % to.PITCH >= 90).all()     # only scale-row padding
     # spot-check the closed form at the tile boundaries
-    assert to.code_dest(0, 0, 0, 0) == 0 and to.code_dest(0, 1, 0, 0) == 16
-    assert to.code_dest(0, 0, 0, 4) == 256 and to.code_dest(0, 0, 1, 0) == 4 and to.code_dest(0, 0, 4, 0) == 1024
-    assert to.code_dest(0, 0, 88, 0) == 22 * 1024 and to.code_dest(1, 0, 0, 0) == 360 * to.BLOCK
+    assert to.code_dest(0, 0, 0, 0) == 0 and to.code_dest(0, 1, 0, 0) == 16 and to.code_dest(0, 0, 0, 15) == 15
+    assert to.code_dest(0, 0, 1, 0) == 256 and to.code_dest(0, 15, 3, 15) == 1023 and to.code_dest(0, 0, 4, 0) == 1024
+    assert to.code_dest(0, 0, 88, 0) == 22 * 1024 and to.code_dest(0, 15, 89, 15) == to.CODE - 1
+    assert to.code_dest(0, 16, 0, 0) == to.BLOCK and to.code_dest(1, 0, 0, 0) == 360 * to.BLOCK
 
 
 def test_round_trips(slot):
@@ -57,27 +58,27 @@ def test_round_trips(slot):
 
 
 def test_dequant_through_tiles_matches_store(slot):
-    """Decode lanes of one t950 block the way the MFMA kernels read them and compare with the store's dequant."""
+    """Decode lanes of one t950 block the way the MFMA kernels read them (lane 16 kb + n of k-tile t: the 16 bytes at
+    1024 t + 16 lane, group 4t + kb of row n, element 2i + h = nibble h of byte i) and compare with the store's
+    dequant."""
     t = tiles.slot_to_t950(slot).reshape(540, tiles.BLOCK_BYTES)
     wg, _ = mo.expert_weights(slot)
     for blk in (0, 7, 359):
         b = t[blk]
         sc = b[tiles.CODE_BYTES:].reshape(16, 96)
         for tt in (0, 13, 22):
-            for lane in (0, 17, 63):
-                n, q = lane % 16, lane // 16
-                ng = 4 if tt < 22 else 2
-                piece = b[tt * 1024 + 16 * lane: tt * 1024 + 16 * lane + 16] if tt < 22 else \
-                    b[22 * 1024 + 8 * lane: 22 * 1024 + 8 * lane + 8]
-                for j in range(ng):
-                    g = 4 * tt + j
-                    word = piece[4 * j: 4 * j + 4]
-                    vals = np.empty(8, np.float32)
-                    vals[0::2] = mo.E2M1[word & 15]
-                    vals[1::2] = mo.E2M1[word >> 4]
-                    vals *= mo.e8m0_value(sc[n, g])
-                    row = 16 * blk + n
-                    assert np.array_equal(vals, wg[row, 32 * g + 8 * q: 32 * g + 8 * q + 8])
+            for lane in (0, 17, 31, 63):
+                n, kb = lane % 16, lane // 16
+                g = 4 * tt + kb
+                if g >= 90:                        # the last k-tile's lanes 32..63 are past K
+                    continue
+                piece = b[tt * 1024 + 16 * lane: tt * 1024 + 16 * lane + 16]
+                vals = np.empty(32, np.float32)
+                vals[0::2] = mo.E2M1[piece & 15]
+                vals[1::2] = mo.E2M1[piece >> 4]
+                vals *= mo.e8m0_value(sc[n, g])
+                row = 16 * blk + n
+                assert np.array_equal(vals, wg[row, 32 * g: 32 * g + 32])
 
 
 # ================================================================================================ GPU
@@ -416,8 +417,8 @@ def test_x8_quantiser_round_trip_and_rounding():
 @pytest.mark.gpu
 def test_block_scaled_mfma_operand_order():
     """One v_mfma_scale_f32_16x16x128_f8f6f4 exactly as the decode kernels issue it: A = E4M3 codes with one E8M0
-    scale per row and 32-K block, B = a t950 k-tile (lane 16 q + n holds bytes 4q .. 4q + 3 of groups 0..3 of row n)
-    put into the MFMA's order by the lane swaps, with one E8M0 scale per row and group; against the fp64 product."""
+    scale per row and 32-K block, B = a t950 k-tile as loaded (lane 16 kb + n holds the 16 code bytes of group kb of
+    row n), with one E8M0 scale per row and group; against the fp64 product."""
     import torch
     from neural_amd import _native as N
     dev = _dev()
@@ -429,13 +430,13 @@ def test_block_scaled_mfma_operand_order():
     sb = rng.integers(118, 135, (16, 4), dtype=np.uint8)
     tile = rng.integers(0, 256, 1024, dtype=np.uint8)
     # B[k][n]: group j = k // 32, element e = k % 32 = nibble e % 2 of code byte e // 2 of (row n, group j), which the
-    # t950 tile holds at lane 16 (byte // 4) + n, dword j, byte byte % 4
+    # t950 tile holds at byte 16 (16 j + n) + e // 2
     B = np.zeros((128, 16))
     for n in range(16):
         for k in range(128):
             j, e = divmod(k, 32)
             byte = e // 2
-            v = tile[16 * (16 * (byte // 4) + n) + 4 * j + byte % 4]
+            v = tile[16 * (16 * j + n) + byte]
             B[k, n] = mo.E2M1[(v >> 4) if e % 2 else (v & 15)] * 2.0 ** (int(sb[n, j]) - 127)
     A = tab[a] * np.repeat(2.0 ** (sa.astype(np.int64) - 127), 32, axis=1)
     want = A @ B
