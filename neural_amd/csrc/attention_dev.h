@@ -10,19 +10,16 @@ namespace na {
 constexpr int kNQ = 64, kNKV = 8, kHD = 64, kRep = 8;
 constexpr int kSub = 256;                          // keys per sub-chunk (4 waves x 64)
 constexpr int kAttnMaxSplit = 64;
-constexpr int kPartFloats = kRep + kRep + kRep * kHD;   // m[8], S[8], acc[8][64] per chunk
+// Split-K partials of one (sequence, KV head) over its ns chunks: acc [8 rows][ns][64] (row r, chunk c at (r ns + c) 64),
+// then m [ns][8] and S [ns][8]: ns x kPartFloats floats.  Chunk-minor acc rows put one lane's values of successive
+// chunks 256 bytes apart, so the combine reads them at immediate offsets from a few base addresses.
+constexpr int kPartFloats = kRep + kRep + kRep * kHD;
 constexpr int kVtPitch = kSub * 2 + 16;            // LDS bytes per V^T row (d), padded against bank conflicts
 constexpr int kPPitch = kSub * 2 + 16;             // LDS bytes per P row
 constexpr float kNegInf = -__builtin_huge_valf();
 
 struct AttnLds {
-  union {
-    __align__(16) uint8_t vt[kHD * kVtPitch];      // V^T of the sub-chunk, bf16 [d][key]
-    struct {                                       // after the last sub-chunk, the combine's chunk maxima and sums
-      float cm[kAttnMaxSplit][kRep];
-      float cs[kAttnMaxSplit][kRep];
-    };
-  };
+  __align__(16) uint8_t vt[kHD * kVtPitch];        // V^T of the sub-chunk, bf16 [d][key]
   __align__(16) uint8_t p[kRep * kPPitch];         // P of the sub-chunk, bf16 [row][key]: the MFMA's A rows 8..15
                                                    // re-read rows 0..7 (their outputs are not used)
   float mx[4][kRep];                               // per-wave row maxima
@@ -79,6 +76,82 @@ NA_DEVICE void tagged_group_rows(const uint64_t* qkv, int h, uint32_t gen, uint3
   }
 }
 
+// The split-K combine of one (sequence, KV head), run by the last of its ns chunk workgroups: head = the head's
+// partials, orow = its 8 output rows; att (the fused block): also the output's tagged words, with tag.  Wave w
+// finishes rows w and w + 4, lane l their column d = l, and the lower (upper) half of the wave stands for row w
+// (w + 4): half-lane j reads chunk j's and chunk 32 + j's maximum and sum of that row.  The row's maximum m (the sink
+// included) is the half's maximum; half-lane j forms its chunks' weights w_c = exp(m_c - m); then every lane takes
+// the weights and sums by v_readlane (wave-uniform) and forms, in chunk order, S = exp(sink - m) + sum_c s_c w_c and
+// o = sum_c acc_c[row][d] w_c for both rows; out = o / S.  One round of device-coherent loads (sc1), all in flight
+// together (the partials were published with device-coherent stores before the count), through a buffer resource
+// over the head's partials: an offset past them reads 0 (the buffer's range check), and every value of a chunk past
+// ns is masked, so no load needs a branch or a clamped address.  No LDS, no barrier.
+NA_DEVICE void attn_combine(const float* __restrict__ head, int ns, float sink, uint16_t* __restrict__ orow,
+                            uint64_t* att, uint32_t tag) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, jw = lane & 31, rh = w + 4 * (lane >> 5);
+  // rs: the head's partials; rs2: the same from chunk 32 on (acc columns only), so that the second round of chunks
+  // uses the first round's offsets
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(head), 0,
+                                                                      ns * kPartFloats * 4, kBufDword3);
+  const __amdgpu_buffer_rsrc_t rs2 = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(head) + 32 * kHD, 0, max(ns * kPartFloats - 32 * kHD, 0) * 4, kBufDword3);
+  auto ldr = [](__amdgpu_buffer_rsrc_t r, int off_bytes) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off_bytes, 0, kBufSc1));
+  };
+  auto ld = [&rs, &ldr](int off_bytes) { return ldr(rs, off_bytes); };
+  const int ms = kRep * kHD * ns;                      // m [ns][8], then S [ns][8]
+  float mc0 = ld(4 * (ms + jw * kRep + rh)), mc1 = ld(4 * (ms + (32 + jw) * kRep + rh));
+  float sc0 = ld(4 * (ms + kRep * ns + jw * kRep + rh)), sc1 = ld(4 * (ms + kRep * ns + (32 + jw) * kRep + rh));
+  float va[32], vb[32];
+  const int a0 = 4 * (w * ns * kHD + lane), b0 = a0 + 4 * 4 * ns * kHD;   // rows w, w + 4 at chunk 0
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    va[j] = ld(a0 + 4 * kHD * j);
+    vb[j] = ld(b0 + 4 * kHD * j);
+  }
+  mc0 = jw < ns ? mc0 : kNegInf;
+  mc1 = 32 + jw < ns ? mc1 : kNegInf;
+  sc0 = jw < ns ? sc0 : 0.f;
+  sc1 = 32 + jw < ns ? sc1 : 0.f;
+  const float mx = row16_max(fmaxf(mc0, mc1));
+  const float m = fmaxf(sink, fmaxf(mx, lane_xor16(mx)));          // the half's row maximum
+  const float s0 = expf(sink - m);
+  const int wl[2] = {__builtin_bit_cast(int, mc0 == kNegInf ? 0.f : expf(mc0 - m)),
+                     __builtin_bit_cast(int, mc1 == kNegInf ? 0.f : expf(mc1 - m))};
+  const int sl[2] = {__builtin_bit_cast(int, sc0), __builtin_bit_cast(int, sc1)};
+  auto lanef = [](int v, int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(v, l)); };
+  float Sa = lanef(__builtin_bit_cast(int, s0), 0), Sb = lanef(__builtin_bit_cast(int, s0), 32), oa = 0.f, ob = 0.f;
+#pragma nounroll
+  for (int rd = 0; rd < 2 && 32 * rd < ns; ++rd) {     // uniform; ns <= 64
+    if (rd > 0) {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        va[j] = ldr(rs2, a0 + 4 * kHD * j);
+        vb[j] = ldr(rs2, b0 + 4 * kHD * j);
+      }
+    }
+    const int wr = rd ? wl[1] : wl[0], sr = rd ? sl[1] : sl[0];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {                     // chunks past ns: s_c = w_c = 0 add fmaf(0, 0, x) = x
+      const float wa = lanef(wr, j), wb = lanef(wr, 32 + j);
+      const bool live = 32 * rd + j < ns;
+      Sa = fmaf(lanef(sr, j), wa, Sa);
+      Sb = fmaf(lanef(sr, 32 + j), wb, Sb);
+      oa = fmaf(live ? va[j] : 0.f, wa, oa);
+      ob = fmaf(live ? vb[j] : 0.f, wb, ob);
+    }
+  }
+  // bf16 pairs (d, d + 1): even lanes write row w's, odd lanes row w + 4's (word 32 row + d / 2 of the tagged output)
+  const uint16_t ba = f32_to_bf16(oa * (1.f / Sa)), bb = f32_to_bf16(ob * (1.f / Sb));
+  const uint32_t na = __builtin_bit_cast(uint32_t, dpp<0xB1>(__builtin_bit_cast(float, (uint32_t)ba)));
+  const uint32_t nb = __builtin_bit_cast(uint32_t, dpp<0xB1>(__builtin_bit_cast(float, (uint32_t)bb)));
+  const bool odd = lane & 1;
+  const int r = odd ? w + 4 : w, d = lane & ~1;
+  const uint32_t o = odd ? (nb | ((uint32_t)bb << 16)) : ((uint32_t)ba | (na << 16));
+  *reinterpret_cast<uint32_t*>(orow + r * kHD + d) = o;
+  if (att) tag_store(att + r * (kHD / 2) + d / 2, o, tag);
+}
+
 template <bool FUSED>
 NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
                                 const uint16_t* __restrict__ vc, long long cache_rows, const uint16_t* __restrict__ sinks,
@@ -107,7 +180,7 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
   float sink_r[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) sink_r[r] = bf16_to_f32(sk[4 * min(g, 1) + r]);
-  const float sink_c = bf16_to_f32(sk[(2 * tid) / kHD]);
+  const float sink_c = bf16_to_f32(sk[wave + 4 * (lane >> 5)]);   // the combine's row (attn_combine)
   if constexpr (!FUSED) {
     qa0 = *reinterpret_cast<const uint4*>(qrow + 8 * g);
     qa1 = *reinterpret_cast<const uint4*>(qrow + 32 + 8 * g);
@@ -205,29 +278,42 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
       }
     }
     __syncthreads();
-    // ---- sub-chunk max (exact, any order), new running max, P = bf16(exp(s - m_new)), row sums
+    // ---- sub-chunk max (exact, any order), new running max, P = bf16(exp(s - m_new)), row sums.  The scores of
+    // query rows 0..7 sit in lanes g < 2; lanes g >= 2 hold the zero query rows 8..15.  Blocks 2 and 3 of the valid
+    // rows move to the upper half (lane 32 + l takes lane l's, v_permlane32_swap), so that lane (g, n) exponentiates
+    // blocks 2 (g >> 1) and 2 (g >> 1) + 1 of rows 4 (g & 1) + r: every lane eight valid scores.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, s[kb][r]),
+                                                        __builtin_bit_cast(uint32_t, s[kb + 2][r]), false, false);
+        s[kb][r] = __builtin_bit_cast(float, (uint32_t)p[0]);
+      }
+    }
+    const int hb = 2 * (g >> 1);                   // this lane's first key block
     float m_new[4], alpha[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 4 * min(g, 1) + r;
+      const int row = 4 * (g & 1) + r;
       float mx = fmaxf(fmaxf(L.mx[0][row], L.mx[1][row]), fmaxf(L.mx[2][row], L.mx[3][row]));
       m_new[r] = fmaxf(m_run[r], mx);
       alpha[r] = m_new[r] == kNegInf ? 1.f : expf(m_run[r] - m_new[r]);
     }
     float psum[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int kcol = 64 * wave + 16 * kb + n;
+    for (int kb = 0; kb < 2; ++kb) {
+      const int kcol = 64 * wave + 16 * (hb + kb) + n;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float e = s[kb][r] == kNegInf ? 0.f : expf(s[kb][r] - m_new[r]);
         const uint16_t pb = f32_to_bf16(e);
         psum[r] += bf16_to_f32(pb);
-        if (g < 2) *reinterpret_cast<uint16_t*>(L.p + (4 * g + r) * kPPitch + 2 * kcol) = pb;
+        *reinterpret_cast<uint16_t*>(L.p + (4 * (g & 1) + r) * kPPitch + 2 * kcol) = pb;
       }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) psum[r] = row16_sum(psum[r]);   // exact in lane n = 0, the one stored
+    for (int r = 0; r < 4; ++r) psum[r] = row16_sum(psum[r] + lane_xor32(psum[r]));   // exact in lane n = 0, g < 2
     if (n == 0 && g < 2) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) L.sm[wave][4 * g + r] = psum[r];
@@ -236,7 +322,7 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
     // ---- running state: S = S alpha + sum of the 4 waves (fixed order); acc = acc alpha + P V
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 4 * min(g, 1) + r;
+      const int row = 4 * (g & 1) + r;
       const float sub = ((L.sm[0][row] + L.sm[1][row]) + L.sm[2][row]) + L.sm[3][row];
       s_run[r] = s_run[r] * alpha[r] + sub;
       m_run[r] = m_new[r];
@@ -278,16 +364,17 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
     }
     return;
   }
-  float* part = work + ((long long)bh * ns + c) * kPartFloats;
+  float* head = work + (long long)bh * ns * kPartFloats;
   if (g < 2) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 4 * g + r;
-      __hip_atomic_store(part + 2 * kRep + row * kHD + 16 * wave + n, acc[r], __ATOMIC_RELAXED,
+      __hip_atomic_store(head + (row * ns + c) * kHD + 16 * wave + n, acc[r], __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
       if (wave == 0 && n == 0) {
-        __hip_atomic_store(part + row, m_run[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(part + kRep + row, s_run[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        float* ms = head + kRep * kHD * ns;
+        __hip_atomic_store(ms + c * kRep + row, m_run[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(ms + kRep * ns + c * kRep + row, s_run[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
@@ -304,76 +391,7 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
   }
   __syncthreads();
   if (!last) return;
-  // Combine.  One round of device-coherent loads (the partials were published with device-coherent stores before
-  // the count), all in flight together: thread tid's two outputs i = 2 tid, 2 tid + 1 (row i / 64) of the first 32
-  // chunks into registers, every chunk's maxima and sums into LDS.  Then each thread forms its row's
-  // maximum m, weights w_c = exp(m_c - m) and S itself (in chunk order) and out[row][d] = sum_c acc_c[row][d] w_c / S.
-  const float* pbase = work + (long long)bh * ns * kPartFloats;
-  const int i = 2 * tid, row = i / kHD;
-  float2 v[32];
-#pragma unroll
-  for (int j = 0; j < 32; ++j)
-    v[j] = j < ns ? load8_coherent(pbase + j * kPartFloats + 2 * kRep + i) : make_float2(0.f, 0.f);
-  // every chunk's maxima and sums (ns x 8 <= 512 of each): both loads of both rounds issued before the LDS stores
-  float lm[2], ls[2];
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int k = min(tid + 256 * it, ns * kRep - 1), cc = k / kRep, r = k - cc * kRep;
-    lm[it] = loadf_coherent(pbase + cc * kPartFloats + r);
-    ls[it] = loadf_coherent(pbase + cc * kPartFloats + kRep + r);
-  }
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int k = tid + 256 * it, cc = k / kRep, r = k - cc * kRep;
-    if (k < ns * kRep) {
-      L.cm[cc][r] = lm[it];
-      L.cs[cc][r] = ls[it];
-    }
-  }
-  __syncthreads();
-  // Branch-free over 32 chunks at a time: every LDS read of a round is issued before the first use (a branch per
-  // chunk would wait out the LDS latency 32 times in a row).  Chunks past ns read in-bounds rows of cm / cs and are
-  // masked: they add fmaf(0, 0, x) = x, so the sums equal the ones over the live chunks, in chunk order.
-  const float sink = sink_c;
-  float m = sink;
-  for (int cb = 0; cb < ns; cb += 32) {                // uniform; ns <= 64
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      const float mc = L.cm[cb + j][row];
-      m = fmaxf(m, cb + j < ns ? mc : kNegInf);
-    }
-  }
-  float S = expf(sink - m), o0 = 0.f, o1 = 0.f;
-  for (int cb = 0; cb < ns; cb += 32) {                // uniform; ns <= 64
-    if (cb > 0) {
-#pragma unroll
-      for (int j = 0; j < 32; ++j)
-        v[j] = cb + j < ns ? load8_coherent(pbase + (cb + j) * kPartFloats + 2 * kRep + i) : make_float2(0.f, 0.f);
-    }
-#pragma unroll
-    for (int j0 = 0; j0 < 32; j0 += 8) {               // 8 chunks' LDS reads in flight, then their arithmetic
-      float mcv[8], csv[8], wv[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        mcv[j] = L.cm[cb + j0 + j][row];
-        csv[j] = L.cs[cb + j0 + j][row];
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) wv[j] = (cb + j0 + j >= ns || mcv[j] == kNegInf) ? 0.f : expf(mcv[j] - m);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        S = fmaf(cb + j0 + j < ns ? csv[j] : 0.f, wv[j], S);
-        o0 = fmaf(v[j0 + j].x, wv[j], o0);
-        o1 = fmaf(v[j0 + j].y, wv[j], o1);
-      }
-    }
-  }
-  {
-    const float inv = 1.f / S;
-    const uint32_t o = (uint32_t)f32_to_bf16(o0 * inv) | ((uint32_t)f32_to_bf16(o1 * inv) << 16);
-    *reinterpret_cast<uint32_t*>(orow + i) = o;
-    if constexpr (FUSED) tag_store(hs.att + bh * (kRep * kHD / 2) + tid, o, launch_tag(hs.gen));
-  }
+  attn_combine(head, ns, sink_c, orow, FUSED ? hs.att + bh * (kRep * kHD / 2) : nullptr, FUSED ? launch_tag(hs.gen) : 0u);
 }
 
 }  // namespace na

@@ -42,6 +42,10 @@ NA_DEVICE float2 load8_coherent(const float* p) {
 NA_DEVICE float loadf_coherent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Dword 3 of a gfx9 buffer resource for raw (stride 0) 32-bit loads: DATA_FORMAT = 32 bit.  Such a load checks its
+// offset against the resource's byte count and reads 0 past it.  Cache policy 16 = sc1: a device-coherent load.
+constexpr int kBufDword3 = 0x00020000;
+constexpr int kBufSc1 = 16;
 // ---- tagged words: a 64-bit word holds a 32-bit payload (low half) and the generation number of the launch that
 // wrote it (high half), written by one 64-bit device-coherent store and read by one 64-bit device-coherent load, so
 // a reader that sees its launch's number sees that launch's payload.  Every word of a tagged area is written once
