@@ -442,7 +442,7 @@ def run_model(A, pool, dev):
     log("model: random-init dense weights")
     w = random_weights(device=dev, seed=77)
     smax = ctx + max(n_new, A.warmup) + 2
-    model = DecodeModel(w, rx, smax=smax, n_split=A.attn_split, sliding_split=A.sliding_split,
+    model = DecodeModel(w, rx, smax=smax, n_split=A.attn_split or None, sliding_split=A.sliding_split,
                         fused_attn=not A.unfused_attn)
     torch.cuda.synchronize()
     rng = np.random.default_rng(4096)
@@ -539,7 +539,7 @@ def run_model(A, pool, dev):
     step_bytes = dense + experts + kv
     cfg = {"workload": f"config4: full 36-layer GPT-OSS-120B-shaped greedy decode, random-init weights, "
                        f"{ctx}-token context, {n_new} tokens, one hipGraph per step, experts t950 resident",
-           "context": ctx, "tokens": n_new, "vocab": int(w.vocab), "attn_split_full": A.attn_split,
+           "context": ctx, "tokens": n_new, "vocab": int(w.vocab), "attn_split_full": model.n_split,
            "attn_split_sliding": A.sliding_split, "deterministic_tokens": same,
            "attention_block": "four launches" if A.unfused_attn else "one launch per layer (na_core_attn_block)",
            "sync_error": model.sync_error(),
@@ -1146,7 +1146,8 @@ def main():
                     help="model: build the context by prompt processing (default) or token by token through the "
                          "decode step")
     ap.add_argument("--prefill-chunk", type=int, default=4096, help="model: prompt block size of the prefill")
-    ap.add_argument("--attn-split", type=int, default=32, help="model: key chunks of full-attention layers")
+    ap.add_argument("--attn-split", type=int, default=0,
+                    help="model: key chunks of full-attention layers (0: attention.auto_split of the cache rows)")
     ap.add_argument("--sliding-split", type=int, default=1, help="model: key chunks of sliding-window layers")
     ap.add_argument("--unfused-attn", action="store_true",
                     help="model: QKV, attention, o_proj and router as four launches per layer instead of one")

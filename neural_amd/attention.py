@@ -24,6 +24,16 @@ from . import _native as N
 H, HP, NQ, NKV, HD, NE, K = 2880, 4096, 64, 8, 64, 128, 4
 REP = NQ // NKV
 MAX_SPLIT = 64
+SUB_KEYS = 256                 # keys one chunk workgroup takes per pass (4 waves x 64)
+
+
+def auto_split(smax: int) -> int:
+    """Key chunks for full-attention layers over caches of ``smax`` positions: as few as keep every chunk within one
+    256-key pass at the longest context.  Under the reference's chunk rule (64-key blocks, ceil(blocks / ns) per
+    chunk) ns = ceil(ceil(smax / 64) / 4) gives chunks of at most 4 blocks; a chunk workgroup's time is that of its
+    passes, so more chunks only add partials to combine, and fewer give some chunk a second pass."""
+    blocks = -(-int(smax) // 64)
+    return max(1, min(MAX_SPLIT, -(-blocks // (SUB_KEYS // 64))))
 
 
 def _check(q, kc, vc, sinks, pos_dev, out, B, ring, sliding):

@@ -21,7 +21,7 @@ constexpr float kNegInf = -__builtin_huge_valf();
 struct AttnLds {
   __align__(16) uint8_t vt[kHD * kVtPitch];        // V^T of the sub-chunk, bf16 [d][key]
   __align__(16) uint8_t p[kRep * kPPitch];         // P of the sub-chunk, bf16 [row][key]: the MFMA's A rows 8..15
-                                                   // re-read rows 0..7 (their outputs are not used)
+                                                   // re-read rows 0..7, so D rows 8..15 repeat rows 0..7
   float mx[4][kRep];                               // per-wave row maxima
   float sm[4][kRep];                               // per-wave row sums
   uint32_t last;                                   // split-K: this workgroup combines
@@ -82,32 +82,36 @@ NA_DEVICE void tagged_group_rows(const uint64_t* qkv, int h, uint32_t gen, uint3
 // (w + 4): half-lane j reads chunk j's and chunk 32 + j's maximum and sum of that row.  The row's maximum m (the sink
 // included) is the half's maximum; half-lane j forms its chunks' weights w_c = exp(m_c - m); then every lane takes
 // the weights and sums by v_readlane (wave-uniform) and forms, in chunk order, S = exp(sink - m) + sum_c s_c w_c and
-// o = sum_c acc_c[row][d] w_c for both rows; out = o / S.  One round of device-coherent loads (sc1), all in flight
-// together (the partials were published with device-coherent stores before the count), through a buffer resource
-// over the head's partials: an offset past them reads 0 (the buffer's range check), and every value of a chunk past
-// ns is masked, so no load needs a branch or a clamped address.  No LDS, no barrier.
+// o = sum_c acc_c[row][d] w_c for both rows over the live chunks; out = o / S.  One round of device-coherent loads
+// (sc1), all in flight together (the partials were published with device-coherent stores before the count),
+// through buffer resources that end where the live chunks end: a load past the end reads 0 without touching memory
+// (the buffer's range check), so no load needs a branch or a clamped address.  No LDS, no barrier.
 NA_DEVICE void attn_combine(const float* __restrict__ head, int ns, float sink, uint16_t* __restrict__ orow,
                             uint64_t* att, uint32_t tag) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, jw = lane & 31, rh = w + 4 * (lane >> 5);
-  // rs: the head's partials; rs2: the same from chunk 32 on (acc columns only), so that the second round of chunks
-  // uses the first round's offsets
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(head), 0,
-                                                                      ns * kPartFloats * 4, kBufDword3);
-  const __amdgpu_buffer_rsrc_t rs2 = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(head) + 32 * kHD, 0, max(ns * kPartFloats - 32 * kHD, 0) * 4, kBufDword3);
+  const int lane = threadIdx.x & 63, jw = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), rh = w + 4 * (lane >> 5);
+  auto rsrc = [](const float* base, int floats) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, max(floats, 0) * 4, kBufDword3);
+  };
   auto ldr = [](__amdgpu_buffer_rsrc_t r, int off_bytes) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off_bytes, 0, kBufSc1));
   };
-  auto ld = [&rs, &ldr](int off_bytes) { return ldr(rs, off_bytes); };
-  const int ms = kRep * kHD * ns;                      // m [ns][8], then S [ns][8]
-  float mc0 = ld(4 * (ms + jw * kRep + rh)), mc1 = ld(4 * (ms + (32 + jw) * kRep + rh));
-  float sc0 = ld(4 * (ms + kRep * ns + jw * kRep + rh)), sc1 = ld(4 * (ms + kRep * ns + (32 + jw) * kRep + rh));
+  // the head's maxima and sums; rows w and w + 4 of acc, chunks 0 .. ns - 1 and (second round) 32 .. ns - 1: a chunk
+  // past ns reads 0 and moves no data
+  const float* ms = head + kRep * kHD * ns;            // m [ns][8], then S [ns][8]
+  const auto rm = rsrc(ms, 2 * kRep * ns);
+  const float* ra = head + w * ns * kHD;
+  const float* rb = head + (w + 4) * ns * kHD;
+  float mc0 = ldr(rm, 4 * (jw * kRep + rh)), mc1 = ldr(rm, 4 * ((32 + jw) * kRep + rh));
+  float sc0 = ldr(rm, 4 * (kRep * ns + jw * kRep + rh)), sc1 = ldr(rm, 4 * (kRep * ns + (32 + jw) * kRep + rh));
   float va[32], vb[32];
-  const int a0 = 4 * (w * ns * kHD + lane), b0 = a0 + 4 * 4 * ns * kHD;   // rows w, w + 4 at chunk 0
+  {
+    const auto r0 = rsrc(ra, ns * kHD), r1 = rsrc(rb, ns * kHD);
 #pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    va[j] = ld(a0 + 4 * kHD * j);
-    vb[j] = ld(b0 + 4 * kHD * j);
+    for (int j = 0; j < 32; ++j) {
+      va[j] = ldr(r0, 4 * (kHD * j + lane));
+      vb[j] = ldr(r1, 4 * (kHD * j + lane));
+    }
   }
   mc0 = jw < ns ? mc0 : kNegInf;
   mc1 = 32 + jw < ns ? mc1 : kNegInf;
@@ -124,21 +128,23 @@ NA_DEVICE void attn_combine(const float* __restrict__ head, int ns, float sink, 
 #pragma nounroll
   for (int rd = 0; rd < 2 && 32 * rd < ns; ++rd) {     // uniform; ns <= 64
     if (rd > 0) {
+      const auto r0 = rsrc(ra + 32 * kHD, (ns - 32) * kHD), r1 = rsrc(rb + 32 * kHD, (ns - 32) * kHD);
 #pragma unroll
       for (int j = 0; j < 32; ++j) {
-        va[j] = ldr(rs2, a0 + 4 * kHD * j);
-        vb[j] = ldr(rs2, b0 + 4 * kHD * j);
+        va[j] = ldr(r0, 4 * (kHD * j + lane));
+        vb[j] = ldr(r1, 4 * (kHD * j + lane));
       }
     }
     const int wr = rd ? wl[1] : wl[0], sr = rd ? sl[1] : sl[0];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {                     // chunks past ns: s_c = w_c = 0 add fmaf(0, 0, x) = x
-      const float wa = lanef(wr, j), wb = lanef(wr, 32 + j);
-      const bool live = 32 * rd + j < ns;
-      Sa = fmaf(lanef(sr, j), wa, Sa);
-      Sb = fmaf(lanef(sr, 32 + j), wb, Sb);
-      oa = fmaf(live ? va[j] : 0.f, wa, oa);
-      ob = fmaf(live ? vb[j] : 0.f, wb, ob);
+    for (int j = 0; j < 32; ++j) {                     // the live chunks, in chunk order
+      if (32 * rd + j < ns) {                          // uniform
+        const float wa = lanef(wr, j), wb = lanef(wr, 32 + j);
+        Sa = fmaf(lanef(sr, j), wa, Sa);
+        Sb = fmaf(lanef(sr, 32 + j), wb, Sb);
+        oa = fmaf(va[j], wa, oa);
+        ob = fmaf(vb[j], wb, ob);
+      }
     }
   }
   // bf16 pairs (d, d + 1): even lanes write row w's, odd lanes row w + 4's (word 32 row + d / 2 of the tagged output)
@@ -177,9 +183,9 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
   uint4 qa0 = make_uint4(0, 0, 0, 0), qa1 = make_uint4(0, 0, 0, 0);
   // the sinks of the rows this thread finishes (constant weights), read now so that no dependent load waits at the end
   const uint16_t* sk = sinks + h * kRep;
-  float sink_r[4];
+  float sink_r[2];                                 // single chunk: rows 4 (g & 1) + 2 (g >> 1) + k (the finish)
 #pragma unroll
-  for (int r = 0; r < 4; ++r) sink_r[r] = bf16_to_f32(sk[4 * min(g, 1) + r]);
+  for (int k = 0; k < 2; ++k) sink_r[k] = bf16_to_f32(sk[4 * (g & 1) + 2 * (g >> 1) + k]);
   const float sink_c = bf16_to_f32(sk[wave + 4 * (lane >> 5)]);   // the combine's row (attn_combine)
   if constexpr (!FUSED) {
     qa0 = *reinterpret_cast<const uint4*>(qrow + 8 * g);
@@ -345,21 +351,26 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
   // ---- finish: a single chunk writes the output; otherwise publish the partial, the last arriver combines
   uint16_t* orow = out + ((long long)b * kNQ + h * kRep) * kHD;
   if (ns == 1) {
-    if (g < 2) {
+    // rows 4 (g & 1) + r: lanes g < 2 finish r = 0, 1, lanes g >= 2 r = 2, 3.  The upper lanes already hold those
+    // rows: their D rows 8..15 are rows 0..7 (P's rows 8..15 re-read rows 0..7), scaled by the same rows' alpha, and
+    // their running maxima and sums are those rows'.
+    const bool up = g >= 2;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float sink = sink_r[r];
-        const float m = fmaxf(sink, m_run[r]);
-        const float a = m_run[r] == kNegInf ? 0.f : expf(m_run[r] - m);
-        const float S = expf(sink - m) + s_run[r] * a;   // the combine's formula, so one chunk == split at pos < 64
-        const uint16_t o = f32_to_bf16((0.f + acc[r] * a) * (1.f / S));
-        orow[(4 * g + r) * kHD + 16 * wave + n] = o;
-        if constexpr (FUSED) {                     // even lanes: (own, lane n + 1) = dims d, d + 1 of the row
-          const uint32_t nb = __builtin_bit_cast(uint32_t, dpp<0xB1>(__builtin_bit_cast(float, (uint32_t)o)));
-          if (!(n & 1))
-            tag_store(hs.att + bh * (kRep * kHD / 2) + ((4 * g + r) * kHD + 16 * wave + n) / 2,
-                      (uint32_t)o | (nb << 16), launch_tag(hs.gen));
-        }
+    for (int k = 0; k < 2; ++k) {
+      const float av = up ? acc[2 + k] : acc[k];
+      const int r = up ? 2 + k : k, row = 4 * (g & 1) + r;
+      const float sink = sink_r[k];
+      const float mr = up ? m_run[2 + k] : m_run[k], sr = up ? s_run[2 + k] : s_run[k];
+      const float m = fmaxf(sink, mr);
+      const float a = mr == kNegInf ? 0.f : expf(mr - m);
+      const float S = expf(sink - m) + sr * a;     // the combine's formula, so one chunk == split at pos < 64
+      const uint16_t o = f32_to_bf16((0.f + av * a) * (1.f / S));
+      orow[row * kHD + 16 * wave + n] = o;
+      if constexpr (FUSED) {                       // even lanes: (own, lane n + 1) = dims d, d + 1 of the row
+        const uint32_t nb = __builtin_bit_cast(uint32_t, dpp<0xB1>(__builtin_bit_cast(float, (uint32_t)o)));
+        if (!(n & 1))
+          tag_store(hs.att + bh * (kRep * kHD / 2) + (row * kHD + 16 * wave + n) / 2, (uint32_t)o | (nb << 16),
+                    launch_tag(hs.gen));
       }
     }
     return;

@@ -25,7 +25,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _native as N
-from .attention import prefill_attention, ring_write
+from .attention import auto_split, prefill_attention, ring_write
 from .moe.experts import ResidentExperts
 
 H, NQ, NKV, HD, NE, TOP_K = 2880, 64, 8, 64, 128, 4
@@ -126,14 +126,15 @@ class DecodeModel:
     ResidentExperts over the same number of layers or more).
 
     smax:       positions the full-attention K/V caches hold (the sequence buffer holds smax tokens)
-    n_split:    key chunks of full-attention layers (1..64); sliding layers use ``sliding_split``
+    n_split:    key chunks of full-attention layers (1..64; None: attention.auto_split(smax)); sliding layers use
+                ``sliding_split``
     ring:       rows of a sliding layer's rolling K/V cache (>= its window; 0: linear caches of smax rows)
     fused_attn: run each layer's QKV, attention, o_proj and router as one launch (na_core_attn_block) instead of four
 
     The step reads its input token from ``seq[pos]`` and writes the argmax to ``pred[pos + 1]`` and, unless
     ``pos + 1 < n_forced``, to ``seq[pos + 1]``; it then advances ``pos``.  All of that state lives on the device."""
 
-    def __init__(self, weights: DecodeWeights, experts: ResidentExperts, smax: int, n_split: int = 32,
+    def __init__(self, weights: DecodeWeights, experts: ResidentExperts, smax: int, n_split: int | None = None,
                  sliding_split: int = 1, ring: int | None = None, keep_logits: bool = False, sample: bool = False,
                  fused_attn: bool = True):
         dev = weights.embed.device
@@ -145,7 +146,8 @@ class DecodeModel:
             raise ValueError("the expert pool holds fewer layers than the model")
         self._check_weights()
         self.smax = int(smax)
-        self.n_split, self.sliding_split = int(n_split), int(sliding_split)
+        self.n_split = auto_split(self.smax) if n_split is None else int(n_split)
+        self.sliding_split = int(sliding_split)
         windows = {ly.sliding for ly in weights.layers if ly.sliding}
         self.ring = (max(windows) if windows else 0) if ring is None else int(ring)
         for win in windows:

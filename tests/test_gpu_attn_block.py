@@ -7,7 +7,7 @@ over consecutive decode steps of a 2-layer model with a sliding layer on a 16-ro
 layer's attention in 1, 4 and 32 chunks (chunks past the position are empty), across the ring wrap; each launch
 leaves its split counters at zero, advances its generation word (the tag of its handoff words) by one and leaves the
 error flag clear; graph replays equal eager steps.  The same bar at configuration 4's geometry (window 128 on a
-128-row ring, 4360 cache rows, 32 chunks) after a 4090-token prefill, across two ring wraps.
+128-row ring, 4360 cache rows, 18 and 32 chunks) after a 4090-token prefill, across two ring wraps.
 """
 import numpy as np
 import pytest
@@ -93,18 +93,19 @@ def test_fused_block_graph_replay_equals_eager(parts):
     assert not fa.sync_error() and err == 0 and counters == 0 and gen > 0
 
 
-def test_fused_block_equals_four_launches_at_model_size(parts):
+@pytest.mark.parametrize("ns", [18, 32])
+def test_fused_block_equals_four_launches_at_model_size(parts, ns):
     """Configuration 4's attention geometry: a sliding layer with window 128 on a 128-row ring and a full layer of
-    4360 cache rows whose attention runs in 32 chunks.  A 4090-token context is prefilled into both models' caches
+    4360 cache rows whose attention runs in 18 chunks (the bench's automatic split: one 256-key pass per chunk) or 32.  A 4090-token context is prefilled into both models' caches
     (the same kernels, so the caches start equal), then 140 greedy steps at positions 4090 .. 4229 (the ring wraps
     at 4096 and 4224): every output of every layer and the caches bit for bit, the error word clear."""
     import torch
     from neural_amd.model import DecodeModel, random_weights
-    print("case attention block fused vs 4 launches at window 128, smax 4360, n_split 32", flush=True)
+    print(f"case attention block fused vs 4 launches at window 128, smax 4360, n_split {ns}", flush=True)
     w = random_weights(n_layers=2, vocab=VOCAB, device="cpu", seed=23, window=128, norm_std=0.1).to(parts["dev"])
     assert [ly.sliding for ly in w.layers] == [128, 0]
-    fa = DecodeModel(w, parts["rx"], smax=4360, n_split=32, fused_attn=True)
-    fb = DecodeModel(w, parts["rx"], smax=4360, n_split=32, fused_attn=False)
+    fa = DecodeModel(w, parts["rx"], smax=4360, n_split=ns, fused_attn=True)
+    fb = DecodeModel(w, parts["rx"], smax=4360, n_split=ns, fused_attn=False)
     assert fa.ring == 128 and tuple(fa.kc[0].shape) == (1, 8, 128, 64) and tuple(fa.kc[1].shape) == (1, 8, 4360, 64)
     prompt = np.random.default_rng(4090).integers(0, VOCAB, 4090)
     for m in (fa, fb):

@@ -93,7 +93,8 @@ def full():
     bdn = (torch.randn(NL * NE, LT.down_n, generator=g, device=dev) * 0.02).to(torch.bfloat16)
     rx = ResidentExperts(pool, LT, bgu, bdn, max_batch=1)
     w = random_weights(device=dev, seed=78)
-    model = DecodeModel(w, rx, smax=CTX + NEW + 8, n_split=32)
+    model = DecodeModel(w, rx, smax=CTX + NEW + 8)          # the bench's key split: auto_split(4360) = 18 chunks
+    assert model.n_split == 18
     prompt = np.random.default_rng(4096).integers(0, w.vocab, CTX)
     trace = []
     model.prefill(prompt, trace=trace)

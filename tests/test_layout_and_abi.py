@@ -304,6 +304,19 @@ def test_ring_reuse_rule_truth_table():
     assert rr == [True, False, True, False, True]
 
 
+def test_auto_split_is_the_fewest_chunks_of_one_pass():
+    """attention.auto_split(smax): under the chunk rule (64-key blocks, ceil(blocks / ns) blocks per chunk) every
+    chunk of a full cache stays within one 256-key pass, and one chunk fewer would give some chunk a second pass
+    (up to the 64-chunk limit).  Brute force over the cache sizes."""
+    from neural_amd import attention as A
+    for smax in list(range(1, 3000, 7)) + [4096, 4354, 4360, 8192, 16384, 16385, 40000]:
+        ns, blocks = A.auto_split(smax), -(-smax // 64)
+        keys = [min(64 * -(-blocks // k), 64 * blocks) for k in range(1, 65)]   # largest chunk at k chunks
+        assert 1 <= ns <= 64 and (keys[ns - 1] <= 256 or ns == 64), smax
+        assert ns == 1 or keys[ns - 2] > 256, smax
+    assert (A.auto_split(4354), A.auto_split(1024), A.auto_split(256), A.auto_split(257)) == (18, 4, 1, 2)
+
+
 def test_attention_workspace_and_argument_checks():
     from neural_amd import _native as N
     lib = N.lib()
