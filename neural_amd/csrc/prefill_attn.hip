@@ -26,6 +26,8 @@
 
 #include <hip/hip_ext.h>
 
+#include <type_traits>
+
 namespace na {
 
 namespace pfa {
@@ -85,12 +87,12 @@ __global__ __launch_bounds__(kThreads) void k_prefill_attn(
   src.h = h;
   const int hq = h * kRep + wave;
   const int q0 = qb * kQB;                            // block-relative first token
-  const long long p0 = src.p0;
-  const long long qpos0 = p0 + q0;
-  const long long hi = p0 + min(q0 + kQB, T);         // one past the last key any query of the block sees
-  long long lo = window > 0 ? qpos0 - window + 1 : 0;
+  const int qpos0 = (int)src.p0 + q0;                 // positions fit 31 bits (the host checks p0 + T)
+  const int hi = (int)src.p0 + min(q0 + kQB, T);      // one past the last key any query of the block sees
+  const int qlast = hi - 1;
+  int lo = window > 0 ? qpos0 - window + 1 : 0;
   lo = lo < 0 ? 0 : (lo / kKeys) * kKeys;
-  const int nt = (int)((hi - lo + kKeys - 1) / kKeys);
+  const int nt = (hi - lo + kKeys - 1) / kKeys;
 
   // Q^T as the B operand: lane (n, g) holds query q0 + 16 qt + n, dims 8g.. (step 0) and 32 + 8g.. (step 1).
   uint4 qf[QT][2];
@@ -101,7 +103,9 @@ __global__ __launch_bounds__(kThreads) void k_prefill_attn(
     qf[qt][0] = *reinterpret_cast<const uint4*>(qr + 8 * g);
     qf[qt][1] = *reinterpret_cast<const uint4*>(qr + 32 + 8 * g);
   }
-  const float sl2 = scaling * kLog2e;                 // scores in the log2 domain: exp(s - m) = exp2(s' - m')
+  // scores in the log2 domain: exp(s scaling - m) = exp2(s scaling log2e - m'), formed as exp2(fma(s, sl2, -m'));
+  // the maximum is taken over the raw scores (s -> s sl2 is monotone, so max(s) sl2 = max(s sl2))
+  const float sl2 = scaling * kLog2e;
   const float sink2 = bf16_to_f32(sinks[hq]) * kLog2e;
   float m[QT], l[QT];
   f32x4_t acc[4][QT];
@@ -118,8 +122,8 @@ __global__ __launch_bounds__(kThreads) void k_prefill_attn(
   const int kk = tid >> 3, kd = tid & 7;
   const int vk = tid & 63, vd = tid >> 6;
   uint4 kreg, vreg;
-  auto load_tile = [&](long long s0) {
-    const long long jk = s0 + kk < hi ? s0 + kk : hi - 1, jv = s0 + vk < hi ? s0 + vk : hi - 1;
+  auto load_tile = [&](int s0) {
+    const int jk = s0 + kk < hi ? s0 + kk : hi - 1, jv = s0 + vk < hi ? s0 + vk : hi - 1;
     kreg = *reinterpret_cast<const uint4*>(src.krow(jk) + 8 * kd);
     vreg = *reinterpret_cast<const uint4*>(src.vrow(jv) + 8 * vd);
   };
@@ -132,13 +136,10 @@ __global__ __launch_bounds__(kThreads) void k_prefill_attn(
           (uint16_t)((i & 1) ? (w4[i >> 1] >> 16) : (w4[i >> 1] & 0xffff));
   };
 
-  load_tile(lo);
-  store_tile(0);
-  __syncthreads();
-  for (int it = 0; it < nt; ++it) {
-    const int buf = it & 1;
-    const long long s0 = lo + (long long)it * kKeys;
-    if (it + 1 < nt) load_tile(s0 + kKeys);
+  // One 64-key tile.  MASK = false: every key of the tile is visible to every query of the block (below the first
+  // query, and inside the window of the last), so no key is masked.
+  auto tile = [&](auto mask_c, int buf, int s0) {
+    constexpr bool MASK = decltype(mask_c)::value;
     // ---- S^T = K Q^T: tile (kt, qt), lane holds keys s0 + 16 kt + 4 g + r of query column n
     float s[4][QT][4];
 #pragma unroll
@@ -157,37 +158,39 @@ __global__ __launch_bounds__(kThreads) void k_prefill_attn(
     }
     // ---- mask, online softmax (per query column), P^T fragments
     uint4 pf[2][QT];
+    bool moved = false;
+    float alpha[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      const long long qp = qpos0 + 16 * qt + n;
+      const int qp = qpos0 + 16 * qt + n;
       float mx = kNegInf;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const long long j = s0 + 16 * kt + 4 * g + r;
-          bool ok = j <= qp && j < hi;
-          if (window > 0) ok = ok && j > qp - window;
-          const float v = ok ? s[kt][qt][r] * sl2 : kNegInf;
-          s[kt][qt][r] = v;
-          mx = fmaxf(mx, v);
+          if constexpr (MASK) {
+            const int j = s0 + 16 * kt + 4 * g + r;
+            bool ok = j <= qp && j < hi;
+            if (window > 0) ok = ok && j > qp - window;
+            s[kt][qt][r] = ok ? s[kt][qt][r] : kNegInf;
+          }
+          mx = fmaxf(mx, s[kt][qt][r]);
         }
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m[qt], mx);           // finite: m starts at the sink
-      const float alpha = __builtin_amdgcn_exp2f(m[qt] - m_new);
+      const float m_new = fmaxf(m[qt], mx * sl2);     // finite: m starts at the sink
+      alpha[qt] = __builtin_amdgcn_exp2f(m[qt] - m_new);
+      moved |= m_new != m[qt];
       m[qt] = m_new;
-      float ls = l[qt] * alpha;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) acc[dt][qt] *= alpha;
+      float ls = l[qt] * alpha[qt];
       uint32_t pk[4][2];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         float e[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          e[r] = __builtin_amdgcn_exp2f(s[kt][qt][r] - m_new);   // exp2(-inf) = +0 for masked keys
+          e[r] = __builtin_amdgcn_exp2f(fmaf(s[kt][qt][r], sl2, -m_new));   // exp2(-inf) = +0 for masked keys
           ls += e[r];
         }
         pk[kt][0] = pack_bf16x2(e[0], e[1]);
@@ -196,6 +199,13 @@ __global__ __launch_bounds__(kThreads) void k_prefill_attn(
       l[qt] = ls;
       pf[0][qt] = make_uint4(pk[0][0], pk[0][1], pk[1][0], pk[1][1]);   // keys 4g.., 16+4g.. of step 0
       pf[1][qt] = make_uint4(pk[2][0], pk[2][1], pk[3][0], pk[3][1]);   // the same of step 1 (+32)
+    }
+    // O^T *= alpha, skipped when no column of the wave moved its maximum (then every alpha is exactly 1)
+    if (__builtin_amdgcn_ballot_w64(moved)) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) acc[dt][qt] *= alpha[qt];
     }
     // ---- O^T += V^T P^T over two 32-key steps
 #pragma unroll
@@ -212,6 +222,20 @@ __global__ __launch_bounds__(kThreads) void k_prefill_attn(
                                                                  0, 0);
       }
     }
+  };
+
+  load_tile(lo);
+  store_tile(0);
+  __syncthreads();
+  for (int it = 0; it < nt; ++it) {
+    const int buf = it & 1;
+    const int s0 = lo + it * kKeys;
+    if (it + 1 < nt) load_tile(s0 + kKeys);
+    const bool inner = s0 + kKeys <= qpos0 && (window == 0 || s0 > qlast - window);   // uniform
+    if (inner)
+      tile(std::false_type{}, buf, s0);
+    else
+      tile(std::true_type{}, buf, s0);
     if (it + 1 < nt) store_tile(buf ^ 1);
     __syncthreads();
   }
@@ -269,6 +293,7 @@ int na_prefill_attention(const void* q, const void* kc, const void* vc, long lon
                          const void* sinks, void* out, long long p0, int T, float scaling, int window, int ring,
                          void* const* events, hipStream_t stream) {
   if (T < 0 || p0 < 0 || window < 0 || ring < 0 || cache_rows <= 0) return kErrArgs;
+  if (p0 + T >= (1LL << 31)) return kErrArgs;           // positions are 32-bit in the kernel
   if (T == 0) return kOk;                             // an empty prompt: nothing to read or write
   if (!q || !kc || !vc || !sinks || !out) return kErrArgs;
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc)) & 15)
