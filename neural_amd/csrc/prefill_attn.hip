@@ -4,11 +4,14 @@
 // s = (q . k) * scaling in fp32; online softmax whose running state starts at (m = sink, l = 1), so the sink joins
 // the denominator; P is rounded to bf16 for the P V product, the row sums use the unrounded P; o = bf16(acc / l).
 //
-// Work layout: one workgroup of 8 waves per (32-token query block, KV head h); wave w is query head 8 h + w, so the
-// eight query heads that share a KV head read each K / V tile from LDS, where it is staged once.  Tiles of 64 keys
-// walk [lo, hi) with lo = max(first query - window + 1, 0) rounded down to 64 (0 on full layers) and hi = one past
-// the block's last query; the next tile's global loads are in flight while the current tile is computed (two LDS
-// buffers, one barrier per tile).  Both products run on v_mfma_f32_16x16x32_bf16 with the queries as the columns:
+// Work layout: one workgroup of 8 waves per (16-token query block, KV head h), two workgroups per CU; wave w is
+// query head 8 h + w, so the eight query heads that share a KV head read each K / V tile from LDS, where it is
+// staged once.  Tiles of 64 keys walk [lo, hi) with lo = max(first query - window + 1, 0) rounded down to 64 (0 on
+// full layers) and hi = one past the block's last query; the next tile's global loads are in flight while the
+// current tile is computed (two LDS buffers, one barrier per tile).  Tiles below the block's first query (and inside
+// the window of its last) need no mask and take a path without one; the O rescale is skipped when no column's
+// running maximum moved.  (Measured on MI355X: 32-token blocks at one workgroup per CU equal on causal layers and
+// slower on sliding ones; 128-key tiles slower.)  Both products run on v_mfma_f32_16x16x32_bf16 with the queries as the columns:
 //   S^T [key][query] = K [key][d] . Q^T [d][query]      (A = K rows from LDS, B = Q held in registers)
 //   O^T [d][query]  += V^T [d][key] . P^T [key][query]   (A = V^T from LDS, B = P^T straight from the S^T registers)
 // A lane then owns one query column in every tile, so the softmax state of that query (running max, the alpha
@@ -33,16 +36,18 @@ namespace na {
 namespace pfa {
 
 constexpr int kNQ = 64, kNKV = 8, kHD = 64, kRep = 8;
-constexpr int kKeys = 64;                  // keys per tile
 constexpr int kKPitch = kHD * 2 + 16;      // LDS bytes per K row: 144 (16-byte reads of 8 rows hit distinct banks)
-constexpr int kVPitch = kKeys * 2 + 8;     // LDS bytes per V^T row: 136 (8-byte reads of 16 rows hit distinct banks)
+// LDS bytes per V^T row of a KEYS-key tile: 136 / 264 (8-byte reads of 16 rows hit distinct banks)
+template <int KEYS>
+constexpr int vt_pitch() { return KEYS * 2 + 8; }
 constexpr int kThreads = 512;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
+template <int KEYS>
 struct Lds {
-  __align__(16) uint8_t k[2][kKeys * kKPitch];
-  __align__(16) uint8_t vt[2][kHD * kVPitch];
+  __align__(16) uint8_t k[2][KEYS * kKPitch];
+  __align__(16) uint8_t vt[2][kHD * vt_pitch<KEYS>()];
 };
 
 NA_DEVICE bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -72,13 +77,14 @@ struct KeySrc {
   }
 };
 
-// QT query tiles of 16 per wave: 16 * QT tokens per workgroup.
-template <int QT>
-__global__ __launch_bounds__(kThreads) void k_prefill_attn(
+// QT query tiles of 16 per wave: 16 * QT tokens per workgroup; KEYS keys per tile (64 or 128).
+template <int QT, int KEYS>
+__global__ __launch_bounds__(kThreads, QT == 1 ? 2 : 1) void k_prefill_attn(
     const uint16_t* __restrict__ q, KeySrc src, const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out,
     int T, float scaling, int window) {
-  constexpr int kQB = 16 * QT;
-  __shared__ Lds L;
+  constexpr int kQB = 16 * QT, kKeys = KEYS, KT = KEYS / 16, KS = KEYS / 32, KP = KEYS / 64;
+  constexpr int kVPitch = vt_pitch<KEYS>();
+  __shared__ Lds<KEYS> L;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, n = lane & 15;
   const int nqb = (T + kQB - 1) / kQB;
@@ -117,33 +123,39 @@ __global__ __launch_bounds__(kThreads) void k_prefill_attn(
     for (int dt = 0; dt < 4; ++dt) acc[dt][qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Staging: K row key tid / 8, dims 8 (tid % 8) (a wave reads 8 whole rows); V key tid % 64, dims 8 (tid / 64),
-  // written transposed (a wave writes 64 consecutive keys of 8 V^T rows).
+  // Staging, per 64 keys of the tile: K row key tid / 8, dims 8 (tid % 8) (a wave reads 8 whole rows); V key
+  // tid % 64, dims 8 (tid / 64), written transposed (a wave writes 64 consecutive keys of 8 V^T rows).
   const int kk = tid >> 3, kd = tid & 7;
   const int vk = tid & 63, vd = tid >> 6;
-  uint4 kreg, vreg;
+  uint4 kreg[KP], vreg[KP];
   auto load_tile = [&](int s0) {
-    const int jk = s0 + kk < hi ? s0 + kk : hi - 1, jv = s0 + vk < hi ? s0 + vk : hi - 1;
-    kreg = *reinterpret_cast<const uint4*>(src.krow(jk) + 8 * kd);
-    vreg = *reinterpret_cast<const uint4*>(src.vrow(jv) + 8 * vd);
+#pragma unroll
+    for (int p = 0; p < KP; ++p) {
+      const int jk = s0 + 64 * p + kk, jv = s0 + 64 * p + vk;
+      kreg[p] = *reinterpret_cast<const uint4*>(src.krow(jk < hi ? jk : hi - 1) + 8 * kd);
+      vreg[p] = *reinterpret_cast<const uint4*>(src.vrow(jv < hi ? jv : hi - 1) + 8 * vd);
+    }
   };
   auto store_tile = [&](int buf) {
-    *reinterpret_cast<uint4*>(L.k[buf] + kk * kKPitch + 16 * kd) = kreg;
-    const uint32_t w4[4] = {vreg.x, vreg.y, vreg.z, vreg.w};
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      *reinterpret_cast<uint16_t*>(L.vt[buf] + (8 * vd + i) * kVPitch + 2 * vk) =
-          (uint16_t)((i & 1) ? (w4[i >> 1] >> 16) : (w4[i >> 1] & 0xffff));
+    for (int p = 0; p < KP; ++p) {
+      *reinterpret_cast<uint4*>(L.k[buf] + (64 * p + kk) * kKPitch + 16 * kd) = kreg[p];
+      const uint32_t w4[4] = {vreg[p].x, vreg[p].y, vreg[p].z, vreg[p].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        *reinterpret_cast<uint16_t*>(L.vt[buf] + (8 * vd + i) * kVPitch + 2 * (64 * p + vk)) =
+            (uint16_t)((i & 1) ? (w4[i >> 1] >> 16) : (w4[i >> 1] & 0xffff));
+    }
   };
 
-  // One 64-key tile.  MASK = false: every key of the tile is visible to every query of the block (below the first
+  // One tile.  MASK = false: every key of the tile is visible to every query of the block (below the first
   // query, and inside the window of the last), so no key is masked.
   auto tile = [&](auto mask_c, int buf, int s0) {
     constexpr bool MASK = decltype(mask_c)::value;
     // ---- S^T = K Q^T: tile (kt, qt), lane holds keys s0 + 16 kt + 4 g + r of query column n
-    float s[4][QT][4];
+    float s[KT][QT][4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
+    for (int kt = 0; kt < KT; ++kt) {
       const uint8_t* kr = L.k[buf] + (16 * kt + n) * kKPitch + 16 * g;
       const uint4 ka0 = *reinterpret_cast<const uint4*>(kr);
       const uint4 ka1 = *reinterpret_cast<const uint4*>(kr + 64);
@@ -157,7 +169,7 @@ __global__ __launch_bounds__(kThreads) void k_prefill_attn(
       }
     }
     // ---- mask, online softmax (per query column), P^T fragments
-    uint4 pf[2][QT];
+    uint4 pf[KS][QT];
     bool moved = false;
     float alpha[QT];
 #pragma unroll
@@ -165,7 +177,7 @@ __global__ __launch_bounds__(kThreads) void k_prefill_attn(
       const int qp = qpos0 + 16 * qt + n;
       float mx = kNegInf;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           if constexpr (MASK) {
@@ -177,16 +189,16 @@ __global__ __launch_bounds__(kThreads) void k_prefill_attn(
           mx = fmaxf(mx, s[kt][qt][r]);
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = fmaxf(mx, lane_xor16(mx));                 // the 4 lanes of column n (VALU lane swaps, no LDS)
+      mx = fmaxf(mx, lane_xor32(mx));
       const float m_new = fmaxf(m[qt], mx * sl2);     // finite: m starts at the sink
       alpha[qt] = __builtin_amdgcn_exp2f(m[qt] - m_new);
       moved |= m_new != m[qt];
       m[qt] = m_new;
       float ls = l[qt] * alpha[qt];
-      uint32_t pk[4][2];
+      uint32_t pk[KT][2];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int kt = 0; kt < KT; ++kt) {
         float e[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -197,8 +209,9 @@ __global__ __launch_bounds__(kThreads) void k_prefill_attn(
         pk[kt][1] = pack_bf16x2(e[2], e[3]);
       }
       l[qt] = ls;
-      pf[0][qt] = make_uint4(pk[0][0], pk[0][1], pk[1][0], pk[1][1]);   // keys 4g.., 16+4g.. of step 0
-      pf[1][qt] = make_uint4(pk[2][0], pk[2][1], pk[3][0], pk[3][1]);   // the same of step 1 (+32)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)                 // step ks: keys 32 ks + 4g.., 32 ks + 16 + 4g..
+        pf[ks][qt] = make_uint4(pk[2 * ks][0], pk[2 * ks][1], pk[2 * ks + 1][0], pk[2 * ks + 1][1]);
     }
     // O^T *= alpha, skipped when no column of the wave moved its maximum (then every alpha is exactly 1)
     if (__builtin_amdgcn_ballot_w64(moved)) {
@@ -207,9 +220,9 @@ __global__ __launch_bounds__(kThreads) void k_prefill_attn(
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) acc[dt][qt] *= alpha[qt];
     }
-    // ---- O^T += V^T P^T over two 32-key steps
+    // ---- O^T += V^T P^T over the 32-key steps
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         const uint8_t* vr = L.vt[buf] + (16 * dt + n) * kVPitch + 2 * (32 * ks + 4 * g);
@@ -308,11 +321,11 @@ int na_prefill_attention(const void* q, const void* kc, const void* vc, long lon
   }
   KeySrc src{(const uint16_t*)kc, (const uint16_t*)vc, (const uint16_t*)k_new, (const uint16_t*)v_new,
              cache_rows, sk_t, sk_h, sv_t, sv_h, p0, ring, 0};
-  constexpr int QT = 2;                               // 32 tokens per workgroup (163 VGPRs: no spills)
+  constexpr int QT = 1;                               // 16 tokens per workgroup, two workgroups per CU
   const int qb = 16 * QT;
   const dim3 grid((unsigned)(((long long)T + qb - 1) / qb * kNKV)), block(kThreads);
   hipEvent_t e0 = events ? (hipEvent_t)events[0] : nullptr, e1 = events ? (hipEvent_t)events[1] : nullptr;
-  auto kern = k_prefill_attn<QT>;
+  auto kern = k_prefill_attn<QT, 64>;
   if (e0 || e1)
     hipExtLaunchKernelGGL(kern, grid, block, 0, stream, e0, e1, 0, (const uint16_t*)q, src, (const uint16_t*)sinks,
                           (uint16_t*)out, T, scaling, window);
