@@ -14,12 +14,12 @@ constexpr int kAttnMaxSplit = 64;
 // then m [ns][8] and S [ns][8]: ns x kPartFloats floats.  Chunk-minor acc rows put one lane's values of successive
 // chunks 256 bytes apart, so the combine reads them at immediate offsets from a few base addresses.
 constexpr int kPartFloats = kRep + kRep + kRep * kHD;
-constexpr int kVtPitch = kSub * 2 + 16;            // LDS bytes per V^T row (d), padded against bank conflicts
+constexpr int kVPitch = kHD * 2 + 8;               // LDS bytes per V row (key): 136, 8-byte aligned
 constexpr int kPPitch = kSub * 2 + 16;             // LDS bytes per P row
 constexpr float kNegInf = -__builtin_huge_valf();
 
 struct AttnLds {
-  __align__(16) uint8_t vt[kHD * kVtPitch];        // V^T of the sub-chunk, bf16 [d][key]
+  __align__(16) uint8_t v[kSub * kVPitch];         // V of the sub-chunk, bf16 [key][d] (read transposed)
   __align__(16) uint8_t p[kRep * kPPitch];         // P of the sub-chunk, bf16 [row][key]: the MFMA's A rows 8..15
                                                    // re-read rows 0..7, so D rows 8..15 repeat rows 0..7
   float mx[4][kRep];                               // per-wave row maxima
@@ -29,6 +29,7 @@ struct AttnLds {
 
 
 NA_DEVICE bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
 
 // Key range [c0, c1) of chunk c (empty when c0 >= c1): the reference's split rule over 64-key blocks of [lo, hi].
 NA_DEVICE void chunk_range(int lo, int hi, int c, int ns, int& c0, int& c1) {
@@ -246,6 +247,17 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
         }
       }
     }
+    // ---- V rows to LDS as they are (the P V step reads them transposed; stored before the scores, so that their
+    // registers are free by then): lane (g, n) holds d = 8g..8g+7 and 32+8g.. of key 16 kb + n of this wave's 64
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      uint8_t* vrow = L.v + (64 * wave + 16 * kb + n) * kVPitch;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        *reinterpret_cast<uint2*>(vrow + 2 * (32 * hf + 8 * g)) = make_uint2(vr[kb][hf].x, vr[kb][hf].y);
+        *reinterpret_cast<uint2*>(vrow + 2 * (32 * hf + 8 * g) + 8) = make_uint2(vr[kb][hf].z, vr[kb][hf].w);
+      }
+    }
     // ---- scores s = bf16(bf16(q . k) * scaling), -inf outside [k0, c1)
     float s[4][4];                                 // [block][r]
     float wmax[4] = {kNegInf, kNegInf, kNegInf, kNegInf};
@@ -267,21 +279,6 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
     if (n == 0 && g < 2) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) L.mx[wave][4 * g + r] = wmax[r];
-    }
-    // ---- V^T to LDS: lane (g, n) holds d = 8g..8g+7 and 32+8g.. of key 16 kb + n of this wave's 64
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int kcol = 64 * wave + 16 * kb + n;
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const uint32_t w4[4] = {vr[kb][hf].x, vr[kb][hf].y, vr[kb][hf].z, vr[kb][hf].w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int dd = 32 * hf + 8 * g + i;
-          *reinterpret_cast<uint16_t*>(L.vt + dd * kVtPitch + 2 * kcol) =
-              (uint16_t)((i & 1) ? (w4[i >> 1] >> 16) : (w4[i >> 1] & 0xffff));
-        }
-      }
     }
     __syncthreads();
     // ---- sub-chunk max (exact, any order), new running max, P = bf16(exp(s - m_new)), row sums.  The scores of
@@ -335,12 +332,23 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
       acc[r] *= alpha[r];
     }
     // every 32-key step of the sub-chunk, with no branch, so that all the LDS reads are in flight together: P is
-    // +0 past c1 (and V^T holds finite cache rows there), so those steps add exact zeros to acc (never -0)
+    // +0 past c1 (and V holds finite cache rows there), so those steps add exact zeros to acc (never -0).  V's B
+    // operand (lane (g, n): keys 32 ks + 8 g .. + 7 of dim 16 wave + n) comes from two transposing LDS reads
+    // (ds_read_b64_tr_b16): in each 16-lane group, lane 4 j + q points at key k0 + j, dims 16 wave + 4 q .. + 3, and
+    // lane n receives element n % 4 of lanes n / 4, 4 + n / 4, 8 + n / 4, 12 + n / 4, i.e. keys k0 .. k0 + 3 of dim
+    // 16 wave + n.
+    // (one LDS base per lane, the steps at constant offsets from it)
+    typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+    lds_v4i16_t* const vt0 = reinterpret_cast<lds_v4i16_t*>(
+        (__attribute__((address_space(3))) uint8_t*)(L.v) + (8 * g + ((lane & 15) >> 2)) * kVPitch +
+        2 * (16 * wave + 4 * (lane & 3)));
     uint4 pa[kSub / 32], vb[kSub / 32];
 #pragma unroll
     for (int ks = 0; ks < kSub / 32; ++ks) {
       pa[ks] = *reinterpret_cast<const uint4*>(L.p + (n & (kRep - 1)) * kPPitch + 2 * (32 * ks + 8 * g));
-      vb[ks] = *reinterpret_cast<const uint4*>(L.vt + (16 * wave + n) * kVtPitch + 2 * (32 * ks + 8 * g));
+      const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt0 + 32 * ks * kVPitch / 8);
+      const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt0 + (32 * ks + 4) * kVPitch / 8);
+      vb[ks] = __builtin_bit_cast(uint4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     }
 #pragma unroll
     for (int ks = 0; ks < kSub / 32; ++ks)
