@@ -37,9 +37,9 @@ namespace pfa {
 
 constexpr int kNQ = 64, kNKV = 8, kHD = 64, kRep = 8;
 constexpr int kKPitch = kHD * 2 + 16;      // LDS bytes per K row: 144 (16-byte reads of 8 rows hit distinct banks)
-// LDS bytes per V^T row of a KEYS-key tile: 136 / 264 (8-byte reads of 16 rows hit distinct banks)
-template <int KEYS>
-constexpr int vt_pitch() { return KEYS * 2 + 8; }
+constexpr int kVPitch = kHD * 2 + 16;      // LDS bytes per V row: 144 (read transposed, ds_read_b64_tr_b16)
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 constexpr int kThreads = 512;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
@@ -47,7 +47,7 @@ constexpr float kNegInf = -__builtin_huge_valf();
 template <int KEYS>
 struct Lds {
   __align__(16) uint8_t k[2][KEYS * kKPitch];
-  __align__(16) uint8_t vt[2][kHD * vt_pitch<KEYS>()];
+  __align__(16) uint8_t v[2][KEYS * kVPitch];
 };
 
 NA_DEVICE bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
@@ -83,7 +83,6 @@ __global__ __launch_bounds__(kThreads, QT == 1 ? 2 : 1) void k_prefill_attn(
     const uint16_t* __restrict__ q, KeySrc src, const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out,
     int T, float scaling, int window) {
   constexpr int kQB = 16 * QT, kKeys = KEYS, KT = KEYS / 16, KS = KEYS / 32, KP = KEYS / 64;
-  constexpr int kVPitch = vt_pitch<KEYS>();
   __shared__ Lds<KEYS> L;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, n = lane & 15;
@@ -124,7 +123,7 @@ __global__ __launch_bounds__(kThreads, QT == 1 ? 2 : 1) void k_prefill_attn(
   }
 
   // Staging, per 64 keys of the tile: K row key tid / 8, dims 8 (tid % 8) (a wave reads 8 whole rows); V key
-  // tid % 64, dims 8 (tid / 64), written transposed (a wave writes 64 consecutive keys of 8 V^T rows).
+  // tid % 64, dims 8 (tid / 64), stored as it is (the P V step reads it transposed).
   const int kk = tid >> 3, kd = tid & 7;
   const int vk = tid & 63, vd = tid >> 6;
   uint4 kreg[KP], vreg[KP];
@@ -140,11 +139,7 @@ __global__ __launch_bounds__(kThreads, QT == 1 ? 2 : 1) void k_prefill_attn(
 #pragma unroll
     for (int p = 0; p < KP; ++p) {
       *reinterpret_cast<uint4*>(L.k[buf] + (64 * p + kk) * kKPitch + 16 * kd) = kreg[p];
-      const uint32_t w4[4] = {vreg[p].x, vreg[p].y, vreg[p].z, vreg[p].w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        *reinterpret_cast<uint16_t*>(L.vt[buf] + (8 * vd + i) * kVPitch + 2 * (64 * p + vk)) =
-            (uint16_t)((i & 1) ? (w4[i >> 1] >> 16) : (w4[i >> 1] & 0xffff));
+      *reinterpret_cast<uint4*>(L.v[buf] + (64 * p + vk) * kVPitch + 16 * vd) = vreg[p];
     }
   };
 
@@ -220,15 +215,21 @@ __global__ __launch_bounds__(kThreads, QT == 1 ? 2 : 1) void k_prefill_attn(
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) acc[dt][qt] *= alpha[qt];
     }
-    // ---- O^T += V^T P^T over the 32-key steps
+    // ---- O^T += V^T P^T over the 32-key steps.  V^T's A operand (lane (g, n): dim 16 dt + n, keys 32 ks + 4 g ..
+    // + 3 and 32 ks + 16 + 4 g .. + 3) comes from two transposing LDS reads (ds_read_b64_tr_b16): in each 16-lane
+    // group, lane 4 j + q points at key k0 + j, dims 16 dt + 4 q .. + 3, and lane n receives element n % 4 of lanes
+    // n / 4, 4 + n / 4, 8 + n / 4, 12 + n / 4, i.e. keys k0 .. k0 + 3 of dim 16 dt + n.  One base per lane, every
+    // (ks, dt) at a constant offset from it.
+    lds_v4i16_t* const vt0 = reinterpret_cast<lds_v4i16_t*>(
+        (__attribute__((address_space(3))) uint8_t*)(L.v[buf]) + (4 * g + ((lane & 15) >> 2)) * kVPitch +
+        8 * (lane & 3));
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const uint8_t* vr = L.vt[buf] + (16 * dt + n) * kVPitch + 2 * (32 * ks + 4 * g);
-        const uint2 a0 = *reinterpret_cast<const uint2*>(vr);
-        const uint2 a1 = *reinterpret_cast<const uint2*>(vr + 32);
-        const uint4 va = make_uint4(a0.x, a0.y, a1.x, a1.y);
+        const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt0 + (32 * ks * kVPitch + 32 * dt) / 8);
+        const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(vt0 + ((32 * ks + 16) * kVPitch + 32 * dt) / 8);
+        const uint4 va = __builtin_bit_cast(uint4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt)
           acc[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(va), as_bf16x8(pf[ks][qt]), acc[dt][qt], 0,
