@@ -329,13 +329,16 @@ int na_core_attn_block(void* mid, const void* g, const float* c, void* xbuf, con
                        const void* bo, const void* post_w, const void* Wr, const void* br, void* hn, float* logits,
                        int64_t* ids, void* wts, unsigned int* sync, void* const* events, hipStream_t stream);
 
-/* Workgroup partials na_core_lm_tail needs for a vocabulary (-1 if vocab <= 0). */
+/* uint64 entries of the part buffer na_core_lm_tail needs for a vocabulary (-1 if vocab <= 0). */
 long long na_core_lm_partials(int vocab);
 
-/* Decode tail: residual combine + final RMSNorm, lm_head GEMV, argmax (first index of the maximum).  Replaces
- * server.py:521-525 (t_body).
- *   mid, g, c as na_core_qkv; final_w bf16 [2880]; Wl bf16 [vocab, 2880]; hn bf16 [2880] scratch;
- *   logits_out bf16 [vocab] or NULL; part uint64 [na_core_lm_partials(vocab)] scratch; tok int64 [1] <- argmax
+/* Decode tail: residual combine + final RMSNorm, lm_head GEMV, argmax (first index of the maximum), one launch.
+ * Replaces server.py:521-525 (t_body).  Every workgroup forms the final norm itself and streams its share of lm_head's
+ * rows; the grid's last workgroup reads every workgroup's best key (tagged words in part) and takes the argmax.
+ *   mid, g, c as na_core_qkv; final_w bf16 [2880]; Wl bf16 [vocab, 2880]; hn bf16 [2880] <- the final norm;
+ *   logits_out bf16 [vocab] or NULL; part uint64 [na_core_lm_partials(vocab)], 8-byte aligned, any initial contents,
+ *   owned by one stream (calls that overlap on one part buffer race); its first uint32 is an error word that a wait
+ *   that gave up raises (never cleared by the call); tok int64 [1] <- argmax
  *   pos int64 [1] (p = *pos): pred[p + 1] <- tok (pred int64 [seq_len] or NULL); seq[p + 1] <- tok unless
  *   p + 1 < *n_forced (n_forced int64 [1] or NULL); *pos <- p + 1 when step_pos.  Needs pos for seq/pred/step_pos. */
 int na_core_lm_tail(const void* mid, const void* g, const float* c, const void* final_w, float eps, const void* Wl,

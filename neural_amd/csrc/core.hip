@@ -89,6 +89,8 @@ constexpr int kQkvTpr = NA_QKV_TPR, kOprojTpr = NA_OPROJ_TPR, kRouterTpr = NA_RO
 // weight.
 struct NormIn {
   uint4 m[2], g[2], w[2], c[2][2];
+  // HAS_C = false: c is absent (cp ignored), so its registers need not be held
+  template <bool HAS_C = true>
   NA_DEVICE void load(const uint16_t* __restrict__ mid, const uint16_t* __restrict__ gp, const float* __restrict__ cp,
                       const uint16_t* __restrict__ wp) {
 #pragma unroll
@@ -100,7 +102,7 @@ struct NormIn {
       // requests queue in the L2 with the launch's weight stream); their values are unused
       g[i] = c[i][0] = c[i][1] = make_uint4(0, 0, 0, 0);
       if (gp) g[i] = *reinterpret_cast<const uint4*>(gp + 8 * ch);
-      if (cp) {
+      if (HAS_C && cp) {
         c[i][0] = *reinterpret_cast<const uint4*>(cp + 8 * ch);
         c[i][1] = *reinterpret_cast<const uint4*>(cp + 8 * ch + 4);
       }
@@ -461,27 +463,12 @@ __global__ __launch_bounds__(256) void k_router_norm(const uint16_t* __restrict_
                           nullptr, nullptr, nullptr, 0, nullptr);
 }
 
-// Tail 1: x = bf16(mid + bf16(g + bf16(c))); hn = bf16(w * (x * r)) (one workgroup).
-__global__ __launch_bounds__(256) void k_final_norm(const uint16_t* __restrict__ mid, const uint16_t* __restrict__ g,
-                                                    const float* __restrict__ cext, const uint16_t* __restrict__ w,
-                                                    float eps, uint16_t* __restrict__ hn) {
-  __shared__ __align__(16) uint16_t hc[kH];
-  NormIn ni;
-  ni.load(mid, g, cext, w);
-  norm_finish(ni, g != nullptr, cext != nullptr, eps, hc, nullptr);
-  for (int i = threadIdx.x; i < kH / 8; i += 256)
-    *reinterpret_cast<uint4*>(hn + 8 * i) = *reinterpret_cast<const uint4*>(hc + 8 * i);
-}
-
 // Monotone map of bf16 bit patterns to unsigned order (-0 equal to +0; NaN patterns above +inf).
 NA_DEVICE uint32_t bf16_order_key(uint16_t b) {
   if (b == 0x8000) b = 0;
   return (b & 0x8000) ? (uint32_t)(~b & 0xffff) : (uint32_t)(b | 0x8000);
 }
 
-// Tail 2: logits = bf16(hn . lm_head[v]) for 16 rows per workgroup; the workgroup's best as a 64-bit key
-// (order key of the logit << 32 | ~index: a larger key is a larger logit, then a smaller index) -> part[wg];
-// optionally the logits themselves.
 // Monotone map of fp32 bit patterns to unsigned order (-0 equal to +0).
 NA_DEVICE uint32_t f32_order_key(float f) {
   uint32_t b = __float_as_uint(f);
@@ -515,15 +502,41 @@ struct SampleArgs {
   const uint64_t* seed;
 };
 
-template <int TPR, bool SAMPLE>
-__global__ __launch_bounds__(256) void k_lmhead(const uint16_t* __restrict__ hn, const uint16_t* __restrict__ Wl,
-                                                int vocab, uint16_t* __restrict__ logits_out,
-                                                uint64_t* __restrict__ part, SampleArgs sa) {
+// ---- the decode tail in one launch (na_core_lm_tail; reference server.py:521-525): kTailWgs workgroups (fewer for
+// a small vocabulary).  Each forms the final norm itself, x = bf16(mid + bf16(g + bf16(c))), hn = bf16(w * (x * r))
+// (norm_finish: the same bits in every workgroup; workgroup 0 also writes hn), then streams the 16-row blocks
+// blockIdx.x, blockIdx.x + gridDim.x, ... of lm_head, logit = bf16(hn . row) over TPR threads per row, keeping its
+// best key (the logit's order key << 32 | ~index: a larger key is a larger logit, then a smaller index), and
+// publishes it as two tagged words (handoff.h: the order key, and ~index).  The grid's last workgroup, once its own
+// rows are done, reads every workgroup's two words, takes the largest key -> tok, and with pos (p = *pos, the
+// position of this step's input token) sets pred[p + 1] = tok when pred is given, seq[p + 1] = tok unless position
+// p + 1 is forced (p + 1 < *n_forced, a prompt token), pos = p + 1 when step_pos (writes stay below seq_len); then it
+// advances the generation word (every workgroup has read the old one: its words carry the number formed from it).
+// One launch instead of three (norm, lm_head, argmax): 175 -> 168 us per step at vocab 201,088.  The workgroups are
+// persistent (3 per CU at this kernel's registers; c, when absent, holds none).  part: [line 0: error word][line 1:
+// generation word][2 x grid tagged words] (uint32 lines of kLine), see na_core_lm_partials; any initial contents
+// work, and a wait that gives up raises the error word.
+constexpr int kTailWgs = 768;                              // 3 per CU (the kernel's occupancy) x 256 CUs
+constexpr int kTailHead = 2 * kLine / 2;                    // uint64 entries of part before the tagged words
+
+template <int TPR, bool SAMPLE, bool HAS_C>
+__global__ __launch_bounds__(256) void k_tail(const uint16_t* __restrict__ mid, const uint16_t* __restrict__ g,
+                                              const float* __restrict__ cext, const uint16_t* __restrict__ fw,
+                                              float eps, const uint16_t* __restrict__ Wl, int vocab,
+                                              uint16_t* __restrict__ hn, uint16_t* __restrict__ logits_out,
+                                              uint32_t* __restrict__ part, int64_t* __restrict__ tok,
+                                              int64_t* __restrict__ pos, int step_pos, int64_t* __restrict__ seq,
+                                              const int64_t* __restrict__ n_forced, int64_t* __restrict__ pred,
+                                              long long seq_len, SampleArgs sa) {
   __shared__ __align__(16) uint16_t hc[kH];
   constexpr int ROWS = 256 / TPR;
-  __shared__ uint64_t best[ROWS];
+  __shared__ uint64_t best_lds[ROWS];
   const int tid = threadIdx.x, r = tid / TPR, j = tid % TPR;
-  const int v = ROWS * blockIdx.x + r;
+  const int nblk = (vocab + ROWS - 1) / ROWS, nwg = gridDim.x;
+  uint32_t* err = part;
+  uint32_t* gen_word = part + kLine;
+  uint64_t* words = reinterpret_cast<uint64_t*>(part) + kTailHead;
+  const uint32_t gen = load_coherent(gen_word);             // raw: the tag is formed where it is first used
   float temp = 0.f;
   uint64_t p = 0, seed = 0;
   if constexpr (SAMPLE) {
@@ -531,66 +544,93 @@ __global__ __launch_bounds__(256) void k_lmhead(const uint16_t* __restrict__ hn,
     p = sa.pos ? (uint64_t)*sa.pos : 0;
     seed = sa.seed ? *sa.seed : 0;
   }
-  VecIn<kH> a;
-  a.load(hn);
+  NormIn ni;
+  ni.load<HAS_C>(mid, g, cext, fw);
+  int rb = blockIdx.x;
+  int v = ROWS * rb + r;
   __builtin_amdgcn_sched_barrier(0);
   RowChunks<kH, TPR> rw;
   rw.load(Wl + (long long)min(v, vocab - 1) * kH, j);
   __builtin_amdgcn_sched_barrier(0);
-  a.store(hc);
-  const float s = rw.dot(hc, j);
-  const uint16_t lb = f32_to_bf16(s);
-  if (j == 0) {
-    if (logits_out && v < vocab) logits_out[v] = lb;
-    uint32_t key = bf16_order_key(lb);
-    if constexpr (SAMPLE) {
-      if (temp > 0.f && v < vocab) {
-        float u = sa.u ? sa.u[v] : uniform_draw(seed, p, (uint32_t)v);
-        u = fminf(fmaxf(u, 1e-12f), 1.0f - 1e-7f);
-        const float gum = -logf(-logf(u));
-        key = f32_order_key(bf16_to_f32(lb) / temp + gum);
+  norm_finish(ni, g != nullptr, HAS_C && cext != nullptr, eps, hc, nullptr);
+  if (blockIdx.x == 0)
+    for (int i = tid; i < kH / 8; i += 256)
+      *reinterpret_cast<uint4*>(hn + 8 * i) = *reinterpret_cast<const uint4*>(hc + 8 * i);
+  uint64_t best = 0;                                        // this row group's best key (lane j == 0)
+  for (;;) {
+    const float s = rw.dot(hc, j);
+    const int vr = v;
+    rb += nwg;
+    v = ROWS * rb + r;
+    __builtin_amdgcn_sched_barrier(0);                  // one block's registers: the next loads after this dot
+    if (rb < nblk) rw.load(Wl + (long long)min(v, vocab - 1) * kH, j);   // uniform
+    __builtin_amdgcn_sched_barrier(0);
+    if (j == 0 && vr < vocab) {
+      const uint16_t lb = f32_to_bf16(s);
+      if (logits_out) logits_out[vr] = lb;
+      uint32_t key = bf16_order_key(lb);
+      if constexpr (SAMPLE) {
+        if (temp > 0.f) {
+          float u = sa.u ? sa.u[vr] : uniform_draw(seed, p, (uint32_t)vr);
+          u = fminf(fmaxf(u, 1e-12f), 1.0f - 1e-7f);
+          const float gum = -logf(-logf(u));
+          key = f32_order_key(bf16_to_f32(lb) / temp + gum);
+        }
       }
+      const uint64_t k = ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)vr);
+      best = k > best ? k : best;
     }
-    best[r] = v < vocab ? ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)v) : 0ull;
+    if (rb >= nblk) break;
   }
+  if (j == 0) best_lds[r] = best;
   __syncthreads();
+  const uint32_t tag = launch_tag(gen);
   if (tid == 0) {
-    uint64_t b = best[0];
-    for (int i = 1; i < ROWS; ++i) b = best[i] > b ? best[i] : b;
-    part[blockIdx.x] = b;
+    uint64_t b = best_lds[0];
+    for (int i = 1; i < ROWS; ++i) b = best_lds[i] > b ? best_lds[i] : b;
+    tag_store(words + 2 * blockIdx.x, (uint32_t)(b >> 32), tag);
+    tag_store(words + 2 * blockIdx.x + 1, (uint32_t)b, tag);
   }
-}
-
-// Tail 3: argmax over the workgroup keys -> tok.  With pos (p = *pos, the position of this step's input token):
-// pred[p + 1] = tok when pred is given; seq[p + 1] = tok unless position p + 1 is forced (p + 1 < *n_forced, a prompt
-// token); pos = p + 1 when step_pos.  Writes stay below seq_len.
-__global__ __launch_bounds__(1024) void k_argmax(const uint64_t* __restrict__ part, int n, int64_t* __restrict__ tok,
-                                                 int64_t* __restrict__ pos, int step_pos, int64_t* __restrict__ seq,
-                                                 const int64_t* __restrict__ n_forced, int64_t* __restrict__ pred,
-                                                 long long seq_len) {
-  __shared__ uint64_t red[16];
+  if ((int)blockIdx.x != nwg - 1) return;
+  // the argmax over every workgroup's key: thread t reads the words of workgroups t, t + 256, t + 512, t + 768
+  __shared__ uint64_t red[4];
   uint64_t b = 0;
-  for (int i = threadIdx.x; i < n; i += 1024) b = part[i] > b ? part[i] : b;
+  for (int w0 = 0; w0 < nwg; w0 += 4 * 256) {
+    const uint64_t* src[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int w = min(w0 + tid + 256 * k, nwg - 1);
+      src[2 * k] = words + 2 * w;
+      src[2 * k + 1] = words + 2 * w + 1;
+    }
+    uint32_t kw[8];
+    tag_read_at<8>(src, tag, kw, err);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint64_t c = ((uint64_t)kw[2 * k] << 32) | kw[2 * k + 1];
+      b = c > b ? c : b;
+    }
+  }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
     const uint64_t ob = ((uint64_t)(uint32_t)__shfl_xor((int)(b >> 32), o) << 32) | (uint32_t)__shfl_xor((int)b, o);
     b = ob > b ? ob : b;
   }
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = b;
+  if ((tid & 63) == 0) red[tid >> 6] = b;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int i = 1; i < 16; ++i) b = red[i] > b ? red[i] : b;
-    const int64_t t = (int64_t)(0xffffffffu - (uint32_t)(b & 0xffffffffu));
-    *tok = t;
-    if (pos) {
-      const long long p = *pos, nx = p + 1;
-      if (nx < seq_len && nx >= 0) {
-        if (pred) pred[nx] = t;
-        if (seq && !(n_forced && nx < *n_forced)) seq[nx] = t;
-      }
-      if (step_pos) *pos = nx;
+  if (tid != 0) return;
+  for (int i = 1; i < 4; ++i) b = red[i] > b ? red[i] : b;
+  const int64_t t = (int64_t)(0xffffffffu - (uint32_t)(b & 0xffffffffu));
+  *tok = t;
+  if (pos) {
+    const long long p0 = *pos, nx = p0 + 1;
+    if (nx < seq_len && nx >= 0) {
+      if (pred) pred[nx] = t;
+      if (seq && !(n_forced && nx < *n_forced)) seq[nx] = t;
     }
+    if (step_pos) *pos = nx;
   }
+  store_coherent(gen_word, tag);
 }
 
 // ---- prompt rows (prefill of T tokens; reference server.py:2357-2403 _rope_tables / _attn_router and
@@ -942,7 +982,10 @@ int na_core_attn_block(void* mid, const void* g, const float* c, void* xbuf, con
 
 long long na_core_attn_block_sync_words(void) { return kSyncWords; }
 
-long long na_core_lm_partials(int vocab) { return vocab > 0 ? (vocab + 256 / kLmTpr - 1) / (256 / kLmTpr) : -1; }
+// Workgroups of the tail's launch: kTailWgs, or one per 16-row block of a smaller vocabulary.
+static int tail_wgs(int vocab) { return min(kTailWgs, (vocab + 256 / kLmTpr - 1) / (256 / kLmTpr)); }
+
+long long na_core_lm_partials(int vocab) { return vocab > 0 ? kTailHead + 2LL * tail_wgs(vocab) : -1; }
 
 int na_core_lm_tail(const void* mid, const void* g, const float* c, const void* final_w, float eps, const void* Wl,
                     int vocab, void* hn, void* logits_out, unsigned long long* part, int64_t* tok, int64_t* pos,
@@ -952,13 +995,12 @@ int na_core_lm_tail(const void* mid, const void* g, const float* c, const void* 
   if ((step_pos || seq || pred) && !pos) return kErrArgs;
   if ((seq || pred) && seq_len <= 0) return kErrArgs;
   if (c && !g) return kErrArgs;
-  const int nwg = (int)na_core_lm_partials(vocab);
-  hipLaunchKernelGGL(k_final_norm, dim3(1), dim3(256), 0, stream, (const uint16_t*)mid, (const uint16_t*)g, c,
-                     (const uint16_t*)final_w, eps, (uint16_t*)hn);
-  hipLaunchKernelGGL((k_lmhead<kLmTpr, false>), dim3(nwg), dim3(256), 0, stream, (const uint16_t*)hn,
-                     (const uint16_t*)Wl, vocab, (uint16_t*)logits_out, (uint64_t*)part, SampleArgs{});
-  hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, stream, (const uint64_t*)part, nwg, tok, pos, step_pos, seq,
-                     n_forced, pred, seq_len);
+  if (reinterpret_cast<uintptr_t>(part) & 7) return kErrArgs;
+  hipLaunchKernelGGL((c ? k_tail<kLmTpr, false, true> : k_tail<kLmTpr, false, false>), dim3(tail_wgs(vocab)), dim3(256), 0,
+                     stream, (const uint16_t*)mid,
+                     (const uint16_t*)g, c, (const uint16_t*)final_w, eps, (const uint16_t*)Wl, vocab, (uint16_t*)hn,
+                     (uint16_t*)logits_out, (uint32_t*)part, tok, pos, step_pos, seq, n_forced, pred, seq_len,
+                     SampleArgs{});
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
@@ -971,14 +1013,12 @@ int na_core_lm_tail_sample(const void* mid, const void* g, const float* c, const
   if ((step_pos || seq || pred) && !pos) return kErrArgs;
   if ((seq || pred) && seq_len <= 0) return kErrArgs;
   if (c && !g) return kErrArgs;
-  const int nwg = (int)na_core_lm_partials(vocab);
-  hipLaunchKernelGGL(k_final_norm, dim3(1), dim3(256), 0, stream, (const uint16_t*)mid, (const uint16_t*)g, c,
-                     (const uint16_t*)final_w, eps, (uint16_t*)hn);
-  hipLaunchKernelGGL((k_lmhead<kLmTpr, true>), dim3(nwg), dim3(256), 0, stream, (const uint16_t*)hn,
-                     (const uint16_t*)Wl, vocab, (uint16_t*)logits_out, (uint64_t*)part,
+  if (reinterpret_cast<uintptr_t>(part) & 7) return kErrArgs;
+  hipLaunchKernelGGL((c ? k_tail<kLmTpr, true, true> : k_tail<kLmTpr, true, false>), dim3(tail_wgs(vocab)), dim3(256), 0,
+                     stream, (const uint16_t*)mid,
+                     (const uint16_t*)g, c, (const uint16_t*)final_w, eps, (const uint16_t*)Wl, vocab, (uint16_t*)hn,
+                     (uint16_t*)logits_out, (uint32_t*)part, tok, pos, step_pos, seq, n_forced, pred, seq_len,
                      SampleArgs{temp, u, pos, (const uint64_t*)seed});
-  hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, stream, (const uint64_t*)part, nwg, tok, pos, step_pos, seq,
-                     n_forced, pred, seq_len);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

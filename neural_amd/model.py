@@ -406,16 +406,18 @@ class DecodeModel:
 
     # ------------------------------------------------------------------------------------------------ graphs
     def sync_error(self) -> bool:
-        """Whether a fused attention block or a single-launch expert body gave up a wait since the last
+        """Whether a fused attention block, a single-launch expert body or the tail gave up a wait since the last
         clear_sync_error() (the outputs of that step are then invalid).  Reads the device (synchronises).  The
         waits rely on every workgroup of a launch being resident together, which a kernel of another stream or
         process on the same GPU can break; a caller replaying captured steps (run(), capture()) polls this after
         its replays and redoes them with the multi-launch path on True, as generate() does."""
-        return bool(int(self.sync[0].item())) or self.rx.sync_error()
+        return bool(int(self.sync[0].item())) or bool(int(self.part[0].item()) & 0xFFFFFFFF) \
+            or self.rx.sync_error()
 
     def clear_sync_error(self) -> None:
         """Zero the error words (the kernels only ever set them)."""
         self.sync[:1].zero_()
+        self.part[:1].zero_()
         self.rx.clear_sync_error()
 
     def capture(self) -> torch.cuda.CUDAGraph:
