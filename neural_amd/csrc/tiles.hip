@@ -707,6 +707,117 @@ NA_DEVICE void down_body(DecodeLds<KS, XT>& L, int item, int b, long long rid, i
   if (all != users) dup_rows_store_w<TAG>(yw, users, all, nt, b, yb[0], yb[1], wts, tg, ytag);   // uniform, rare
 }
 
+// down for batches of several tokens, two row blocks per workgroup (b and b + 90, grid items x 90): the staging of
+// the tokens' h rows, the routing, the barrier, the K reduction and the epilogue are shared by twice the weight bytes
+// (like gate_up's gate and up blocks), so half as many workgroups carry the same stream, each with twice its bytes in
+// flight.  Each block's arithmetic is down_body's (the same MFMA sums, reduction order and epilogue): the outputs
+// are bit-identical.
+template <int KS, int XT>
+NA_DEVICE void down_body2(DecodeLds<KS, XT>& L, int item, int bb, long long rid, int B, const uint8_t* __restrict__ pool,
+                          long long slot_bytes, const int64_t* __restrict__ slot_tab, long long expert_base,
+                          const uint8_t* __restrict__ h8, const uint16_t* __restrict__ wts,
+                          const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw) {
+  static_assert(KS > 1 && XT > 1, "several tokens, K split over the waves");
+  constexpr int MT = (kTTiles + KS - 1) / KS;
+  constexpr int NTH = 64 * KS;
+  constexpr int kHalf = kTDownBlocks / 2;
+  int nt, distinct, valid;
+  uint64_t users, all;
+  const int e = route_t950<4 * XT>(rid, 4 * B, item, nt, users, all, distinct, valid);
+  if (e < 0) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int bl[2] = {bb, bb + kHalf};
+  if (e == 128) {                                      // invalid ids: each of their pairs contributes +0
+    for (int i = tid; i < 2 * 4 * B * (kTRows / 2); i += NTH) {
+      const int k = i / (4 * B * (kTRows / 2)), r = i - k * (4 * B * (kTRows / 2));
+      const int q = r / (kTRows / 2), c = r - q * (kTRows / 2);
+      if ((all >> q) & 1) *reinterpret_cast<uint32_t*>(yw + (long long)q * kH + 16 * bl[k] + 2 * c) = 0u;
+    }
+    return;
+  }
+  const long long gid = expert_base + e;
+  const long long slot = slot_tab ? slot_tab[gid] : gid;
+  const uint8_t* blk0 = pool + slot * slot_bytes + kTDownOff + (long long)bl[0] * kTBlock;
+  const uint8_t* blk1 = blk0 + (long long)kHalf * kTBlock;
+  int t0, t1;
+  ktile_range<KS>(wave, t0, t1);
+  ScaleRegs<2, NTH> sr;
+  scale_load<2, NTH>(tid, blk0, blk1, sr);
+  XRegs<XT, NTH> xr;
+  h8_load<XT, NTH>(tid, h8, [users](int t) { return pair_at(users, t); }, nt, xr);
+  // epilogue operands are loaded now and converted at their use, so no wait is placed before the barrier
+  uint16_t bdn[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int n = 16 * bl[k] + (lane & 15);
+    bdn[k] = (bias_dn ? bias_dn + gid * kH : wts)[bias_dn ? n : 0];   // unconditional load
+  }
+  uint16_t wr[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) wr[q] = wts[pair_at(users, min(2 * (lane >> 4) + q, nt - 1))];
+  CodeRegs<MT> r0, r1;
+  code_load<MT>(blk0, lane, t0, t1, r0);
+  code_load<MT>(blk1, lane, t0, t1, r1);
+  __builtin_amdgcn_sched_barrier(0);
+  x8_store<XT, NTH>(tid, L.x, nt, xr);
+  scale_store<2, NTH>(tid, L.sc, sr);
+  __syncthreads();
+  const uint8_t* arow = a_row(L.x, lane, nt);
+  const uint8_t* asc = a_scales(L.x, lane);
+  const uint8_t* srow = L.sc + (lane & 15) * kScPitch;
+  f32x4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+  block_compute<MT>(r0, srow, arow, asc, L.x.zero, lane, t0, t1, a0);
+  block_compute<MT>(r1, srow + kScLds, arow, asc, L.x.zero, lane, t0, t1, a1);
+  float y[2][2];
+  token_sums(a0, y[0][0], y[0][1]);
+  token_sums(a1, y[1][0], y[1][1]);
+  float* red = L.red();                                // [KS][2 blocks][64][2]
+  if constexpr (DecodeLds<KS, XT>::kAliasRed) __syncthreads();   // every wave is done with the staged rows
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+    *reinterpret_cast<float2*>(red + ((2 * wave + k) * 64 + lane) * 2) = make_float2(y[k][0], y[k][1]);
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    float2 sm = *reinterpret_cast<const float2*>(red + (k * 64 + lane) * 2);
+#pragma unroll
+    for (int w = 1; w < KS; ++w) {
+      const float2 v = *reinterpret_cast<const float2*>(red + ((2 * w + k) * 64 + lane) * 2);
+      sm.x += v.x;
+      sm.y += v.y;
+    }
+    y[k][0] = sm.x;
+    y[k][1] = sm.y;
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    float yb[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int u = 2 * (lane >> 4) + q;
+      float v = rb(y[k][q]);
+      if (bias_dn) v = rb(v + bf16_to_f32(bdn[k]));
+      yb[q] = v;
+      const uint16_t o = f32_to_bf16(v * bf16_to_f32(wr[q]));
+      store_row_pairs(yw + (long long)pair_at(users, min(u, nt - 1)) * kH + 16 * bl[k], o, u < nt);
+    }
+    if (all != users) dup_rows_store_w<false>(yw, users, all, nt, bl[k], yb[0], yb[1], wts, OneTags{}, 0u);   // rare
+  }
+}
+
+template <int KS, int XT>
+__global__ __launch_bounds__(64 * KS) void k_moe_down2_t950(
+    const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
+    const int64_t* __restrict__ slot_tab, long long expert_base, const uint8_t* __restrict__ h8,
+    const uint16_t* __restrict__ wts, const uint16_t* __restrict__ bias_dn, uint16_t* __restrict__ yw) {
+  __shared__ DecodeLds<KS, XT> L;
+  const long long rid = route_ids_load(ids, 4 * B);
+  args_at_entry(h8, wts, bias_dn, yw);                // past the preloaded arguments: fetched while the ids fly
+  down_body2<KS, XT>(L, blockIdx.x, blockIdx.y, rid, B, pool, slot_bytes, slot_tab, expert_base, h8, wts, bias_dn,
+                     yw);
+}
+
 template <int KS, int XT>
 __global__ __launch_bounds__(64 * KS) void k_moe_down_t950(
     const int64_t* __restrict__ ids, int B, const uint8_t* __restrict__ pool, long long slot_bytes,
@@ -996,9 +1107,15 @@ static int decode_t950(const void* x, const int64_t* topk_ids, const void* topk_
              (const uint16_t*)topk_w, (const uint16_t*)bias_dn, (uint16_t*)out);
     return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
   }
-  launch_t(pick_down_t950(k_split, xt), g1, blk, stream, ev[2], ev[3], topk_ids, B, (const uint8_t*)pool, slot_bytes,
-           slot_tab, expert_base, (const uint8_t*)h_scratch, (const uint16_t*)topk_w, (const uint16_t*)bias_dn,
-           (uint16_t*)yw_scratch);
+  if (xt == 8) {                                      // two row blocks per workgroup
+    launch_t(k_split == 4 ? k_moe_down2_t950<4, 8> : k_moe_down2_t950<8, 8>, dim3(items, kTDownBlocks / 2), blk,
+             stream, ev[2], ev[3], topk_ids, B, (const uint8_t*)pool, slot_bytes, slot_tab, expert_base,
+             (const uint8_t*)h_scratch, (const uint16_t*)topk_w, (const uint16_t*)bias_dn, (uint16_t*)yw_scratch);
+  } else {
+    launch_t(pick_down_t950(k_split, xt), g1, blk, stream, ev[2], ev[3], topk_ids, B, (const uint8_t*)pool,
+             slot_bytes, slot_tab, expert_base, (const uint8_t*)h_scratch, (const uint16_t*)topk_w,
+             (const uint16_t*)bias_dn, (uint16_t*)yw_scratch);
+  }
   if (out)
     launch_t(k_combine_t950, dim3((B * kH / 2 + 255) / 256), dim3(256), stream, ev[4], ev[5],
              (const uint32_t*)yw_scratch, B, (uint32_t*)out);

@@ -449,6 +449,38 @@ def test_block_scaled_mfma_operand_order():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("B,k_split", [(5, 4), (8, 4), (8, 8)])
+def test_batch_rows_equal_each_token_alone(B, k_split):
+    """Batches of 5 .. 8 tokens run down in two parts (the experts holding at most two of the tokens, staged two rows
+    at a time, then the others): every row of the batch equals that token decoded alone, bit for bit, with experts
+    shared by 6, 3 and 2 tokens and a duplicated id in one token."""
+    import torch
+    from neural_amd.moe.experts import ResidentExperts
+    from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
+    dev = _dev()
+    slots, x, ids, w, tab, bgu, bdn = _t950_case(B, 1700 + B + k_split, True, nslot=8)
+    print(f"case batch rows vs single tokens B={B} k_split={k_split}", flush=True)
+    ids = ids.copy()
+    ids[:6 if B >= 6 else 3, 0] = 11                   # one expert in 6 (B = 5: 3) tokens: the second part
+    ids[0, 1], ids[2, 2] = 37, 37                      # one expert in two tokens: the first part
+    ids[4, 3] = ids[4, 2]                              # a duplicated id in one token
+    raw =torch.from_numpy(np.stack(slots)).to(dev)
+    tp = torch.empty((len(slots), tiles.SLOT_T950), dtype=torch.uint8, device=dev)
+    tiles.repack_to_t950(raw, tp)
+    rt = ResidentExperts(tp, GPTOSS_LAYOUT_T950, bgu.to(dev), bdn.to(dev), torch.from_numpy(tab).to(dev),
+                         k_split=k_split)
+    xd, idd = x.to(dev), torch.from_numpy(ids).to(dev)
+    wd = torch.from_numpy(w).to(torch.bfloat16).to(dev)
+    layer = 5
+    batch = rt.forward_decode(layer, xd, idd, wd).clone()
+    for b in range(B):
+        alone = rt.forward_decode(layer, xd[b:b + 1], idd[b:b + 1], wd[b:b + 1])
+        torch.cuda.synchronize()
+        assert torch.equal(batch[b:b + 1], alone), (B, k_split, b)
+    assert not rt.sync_error()
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("B", [1, 2, 8])
 def test_duplicate_ids_in_a_token(B):
     """A token whose top-4 list names one expert more than once (and an invalid id twice): each pair is that expert's
