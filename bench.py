@@ -432,7 +432,7 @@ def run_model(A, pool, dev):
     Per-launch times come from dispatch-timestamped events over eager steps.  Returns a dict of the results."""
     import torch
 
-    from neural_amd.model import DecodeModel, random_weights
+    from neural_amd.model import DecodeModel, random_weights, use_tuned_prompt_gemms
     from neural_amd.moe.experts import ResidentExperts
     from neural_amd.moe.layout import GPTOSS_LAYOUT_T950
 
@@ -447,6 +447,11 @@ def run_model(A, pool, dev):
     torch.cuda.synchronize()
     rng = np.random.default_rng(4096)
     prompt = rng.integers(0, w.vocab, ctx)
+    # the prompt's library GEMMs: the committed hipBLASLt choices for these shapes (TunableOp, tuning off), or the
+    # library's default heuristic
+    tuned_read = use_tuned_prompt_gemms(A.prompt_gemms == "tuned")
+    if A.prompt_gemms == "tuned":
+        log(f"model: prompt GEMMs from the committed TunableOp results: {'read' if tuned_read else 'not read'}")
     if A.context_mode == "prefill":
         model.prefill(prompt, chunk=A.prefill_chunk)      # warm-up of the same shapes: library GEMM selection
         torch.cuda.synchronize()
@@ -550,6 +555,8 @@ def run_model(A, pool, dev):
                          "attention_full": round(att_full / (n_l / 2), 2),
                          "attention_sliding": round(att_slide / (n_l / 2), 2)},
            "context_mode": A.context_mode,
+           "prompt_gemms": ("hipBLASLt algorithms from neural_amd/tunableop_mi355x.csv (PyTorch TunableOp, tuning off)"
+                            if tuned_read else "hipBLASLt default heuristic"),
            **({"context_prefill_ms": round(t_ctx * 1e3, 1), "prefill_tok_s": round(ctx / t_ctx, 1),
                "prefill_chunk": A.prefill_chunk} if A.context_mode == "prefill" else
               {"context_steps_per_s": round((ctx - 1) / t_ctx, 1)})}
@@ -1146,6 +1153,9 @@ def main():
                     help="model: build the context by prompt processing (default) or token by token through the "
                          "decode step")
     ap.add_argument("--prefill-chunk", type=int, default=4096, help="model: prompt block size of the prefill")
+    ap.add_argument("--prompt-gemms", choices=("tuned", "default"), default="tuned",
+                    help="model: the context prefill's library GEMMs take the committed TunableOp choices (tuned) or "
+                         "hipBLASLt's default heuristic")
     ap.add_argument("--attn-split", type=int, default=0,
                     help="model: key chunks of full-attention layers (0: attention.auto_split of the cache rows)")
     ap.add_argument("--sliding-split", type=int, default=1, help="model: key chunks of sliding-window layers")

@@ -20,6 +20,7 @@ Shapes (reference neural/moe/layout.py and the model config): hidden 2880, 64 qu
 from __future__ import annotations
 
 import math
+import os
 from dataclasses import dataclass, field
 
 import torch
@@ -96,6 +97,30 @@ class DecodeWeights:
     def to(self, dev):
         return DecodeWeights(self.embed.to(dev), [ly.to(dev) for ly in self.layers], self.final_w.to(dev),
                              self.lm_head.to(dev))
+
+
+TUNED_PROMPT_GEMMS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tunableop_mi355x.csv")
+
+
+def use_tuned_prompt_gemms(enable: bool = True) -> bool:
+    """Let the prompt path's library GEMMs (F.linear: Q|K|V, o_proj, router logits) take the hipBLASLt algorithms
+    measured fastest on MI355X for configuration 4's 4,096-token prompt instead of the library's default choice.
+    This is PyTorch's TunableOp with tuning off: the choices come from ``TUNED_PROMPT_GEMMS``, whose validator lines
+    name the PyTorch, HIP, hipBLASLt and rocBLAS versions and the gfx950 target.  On a mismatch, and for a shape the
+    file does not hold, the library's default algorithm runs.  The setting is process-wide, like every TunableOp
+    setting.  TunableOp's own results file is pointed at the temp directory, so the committed file is only read.
+    Returns whether the file's results were taken; with enable=False, TunableOp is switched off and it returns
+    False."""
+    import tempfile
+
+    import torch.cuda.tunable as tun
+    if not enable:
+        tun.enable(False)
+        return False
+    tun.enable(True)
+    tun.tuning_enable(False)
+    tun.set_filename(os.path.join(tempfile.gettempdir(), "neural_amd_tunableop.csv"))
+    return bool(tun.read_file(TUNED_PROMPT_GEMMS))
 
 
 def random_weights(n_layers: int = N_LAYERS, vocab: int = VOCAB, device="cpu", seed: int = 0, std: float = 0.02,

@@ -15,7 +15,8 @@ Bars (the oracle is oracle/model_oracle.py, pinned against transformers' gpt-oss
   flips, attention over the GPU's own 4352-position (full) or 128-row ring (sliding) cache within 1e-2 relative /
   2e-2 absolute, the routing exactly or a near tie, the experts within the expert tolerance;
 - at sampled rows of the 4096-token prefill (layers 0, 1, 34, 35) the same stage checks on the prompt path, the
-  attention against the fp64 closed form at the row's position;
+  attention against the fp64 closed form at the row's position; the prefill runs its library GEMMs as the bench
+  does, with the committed TunableOp choices (model.use_tuned_prompt_gemms);
 - the decode tail alone at the full vocabulary: logits against the oracle, the first index among tied rows planted
   more than 1024 partial keys apart (the argmax reduces 12,568 partial keys in several passes), and the sampling
   tail's draw against the oracle's Gumbel-max over the kernel's own logits;
@@ -79,7 +80,7 @@ class Experts:
 def full():
     import torch
     from neural_amd import synth
-    from neural_amd.model import DecodeModel, random_weights, yarn_inv_freq
+    from neural_amd.model import DecodeModel, random_weights, use_tuned_prompt_gemms, yarn_inv_freq
     from neural_amd.moe.experts import ResidentExperts
     from neural_amd.moe.layout import GPTOSS_LAYOUT_T950 as LT
 
@@ -96,6 +97,8 @@ def full():
     model = DecodeModel(w, rx, smax=CTX + NEW + 8)          # the bench's key split: auto_split(4360) = 18 chunks
     assert model.n_split == 18
     prompt = np.random.default_rng(4096).integers(0, w.vocab, CTX)
+    # the bench's prompt GEMMs: the committed hipBLASLt choices for these shapes (the stage checks below pin them)
+    assert use_tuned_prompt_gemms(), "the committed TunableOp results do not match this PyTorch / ROCm build"
     trace = []
     model.prefill(prompt, trace=trace)
     torch.cuda.synchronize()
@@ -106,6 +109,7 @@ def full():
                  inv=inv.numpy(), att=att, first_state=(_f(model.mid)[0], _f(model.g)[0]),
                  first_tok=int(model.seq[CTX].item()))
     print("full model prefilled", flush=True)
+    use_tuned_prompt_gemms(False)
     yield state
     state.clear()
     del model, rx, pool, w, bgu, bdn, trace
