@@ -24,6 +24,7 @@ struct AttnLds {
                                                    // re-read rows 0..7, so D rows 8..15 repeat rows 0..7
   float mx[4][kRep];                               // per-wave row maxima
   float sm[4][kRep];                               // per-wave row sums
+  float sink[kRep];                                // the KV group's sinks (written in the first pass)
   uint32_t last;                                   // split-K: this workgroup combines
 };
 
@@ -182,12 +183,20 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
   // A operand: query rows (row n of the head for lanes n < 8, zero rows otherwise), d = 8g.. and 32 + 8g..
   const uint16_t* qrow = q + ((long long)b * kNQ + h * kRep + min(n, kRep - 1)) * kHD;
   uint4 qa0 = make_uint4(0, 0, 0, 0), qa1 = make_uint4(0, 0, 0, 0);
-  // the sinks of the rows this thread finishes (constant weights), read now so that no dependent load waits at the end
+  // the sinks of the rows this thread finishes (constant weights), read now so that no dependent load waits at the
+  // end.  FUSED (a kernel at its register limit): threads 0..7 hold one each until the first pass puts them in LDS,
+  // where the finish and the combine read them (held in registers until the end, one was spilled and its reload
+  // waited for every outstanding load); otherwise each thread holds its rows' sinks.
   const uint16_t* sk = sinks + h * kRep;
-  float sink_r[2];                                 // single chunk: rows 4 (g & 1) + 2 (g >> 1) + k (the finish)
+  uint16_t sk_own = 0;
+  float sink_r[2] = {0.f, 0.f}, sink_c = 0.f;      // single chunk: rows 4 (g & 1) + 2 (g >> 1) + k; the combine's row
+  if constexpr (FUSED) {
+    sk_own = sk[min(tid, kRep - 1)];
+  } else {
 #pragma unroll
-  for (int k = 0; k < 2; ++k) sink_r[k] = bf16_to_f32(sk[4 * (g & 1) + 2 * (g >> 1) + k]);
-  const float sink_c = bf16_to_f32(sk[wave + 4 * (lane >> 5)]);   // the combine's row (attn_combine)
+    for (int k = 0; k < 2; ++k) sink_r[k] = bf16_to_f32(sk[4 * (g & 1) + 2 * (g >> 1) + k]);
+    sink_c = bf16_to_f32(sk[wave + 4 * (lane >> 5)]);
+  }
   if constexpr (!FUSED) {
     qa0 = *reinterpret_cast<const uint4*>(qrow + 8 * g);
     qa1 = *reinterpret_cast<const uint4*>(qrow + 32 + 8 * g);
@@ -247,6 +256,7 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
         }
       }
     }
+    if (FUSED && k0 == c0 && tid < kRep) L.sink[tid] = bf16_to_f32(sk_own);   // read after the pass's first barrier
     // ---- V rows to LDS as they are (the P V step reads them transposed; stored before the scores, so that their
     // registers are free by then): lane (g, n) holds d = 8g..8g+7 and 32+8g.. of key 16 kb + n of this wave's 64
 #pragma unroll
@@ -356,7 +366,13 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
     __syncthreads();                               // LDS is rewritten by the next sub-chunk
   }
 
-  // ---- finish: a single chunk writes the output; otherwise publish the partial, the last arriver combines
+  // ---- finish: a single chunk writes the output; otherwise publish the partial, the last arriver combines.  FUSED:
+  // the lane's indices are formed again (in this scope) from an opaque copy of the thread id, since the ones from
+  // before the loop would be held across it (one was spilled, and its reload waited for every outstanding load).
+  int tidf = tid;
+  if constexpr (FUSED) asm volatile("" : "+v"(tidf));
+  {
+  const int lane = tidf & 63, wave = tidf >> 6, g = lane >> 4, n = lane & 15;
   uint16_t* orow = out + ((long long)b * kNQ + h * kRep) * kHD;
   if (ns == 1) {
     // rows 4 (g & 1) + r: lanes g < 2 finish r = 0, 1, lanes g >= 2 r = 2, 3.  The upper lanes already hold those
@@ -367,7 +383,7 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
     for (int k = 0; k < 2; ++k) {
       const float av = up ? acc[2 + k] : acc[k];
       const int r = up ? 2 + k : k, row = 4 * (g & 1) + r;
-      const float sink = sink_r[k];
+      const float sink = FUSED ? L.sink[row] : sink_r[k];
       const float mr = up ? m_run[2 + k] : m_run[k], sr = up ? s_run[2 + k] : s_run[k];
       const float m = fmaxf(sink, mr);
       const float a = mr == kNegInf ? 0.f : expf(mr - m);
@@ -410,7 +426,12 @@ NA_DEVICE void decode_attn_body(AttnLds& L, int blk, const uint16_t* __restrict_
   }
   __syncthreads();
   if (!last) return;
-  attn_combine(head, ns, sink_c, orow, FUSED ? hs.att + bh * (kRep * kHD / 2) : nullptr, FUSED ? launch_tag(hs.gen) : 0u);
+  // FUSED: an empty chunk ran no pass, so its LDS holds no sinks (then the sink is read here: rare, an empty chunk
+  // arriving last)
+  const int crow = wave + 4 * (lane >> 5);                     // the combine's row (attn_combine)
+  const float sink_row = !FUSED ? sink_c : c0 < c1 ? L.sink[crow] : bf16_to_f32(sk[crow]);
+  attn_combine(head, ns, sink_row, orow, FUSED ? hs.att + bh * (kRep * kHD / 2) : nullptr, FUSED ? launch_tag(hs.gen) : 0u);
+  }
 }
 
 }  // namespace na
