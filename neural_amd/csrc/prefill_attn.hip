@@ -79,7 +79,7 @@ struct KeySrc {
 
 // QT query tiles of 16 per wave: 16 * QT tokens per workgroup; KEYS keys per tile (64 or 128).
 template <int QT, int KEYS>
-__global__ __launch_bounds__(kThreads, QT == 1 ? 2 : 1) void k_prefill_attn(
+__global__ __launch_bounds__(kThreads, QT == 1 ? 4 : 2) void k_prefill_attn(
     const uint16_t* __restrict__ q, KeySrc src, const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out,
     int T, float scaling, int window) {
   constexpr int kQB = 16 * QT, kKeys = KEYS, KT = KEYS / 16, KS = KEYS / 32, KP = KEYS / 64;
@@ -122,33 +122,39 @@ __global__ __launch_bounds__(kThreads, QT == 1 ? 2 : 1) void k_prefill_attn(
     for (int dt = 0; dt < 4; ++dt) acc[dt][qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  // Staging, per 64 keys of the tile: K row key tid / 8, dims 8 (tid % 8) (a wave reads 8 whole rows); V key
-  // tid % 64, dims 8 (tid / 64), stored as it is (the P V step reads it transposed).
+  // Staging, per 64 keys of a tile: K row key tid / 8, dims 8 (tid % 8) (a wave reads 8 whole rows); V key
+  // tid % 64, dims 8 (tid / 64), stored as it is (the P V step reads it transposed).  Tile it + 1's loads are in
+  // flight over tile it's work (two LDS buffers, one barrier per tile).  Every global load and LDS store is
+  // unconditional: rows past hi - 1 read row hi - 1, and the store of tile it + 1 goes to buffer (it + 1) & 1, which
+  // no wave reads in iteration it (its last reads were in iteration it - 1, before that iteration's barrier).
   const int kk = tid >> 3, kd = tid & 7;
   const int vk = tid & 63, vd = tid >> 6;
   uint4 kreg[KP], vreg[KP];
-  auto load_tile = [&](int s0) {
+  auto load_k = [&](int s0) {
 #pragma unroll
     for (int p = 0; p < KP; ++p) {
-      const int jk = s0 + 64 * p + kk, jv = s0 + 64 * p + vk;
+      const int jk = s0 + 64 * p + kk;
       kreg[p] = *reinterpret_cast<const uint4*>(src.krow(jk < hi ? jk : hi - 1) + 8 * kd);
+    }
+  };
+  auto load_v = [&](int s0) {
+#pragma unroll
+    for (int p = 0; p < KP; ++p) {
+      const int jv = s0 + 64 * p + vk;
       vreg[p] = *reinterpret_cast<const uint4*>(src.vrow(jv < hi ? jv : hi - 1) + 8 * vd);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_k = [&](int buf) {
 #pragma unroll
-    for (int p = 0; p < KP; ++p) {
-      *reinterpret_cast<uint4*>(L.k[buf] + (64 * p + kk) * kKPitch + 16 * kd) = kreg[p];
-      *reinterpret_cast<uint4*>(L.v[buf] + (64 * p + vk) * kVPitch + 16 * vd) = vreg[p];
-    }
+    for (int p = 0; p < KP; ++p) *reinterpret_cast<uint4*>(L.k[buf] + (64 * p + kk) * kKPitch + 16 * kd) = kreg[p];
+  };
+  auto store_v = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < KP; ++p) *reinterpret_cast<uint4*>(L.v[buf] + (64 * p + vk) * kVPitch + 16 * vd) = vreg[p];
   };
 
-  // One tile.  MASK = false: every key of the tile is visible to every query of the block (below the first
-  // query, and inside the window of the last), so no key is masked.
-  auto tile = [&](auto mask_c, int buf, int s0) {
-    constexpr bool MASK = decltype(mask_c)::value;
-    // ---- S^T = K Q^T: tile (kt, qt), lane holds keys s0 + 16 kt + 4 g + r of query column n
-    float s[KT][QT][4];
+  // S^T = K Q^T of the tile in K buffer buf: tile (kt, qt), lane holds keys 16 kt + 4 g + r of query column n
+  auto scores = [&](int buf, float (&s)[KT][QT][4]) {
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
       const uint8_t* kr = L.k[buf] + (16 * kt + n) * kKPitch + 16 * g;
@@ -163,10 +169,17 @@ __global__ __launch_bounds__(kThreads, QT == 1 ? 2 : 1) void k_prefill_attn(
         for (int r = 0; r < 4; ++r) s[kt][qt][r] = d[r];
       }
     }
-    // ---- mask, online softmax (per query column), P^T fragments
-    uint4 pf[KS][QT];
+  };
+
+  // One tile (keys s0 .., buffer buf): S^T, the online softmax, then O^T += V^T P^T.  MASK = false: every key of
+  // the tile is visible to every query of the block (below the first query, and inside the window of the last), so
+  // no key is masked.
+  auto tile = [&](auto mask_c, int buf, int s0) {
+    constexpr bool MASK = decltype(mask_c)::value;
+    float s[KT][QT][4];
+    scores(buf, s);
     bool moved = false;
-    float alpha[QT];
+    float alpha[QT], mnew[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       const int qp = qpos0 + 16 * qt + n;
@@ -186,10 +199,22 @@ __global__ __launch_bounds__(kThreads, QT == 1 ? 2 : 1) void k_prefill_attn(
       }
       mx = fmaxf(mx, lane_xor16(mx));                 // the 4 lanes of column n (VALU lane swaps, no LDS)
       mx = fmaxf(mx, lane_xor32(mx));
-      const float m_new = fmaxf(m[qt], mx * sl2);     // finite: m starts at the sink
-      alpha[qt] = __builtin_amdgcn_exp2f(m[qt] - m_new);
-      moved |= m_new != m[qt];
-      m[qt] = m_new;
+      mnew[qt] = fmaxf(m[qt], mx * sl2);              // finite: m starts at the sink
+      alpha[qt] = __builtin_amdgcn_exp2f(m[qt] - mnew[qt]);
+      moved |= mnew[qt] != m[qt];
+      m[qt] = mnew[qt];
+    }
+    // O^T *= alpha, skipped when no column of the wave moved its maximum (then every alpha is exactly 1)
+    if (__builtin_amdgcn_ballot_w64(moved)) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) acc[dt][qt] *= alpha[qt];
+    }
+    // P^T fragments: P = exp2(s sl2 - m') rounded to bf16; the row sums take the unrounded values
+    uint4 pf[KS][QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
       float ls = l[qt] * alpha[qt];
       uint32_t pk[KT][2];
 #pragma unroll
@@ -197,7 +222,7 @@ __global__ __launch_bounds__(kThreads, QT == 1 ? 2 : 1) void k_prefill_attn(
         float e[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          e[r] = __builtin_amdgcn_exp2f(fmaf(s[kt][qt][r], sl2, -m_new));   // exp2(-inf) = +0 for masked keys
+          e[r] = __builtin_amdgcn_exp2f(fmaf(s[kt][qt][r], sl2, -mnew[qt]));   // exp2(-inf) = +0 for masked keys
           ls += e[r];
         }
         pk[kt][0] = pack_bf16x2(e[0], e[1]);
@@ -207,13 +232,6 @@ __global__ __launch_bounds__(kThreads, QT == 1 ? 2 : 1) void k_prefill_attn(
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)                 // step ks: keys 32 ks + 4g.., 32 ks + 16 + 4g..
         pf[ks][qt] = make_uint4(pk[2 * ks][0], pk[2 * ks][1], pk[2 * ks + 1][0], pk[2 * ks + 1][1]);
-    }
-    // O^T *= alpha, skipped when no column of the wave moved its maximum (then every alpha is exactly 1)
-    if (__builtin_amdgcn_ballot_w64(moved)) {
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) acc[dt][qt] *= alpha[qt];
     }
     // ---- O^T += V^T P^T over the 32-key steps.  V^T's A operand (lane (g, n): dim 16 dt + n, keys 32 ks + 4 g ..
     // + 3 and 32 ks + 16 + 4 g .. + 3) comes from two transposing LDS reads (ds_read_b64_tr_b16): in each 16-lane
@@ -238,21 +256,38 @@ __global__ __launch_bounds__(kThreads, QT == 1 ? 2 : 1) void k_prefill_attn(
     }
   };
 
-  load_tile(lo);
-  store_tile(0);
-  __syncthreads();
-  for (int it = 0; it < nt; ++it) {
-    const int buf = it & 1;
-    const int s0 = lo + it * kKeys;
-    if (it + 1 < nt) load_tile(s0 + kKeys);
-    const bool inner = s0 + kKeys <= qpos0 && (window == 0 || s0 > qlast - window);   // uniform
-    if (inner)
-      tile(std::false_type{}, buf, s0);
-    else
-      tile(std::true_type{}, buf, s0);
-    if (it + 1 < nt) store_tile(buf ^ 1);
-    __syncthreads();
+  // Tiles [ia, ib) need no mask: s0 + kKeys <= qpos0 (it < nA) and, on sliding layers, s0 > qlast - window
+  // (it >= nB).  Masking is exact for every tile, so the split only has to leave no masked key unmasked.
+  const int nA = (qpos0 - lo) / kKeys;                // qpos0 >= lo
+  int nB = 0;
+  if (window > 0) {
+    const int x = qlast - window - lo;
+    nB = x < 0 ? 0 : x / kKeys + 1;
   }
+  const int ia = min(nA, nB), ib = nA;
+
+  load_k(lo);
+  load_v(lo);
+  store_k(0);
+  store_v(0);
+  __syncthreads();
+  // the masked and unmasked tiles as separate loops (one code path per loop, no copies of the accumulators between
+  // two paths at every tile)
+  int it = 0;
+  auto run = [&](auto mask_c, int end) {
+    for (; it < end; ++it) {
+      const int s0 = lo + it * kKeys, buf = it & 1;
+      load_k(s0 + kKeys);
+      load_v(s0 + kKeys);
+      tile(mask_c, buf, s0);
+      store_k(buf ^ 1);
+      store_v(buf ^ 1);
+      __syncthreads();
+    }
+  };
+  run(std::true_type{}, ia);
+  run(std::false_type{}, ib);
+  run(std::true_type{}, nt);
 
   // ---- o = acc / l; lane holds dims 16 dt + 4 g + r of query column n
 #pragma unroll
