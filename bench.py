@@ -64,12 +64,15 @@ N_LAYERS, N_EXPERTS, TOPK, H = 36, 128, 4, 2880
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 KERNEL_SOURCES = ("neural_amd/csrc/common.h", "neural_amd/csrc/t950.h", "neural_amd/csrc/handoff.h",
                   "neural_amd/csrc/topk.h", "neural_amd/csrc/tiles.hip", "neural_amd/csrc/moe_decode.hip")
+# the attention block's sources (its traffic entries name them in "sources")
+ATTN_BLOCK_SOURCES = ("neural_amd/csrc/common.h", "neural_amd/csrc/handoff.h", "neural_amd/csrc/attention_dev.h",
+                      "neural_amd/csrc/core.hip")
 
 
-def sources_sha256():
+def sources_sha256(files=KERNEL_SOURCES):
     import hashlib
     h = hashlib.sha256()
-    for f in KERNEL_SOURCES:
+    for f in files:
         with open(os.path.join(ROOT, f), "rb") as fh:
             h.update(fh.read())
     return h.hexdigest()
@@ -91,12 +94,22 @@ def measured_traffic(kernel, layout, batch, k_split):
 
 
 def traffic_entry(tab, kernel, layout, batch, k_split):
-    """The committed profile entry of a workload, if it was measured on the current kernel sources."""
-    sha = sources_sha256()
+    """The committed profile entry of a workload, if it was measured on the current kernel sources (the files the
+    entry lists under "sources", else the expert kernels' KERNEL_SOURCES)."""
     for e in tab.get("entries", []):
         if (e["kernel"], e["layout"], e["batch"], e["k_split"]) == (kernel, layout, batch, k_split):
-            return e if e["sources_sha256"] == sha else None
+            files = tuple(e.get("sources", KERNEL_SOURCES))
+            return e if e["sources_sha256"] == sources_sha256(files) else None
     return None
+
+
+def attn_block_entry(kind):
+    """The attention block's committed traffic entry for a sliding or full layer of configuration 4, or None."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            return traffic_entry(json.load(fh), "k_attn_block", kind, 1, 0)
+    except (OSError, ValueError):
+        return None
 
 
 def rocprof_avg_us(kernel, layout, batch, k_split):
@@ -532,12 +545,23 @@ def run_model(A, pool, dev):
         per = {k: {"avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": int(b),
                    "gbps": round(b / us / 1e3, 1), "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
                for k, (us, b) in kinds.items()}
+        # measured HBM bytes and rocprof durations per launch (profiles/traffic.json, current block sources)
+        ents = {k: attn_block_entry(k) for k in kinds}
+        for k, e in ents.items():
+            if e is not None:
+                per[k]["traffic"] = int(e["hbm_bytes_per_launch"])
+                per[k]["rocprof_avg_launch_us"] = e["rocprof_avg_us"]
+                per[k]["frac_rocprof"] = round(kinds[k][1] / e["rocprof_avg_us"] / 1e3 / HBM_PEAK_GBS, 4)
+        pair_traffic = (sum(int(e["hbm_bytes_per_launch"]) for e in ents.values())
+                        if all(e is not None for e in ents.values()) else None)
+        log(f"model: attention block traffic per (sliding, full) launch pair: {pair_traffic}")
         tot_b, tot_us = sum(b for _, b in kinds.values()), sum(us for us, _ in kinds.values())
         attn_roof = {"kernel": "k_attn_block", "bound": "hbm", "achieved": round(tot_b / tot_us / 1e3, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 4),
-                     "traffic": None, **per,
+                     "traffic": pair_traffic, **per,
                      "workload": f"config4 decode step at context {ctx}: one sliding and one full layer's block "
-                                 "(18 of each per token), dispatch-stamped events over eager steps"}
+                                 "(18 of each per token), dispatch-stamped events over eager steps; achieved, frac "
+                                 "and traffic per pair of launches (one of each kind)"}
     dense = N_LAYERS * 2 * (5120 * 2880 + 2880 * 4096 + 128 * 2880) + 2 * 201088 * 2880
     experts = N_LAYERS * TOPK * SLOT_ALGO_BYTES
     kv = 2 * 2 * 8 * 64 * (18 * (ctx + n_new / 2) + 18 * 128)
